@@ -1,0 +1,141 @@
+/*
+ * sepal_mlp_hip: the W8g128 quantized-MLP path of Sepal-Runner on MI355X (gfx950), as a C ABI.
+ *
+ * Conventions (the reference's C ABI, runner/include/sepal/c_api.h:5-8 and runner/src/capi/c_api.cpp:28-43, applied to
+ * its kernel-level interface, runner/cuda/src/device.hpp:1-29):
+ *   - every entry point returns int32 status: 0 on success, non-zero on failure; the message of the last failure on the
+ *     calling thread is sepal_hip_last_error(); no exception crosses the ABI;
+ *   - SEPAL_HIP_EINVAL for a violated shape / stride / alignment / null rule (the reference throws
+ *     std::invalid_argument there), SEPAL_HIP_ELAUNCH for a failed launch (std::runtime_error there);
+ *   - all pointers are device pointers the caller owns (hipMalloc'd or from PyTorch); strides count elements;
+ *   - work is enqueued on `stream` (a hipStream_t, NULL for the default stream) and the call returns without waiting;
+ *   - a row count of 0 is a no-op;
+ *   - a row's result depends on that row, the weights and K only, never on the other rows of the batch or the tile
+ *     picked, within one path (large-M and small-M paths round the fp32 sums in different orders);
+ *   - calls on one device are serialised by the caller (the library keeps one workspace per device; the reference's
+ *     engine holds one stream and a call lock for the same reason, runner/src/capi/c_api.cpp:20-24).
+ *
+ * Element types (`*_type` arguments): SEPAL_HIP_F32 = float32, SEPAL_HIP_BF16 = bfloat16, SEPAL_HIP_F16 = binary16.
+ * Epilogues: STORE y = acc; ADD y = y + acc (one float32 addition); SWIGLU: the weight rows are gate and up interleaved
+ * in blocks of 64 (packed row 128b + r is gate row 64b + r, packed row 128b + 64 + r is up row 64b + r), N = 2I and
+ * Y[t, 64b + r] = silu(acc[t, 128b + r]) * acc[t, 128b + 64 + r].
+ */
+#ifndef SEPAL_MLP_HIP_H
+#define SEPAL_MLP_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SEPAL_HIP_API_VERSION 1
+
+/* Exported from the shared library (built with hidden visibility; only these symbols are public). */
+#if defined(__GNUC__)
+#define SEPAL_HIP_API __attribute__((visibility("default")))
+#else
+#define SEPAL_HIP_API
+#endif
+
+enum { SEPAL_HIP_OK = 0, SEPAL_HIP_EINVAL = 1, SEPAL_HIP_ELAUNCH = 2, SEPAL_HIP_ENOMEM = 3 };
+enum { SEPAL_HIP_F32 = 0, SEPAL_HIP_BF16 = 1, SEPAL_HIP_F16 = 2 };
+enum { SEPAL_HIP_STORE = 0, SEPAL_HIP_ADD = 1, SEPAL_HIP_SWIGLU = 2 };
+/* Quantizer rounding rules. DIVIDE: s = m / 127, q = rint(w / s), zero group s = 0 (the gpu-w8g packer,
+ * runner/cuda/src/gemm_simt_kernels.cu:266-286). RECIPROCAL: s = m > 0 ? m / 127 : 1, q = nearbyint(w * (1 / s))
+ * (cpu-q8, runner/src/cpu/gemm.cpp:103-106, 141-163, 288-303). Both clamp to [-127, 127]. */
+enum { SEPAL_HIP_RULE_DIVIDE = 0, SEPAL_HIP_RULE_RECIPROCAL = 1 };
+
+/* ABI version (c_api.h sepal_api_version) and the last error message of this thread (c_api.h sepal_last_error). */
+SEPAL_HIP_API int32_t sepal_hip_api_version(void);
+SEPAL_HIP_API const char* sepal_hip_last_error(void);
+
+/* Load-time weight packer: int8 with one float32 scale per row and group of 128 values of k.
+ * src [rows, ld_src] of src_type (fp16 and bf16 are widened to float32 exactly first); q [rows, ld_q] int8;
+ * s [rows, ld_s] float32 (K/128 used). K a multiple of 128; ld_src, ld_q multiples of 16; 16-byte aligned src and q.
+ * Replaces launch_quantize_group_s8 (runner/cuda/src/gemm_simt_kernels.hpp:62-67, .cu:334-343) with rule DIVIDE, and
+ * the I8 branch of PanelPacker::pack (runner/src/cpu/gemm.cpp:137-164) with rule RECIPROCAL (row-major instead of
+ * panels). */
+SEPAL_HIP_API int32_t sepal_hip_quantize_group_s8(const void* src, int32_t src_type, size_t ld_src, int8_t* q, size_t ld_q, float* s,
+                                    size_t ld_s, size_t rows, size_t k, int32_t rule, void* stream);
+
+/* The same packer for a SwiGLU gate/up pair (gate, up [inter, ld_src] each): writes the 2*inter packed rows in the
+ * 64-row interleave of the fused multiply. inter a multiple of 64. Replaces the interleaving copy of put_simt
+ * (runner/cuda/src/cuda_engine.cpp:597-611, pack_gate_up_source gemm_simt_kernels.hpp:72-77) followed by
+ * launch_quantize_group_s8 (cuda_engine.cpp:622-623); with rule RECIPROCAL, pack_weight_swiglu (gemm.cpp:209-245). */
+SEPAL_HIP_API int32_t sepal_hip_quantize_gate_up_s8(const void* gate, const void* up, int32_t src_type, size_t ld_src, int8_t* q,
+                                      size_t ld_q, float* s, size_t ld_s, size_t inter, size_t k, int32_t rule,
+                                      void* stream);
+
+/* gpu-w8g multiply: Y = epilogue(X * dequant(W)^T), W int8 [N, ld_w] with scales s [N, ld_s] per 128 values of k.
+ * X [T, ld_x] of x_type BF16 or F16 (the contraction runs on MFMA in that type with float32 accumulation, the weight
+ * bytes widened exactly; each 128-group's partial sum is scaled by its weight scale in float32; the reference's float32
+ * X is taken as bf16 when it holds bf16 values, as the engine's bf16 activations do). Y float32 [T, ld_y] for STORE/ADD; for SWIGLU Y is [T, ld_y] of y_type
+ * (F32, BF16 or F16) with N/2 columns. K a multiple of 128; N a multiple of 128 for SWIGLU, of 16 otherwise; ld_x,
+ * ld_w multiples of 16; ld_y a multiple of 4; 16-byte aligned pointers. `config` -1 picks a path by T (small-M at T <= 64);
+ * 0 forces the large-M tiled path, 1 the small-M weight-streaming path, 2 the small-M path without a split of K (the
+ * whole K of a column block in one block; K at most 2048 / ceil(T/16) for w8g, 4096 / ceil(T/16) for q8).
+ * Replaces launch_gemm_simt with SimtWeight::Int8Group (runner/cuda/src/gemm_simt_kernels.hpp:53-56, .cu:312-332). */
+SEPAL_HIP_API int32_t sepal_hip_gemm_w8g(const void* x, int32_t x_type, size_t ld_x, const int8_t* w, size_t ld_w, const float* s,
+                           size_t ld_s, void* y, int32_t y_type, size_t ld_y, size_t t, size_t n, size_t k,
+                           int32_t epilogue, int32_t config, void* stream);
+
+/* 1 when sepal_hip_gemm_w8g takes these dimensions and strides (pointer alignment is the caller's), else 0.
+ * Replaces gemm_simt_supports (runner/cuda/src/gemm_simt_kernels.hpp:58-60). */
+SEPAL_HIP_API int32_t sepal_hip_gemm_w8g_supports(int32_t x_type, size_t n, size_t k, size_t ld_x, size_t ld_w, size_t ld_y,
+                                    int32_t epilogue);
+
+/* Dynamic activation quantizer (rule RECIPROCAL): per row and block of `block` values (128, or cols for one scale per
+ * token) amax = max|x|, s = amax > 0 ? amax / 127 : 1, q = clamp(nearbyint(x * (1 / s))). x [rows, ld_x] of x_type;
+ * q int8 [rows, ld_q]; scales float32 [rows, ld_s] (cols/block used). cols a multiple of 128 (of 16 when block = cols);
+ * strides multiples of 16, 16-byte aligned x and q.
+ * Replaces the I8 branch of pack_acts (runner/src/cpu/gemm.cpp:285-306) and launch_quantize_rows_s8
+ * (runner/cuda/src/gemm_s8_kernels.hpp:20-27; that one rounds by 127/amax, this one by the cpu-q8 rule). */
+SEPAL_HIP_API int32_t sepal_hip_quantize_rows_s8(const void* x, int32_t x_type, size_t ld_x, int8_t* q, size_t ld_q, float* scales,
+                                   size_t ld_s, size_t rows, size_t cols, size_t block, void* stream);
+
+/* gpu-q8w multiply: int8 X [T, ld_x] with activation scales xs [T, ld_xs] per `act_block` values (128 or K) times int8
+ * W [N, ld_w] with scales ws [N, ld_ws] per 128 values. Per 128-group the int32 sum S_b is exact (int8 MFMA).
+ * act_block = 128 (cpu-q8 I8_Z): y = f_0 * (ws_0 * xs_0), then y = fma(f_b, ws_b * xs_b, y), f_b = float(S_b), so the
+ * large-M path reproduces cpu-q8 bit for bit. act_block = K (one scale per token): y = (f_0 * ws_0, then
+ * fma(f_b, ws_b, y)) * xs. Epilogues STORE / ADD / SWIGLU (silu with the cpu-q8 exp polynomial); Y float32
+ * [T, ld_y], or y_type for SWIGLU. K a multiple of 128; strides multiples of 16; 16-byte aligned pointers. `config` as
+ * sepal_hip_gemm_w8g; the small-M path splits K across blocks when N is narrow, which keeps the sums exact but adds
+ * the splits' partial chains (within tolerance, not bit for bit); config 2 keeps the chain whole (bit for bit).
+ * Replaces kernel_i8_z + finish_tile (runner/src/cpu/gemm_kernels_avx512.cpp:67-115, gemm.cpp:417-447, 545-569) and
+ * launch_gemm_s8 (runner/cuda/src/gemm_s8_kernels.hpp:43-49) with per-group scales. */
+SEPAL_HIP_API int32_t sepal_hip_gemm_q8(const int8_t* xq, size_t ld_x, const float* xs, size_t ld_xs, size_t act_block,
+                          const int8_t* w, size_t ld_w, const float* ws, size_t ld_ws, void* y, int32_t y_type,
+                          size_t ld_y, size_t t, size_t n, size_t k, int32_t epilogue, int32_t config, void* stream);
+
+/* The exact int32 per-group sums of the q8 multiply, sums[g][t][n] = sum over k in group g of xq[t,k] * w[n,k]
+ * (int8 MFMA, the same kernel body as sepal_hip_gemm_q8's large-M path). For checking the integer part bit for bit. */
+SEPAL_HIP_API int32_t sepal_hip_q8_group_sums(const int8_t* xq, size_t ld_x, const int8_t* w, size_t ld_w, int32_t* sums, size_t t,
+                                size_t n, size_t k, void* stream);
+
+/* RMSNorm of rows with the cpu-q8 summation order (runner/src/cpu/elementwise.cpp:22-59): y = (x * inv) * w1 with
+ * inv = (float)(1 / sqrt(mean(x^2) + eps)); w1 NULL means ones. x float32 [rows, ld_x]; y of y_type [rows, ld_y].
+ * cols a multiple of 8. Glue of the layer stack (the MLP input norm, cuda_engine.cpp:1915-1918). */
+SEPAL_HIP_API int32_t sepal_hip_rmsnorm_rows(const float* x, size_t ld_x, void* y, int32_t y_type, size_t ld_y, const float* w1,
+                               size_t rows, size_t cols, double eps, void* stream);
+
+/* float32 -> bfloat16, nearest even, NaN stays NaN (launch_float_to_bf16, runner/cuda/src/gemm_simt_kernels.hpp:69-70). */
+SEPAL_HIP_API int32_t sepal_hip_float_to_bf16(const float* src, uint16_t* dst, size_t count, void* stream);
+
+/* One MLP block per layer for `layers` layers, the engine's MLP step (runner/cuda/src/cuda_engine.cpp:1915-1934) with
+ * the stack glue of the benchmark: x_0 = x; for each layer l: H = SwiGLU(x_l * Wgu_l^T) (path `kind`), Y_l = H * Wd_l^T
+ * (float32, written to y), and, when l + 1 < layers, x_{l+1} = bf16(RMSNorm(Y_l)) (identity weight, eps).
+ * kind 0 = w8g (x bf16 [T, hidden]; H binary16), kind 1 = q8 (x bf16; activations quantised per act_block before each
+ * multiply; H float32). Weight arrays hold `layers` device pointers each: gate_up int8 [2*inter, hidden] + scales
+ * [2*inter, hidden/128]; down int8 [hidden, inter] + scales [hidden, inter/128]. x is overwritten with the last layer's
+ * input. Scratch (H, quantised activations) comes from the library's per-device workspace. */
+SEPAL_HIP_API int32_t sepal_hip_mlp_stack(int32_t kind, size_t layers, size_t t, size_t hidden, size_t inter, void* x,
+                            const int8_t* const* w_gate_up, const float* const* s_gate_up, const int8_t* const* w_down,
+                            const float* const* s_down, float* y, size_t act_block, double eps, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,357 @@
+// The C ABI of sepal_mlp_hip (declarations and conventions: include/sepal_mlp_hip.h).
+//
+// Error handling follows runner/src/capi/c_api.cpp:28-43: every entry point runs its body under one guard that turns
+// std::invalid_argument into SEPAL_HIP_EINVAL and any other exception into SEPAL_HIP_ELAUNCH, keeping the message in a
+// thread-local string for sepal_hip_last_error(). The argument checks restate the reference's requirement functions
+// (gemm_simt_supports, runner/cuda/src/gemm_simt_kernels.cu:303-310; the checks of launch_quantize_rows_s8 and
+// launch_gemm_s8, runner/cuda/src/gemm_s8_kernels.cu:472-546) for the shapes this library takes.
+#include <hip/hip_runtime.h>
+
+#include <cstring>
+#include <mutex>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "common.hpp"
+#include "gemm_kernels.hpp"
+
+namespace sepal::hip {
+
+namespace {
+
+thread_local std::string g_error;
+
+template <class F>
+int32_t guarded(F&& f) {
+    try {
+        f();
+        return SEPAL_HIP_OK;
+    } catch (const std::invalid_argument& e) {
+        g_error = e.what();
+        return SEPAL_HIP_EINVAL;
+    } catch (const std::bad_alloc& e) {
+        g_error = std::string("out of memory: ") + e.what();
+        return SEPAL_HIP_ENOMEM;
+    } catch (const std::exception& e) {
+        g_error = e.what();
+        return SEPAL_HIP_ELAUNCH;
+    } catch (...) {
+        g_error = "unknown error";
+        return SEPAL_HIP_ELAUNCH;
+    }
+}
+
+inline hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
+
+bool valid_type(int t) { return t == SEPAL_HIP_F32 || t == SEPAL_HIP_BF16 || t == SEPAL_HIP_F16; }
+
+struct Workspace {
+    void* ptr = nullptr;
+    std::size_t bytes = 0;
+};
+std::mutex g_ws_mutex;
+std::vector<Workspace> g_ws;
+
+} // namespace
+
+void* workspace(std::size_t bytes, hipStream_t stream) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) throw LaunchError("hipGetDevice failed");
+    std::lock_guard<std::mutex> lock(g_ws_mutex);
+    if (g_ws.size() <= static_cast<std::size_t>(dev)) g_ws.resize(static_cast<std::size_t>(dev) + 1);
+    Workspace& w = g_ws[static_cast<std::size_t>(dev)];
+    if (w.bytes < bytes) {
+        // the old buffer may still be read by work queued on the stream: wait for it before freeing
+        if (w.ptr != nullptr) {
+            if (hipStreamSynchronize(stream) != hipSuccess) throw LaunchError("hipStreamSynchronize failed");
+            (void)hipFree(w.ptr);
+            w.ptr = nullptr;
+            w.bytes = 0;
+        }
+        const std::size_t grown = bytes < (std::size_t{64} << 20) ? (std::size_t{64} << 20) : bytes;
+        if (hipMalloc(&w.ptr, grown) != hipSuccess) throw std::bad_alloc();
+        if (hipMemset(w.ptr, 0, grown) != hipSuccess) throw LaunchError("hipMemset of the workspace failed");
+        w.bytes = grown;
+    }
+    return w.ptr;
+}
+
+namespace {
+
+void check_gemm_common(const char* who, const void* x, std::size_t ld_x, const void* w, std::size_t ld_w,
+                       const void* s, std::size_t ld_s, const void* y, std::size_t ld_y, std::size_t n, std::size_t k,
+                       int epilogue) {
+    const std::string w_ = who;
+    require(x != nullptr && w != nullptr && s != nullptr && y != nullptr, w_ + ": null pointer");
+    require(epilogue == SEPAL_HIP_STORE || epilogue == SEPAL_HIP_ADD || epilogue == SEPAL_HIP_SWIGLU, w_ + ": unknown epilogue");
+    require(n != 0 && k != 0 && k % 128 == 0, w_ + ": K must be a non-zero multiple of 128 and N non-zero");
+    require(ld_x >= k && ld_w >= k && ld_x % 16 == 0 && ld_w % 16 == 0, w_ + ": row strides of X and W must be multiples of 16 and at least K");
+    require(ld_s >= k / 128, w_ + ": the scale row stride must hold K/128 scales");
+    require(aligned16(x) && aligned16(w) && aligned16(y), w_ + ": X, W and Y must be 16-byte aligned");
+    if (epilogue == SEPAL_HIP_SWIGLU) require(n % 128 == 0 && ld_y >= n / 2, w_ + ": SwiGLU needs N a multiple of 128 and ld_y >= N/2");
+    else require(n % 16 == 0 && ld_y >= n, w_ + ": N must be a multiple of 16 and ld_y >= N");
+    require(ld_y % 4 == 0, w_ + ": ld_y must be a multiple of 4");
+    require(n < 0x7FFFFFFFu && k < 0x7FFFFFFFu, w_ + ": dimension beyond 2^31");
+}
+
+} // namespace
+} // namespace sepal::hip
+
+using namespace sepal::hip;
+
+extern "C" {
+
+int32_t sepal_hip_api_version(void) { return SEPAL_HIP_API_VERSION; }
+
+const char* sepal_hip_last_error(void) { return g_error.c_str(); }
+
+int32_t sepal_hip_quantize_group_s8(const void* src, int32_t src_type, size_t ld_src, int8_t* q, size_t ld_q, float* s,
+                                    size_t ld_s, size_t rows, size_t k, int32_t rule, void* stream) {
+    return guarded([&] {
+        require(valid_type(src_type), "quantize_group_s8: unknown source type");
+        require(rule == SEPAL_HIP_RULE_DIVIDE || rule == SEPAL_HIP_RULE_RECIPROCAL, "quantize_group_s8: unknown rule");
+        require(k % 128 == 0, "quantize_group_s8: K must be a multiple of 128");
+        if (rows == 0 || k == 0) return;
+        require(src != nullptr && q != nullptr && s != nullptr, "quantize_group_s8: null pointer");
+        require(ld_src >= k && ld_q >= k && ld_s >= k / 128 && ld_src % 16 == 0 && ld_q % 16 == 0,
+                "quantize_group_s8: strides must be at least K (K/128 for scales) and multiples of 16");
+        require(aligned16(src) && aligned16(q), "quantize_group_s8: src and q must be 16-byte aligned");
+        launch_quantize_group(src, src_type, ld_src, nullptr, q, ld_q, s, ld_s, rows, k, rule, 0, as_stream(stream));
+    });
+}
+
+int32_t sepal_hip_quantize_gate_up_s8(const void* gate, const void* up, int32_t src_type, size_t ld_src, int8_t* q,
+                                      size_t ld_q, float* s, size_t ld_s, size_t inter, size_t k, int32_t rule,
+                                      void* stream) {
+    return guarded([&] {
+        require(valid_type(src_type), "quantize_gate_up_s8: unknown source type");
+        require(rule == SEPAL_HIP_RULE_DIVIDE || rule == SEPAL_HIP_RULE_RECIPROCAL, "quantize_gate_up_s8: unknown rule");
+        require(k % 128 == 0 && inter % 64 == 0, "quantize_gate_up_s8: K must be a multiple of 128 and inter of 64");
+        if (inter == 0 || k == 0) return;
+        require(gate != nullptr && up != nullptr && q != nullptr && s != nullptr, "quantize_gate_up_s8: null pointer");
+        require(ld_src >= k && ld_q >= k && ld_s >= k / 128 && ld_src % 16 == 0 && ld_q % 16 == 0,
+                "quantize_gate_up_s8: strides must be at least K (K/128 for scales) and multiples of 16");
+        require(aligned16(gate) && aligned16(up) && aligned16(q), "quantize_gate_up_s8: pointers must be 16-byte aligned");
+        launch_quantize_group(gate, src_type, ld_src, up, q, ld_q, s, ld_s, 2 * inter, k, rule, inter, as_stream(stream));
+    });
+}
+
+int32_t sepal_hip_gemm_w8g_supports(int32_t x_type, size_t n, size_t k, size_t ld_x, size_t ld_w, size_t ld_y,
+                                    int32_t epilogue) {
+    if (x_type != SEPAL_HIP_BF16 && x_type != SEPAL_HIP_F16) return 0;
+    if (n == 0 || k == 0 || k % 128 != 0 || ld_x < k || ld_w < k || ld_x % 16 != 0 || ld_w % 16 != 0 || ld_y % 4 != 0) return 0;
+    if (epilogue == SEPAL_HIP_SWIGLU) return n % 128 == 0 && ld_y >= n / 2 ? 1 : 0;
+    if (epilogue != SEPAL_HIP_STORE && epilogue != SEPAL_HIP_ADD) return 0;
+    return n % 16 == 0 && ld_y >= n ? 1 : 0;
+}
+
+int32_t sepal_hip_gemm_w8g(const void* x, int32_t x_type, size_t ld_x, const int8_t* w, size_t ld_w, const float* s,
+                           size_t ld_s, void* y, int32_t y_type, size_t ld_y, size_t t, size_t n, size_t k,
+                           int32_t epilogue, int32_t config, void* stream) {
+    return guarded([&] {
+        require(x_type == SEPAL_HIP_BF16 || x_type == SEPAL_HIP_F16, "gemm_w8g: X must be bf16 or binary16");
+        require(valid_type(y_type), "gemm_w8g: unknown output type");
+        require(epilogue == SEPAL_HIP_SWIGLU || y_type == SEPAL_HIP_F32, "gemm_w8g: Store and Add write float32");
+        require(config >= -1 && config <= 2, "gemm_w8g: config must be -1, 0, 1 or 2");
+        check_gemm_common("gemm_w8g", x, ld_x, w, ld_w, s, ld_s, y, ld_y, n, k, epilogue);
+        if (t == 0) return;
+        require(t < 0x7FFFFFFFu, "gemm_w8g: dimension beyond 2^31");
+        if (config >= 1) require(t <= kSmallM, "gemm_w8g: the small-M path takes at most 64 rows");
+        GemmArgs a;
+        a.x = x;
+        a.x_type = x_type;
+        a.ld_x = ld_x;
+        a.w = w;
+        a.ld_w = ld_w;
+        a.s = s;
+        a.ld_s = ld_s;
+        a.y = y;
+        a.y_type = y_type;
+        a.ld_y = ld_y;
+        a.t = t;
+        a.n = n;
+        a.k = k;
+        a.epilogue = epilogue;
+        a.config = config == 2 ? 1 : config;
+        a.force_splits = config == 2 ? 1 : 0;
+        launch_gemm_w8g(a, as_stream(stream));
+    });
+}
+
+int32_t sepal_hip_quantize_rows_s8(const void* x, int32_t x_type, size_t ld_x, int8_t* q, size_t ld_q, float* scales,
+                                   size_t ld_s, size_t rows, size_t cols, size_t block, void* stream) {
+    return guarded([&] {
+        require(valid_type(x_type), "quantize_rows_s8: unknown source type");
+        require(block == 128 || block == cols, "quantize_rows_s8: block must be 128 or cols");
+        if (rows == 0 || cols == 0) return;
+        require(x != nullptr && q != nullptr && scales != nullptr, "quantize_rows_s8: null pointer");
+        require(block == 128 ? cols % 128 == 0 : cols % 16 == 0, "quantize_rows_s8: cols must be a multiple of 128 (of 16 per token)");
+        require(ld_x >= cols && ld_q >= cols && ld_x % 16 == 0 && ld_q % 16 == 0 && ld_s >= cols / block,
+                "quantize_rows_s8: strides must be multiples of 16 and hold the row");
+        require(aligned16(x) && aligned16(q), "quantize_rows_s8: pointers must be 16-byte aligned");
+        launch_quantize_rows(x, x_type, ld_x, q, ld_q, scales, ld_s, rows, cols, block, as_stream(stream));
+    });
+}
+
+int32_t sepal_hip_gemm_q8(const int8_t* xq, size_t ld_x, const float* xs, size_t ld_xs, size_t act_block,
+                          const int8_t* w, size_t ld_w, const float* ws, size_t ld_ws, void* y, int32_t y_type,
+                          size_t ld_y, size_t t, size_t n, size_t k, int32_t epilogue, int32_t config, void* stream) {
+    return guarded([&] {
+        require(valid_type(y_type), "gemm_q8: unknown output type");
+        require(epilogue == SEPAL_HIP_SWIGLU || y_type == SEPAL_HIP_F32, "gemm_q8: Store and Add write float32");
+        require(config >= -1 && config <= 2, "gemm_q8: config must be -1, 0, 1 or 2");
+        check_gemm_common("gemm_q8", xq, ld_x, w, ld_w, ws, ld_ws, y, ld_y, n, k, epilogue);
+        require(act_block == 128 || act_block == k, "gemm_q8: act_block must be 128 or K");
+        require(xs != nullptr && ld_xs >= k / act_block, "gemm_q8: activation scales missing or stride too small");
+        if (t == 0) return;
+        require(t < 0x7FFFFFFFu, "gemm_q8: dimension beyond 2^31");
+        if (config >= 1) require(t <= kSmallM, "gemm_q8: the small-M path takes at most 64 rows");
+        GemmArgs a;
+        a.x = xq;
+        a.ld_x = ld_x;
+        a.xs = xs;
+        a.ld_xs = ld_xs;
+        a.act_block = act_block;
+        a.w = w;
+        a.ld_w = ld_w;
+        a.s = ws;
+        a.ld_s = ld_ws;
+        a.y = y;
+        a.y_type = y_type;
+        a.ld_y = ld_y;
+        a.t = t;
+        a.n = n;
+        a.k = k;
+        a.epilogue = epilogue;
+        a.config = config == 2 ? 1 : config;
+        a.force_splits = config == 2 ? 1 : 0;
+        launch_gemm_q8(a, as_stream(stream));
+    });
+}
+
+int32_t sepal_hip_q8_group_sums(const int8_t* xq, size_t ld_x, const int8_t* w, size_t ld_w, int32_t* sums, size_t t,
+                                size_t n, size_t k, void* stream) {
+    return guarded([&] {
+        require(xq != nullptr && w != nullptr && sums != nullptr, "q8_group_sums: null pointer");
+        require(k % 128 == 0 && k != 0 && n != 0, "q8_group_sums: K must be a non-zero multiple of 128");
+        require(ld_x >= k && ld_w >= k && ld_x % 16 == 0 && ld_w % 16 == 0, "q8_group_sums: strides");
+        require(aligned16(xq) && aligned16(w), "q8_group_sums: pointers must be 16-byte aligned");
+        if (t == 0) return;
+        GemmArgs a;
+        a.x = xq;
+        a.ld_x = ld_x;
+        a.w = w;
+        a.ld_w = ld_w;
+        a.s = nullptr;
+        a.t = t;
+        a.n = n;
+        a.k = k;
+        a.sums = sums;
+        launch_q8_group_sums(a, as_stream(stream));
+    });
+}
+
+int32_t sepal_hip_rmsnorm_rows(const float* x, size_t ld_x, void* y, int32_t y_type, size_t ld_y, const float* w1,
+                               size_t rows, size_t cols, double eps, void* stream) {
+    return guarded([&] {
+        require(valid_type(y_type), "rmsnorm_rows: unknown output type");
+        require(cols % 8 == 0, "rmsnorm_rows: cols must be a multiple of 8");
+        if (rows == 0 || cols == 0) return;
+        require(x != nullptr && y != nullptr, "rmsnorm_rows: null pointer");
+        require(ld_x >= cols && ld_y >= cols, "rmsnorm_rows: strides below cols");
+        require(eps > 0.0, "rmsnorm_rows: eps must be positive");
+        launch_rmsnorm(x, ld_x, y, y_type, ld_y, w1, rows, cols, eps, as_stream(stream));
+    });
+}
+
+int32_t sepal_hip_float_to_bf16(const float* src, uint16_t* dst, size_t count, void* stream) {
+    return guarded([&] {
+        if (count == 0) return;
+        require(src != nullptr && dst != nullptr, "float_to_bf16: null pointer");
+        launch_f32_to_bf16(src, dst, count, as_stream(stream));
+    });
+}
+
+int32_t sepal_hip_mlp_stack(int32_t kind, size_t layers, size_t t, size_t hidden, size_t inter, void* x,
+                            const int8_t* const* w_gate_up, const float* const* s_gate_up, const int8_t* const* w_down,
+                            const float* const* s_down, float* y, size_t act_block, double eps, void* stream) {
+    return guarded([&] {
+        require(kind == 0 || kind == 1, "mlp_stack: kind must be 0 (w8g) or 1 (q8)");
+        require(hidden % 128 == 0 && inter % 128 == 0 && hidden != 0 && inter != 0, "mlp_stack: hidden and inter must be multiples of 128");
+        require(w_gate_up != nullptr && s_gate_up != nullptr && w_down != nullptr && s_down != nullptr && x != nullptr && y != nullptr,
+                "mlp_stack: null pointer");
+        require(kind == 0 || act_block == 128 || act_block == 0, "mlp_stack: act_block must be 128 or 0 (one scale per token)");
+        if (layers == 0 || t == 0) return;
+        const hipStream_t st = as_stream(stream);
+        // workspace: H [t, inter] (binary16 for w8g, float32 for q8); q8 also xq [t, max(h, i)] int8 and scales
+        const std::size_t h_bytes = t * inter * (kind == 0 ? 2 : 4);
+        const std::size_t kmax = hidden > inter ? hidden : inter;
+        const std::size_t q_bytes = kind == 1 ? t * kmax : 0;
+        const std::size_t s_bytes = kind == 1 ? t * (kmax / 128) * 4 : 0;
+        const std::size_t off_h = kScratchOffset;
+        const std::size_t off_q = off_h + (h_bytes + 255) / 256 * 256;
+        const std::size_t off_s = off_q + (q_bytes + 255) / 256 * 256;
+        char* ws = static_cast<char*>(workspace(off_s + s_bytes, st));
+        void* h = ws + off_h;
+        std::int8_t* xq = reinterpret_cast<std::int8_t*>(ws + off_q);
+        float* xsc = reinterpret_cast<float*>(ws + off_s);
+        for (std::size_t l = 0; l < layers; ++l) {
+            GemmArgs gu;
+            gu.t = t;
+            gu.n = 2 * inter;
+            gu.k = hidden;
+            gu.w = w_gate_up[l];
+            gu.ld_w = hidden;
+            gu.s = s_gate_up[l];
+            gu.ld_s = hidden / 128;
+            gu.y = h;
+            gu.ld_y = inter;
+            gu.epilogue = SEPAL_HIP_SWIGLU;
+            GemmArgs dn;
+            dn.t = t;
+            dn.n = hidden;
+            dn.k = inter;
+            dn.w = w_down[l];
+            dn.ld_w = inter;
+            dn.s = s_down[l];
+            dn.ld_s = inter / 128;
+            dn.y = y;
+            dn.ld_y = hidden;
+            dn.epilogue = SEPAL_HIP_STORE;
+            if (kind == 0) {
+                gu.x = x;
+                gu.x_type = SEPAL_HIP_BF16;
+                gu.ld_x = hidden;
+                gu.y_type = SEPAL_HIP_F16;
+                launch_gemm_w8g(gu, st);
+                dn.x = h;
+                dn.x_type = SEPAL_HIP_F16;
+                dn.ld_x = inter;
+                dn.y_type = SEPAL_HIP_F32;
+                launch_gemm_w8g(dn, st);
+            } else {
+                const std::size_t ab_h = act_block == 0 ? hidden : 128, ab_i = act_block == 0 ? inter : 128;
+                launch_quantize_rows(x, SEPAL_HIP_BF16, hidden, xq, hidden, xsc, hidden / ab_h, t, hidden, ab_h, st);
+                gu.x = xq;
+                gu.ld_x = hidden;
+                gu.xs = xsc;
+                gu.ld_xs = hidden / ab_h;
+                gu.act_block = ab_h;
+                gu.y_type = SEPAL_HIP_F32;
+                launch_gemm_q8(gu, st);
+                launch_quantize_rows(h, SEPAL_HIP_F32, inter, xq, inter, xsc, inter / ab_i, t, inter, ab_i, st);
+                dn.x = xq;
+                dn.ld_x = inter;
+                dn.xs = xsc;
+                dn.ld_xs = inter / ab_i;
+                dn.act_block = ab_i;
+                dn.y_type = SEPAL_HIP_F32;
+                launch_gemm_q8(dn, st);
+            }
+            if (l + 1 < layers) launch_rmsnorm(y, hidden, x, SEPAL_HIP_BF16, hidden, nullptr, t, hidden, eps, st);
+        }
+    });
+}
+
+} // extern "C"

@@ -1,0 +1,49 @@
+// Launchers of the HIP kernels (internal). The C ABI (capi.cpp) validates the arguments and calls these.
+#pragma once
+
+#include "common.hpp"
+
+namespace sepal::hip {
+
+// Rows at or below which the multiplies take the weight-streaming small-M path.
+inline constexpr std::size_t kSmallM = 64;
+
+// K values of X one small-M split holds in LDS (64 KB of 16-bit values, a multiple of 128).
+__host__ __device__ constexpr int small_kr_max(int mt) { return (2048 / mt) / 128 * 128; }
+
+struct GemmArgs {
+    const void* x = nullptr;
+    int x_type = SEPAL_HIP_BF16;
+    std::size_t ld_x = 0;
+    const std::int8_t* w = nullptr;
+    std::size_t ld_w = 0;
+    const float* s = nullptr;
+    std::size_t ld_s = 0;
+    void* y = nullptr;
+    int y_type = SEPAL_HIP_F32;
+    std::size_t ld_y = 0;
+    std::size_t t = 0, n = 0, k = 0;
+    int epilogue = SEPAL_HIP_STORE;
+    int config = -1;
+    int force_splits = 0;  // small-M: > 0 forces the number of K splits (tests)
+    // q8 only
+    const float* xs = nullptr;
+    std::size_t ld_xs = 0;
+    std::size_t act_block = 128;
+    std::int32_t* sums = nullptr;  // group-sum mode
+};
+
+void launch_gemm_w8g(const GemmArgs& a, hipStream_t stream);
+void launch_gemm_q8(const GemmArgs& a, hipStream_t stream);
+void launch_q8_group_sums(const GemmArgs& a, hipStream_t stream);
+
+void launch_quantize_group(const void* src, int src_type, std::size_t ld_src, const void* src_up, std::int8_t* q,
+                           std::size_t ld_q, float* s, std::size_t ld_s, std::size_t rows, std::size_t k, int rule,
+                           std::size_t inter, hipStream_t stream);
+void launch_quantize_rows(const void* x, int x_type, std::size_t ld_x, std::int8_t* q, std::size_t ld_q, float* scales,
+                          std::size_t ld_s, std::size_t rows, std::size_t cols, std::size_t block, hipStream_t stream);
+void launch_rmsnorm(const float* x, std::size_t ld_x, void* y, int y_type, std::size_t ld_y, const float* w1,
+                    std::size_t rows, std::size_t cols, double eps, hipStream_t stream);
+void launch_f32_to_bf16(const float* src, std::uint16_t* dst, std::size_t count, hipStream_t stream);
+
+} // namespace sepal::hip

@@ -1,0 +1,510 @@
+// gpu-q8w on gfx950: int8 activations (one scale per row and 128 values, or per row) times int8 weights (one scale per
+// row and 128 values), int32 per-group sums on the int8 MFMA, float32 scale chain over the groups.
+//
+// Semantics (cpu-q8 I8_Z, runner/src/cpu/gemm_kernels_avx512.cpp:67-115 with finish_tile, gemm.cpp:417-447):
+//   S_b = sum over the 128 k of group b of xq * wq            exact int32 (MFMA i32 accumulate)
+//   act_block 128:  y = f_0 * (ws_0 * xs_0); y = fma(f_b, ws_b * xs_b, y) for b >= 1, f_b = float(S_b)
+//   act_block K:    y = (f_0 * ws_0; y = fma(f_b, ws_b, y)) * xs           (one activation scale per token)
+//   epilogue: Store, Add (y + acc), SwiGLU (silu with the cpu-q8 exp polynomial; gate/up rows in the 64-row interleave)
+// Every step is one IEEE operation in the reference's order, so the large-M path equals cpu-q8 bit for bit.
+//
+// Large-M path: 128 x 256 tiles of 8 waves, each 64 x 64 outputs (2 x 2 blocks of MFMA 32x32x32 i8); K in steps of
+// one group (128 bytes) through a double-buffered LDS tile; the int32 sums of a group are turned into the float chain
+// in registers before the next group starts (a second set of accumulators holds the chain).
+// Small-M path: weight streaming as in gemm_w8g.hip with MFMA 16x16x64 i8; a split of K keeps the sums exact but
+// adds the splits' partial chains in split order (within tolerance, not bit for bit).
+#include "common.hpp"
+#include "gemm_kernels.hpp"
+
+namespace sepal::hip {
+namespace q8 {
+
+enum { MODE_CHAIN = 0, MODE_SUMS = 1 };
+
+__device__ __forceinline__ i32x16 mfma_i8_32(const u32x4 a, const u32x4 b, i32x16 c) {
+    return __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(i32x4, a), __builtin_bit_cast(i32x4, b), c, 0, 0, 0);
+}
+__device__ __forceinline__ i32x4 mfma_i8_16(const u32x4 a, const u32x4 b, i32x4 c) {
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i32x4, a), __builtin_bit_cast(i32x4, b), c, 0, 0, 0);
+}
+
+// One link of the chain: the first group multiplies, later groups fuse.
+template <bool PER_TOKEN>
+__device__ __forceinline__ float chain(float acc, int sum, float ws, float xs, bool first) {
+    const float f = static_cast<float>(sum);
+    const float sc = PER_TOKEN ? ws : __fmul_rn(ws, xs);
+    return first ? __fmul_rn(f, sc) : __builtin_fmaf(f, sc, acc);
+}
+
+template <int EP, int YT>
+__device__ __forceinline__ void put(void* y, std::size_t ld_y, int row, int col, float v) {
+    float* yf = static_cast<float*>(y);
+    const std::size_t idx = static_cast<std::size_t>(row) * ld_y + col;
+    if constexpr (EP == SEPAL_HIP_ADD) yf[idx] = __fadd_rn(yf[idx], v);
+    else yf[idx] = v;
+}
+
+struct Params {
+    const signed char* x;   // [T, ld_x]
+    std::size_t ld_x;
+    const float* xs;        // [T, ld_xs]
+    std::size_t ld_xs;
+    int act_shift;          // log2(act_block / 128) when per-group; unused per token
+    const signed char* w;   // [N, ld_w]
+    std::size_t ld_w;
+    const float* ws;        // [N, ld_ws]
+    std::size_t ld_ws;
+    void* y;
+    std::size_t ld_y;
+    int t, n, k;
+    int tiles_m, tiles_n;
+    std::int32_t* sums;     // MODE_SUMS: [groups][T][N]
+    // small-M
+    int splits, groups_per_split, col_blocks;
+    float* partial;
+    unsigned* counters;
+};
+
+__device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int& tm, int& tn) {
+    const int total = tiles_m * tiles_n;
+    const int q = total / 8, r = total % 8;
+    const int xcd = bid % 8, idx = bid / 8;
+    const int id = xcd * q + min(xcd, r) + idx;
+    constexpr int GM = 4;
+    const int per_group = GM * tiles_n;
+    const int group = id / per_group, first_m = group * GM;
+    const int gm = min(tiles_m - first_m, GM);
+    const int in_group = id % per_group;
+    tm = first_m + in_group % gm;
+    tn = in_group / gm;
+}
+
+// 128-byte LDS rows of 8 chunks; chunk c of row r stored at c ^ (r & 7).
+__device__ __forceinline__ int sw8(int r) { return r & 7; }
+
+template <int EP, int YT, bool PER_TOKEN, int MODE>
+__global__ void __launch_bounds__(512) gemm_big(const Params p) {
+    constexpr int BM = 128, BN = 256, NT = 512;
+    constexpr int XCH = BM * 8 / NT;   // 2
+    constexpr int WCH = BN * 8 / NT;   // 4
+    __shared__ __align__(16) u32x4 lds_x[2][BM * 8];
+    __shared__ __align__(16) u32x4 lds_w[2][BN * 8];
+    __shared__ float lds_xs[2][BM];
+
+    const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
+    const int wm = wave % 2, wn = wave / 2;
+    int tm, tn;
+    tile_of(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int groups = p.k / 128;
+
+    u32x4 xr[XCH], wr[WCH];
+    float xsr = 0.0f;
+    const auto gload = [&](int g) {
+        const int k0 = g * 128;
+#pragma unroll
+        for (int e = 0; e < XCH; ++e) {
+            const int id = tid + e * NT, row = id / 8, c = id % 8;
+            const int m = m0 + row;
+            xr[e] = m < p.t ? *reinterpret_cast<const u32x4*>(p.x + static_cast<std::size_t>(m) * p.ld_x + k0 + 16 * c) : u32x4{0u, 0u, 0u, 0u};
+        }
+#pragma unroll
+        for (int e = 0; e < WCH; ++e) {
+            const int id = tid + e * NT, row = id / 8, c = id % 8;
+            const int nn = n0 + row;
+            wr[e] = nn < p.n ? *reinterpret_cast<const u32x4*>(p.w + static_cast<std::size_t>(nn) * p.ld_w + k0 + 16 * c) : u32x4{0u, 0u, 0u, 0u};
+        }
+        if (!PER_TOKEN && MODE == MODE_CHAIN && tid < BM) {
+            const int m = m0 + tid;
+            xsr = m < p.t ? p.xs[static_cast<std::size_t>(m) * p.ld_xs + (g >> p.act_shift)] : 0.0f;
+        }
+    };
+    const auto lstore = [&](int buf) {
+#pragma unroll
+        for (int e = 0; e < XCH; ++e) {
+            const int id = tid + e * NT, row = id / 8, c = id % 8;
+            lds_x[buf][row * 8 + (c ^ sw8(row))] = xr[e];
+        }
+#pragma unroll
+        for (int e = 0; e < WCH; ++e) {
+            const int id = tid + e * NT, row = id / 8, c = id % 8;
+            lds_w[buf][row * 8 + (c ^ sw8(row))] = wr[e];
+        }
+        if (!PER_TOKEN && MODE == MODE_CHAIN && tid < BM) lds_xs[buf][tid] = xsr;
+    };
+
+    const int ib = wn / 2, hh = wn % 2;
+    const int colrel[2] = {128 * ib + 32 * hh + lane % 32, 128 * ib + 64 + 32 * hh + lane % 32};
+    int col[2];
+    const float* wsrow[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        col[j] = n0 + colrel[j];
+        wsrow[j] = col[j] < p.n ? p.ws + static_cast<std::size_t>(col[j]) * p.ld_ws : nullptr;
+    }
+
+    float acc[2][2][16];
+    i32x16 sacc[2][2];
+    const i32x16 zero16 = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    float wsn[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) wsn[j] = wsrow[j] != nullptr ? wsrow[j][0] : 0.0f;
+
+    gload(0);
+    lstore(0);
+    __syncthreads();
+    for (int g = 0; g < groups; ++g) {
+        const int buf = g & 1;
+        if (g + 1 < groups) gload(g + 1);
+        float wsc[2] = {wsn[0], wsn[1]};
+        if (g + 1 < groups)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) wsn[j] = wsrow[j] != nullptr ? wsrow[j][g + 1] : 0.0f;
+        const u32x4* tx = lds_x[buf];
+        const u32x4* tw = lds_w[buf];
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+            const int c = 2 * st + lane / 32;
+            u32x4 a[2], b[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int row = wm * 64 + i * 32 + lane % 32;
+                a[i] = tx[row * 8 + (c ^ sw8(row))];
+            }
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int row = colrel[j];
+                b[j] = tw[row * 8 + (c ^ sw8(row))];
+            }
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) sacc[i][j] = mfma_i8_32(a[i], b[j], st == 0 ? zero16 : sacc[i][j]);
+        }
+        if constexpr (MODE == MODE_SUMS) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int row = m0 + wm * 64 + i * 32 + 8 * (r / 4) + 4 * (lane / 32) + (r % 4);
+                    if (row >= p.t) continue;
+#pragma unroll
+                    for (int j = 0; j < 2; ++j)
+                        if (col[j] < p.n) p.sums[(static_cast<std::size_t>(g) * p.t + row) * p.n + col[j]] = sacc[i][j][r];
+                }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int rl = wm * 64 + i * 32 + 8 * (r / 4) + 4 * (lane / 32) + (r % 4);
+                    const float xsv = PER_TOKEN ? 1.0f : lds_xs[buf][rl];
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) acc[i][j][r] = chain<PER_TOKEN>(acc[i][j][r], sacc[i][j][r], wsc[j], xsv, g == 0);
+                }
+        }
+        if (g + 1 < groups) lstore(buf ^ 1);
+        __syncthreads();
+    }
+    if constexpr (MODE == MODE_SUMS) return;
+
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int row = m0 + wm * 64 + i * 32 + 8 * (r / 4) + 4 * (lane / 32) + (r % 4);
+            if (row >= p.t) continue;
+            float v0 = acc[i][0][r], v1 = acc[i][1][r];
+            if constexpr (PER_TOKEN) {
+                const float xs = p.xs[static_cast<std::size_t>(row) * p.ld_xs];
+                v0 = __fmul_rn(v0, xs);
+                v1 = __fmul_rn(v1, xs);
+            }
+            if constexpr (EP == SEPAL_HIP_SWIGLU) {
+                const int f = n0 / 2 + 64 * ib + 32 * hh + lane % 32;
+                store_out<YT>(p.y, static_cast<std::size_t>(row) * p.ld_y + f, swiglu_cephes(v0, v1));
+            } else {
+                if (col[0] < p.n) put<EP, YT>(p.y, p.ld_y, row, col[0], v0);
+                if (col[1] < p.n) put<EP, YT>(p.y, p.ld_y, row, col[1], v1);
+            }
+        }
+    }
+}
+
+// ---- small-M ---------------------------------------------------------------------------------------------------------
+
+template <int EP>
+__device__ __forceinline__ int small_col(int cb, int slot) {
+    if constexpr (EP == SEPAL_HIP_SWIGLU) {
+        const int b = cb / 2, h = cb % 2;
+        return slot < 32 ? 128 * b + 32 * h + slot : 128 * b + 64 + 32 * h + (slot - 32);
+    } else {
+        return 64 * cb + slot;
+    }
+}
+
+// int8 X slice [16 MT][KR] in LDS (KR <= 4096 / MT bytes) and its activation scales.
+__host__ __device__ constexpr int q8_kr_max(int mt) { return (4096 / mt) / 128 * 128; }
+
+template <int EP, int YT, bool PER_TOKEN, int MT>
+__global__ void __launch_bounds__(256) gemm_small(const Params p) {
+    constexpr int KR_MAX = q8_kr_max(MT);
+    __shared__ __align__(16) signed char lds_x[16 * MT * KR_MAX];
+    __shared__ float lds_xs[16 * MT][KR_MAX / 128];
+    __shared__ float red[4][16 * MT][16];
+
+    const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
+    const int cb = blockIdx.x % p.col_blocks, ks = blockIdx.x / p.col_blocks;
+    const int g0 = ks * p.groups_per_split;
+    const int g1 = min(g0 + p.groups_per_split, p.k / 128);
+    const int kbeg = g0 * 128, klen = (g1 - g0) * 128;
+    {
+        const int cpr = klen / 16;
+        for (int id = tid; id < 16 * MT * cpr; id += 256) {
+            const int r = id / cpr, c = id % cpr;
+            u32x4 v = u32x4{0u, 0u, 0u, 0u};
+            if (r < p.t) v = *reinterpret_cast<const u32x4*>(p.x + static_cast<std::size_t>(r) * p.ld_x + kbeg + 16 * c);
+            *reinterpret_cast<u32x4*>(&lds_x[r * KR_MAX + 16 * c]) = v;
+        }
+        if (!PER_TOKEN) {
+            const int ng = g1 - g0;
+            for (int id = tid; id < 16 * MT * ng; id += 256) {
+                const int r = id / ng, gg = id % ng;
+                lds_xs[r][gg] = r < p.t ? p.xs[static_cast<std::size_t>(r) * p.ld_xs + ((g0 + gg) >> p.act_shift)] : 0.0f;
+            }
+        }
+    }
+    __syncthreads();
+
+    const int slot0 = wave * 16;
+    const int colw = small_col<EP>(cb, slot0 + lane % 16);
+    const bool col_ok = colw < p.n;
+    const signed char* wrow = p.w + static_cast<std::size_t>(col_ok ? colw : 0) * p.ld_w;
+    const float* wsrow = p.ws + static_cast<std::size_t>(col_ok ? colw : 0) * p.ld_ws;
+
+    float acc[MT][4];
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[i][r] = 0.0f;
+
+    constexpr int PF = 4;
+    u32x4 wbuf[PF][2];
+    const auto wload = [&](int g, u32x4 (&dst)[2]) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int k = g * 128 + 64 * h + 16 * (lane / 16);
+            dst[h] = col_ok ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wrow + k)) : u32x4{0u, 0u, 0u, 0u};
+        }
+    };
+#pragma unroll
+    for (int i = 0; i < PF; ++i)
+        if (g0 + i < g1) wload(g0 + i, wbuf[i]);
+
+    const i32x4 zero4 = {0, 0, 0, 0};
+    for (int gb = g0; gb < g1; gb += PF) {
+#pragma unroll
+        for (int u = 0; u < PF; ++u) {
+            const int g = gb + u;
+            if (g >= g1) break;
+            const float wsv = col_ok ? wsrow[g] : 0.0f;
+            const u32x4 cur0 = wbuf[u][0], cur1 = wbuf[u][1];
+            if (g + PF < g1) wload(g + PF, wbuf[u]);
+            const int kl = (g - g0) * 128 + 16 * (lane / 16);
+#pragma unroll
+            for (int i = 0; i < MT; ++i) {
+                const signed char* xr = &lds_x[(16 * i + lane % 16) * KR_MAX + kl];
+                const u32x4 a0 = *reinterpret_cast<const u32x4*>(xr);
+                const u32x4 a1 = *reinterpret_cast<const u32x4*>(xr + 64);
+                i32x4 s = mfma_i8_16(a0, cur0, zero4);
+                s = mfma_i8_16(a1, cur1, s);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int row = 16 * i + 4 * (lane / 16) + r;
+                    const float xsv = PER_TOKEN ? 1.0f : lds_xs[row][g - g0];
+                    acc[i][r] = chain<PER_TOKEN>(acc[i][r], s[r], wsv, xsv, g == g0);
+                }
+            }
+        }
+    }
+
+    const int ncols_pad = p.col_blocks * 64;
+    if (p.splits > 1) {
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int row = 16 * i + 4 * (lane / 16) + r;
+                p.partial[(static_cast<std::size_t>(ks) * 16 * MT + row) * ncols_pad + cb * 64 + slot0 + lane % 16] = acc[i][r];
+            }
+        __threadfence();
+        __syncthreads();
+        __shared__ unsigned last;
+        if (tid == 0) {
+            const unsigned prev = atomicAdd(&p.counters[cb], 1u);
+            last = prev == static_cast<unsigned>(p.splits - 1) ? 1u : 0u;
+        }
+        __syncthreads();
+        if (last == 0u) return;
+        __threadfence();
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int row = 16 * i + 4 * (lane / 16) + r;
+                float v = 0.0f;
+                for (int s = 0; s < p.splits; ++s) {
+                    const float pv = p.partial[(static_cast<std::size_t>(s) * 16 * MT + row) * ncols_pad + cb * 64 + slot0 + lane % 16];
+                    v = s == 0 ? pv : __fadd_rn(v, pv);
+                }
+                acc[i][r] = v;
+            }
+        if (tid == 0) p.counters[cb] = 0u;
+    }
+    if constexpr (PER_TOKEN) {
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int row = 16 * i + 4 * (lane / 16) + r;
+                acc[i][r] = __fmul_rn(acc[i][r], row < p.t ? p.xs[static_cast<std::size_t>(row) * p.ld_xs] : 0.0f);
+            }
+    }
+
+    if constexpr (EP == SEPAL_HIP_SWIGLU) {
+        if (wave >= 2) {
+#pragma unroll
+            for (int i = 0; i < MT; ++i)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) red[wave - 2][16 * i + 4 * (lane / 16) + r][lane % 16] = acc[i][r];
+        }
+        __syncthreads();
+        if (wave < 2) {
+            const int f = (cb / 2) * 64 + (cb % 2) * 32 + wave * 16 + lane % 16;
+#pragma unroll
+            for (int i = 0; i < MT; ++i)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int row = 16 * i + 4 * (lane / 16) + r;
+                    if (row < p.t && 2 * f < p.n)
+                        store_out<YT>(p.y, static_cast<std::size_t>(row) * p.ld_y + f, swiglu_cephes(acc[i][r], red[wave][row][lane % 16]));
+                }
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int row = 16 * i + 4 * (lane / 16) + r;
+                if (row < p.t && col_ok) put<EP, YT>(p.y, p.ld_y, row, colw, acc[i][r]);
+            }
+    }
+}
+
+// ---- launch ----------------------------------------------------------------------------------------------------------
+
+inline Params make_params(const GemmArgs& a) {
+    Params p{};
+    p.x = reinterpret_cast<const signed char*>(a.x);
+    p.ld_x = a.ld_x;
+    p.xs = a.xs;
+    p.ld_xs = a.ld_xs;
+    int shift = 0;
+    while ((static_cast<std::size_t>(128) << shift) < a.act_block) ++shift;
+    p.act_shift = shift;
+    p.w = reinterpret_cast<const signed char*>(a.w);
+    p.ld_w = a.ld_w;
+    p.ws = a.s;
+    p.ld_ws = a.ld_s;
+    p.y = a.y;
+    p.ld_y = a.ld_y;
+    p.t = static_cast<int>(a.t);
+    p.n = static_cast<int>(a.n);
+    p.k = static_cast<int>(a.k);
+    p.sums = a.sums;
+    return p;
+}
+
+template <int EP, int YT, bool PT, int MODE>
+void launch_big(const GemmArgs& a, hipStream_t stream) {
+    Params p = make_params(a);
+    p.tiles_m = static_cast<int>((a.t + 127) / 128);
+    p.tiles_n = static_cast<int>((a.n + 255) / 256);
+    gemm_big<EP, YT, PT, MODE><<<dim3(p.tiles_m * p.tiles_n), dim3(512), 0, stream>>>(p);
+    check_launch("gemm_q8 large-M kernel launch");
+}
+
+template <int EP, int YT, bool PT, int MT>
+void launch_small_mt(const GemmArgs& a, hipStream_t stream) {
+    Params p = make_params(a);
+    p.col_blocks = static_cast<int>((a.n + 63) / 64);
+    const int groups = p.k / 128;
+    const int max_gps = q8_kr_max(MT) / 128;
+    int splits = (2 * 256 + p.col_blocks - 1) / p.col_blocks;
+    splits = max(splits, (groups + max_gps - 1) / max_gps);
+    splits = min(splits, groups);
+    if (a.force_splits > 0) splits = max((groups + max_gps - 1) / max_gps, min(a.force_splits, groups));
+    p.groups_per_split = (groups + splits - 1) / splits;
+    splits = (groups + p.groups_per_split - 1) / p.groups_per_split;
+    require(p.groups_per_split <= max_gps, "gemm_q8 small-M: split too long for LDS");
+    p.splits = splits;
+    if (splits > 1) {
+        const std::size_t part = static_cast<std::size_t>(splits) * 16 * MT * p.col_blocks * 64 * sizeof(float);
+        require(static_cast<std::size_t>(p.col_blocks) * sizeof(unsigned) <= kCounterBytes && part <= kPartialBytes,
+                "small-M multiply: workspace zone too small for this shape");
+        char* ws = static_cast<char*>(workspace(kScratchOffset, stream));
+        p.counters = reinterpret_cast<unsigned*>(ws);
+        p.partial = reinterpret_cast<float*>(ws + kCounterBytes);
+    }
+    gemm_small<EP, YT, PT, MT><<<dim3(p.col_blocks * splits), dim3(256), 0, stream>>>(p);
+    check_launch("gemm_q8 small-M kernel launch");
+}
+
+template <int EP, int YT, bool PT>
+void dispatch_path(const GemmArgs& a, hipStream_t stream) {
+    const bool small = a.config == 1 || (a.config < 0 && a.t <= kSmallM);
+    if (!small) {
+        launch_big<EP, YT, PT, MODE_CHAIN>(a, stream);
+        return;
+    }
+    switch ((a.t + 15) / 16) {
+    case 1: launch_small_mt<EP, YT, PT, 1>(a, stream); break;
+    case 2: launch_small_mt<EP, YT, PT, 2>(a, stream); break;
+    case 3: launch_small_mt<EP, YT, PT, 3>(a, stream); break;
+    default: launch_small_mt<EP, YT, PT, 4>(a, stream); break;
+    }
+}
+
+template <bool PT>
+void dispatch_ep(const GemmArgs& a, hipStream_t stream) {
+    switch (a.epilogue) {
+    case SEPAL_HIP_STORE: dispatch_path<SEPAL_HIP_STORE, SEPAL_HIP_F32, PT>(a, stream); break;
+    case SEPAL_HIP_ADD: dispatch_path<SEPAL_HIP_ADD, SEPAL_HIP_F32, PT>(a, stream); break;
+    default:
+        switch (a.y_type) {
+        case SEPAL_HIP_F32: dispatch_path<SEPAL_HIP_SWIGLU, SEPAL_HIP_F32, PT>(a, stream); break;
+        case SEPAL_HIP_BF16: dispatch_path<SEPAL_HIP_SWIGLU, SEPAL_HIP_BF16, PT>(a, stream); break;
+        default: dispatch_path<SEPAL_HIP_SWIGLU, SEPAL_HIP_F16, PT>(a, stream); break;
+        }
+    }
+}
+
+} // namespace q8
+
+void launch_gemm_q8(const GemmArgs& a, hipStream_t stream) {
+    if (a.act_block == a.k && a.k != 128) q8::dispatch_ep<true>(a, stream);
+    else q8::dispatch_ep<false>(a, stream);
+}
+
+void launch_q8_group_sums(const GemmArgs& a, hipStream_t stream) {
+    q8::launch_big<SEPAL_HIP_STORE, SEPAL_HIP_F32, true, q8::MODE_SUMS>(a, stream);
+}
+
+} // namespace sepal::hip

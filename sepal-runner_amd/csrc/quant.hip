@@ -1,0 +1,248 @@
+// Quantizers and glue kernels of the W8g128 MLP path (HBM-bound, one pass each).
+//
+//   quantize_group: the load-time weight packer and the per-128 activation quantizer. 16 lanes own one (row, 128-group)
+//     (8 values each, one 16- or 32-byte load), the group maximum is a 16-lane butterfly (exact in any order), each
+//     value is quantized on its own, 8 bytes are stored per lane. Rule DIVIDE restates quantize_group_s8_kernel
+//     (runner/cuda/src/gemm_simt_kernels.cu:266-286), rule RECIPROCAL the cpu-q8 quantise (runner/src/cpu/gemm.cpp:
+//     103-106, 141-163, 288-303). With a second source the rows are read in the 64-row gate/up interleave
+//     (gemm_simt_kernels.hpp:72-77).
+//   quantize_rows_token: one scale per row (block = cols), rule RECIPROCAL; a block of 256 threads per row.
+//   rmsnorm: the cpu-q8 RMSNorm with its exact summation order (runner/src/cpu/elementwise.cpp:22-59): 32 lanes stand
+//     for the reference's 4 x 8 accumulator lanes, then the same combining order.
+#include "common.hpp"
+#include "gemm_kernels.hpp"
+
+namespace sepal::hip {
+namespace quant {
+
+template <int ST>
+__device__ __forceinline__ void load8(const void* base, std::size_t idx, float (&v)[8]) {
+    if constexpr (ST == SEPAL_HIP_F32) {
+        const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(base) + idx);
+        const float4 a = p[0], b = p[1];
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+        v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    } else {
+        const u32x4 u = *reinterpret_cast<const u32x4*>(static_cast<const unsigned short*>(base) + idx);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const unsigned short lo = static_cast<unsigned short>(u[i] & 0xFFFFu), hi = static_cast<unsigned short>(u[i] >> 16);
+            if constexpr (ST == SEPAL_HIP_BF16) {
+                v[2 * i] = bf16_bits_to_f32(lo);
+                v[2 * i + 1] = bf16_bits_to_f32(hi);
+            } else {
+                v[2 * i] = f16_bits_to_f32(lo);
+                v[2 * i + 1] = f16_bits_to_f32(hi);
+            }
+        }
+    }
+}
+
+template <int RULE>
+__device__ __forceinline__ int quantize_value(float w, float scale, float inverse) {
+    if constexpr (RULE == SEPAL_HIP_RULE_DIVIDE) {
+        if (!(scale > 0.0f)) return 0;
+        const float r = __builtin_rintf(__fdiv_rn(w, scale));
+        return static_cast<int>(fminf(fmaxf(r, -127.0f), 127.0f));
+    } else {
+        float r = __builtin_rintf(__fmul_rn(w, inverse));
+        r = r < -127.0f ? -127.0f : (r > 127.0f ? 127.0f : r);
+        return static_cast<int>(r);
+    }
+}
+
+template <int ST, int RULE>
+__global__ void __launch_bounds__(256) quantize_group_kernel(const void* __restrict__ src, std::size_t ld_src,
+                                                             const void* __restrict__ src_up, std::int8_t* __restrict__ q,
+                                                             std::size_t ld_q, float* __restrict__ s, std::size_t ld_s,
+                                                             std::size_t rows, std::size_t groups, std::size_t inter) {
+    const std::size_t gid = (static_cast<std::size_t>(blockIdx.x) * 256 + threadIdx.x) / 16;
+    const int sub = threadIdx.x % 16;
+    const bool live = gid < rows * groups;
+    const std::size_t row = live ? gid / groups : 0, g = live ? gid % groups : 0;
+    // source row: plain, or the 64-row gate/up interleave of the fused SwiGLU weights
+    const void* base = src;
+    std::size_t srow = row;
+    if (src_up != nullptr) {
+        const std::size_t b = row / 128, r = row % 128;
+        if (r < 64) srow = 64 * b + r;
+        else {
+            srow = 64 * b + (r - 64);
+            base = src_up;
+        }
+    }
+    float v[8];
+    if (live) load8<ST>(base, srow * ld_src + g * 128 + sub * 8, v);
+    else
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = 0.0f;
+    float m = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float a = fabsf(v[i]);
+        m = a > m ? a : m;
+    }
+#pragma unroll
+    for (int o = 8; o > 0; o >>= 1) {
+        const float other = __shfl_xor(m, o, 16);
+        m = other > m ? other : m;
+    }
+    float scale, inverse = 0.0f;
+    if constexpr (RULE == SEPAL_HIP_RULE_DIVIDE) {
+        scale = __fdiv_rn(m, 127.0f);
+    } else {
+        scale = m > 0.0f ? __fdiv_rn(m, 127.0f) : 1.0f;
+        inverse = __fdiv_rn(1.0f, scale);
+    }
+    if (!live) return;
+    unsigned packed[2] = {0u, 0u};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) packed[i / 4] |= (static_cast<unsigned>(quantize_value<RULE>(v[i], scale, inverse)) & 0xFFu) << (8 * (i % 4));
+    *reinterpret_cast<uint2*>(q + row * ld_q + g * 128 + sub * 8) = make_uint2(packed[0], packed[1]);
+    if (sub == 0) s[row * ld_s + g] = scale;
+}
+
+// One scale per row: pass 1 the row maximum (block reduction), pass 2 the quantization (rule RECIPROCAL).
+template <int ST>
+__global__ void __launch_bounds__(256) quantize_rows_token_kernel(const void* __restrict__ x, std::size_t ld_x,
+                                                                  std::int8_t* __restrict__ q, std::size_t ld_q,
+                                                                  float* __restrict__ scales, std::size_t ld_s, int cols) {
+    __shared__ float red[4];
+    const std::size_t row = blockIdx.x;
+    const int chunks = cols / 8;
+    float m = 0.0f;
+    for (int c = threadIdx.x; c < chunks; c += 256) {
+        float v[8];
+        load8<ST>(x, row * ld_x + 8 * c, v);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float a = fabsf(v[i]);
+            m = a > m ? a : m;
+        }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float other = __shfl_xor(m, o, 64);
+        m = other > m ? other : m;
+    }
+    if (threadIdx.x % 64 == 0) red[threadIdx.x / 64] = m;
+    __syncthreads();
+    m = red[0];
+#pragma unroll
+    for (int i = 1; i < 4; ++i) m = red[i] > m ? red[i] : m;
+    const float scale = m > 0.0f ? __fdiv_rn(m, 127.0f) : 1.0f;
+    const float inverse = __fdiv_rn(1.0f, scale);
+    if (threadIdx.x == 0) scales[row * ld_s] = scale;
+    for (int c = threadIdx.x; c < chunks; c += 256) {
+        float v[8];
+        load8<ST>(x, row * ld_x + 8 * c, v);
+        unsigned packed[2] = {0u, 0u};
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            packed[i / 4] |= (static_cast<unsigned>(quantize_value<SEPAL_HIP_RULE_RECIPROCAL>(v[i], scale, inverse)) & 0xFFu) << (8 * (i % 4));
+        *reinterpret_cast<uint2*>(q + row * ld_q + 8 * c) = make_uint2(packed[0], packed[1]);
+    }
+}
+
+// Two rows per wave (one per 32-lane half). Lane L of a half is the reference's accumulator register L / 8, lane L % 8.
+template <int YT>
+__global__ void __launch_bounds__(256) rmsnorm_kernel(const float* __restrict__ x, std::size_t ld_x, void* __restrict__ y,
+                                                      std::size_t ld_y, const float* __restrict__ w1, int rows, int cols,
+                                                      double eps) {
+    const int lane = threadIdx.x % 64, half = lane / 32, L = lane % 32;
+    const int row = (blockIdx.x * 256 + threadIdx.x) / 32;
+    const bool live = row < rows;
+    const float* xr = x + static_cast<std::size_t>(live ? row : 0) * ld_x;
+    float a = 0.0f;
+    int i = 0;
+    for (; i + 32 <= cols; i += 32) {
+        const float v = xr[i + L];
+        a = __builtin_fmaf(v, v, a);
+    }
+    for (; i + 8 <= cols; i += 8) {
+        if (L < 8) {
+            const float v = xr[i + L];
+            a = __builtin_fmaf(v, v, a);
+        }
+    }
+    const int base = half * 32;
+    const int l8 = L % 8;
+    const float a0 = __shfl(a, base + l8), a1 = __shfl(a, base + 8 + l8), a2 = __shfl(a, base + 16 + l8), a3 = __shfl(a, base + 24 + l8);
+    const float sl = __fadd_rn(__fadd_rn(a0, a1), __fadd_rn(a2, a3));  // s[l8] on every lane
+    const float sl4 = __shfl(sl, base + (l8 + 4) % 8);
+    const float h = __fadd_rn(sl, sl4);                                 // h[l8 % 4] on lanes l8 < 4
+    const float h0 = __shfl(h, base + 0), h1 = __shfl(h, base + 1), h2 = __shfl(h, base + 2), h3 = __shfl(h, base + 3);
+    const float sum = __fadd_rn(__fadd_rn(h0, h2), __fadd_rn(h1, h3));
+    if (!live) return;
+    const double mean = static_cast<double>(sum) / static_cast<double>(cols);
+    const float inv = static_cast<float>(1.0 / __builtin_sqrt(mean + eps));
+    for (int c = L; c < cols; c += 32) {
+        const float v = __fmul_rn(xr[c], inv);
+        store_out<YT>(y, static_cast<std::size_t>(row) * ld_y + c, __fmul_rn(v, w1 != nullptr ? w1[c] : 1.0f));
+    }
+}
+
+__global__ void f32_to_bf16_kernel(const float* __restrict__ src, std::uint16_t* __restrict__ dst, std::size_t count) {
+    const std::size_t i = static_cast<std::size_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (i < count) dst[i] = f32_to_bf16_bits(src[i]);
+}
+
+template <int ST>
+void launch_group(const void* src, std::size_t ld_src, const void* src_up, std::int8_t* q, std::size_t ld_q, float* s,
+                  std::size_t ld_s, std::size_t rows, std::size_t k, int rule, std::size_t inter, hipStream_t stream) {
+    const std::size_t groups = k / 128;
+    const std::size_t blocks = (rows * groups * 16 + 255) / 256;
+    if (rule == SEPAL_HIP_RULE_DIVIDE)
+        quantize_group_kernel<ST, SEPAL_HIP_RULE_DIVIDE><<<dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream>>>(
+            src, ld_src, src_up, q, ld_q, s, ld_s, rows, groups, inter);
+    else
+        quantize_group_kernel<ST, SEPAL_HIP_RULE_RECIPROCAL><<<dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream>>>(
+            src, ld_src, src_up, q, ld_q, s, ld_s, rows, groups, inter);
+    check_launch("quantize_group kernel launch");
+}
+
+} // namespace quant
+
+void launch_quantize_group(const void* src, int src_type, std::size_t ld_src, const void* src_up, std::int8_t* q,
+                           std::size_t ld_q, float* s, std::size_t ld_s, std::size_t rows, std::size_t k, int rule,
+                           std::size_t inter, hipStream_t stream) {
+    switch (src_type) {
+    case SEPAL_HIP_F32: quant::launch_group<SEPAL_HIP_F32>(src, ld_src, src_up, q, ld_q, s, ld_s, rows, k, rule, inter, stream); break;
+    case SEPAL_HIP_BF16: quant::launch_group<SEPAL_HIP_BF16>(src, ld_src, src_up, q, ld_q, s, ld_s, rows, k, rule, inter, stream); break;
+    default: quant::launch_group<SEPAL_HIP_F16>(src, ld_src, src_up, q, ld_q, s, ld_s, rows, k, rule, inter, stream); break;
+    }
+}
+
+void launch_quantize_rows(const void* x, int x_type, std::size_t ld_x, std::int8_t* q, std::size_t ld_q, float* scales,
+                          std::size_t ld_s, std::size_t rows, std::size_t cols, std::size_t block, hipStream_t stream) {
+    if (block == 128) {
+        launch_quantize_group(x, x_type, ld_x, nullptr, q, ld_q, scales, ld_s, rows, cols, SEPAL_HIP_RULE_RECIPROCAL, 0, stream);
+        return;
+    }
+    const dim3 grid(static_cast<unsigned>(rows));
+    switch (x_type) {
+    case SEPAL_HIP_F32: quant::quantize_rows_token_kernel<SEPAL_HIP_F32><<<grid, dim3(256), 0, stream>>>(x, ld_x, q, ld_q, scales, ld_s, static_cast<int>(cols)); break;
+    case SEPAL_HIP_BF16: quant::quantize_rows_token_kernel<SEPAL_HIP_BF16><<<grid, dim3(256), 0, stream>>>(x, ld_x, q, ld_q, scales, ld_s, static_cast<int>(cols)); break;
+    default: quant::quantize_rows_token_kernel<SEPAL_HIP_F16><<<grid, dim3(256), 0, stream>>>(x, ld_x, q, ld_q, scales, ld_s, static_cast<int>(cols)); break;
+    }
+    check_launch("quantize_rows kernel launch");
+}
+
+void launch_rmsnorm(const float* x, std::size_t ld_x, void* y, int y_type, std::size_t ld_y, const float* w1,
+                    std::size_t rows, std::size_t cols, double eps, hipStream_t stream) {
+    const dim3 grid(static_cast<unsigned>((rows * 32 + 255) / 256));
+    const int r = static_cast<int>(rows), c = static_cast<int>(cols);
+    switch (y_type) {
+    case SEPAL_HIP_F32: quant::rmsnorm_kernel<SEPAL_HIP_F32><<<grid, dim3(256), 0, stream>>>(x, ld_x, y, ld_y, w1, r, c, eps); break;
+    case SEPAL_HIP_BF16: quant::rmsnorm_kernel<SEPAL_HIP_BF16><<<grid, dim3(256), 0, stream>>>(x, ld_x, y, ld_y, w1, r, c, eps); break;
+    default: quant::rmsnorm_kernel<SEPAL_HIP_F16><<<grid, dim3(256), 0, stream>>>(x, ld_x, y, ld_y, w1, r, c, eps); break;
+    }
+    check_launch("rmsnorm kernel launch");
+}
+
+void launch_f32_to_bf16(const float* src, std::uint16_t* dst, std::size_t count, hipStream_t stream) {
+    quant::f32_to_bf16_kernel<<<dim3(static_cast<unsigned>((count + 255) / 256)), dim3(256), 0, stream>>>(src, dst, count);
+    check_launch("f32_to_bf16 kernel launch");
+}
+
+} // namespace sepal::hip

@@ -1,0 +1,221 @@
+"""Python front end of the MI355X W8g128 quantized-MLP path: ctypes over the C ABI of include/sepal_mlp_hip.h.
+
+It mirrors how the reference's Python front end drives its engine (sepal_runner/engine.py:128-214, ctypes over
+c_api.h): one shared library, int32 status codes turned into exceptions with the library's last-error text. The
+kernel-level names follow the reference's CUDA launchers (runner/cuda/src/gemm_simt_kernels.hpp:53-70,
+runner/cuda/src/gemm_s8_kernels.hpp:20-57); invalid arguments raise ValueError (std::invalid_argument there), failed
+launches RuntimeError (std::runtime_error there).
+
+Tensors are PyTorch device tensors (PyTorch is only the allocator and the stream here). There is no CPU fallback:
+loading fails loudly when the HIP library has not been built.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libsepal_mlp_hip.so")
+HEADER = os.path.join(os.path.dirname(os.path.dirname(HERE)), "include", "sepal_mlp_hip.h")
+
+OK, EINVAL, ELAUNCH, ENOMEM = 0, 1, 2, 3
+F32, BF16, F16 = 0, 1, 2
+STORE, ADD, SWIGLU = 0, 1, 2
+RULE_DIVIDE, RULE_RECIPROCAL = 0, 1
+
+_lib = None
+
+
+class SepalHipError(RuntimeError):
+    """A failed launch or an allocation failure reported by the library."""
+
+
+class SepalHipInvalid(ValueError):
+    """Arguments the library refuses (shape, stride, alignment, null pointer)."""
+
+
+def library() -> C.CDLL:
+    """The loaded HIP library (built by sepal-runner_amd/build.py). Raises when it is missing."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(f"{LIB_PATH} is missing: build it with `python sepal-runner_amd/build.py` "
+                              "(there is no CPU fallback)")
+        L = C.CDLL(LIB_PATH)
+        sz, vp, i32, d = C.c_size_t, C.c_void_p, C.c_int32, C.c_double
+        L.sepal_hip_api_version.restype = i32
+        L.sepal_hip_last_error.restype = C.c_char_p
+        L.sepal_hip_quantize_group_s8.argtypes = [vp, i32, sz, vp, sz, vp, sz, sz, sz, i32, vp]
+        L.sepal_hip_quantize_gate_up_s8.argtypes = [vp, vp, i32, sz, vp, sz, vp, sz, sz, sz, i32, vp]
+        L.sepal_hip_gemm_w8g.argtypes = [vp, i32, sz, vp, sz, vp, sz, vp, i32, sz, sz, sz, sz, i32, i32, vp]
+        L.sepal_hip_gemm_w8g_supports.argtypes = [i32, sz, sz, sz, sz, sz, i32]
+        L.sepal_hip_quantize_rows_s8.argtypes = [vp, i32, sz, vp, sz, vp, sz, sz, sz, sz, vp]
+        L.sepal_hip_gemm_q8.argtypes = [vp, sz, vp, sz, sz, vp, sz, vp, sz, vp, i32, sz, sz, sz, sz, i32, i32, vp]
+        L.sepal_hip_q8_group_sums.argtypes = [vp, sz, vp, sz, vp, sz, sz, sz, vp]
+        L.sepal_hip_rmsnorm_rows.argtypes = [vp, sz, vp, i32, sz, vp, sz, sz, d, vp]
+        L.sepal_hip_float_to_bf16.argtypes = [vp, vp, sz, vp]
+        L.sepal_hip_mlp_stack.argtypes = [i32, sz, sz, sz, sz, vp, vp, vp, vp, vp, vp, sz, d, vp]
+        for name in ("sepal_hip_quantize_group_s8", "sepal_hip_quantize_gate_up_s8", "sepal_hip_gemm_w8g",
+                     "sepal_hip_quantize_rows_s8", "sepal_hip_gemm_q8", "sepal_hip_q8_group_sums",
+                     "sepal_hip_rmsnorm_rows", "sepal_hip_float_to_bf16", "sepal_hip_mlp_stack"):
+            getattr(L, name).restype = i32
+        L.sepal_hip_gemm_w8g_supports.restype = i32
+        _lib = L
+    return _lib
+
+
+def declared_symbols() -> list[str]:
+    """Every function the public header declares (the exports the library must provide)."""
+    import re
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"\b(sepal_hip_\w+)\s*\(", text)))
+
+
+def _check(rc: int) -> None:
+    if rc == OK:
+        return
+    msg = library().sepal_hip_last_error().decode()
+    if rc == EINVAL:
+        raise SepalHipInvalid(msg)
+    raise SepalHipError(msg)
+
+
+# ---- torch plumbing ----------------------------------------------------------------------------------------------------
+
+def _torch():
+    import torch
+    return torch
+
+
+def _ptr(t) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(stream=None) -> int | None:
+    torch = _torch()
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return s.cuda_stream or None
+
+
+def _type_of(t) -> int:
+    torch = _torch()
+    return {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16}[t.dtype]
+
+
+def _ld(t) -> int:
+    """Row stride in elements of a 2-D tensor whose rows are contiguous."""
+    if t.dim() != 2 or t.stride(1) != 1:
+        raise SepalHipInvalid("expected a 2-D tensor with contiguous rows")
+    return t.stride(0)
+
+
+# ---- entry points ------------------------------------------------------------------------------------------------------
+
+def quantize_group_s8(src, q=None, s=None, rule: int = RULE_DIVIDE, stream=None):
+    """Load-time packer: int8 q [rows, K] and float32 scales s [rows, K/128] from src [rows, K] (fp32/bf16/fp16)."""
+    torch = _torch()
+    rows, k = src.shape
+    q = torch.empty(rows, k, dtype=torch.int8, device=src.device) if q is None else q
+    s = torch.empty(rows, k // 128, dtype=torch.float32, device=src.device) if s is None else s
+    _check(library().sepal_hip_quantize_group_s8(_ptr(src), _type_of(src), _ld(src), _ptr(q), _ld(q), _ptr(s), _ld(s),
+                                                 rows, k, rule, _stream(stream)))
+    return q, s
+
+
+def quantize_gate_up_s8(gate, up, rule: int = RULE_DIVIDE, stream=None):
+    """Packer of a SwiGLU pair: q [2I, K] int8 and s [2I, K/128] in the 64-row gate/up interleave."""
+    torch = _torch()
+    inter, k = gate.shape
+    q = torch.empty(2 * inter, k, dtype=torch.int8, device=gate.device)
+    s = torch.empty(2 * inter, k // 128, dtype=torch.float32, device=gate.device)
+    if up.stride() != gate.stride() or up.dtype != gate.dtype:
+        raise SepalHipInvalid("gate and up must share dtype and strides")
+    _check(library().sepal_hip_quantize_gate_up_s8(_ptr(gate), _ptr(up), _type_of(gate), _ld(gate), _ptr(q), _ld(q),
+                                                   _ptr(s), _ld(s), inter, k, rule, _stream(stream)))
+    return q, s
+
+
+def gemm_w8g_supports(x_type: int, n: int, k: int, ld_x: int, ld_w: int, ld_y: int, epilogue: int) -> bool:
+    return bool(library().sepal_hip_gemm_w8g_supports(x_type, n, k, ld_x, ld_w, ld_y, epilogue))
+
+
+def gemm_w8g(x, w, s, y=None, epilogue: int = STORE, y_dtype=None, config: int = -1, stream=None):
+    """gpu-w8g multiply. x [T, K] bf16/fp16; w int8 [N, K]; s float32 [N, K/128]. Returns y (float32, or y_dtype for
+    SwiGLU, with N/2 columns)."""
+    torch = _torch()
+    t, k = x.shape
+    n = w.shape[0]
+    cols = n // 2 if epilogue == SWIGLU else n
+    if y is None:
+        y = torch.empty(t, cols, dtype=y_dtype or torch.float32, device=x.device)
+    _check(library().sepal_hip_gemm_w8g(_ptr(x), _type_of(x), _ld(x), _ptr(w), _ld(w), _ptr(s), _ld(s), _ptr(y),
+                                        _type_of(y), _ld(y), t, n, k, epilogue, config, _stream(stream)))
+    return y
+
+
+def quantize_rows_s8(x, block: int = 128, stream=None):
+    """Dynamic activation quantizer (cpu-q8 rule): int8 q [T, K] and scales [T, K/block]."""
+    torch = _torch()
+    rows, cols = x.shape
+    q = torch.empty(rows, cols, dtype=torch.int8, device=x.device)
+    sc = torch.empty(rows, max(cols // block, 1), dtype=torch.float32, device=x.device)
+    _check(library().sepal_hip_quantize_rows_s8(_ptr(x), _type_of(x), _ld(x), _ptr(q), _ld(q), _ptr(sc), _ld(sc), rows,
+                                                cols, block, _stream(stream)))
+    return q, sc
+
+
+def gemm_q8(xq, xs, w, ws, y=None, epilogue: int = STORE, act_block: int = 128, y_dtype=None, config: int = -1,
+            stream=None):
+    """gpu-q8w multiply of int8 activations (scales xs per act_block) and int8 weights (scales ws per 128)."""
+    torch = _torch()
+    t, k = xq.shape
+    n = w.shape[0]
+    cols = n // 2 if epilogue == SWIGLU else n
+    if y is None:
+        y = torch.empty(t, cols, dtype=y_dtype or torch.float32, device=xq.device)
+    _check(library().sepal_hip_gemm_q8(_ptr(xq), _ld(xq), _ptr(xs), _ld(xs), act_block, _ptr(w), _ld(w), _ptr(ws),
+                                       _ld(ws), _ptr(y), _type_of(y), _ld(y), t, n, k, epilogue, config,
+                                       _stream(stream)))
+    return y
+
+
+def q8_group_sums(xq, w, stream=None):
+    """Exact int32 per-group sums [K/128, T, N] of the int8 multiply (for bit-exact checks)."""
+    torch = _torch()
+    t, k = xq.shape
+    n = w.shape[0]
+    out = torch.empty(k // 128, t, n, dtype=torch.int32, device=xq.device)
+    _check(library().sepal_hip_q8_group_sums(_ptr(xq), _ld(xq), _ptr(w), _ld(w), _ptr(out), t, n, k, _stream(stream)))
+    return out
+
+
+def rmsnorm_rows(x, y_dtype=None, w1=None, eps: float = 1e-6, stream=None):
+    torch = _torch()
+    rows, cols = x.shape
+    y = torch.empty(rows, cols, dtype=y_dtype or torch.float32, device=x.device)
+    _check(library().sepal_hip_rmsnorm_rows(_ptr(x), _ld(x), _ptr(y), _type_of(y), _ld(y), _ptr(w1), rows, cols, eps,
+                                            _stream(stream)))
+    return y
+
+
+def float_to_bf16(x, stream=None):
+    torch = _torch()
+    out = torch.empty(x.shape, dtype=torch.bfloat16, device=x.device)
+    _check(library().sepal_hip_float_to_bf16(_ptr(x), _ptr(out), x.numel(), _stream(stream)))
+    return out
+
+
+def mlp_stack(kind: int, x, layers, y=None, act_block: int = 128, eps: float = 1e-6, stream=None):
+    """Runs the per-layer MLP stack in one call. kind 0 = w8g, 1 = q8. x bf16 [T, H] (overwritten with the last layer's
+    input); layers: list of (w_gate_up, s_gate_up, w_down, s_down) device tensors. Returns y float32 [T, H]."""
+    torch = _torch()
+    t, hidden = x.shape
+    inter = layers[0][2].shape[1]
+    y = torch.empty(t, hidden, dtype=torch.float32, device=x.device) if y is None else y
+    def arr(i):
+        return (C.c_void_p * len(layers))(*[l[i].data_ptr() for l in layers])
+
+    wgu, sgu, wd, sd = arr(0), arr(1), arr(2), arr(3)
+    _check(library().sepal_hip_mlp_stack(kind, len(layers), t, hidden, inter, _ptr(x), wgu, sgu, wd, sd, _ptr(y),
+                                         act_block, eps, _stream(stream)))
+    return y
