@@ -229,7 +229,7 @@ __global__ void __launch_bounds__(512) gemm_big(const Params p) {
             }
             if constexpr (EP == SEPAL_HIP_SWIGLU) {
                 const int f = n0 / 2 + 64 * ib + 32 * hh + lane % 32;
-                store_out<YT>(p.y, static_cast<std::size_t>(row) * p.ld_y + f, swiglu_cephes(v0, v1));
+                if (2 * f < p.n) store_out<YT>(p.y, static_cast<std::size_t>(row) * p.ld_y + f, swiglu_cephes(v0, v1));
             } else {
                 if (col[0] < p.n) put<EP, YT>(p.y, p.ld_y, row, col[0], v0);
                 if (col[1] < p.n) put<EP, YT>(p.y, p.ld_y, row, col[1], v1);

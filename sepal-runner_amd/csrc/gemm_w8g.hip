@@ -237,7 +237,7 @@ __global__ void __launch_bounds__(128 * WN) gemm_big(const BigParams p) {
             const float v0 = __fmul_rn(acc[i][0][r], e[0]), v1 = __fmul_rn(acc[i][1][r], e[1]);
             if constexpr (EP == SEPAL_HIP_SWIGLU) {
                 const int f = n0 / 2 + 64 * ib + 32 * hh + lane % 32;
-                store_out<YT>(p.y, static_cast<std::size_t>(row) * p.ld_y + f, swiglu_libm(v0, v1));
+                if (2 * f < p.n) store_out<YT>(p.y, static_cast<std::size_t>(row) * p.ld_y + f, swiglu_libm(v0, v1));
             } else {
                 float* y = static_cast<float*>(p.y);
                 if (col[0] < p.n) put_plain<EP>(y, static_cast<std::size_t>(row) * p.ld_y + col[0], v0);
