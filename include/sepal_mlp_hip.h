@@ -75,7 +75,7 @@ SEPAL_HIP_API int32_t sepal_hip_quantize_gate_up_s8(const void* gate, const void
  * (F32, BF16 or F16) with N/2 columns. K a multiple of 128; N a multiple of 128 for SWIGLU, of 16 otherwise; ld_x,
  * ld_w multiples of 16; ld_y a multiple of 4; 16-byte aligned pointers. `config` -1 picks a path by T (small-M at T <= 64);
  * 0 forces the large-M tiled path, 1 the small-M weight-streaming path, 2 the small-M path without a split of K (the
- * whole K of a column block in one block; K at most 2048 / ceil(T/16) for w8g, 4096 / ceil(T/16) for q8).
+ * whole K of a column block in one block; K at most 1280).
  * Replaces launch_gemm_simt with SimtWeight::Int8Group (runner/cuda/src/gemm_simt_kernels.hpp:53-56, .cu:312-332). */
 SEPAL_HIP_API int32_t sepal_hip_gemm_w8g(const void* x, int32_t x_type, size_t ld_x, const int8_t* w, size_t ld_w, const float* s,
                            size_t ld_s, void* y, int32_t y_type, size_t ld_y, size_t t, size_t n, size_t k,

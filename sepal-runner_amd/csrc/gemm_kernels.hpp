@@ -8,9 +8,6 @@ namespace sepal::hip {
 // Rows at or below which the multiplies take the weight-streaming small-M path.
 inline constexpr std::size_t kSmallM = 64;
 
-// K values of X one small-M split holds in LDS (64 KB of 16-bit values, a multiple of 128).
-__host__ __device__ constexpr int small_kr_max(int mt) { return (2048 / mt) / 128 * 128; }
-
 struct GemmArgs {
     const void* x = nullptr;
     int x_type = SEPAL_HIP_BF16;
@@ -34,6 +31,8 @@ struct GemmArgs {
 };
 
 void launch_gemm_w8g(const GemmArgs& a, hipStream_t stream);
+void launch_stream_w8g(const GemmArgs& a, hipStream_t stream);
+void launch_stream_q8(const GemmArgs& a, hipStream_t stream);
 void launch_gemm_q8(const GemmArgs& a, hipStream_t stream);
 void launch_q8_group_sums(const GemmArgs& a, hipStream_t stream);
 
