@@ -99,6 +99,14 @@ __device__ __forceinline__ float swiglu_libm(float g, float u) {
     return __fmul_rn(__fmul_rn(g, expf(-softplus)), u);
 }
 
+// silu(g) * u for the tolerance-pinned w8g epilogue: g * u / (1 + 2^(-g log2 e)) with the hardware exp2 and reciprocal
+// (about one ulp each; the result is within a few ulp of silu(g) * u). Large negative g gives 2^(+inf) = inf and a
+// reciprocal of 0, so the product is 0; large positive g gives g * u.
+__device__ __forceinline__ float swiglu_fast(float g, float u) {
+    const float e = __builtin_amdgcn_exp2f(-g * 1.44269504088896341f);
+    return (g * u) * __builtin_amdgcn_rcpf(1.0f + e);
+}
+
 // exp(x) by Cody-Waite reduction with the two-part ln 2 and the degree-5 polynomial of the cpu-q8 path, with its clamps
 // (runner/src/cpu/vmath.hpp:16-32, the Cephes expf method), one lane at a time: every step is one IEEE operation
 // or one fused multiply-add, so the result equals the CPU's bit for bit.

@@ -90,79 +90,99 @@ __device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int& 
     tn = in_group / gm;
 }
 
-// LDS tiles hold rows of BK 16-bit elements in 16-byte chunks; chunk c of row r is stored at chunk c ^ swz(r).
-template <int BK>
-__device__ __forceinline__ int swz(int r) {
-    constexpr int CPR = BK / 8;
-    return CPR == 8 ? (r & 7) : ((r >> 1) & (CPR - 1));
+// ---- large-M kernel: fragment-order LDS, direct global->LDS X tiles, 4-stage pipeline ----------------------------
+//
+// LDS holds every MFMA operand fragment in the order a wave reads it: fragment (block b, substep st) is 64 lanes x 16
+// bytes, lane l at byte 16 l, so an operand read is one contiguous kilobyte (no bank conflicts, one address per lane
+// for the whole kernel). A fragment of X (m-block mb of 32 rows, 16 values of k) is filled straight from global memory
+// by global_load_lds_dwordx4 (each lane loads the 16 bytes it will later read: row mb*32 + l%32, k 16st + 8(l/32));
+// a W fragment is filled by the wave that widens the weight bytes (row nb*32 + l%32, k 16st .. 16st + 15 -> lanes l%32
+// and 32 + l%32). K runs in steps of 32 through 4 LDS stages; the loads of step kt + 3 are issued while step kt is
+// multiplied, and one barrier per step publishes step kt + 1. Each lane's two column scales come with the step's
+// loads.
+namespace v2 {
+
+constexpr int BM = 256, BK = 32, STAGES = 4;
+
+typedef __attribute__((address_space(3))) unsigned char lds_byte;
+typedef const __attribute__((address_space(1))) void global_void;
+
+// s_waitcnt with only the vector memory counter limited (gfx9 encoding: vmcnt[3:0] bits 3:0, vmcnt[5:4] bits 15:14;
+// expcnt and lgkmcnt left at their maxima).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
-template <int XT, int EP, int YT, int WN, int BK>
-__global__ void __launch_bounds__(128 * WN) gemm_big(const BigParams p) {
-    constexpr int NT = 128 * WN;        // threads (2 waves along M, WN along N)
-    constexpr int BM = 256, BN = 64 * WN;
-    constexpr int CPR = BK / 8;         // 16-byte chunks per LDS row
-    constexpr int XCH = BM * CPR / NT;  // X chunks per thread per stage
-    constexpr int WCH = BN * (BK / 16) / NT;  // 16-byte weight chunks per thread per stage
-    constexpr int GPS = 128 / BK;       // K steps per scale group
-    static_assert(XCH >= 1 && WCH >= 1 && GPS >= 1, "tile");
-
-    __shared__ __align__(16) u32x4 lds_x[2][BM * CPR];
-    __shared__ __align__(16) u32x4 lds_w[2][BN * CPR];
+template <int XT, int EP, int YT, int WN>
+__global__ void __launch_bounds__(128 * WN) gemm_big2(const BigParams p) {
+    constexpr int NT = 128 * WN, NW = NT / 64;   // threads, waves (2 along M, WN along N)
+    constexpr int BN = 64 * WN;
+    constexpr int XF = (BM / 32) * (BK / 16);     // X fragments per stage (16)
+    constexpr int WF = (BN / 32) * (BK / 16);     // W fragments per stage
+    constexpr int XFPW = XF / NW;                 // X fragments each wave loads per stage
+    constexpr int XSTAGE = XF * 1024, WSTAGE = WF * 1024;
+    static_assert(WF == 2 * NW, "one W chunk per thread per stage");
+    extern __shared__ __align__(16) unsigned char smem[];
+    lds_byte* lds = (lds_byte*)smem;  // generic -> LDS address space (a C cast is the one that may change it)
+    lds_byte* xs_base = lds;                                 // [STAGES][XF][1 KB]
+    lds_byte* ws_base = lds + STAGES * XSTAGE;                // [STAGES][WF][1 KB]
 
     const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
     const int wm = wave % 2, wn = wave / 2;
     int tm, tn;
     tile_of(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
     const int m0 = tm * BM, n0 = tn * BN;
+    const int KT = p.k / BK;
 
-    // global -> register staging
-    u32x4 xr[XCH], wr[WCH];
-    const auto gload = [&](int kt) {
-        const int k0 = kt * BK;
+    // ---- per-lane global sources (clamped: rows past T repeat row T-1, never stored) ----
+    const unsigned char* xsrc[XFPW];
 #pragma unroll
-        for (int e = 0; e < XCH; ++e) {
-            const int id = tid + e * NT, row = id / CPR, c = id % CPR;
-            const int m = m0 + row;
-            if (m < p.t) xr[e] = *reinterpret_cast<const u32x4*>(p.x + static_cast<std::size_t>(m) * p.ld_x + k0 + 8 * c);
-            else xr[e] = u32x4{0u, 0u, 0u, 0u};
-        }
-#pragma unroll
-        for (int e = 0; e < WCH; ++e) {
-            const int id = tid + e * NT, row = id / (BK / 16), c = id % (BK / 16);
-            const int nn = n0 + row;
-            if (nn < p.n) wr[e] = *reinterpret_cast<const u32x4*>(p.w + static_cast<std::size_t>(nn) * p.ld_w + k0 + 16 * c);
-            else wr[e] = u32x4{0u, 0u, 0u, 0u};
-        }
-    };
-    const auto lstore = [&](int buf) {
-#pragma unroll
-        for (int e = 0; e < XCH; ++e) {
-            const int id = tid + e * NT, row = id / CPR, c = id % CPR;
-            lds_x[buf][row * CPR + (c ^ swz<BK>(row))] = xr[e];
-        }
-#pragma unroll
-        for (int e = 0; e < WCH; ++e) {
-            const int id = tid + e * NT, row = id / (BK / 16), c = id % (BK / 16);
-            unsigned o[8];
-            widen16<XT>(wr[e], o);
-            const int c0 = 2 * c, c1 = 2 * c + 1;
-            lds_w[buf][row * CPR + (c0 ^ swz<BK>(row))] = u32x4{o[0], o[1], o[2], o[3]};
-            lds_w[buf][row * CPR + (c1 ^ swz<BK>(row))] = u32x4{o[4], o[5], o[6], o[7]};
-        }
-    };
+    for (int i = 0; i < XFPW; ++i) {
+        const int f = wave * XFPW + i, mb = f / (BK / 16), st = f % (BK / 16);
+        const int row = min(m0 + mb * 32 + lane % 32, p.t - 1);
+        xsrc[i] = reinterpret_cast<const unsigned char*>(p.x + static_cast<std::size_t>(row) * p.ld_x + 16 * st + 8 * (lane / 32));
+    }
+    const int wrow_n = min(n0 + 32 * wave + lane % 32, p.n - 1);
+    const signed char* wsrc = p.w + static_cast<std::size_t>(wrow_n) * p.ld_w + 16 * (lane / 32);
+    // LDS destinations: X fragments (wave-uniform bases), the W fragment halves of this lane
+    const int wfrag = wave * 2 + lane / 32;  // W fragment (nb = wave, st = lane / 32)
 
-    // This lane's output columns: block nb = 0 (gate half for SwiGLU) and 1 (the matching up half).
+    // this lane's output columns: n-block j = 0 (gate half for SwiGLU) and 1 (the matching up half)
     const int ib = wn / 2, hh = wn % 2;
-    const int colrel[2] = {128 * ib + 32 * hh + lane % 32, 128 * ib + 64 + 32 * hh + lane % 32};
+    const int nbj[2] = {4 * ib + hh, 4 * ib + 2 + hh};
     int col[2];
-    const float* srow[2];
+    const float* ssrc[2];  // scale rows of the two columns (past N: row N-1, never stored)
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-        col[j] = n0 + colrel[j];
-        srow[j] = col[j] < p.n ? p.s + static_cast<std::size_t>(col[j]) * p.ld_s : nullptr;
+        col[j] = n0 + 32 * nbj[j] + lane % 32;
+        ssrc[j] = p.s + static_cast<std::size_t>(min(col[j], p.n - 1)) * p.ld_s;
     }
-    const auto scale_at = [&](int j, int g) -> float { return srow[j] != nullptr ? srow[j][g] : 1.0f; };
+
+    // one step's loads: X fragments straight into LDS, the W chunk into registers and, on a group's first step, the
+    // two column scales of the group (XFPW + 1 vector loads, + 2 on a group's first step, in this order)
+    const auto issue = [&](int kt, u32x4& wreg, float2& sreg) {
+        const int stage = kt % STAGES;
+#pragma unroll
+        for (int i = 0; i < XFPW; ++i) {
+            const int f = wave * XFPW + i;
+            __builtin_amdgcn_global_load_lds((global_void*)(xsrc[i] + static_cast<std::size_t>(kt) * BK * 2),
+                                             xs_base + stage * XSTAGE + f * 1024, 16, 0, 0);
+        }
+        wreg = *reinterpret_cast<const u32x4*>(wsrc + static_cast<std::size_t>(kt) * BK);
+        if (kt % (128 / BK) == 0) {
+            sreg.x = ssrc[0][kt / (128 / BK)];
+            sreg.y = ssrc[1][kt / (128 / BK)];
+        }
+    };
+    const auto convert = [&](int kt, const u32x4 wreg) {
+        unsigned o[8];
+        widen16<XT>(wreg, o);
+        lds_byte* d = ws_base + (kt % STAGES) * WSTAGE + wfrag * 1024;
+        *reinterpret_cast<__attribute__((address_space(3))) u32x4*>(d + 16 * (lane % 32)) = u32x4{o[0], o[1], o[2], o[3]};
+        *reinterpret_cast<__attribute__((address_space(3))) u32x4*>(d + 16 * (32 + lane % 32)) = u32x4{o[4], o[5], o[6], o[7]};
+    };
 
     f32x16 acc[4][2];
 #pragma unroll
@@ -172,58 +192,81 @@ __global__ void __launch_bounds__(128 * WN) gemm_big(const BigParams p) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-    float e[2], snext[2];
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        e[j] = next_scale(scale_at(j, 0), 1.0f);
-        snext[j] = p.k > 128 ? scale_at(j, 1) : 1.0f;
-    }
-
-    const int KT = p.k / BK;
-    gload(0);
-    lstore(0);
+    // ---- prologue: steps 0, 1, 2 in flight; step 0 published ----
+    u32x4 wr0, wr1, wr2;
+    float2 sr0, sr1, sr2;
+    issue(0, wr0, sr0);
+    if (KT > 1) issue(1, wr1, sr1);
+    if (KT > 2) issue(2, wr2, sr2);
+    convert(0, wr0);
+    wait_vmcnt<0>();
     __syncthreads();
-    for (int kt = 0; kt < KT; ++kt) {
-        const int buf = kt & 1;
-        if (kt + 1 < KT) gload(kt + 1);
-        if (kt > 0 && kt % GPS == 0) {
-            const int g = kt / GPS;
+    float e[2] = {sr0.x > 0.0f ? sr0.x : 1.0f, sr0.y > 0.0f ? sr0.y : 1.0f};
+
+    // The weight registers rotate through three names, W(s) in R[s % 3]; the loop is unrolled by three so the rotation
+    // is a renaming (a register copy would wait for the load in flight into it).
+    const auto step = [&](int kt, u32x4& r_next, u32x4& r_free, float2& s_free) {
+        // (a) widen step kt + 1's weights (loaded two steps ago) into their stage
+        if (kt + 1 < KT) convert(kt + 1, r_next);
+        // the scales of step kt's group when kt starts one (loaded before step kt + 1's weights, so already here),
+        // read before (b) reuses their registers
+        const float sk[2] = {s_free.x, s_free.y};
+        // (b) loads of step kt + 3 into the registers step kt used (its stage was last read by step kt - 1)
+        if (kt + 3 < KT) issue(kt + 3, r_free, s_free);
+        // (c) Horner step at a group boundary, then the multiply of step kt
+        if (kt > 0 && kt % (128 / BK) == 0) {
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
-                const float en = next_scale(snext[j], e[j]);
-                const float ratio = e[j] / en;
+                const float sg = sk[j];
+                const float en = sg > 0.0f ? sg : e[j];
+                const float ratio = __fmul_rn(e[j], __builtin_amdgcn_rcpf(en));
                 e[j] = en;
-                snext[j] = (g + 1) * 128 < p.k ? scale_at(j, g + 1) : 1.0f;
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
 #pragma unroll
                     for (int r = 0; r < 16; ++r) acc[i][j][r] = __fmul_rn(acc[i][j][r], ratio);
             }
         }
-        const u32x4* tx = lds_x[buf];
-        const u32x4* tw = lds_w[buf];
+        const lds_byte* xs = xs_base + (kt % STAGES) * XSTAGE + 16 * lane;
+        const lds_byte* ws = ws_base + (kt % STAGES) * WSTAGE + 16 * lane;
 #pragma unroll
         for (int st = 0; st < BK / 16; ++st) {
-            const int c = 2 * st + lane / 32;
             u32x4 a[4], b[2];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int row = wm * 128 + i * 32 + lane % 32;
-                a[i] = tx[row * CPR + (c ^ swz<BK>(row))];
-            }
+            for (int i = 0; i < 4; ++i)
+                a[i] = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(xs + ((wm * 4 + i) * (BK / 16) + st) * 1024);
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const int row = colrel[j];
-                b[j] = tw[row * CPR + (c ^ swz<BK>(row))];
-            }
+            for (int j = 0; j < 2; ++j)
+                b[j] = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(ws + (nbj[j] * (BK / 16) + st) * 1024);
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
                 for (int j = 0; j < 2; ++j) acc[i][j] = mfma32<XT>(a[i], b[j], acc[i][j]);
         }
-        if (kt + 1 < KT) lstore(buf ^ 1);
+        // (d) step kt + 1's X fragments have landed (its weights were waited for in (a), and those were issued after
+        // them), then publish
+        // (loads issued after them, at least: steps kt + 2 and kt + 3, the scale pair on a group's first step)
+        constexpr int SPG = 128 / BK;
+        if (kt + 3 < KT) {
+            if ((kt + 2) % SPG == 0 || (kt + 3) % SPG == 0) wait_vmcnt<2 * (XFPW + 1) + 2>();
+            else wait_vmcnt<2 * (XFPW + 1)>();
+        } else if (kt + 2 < KT) {
+            if ((kt + 2) % SPG == 0) wait_vmcnt<XFPW + 3>();
+            else wait_vmcnt<XFPW + 1>();
+        } else {
+            wait_vmcnt<0>();
+        }
         __syncthreads();
+    };
+    // R0 = wr0 held W(0) (converted in the prologue), R1 = W(1), R2 = W(2)
+    int kt = 0;
+    for (; kt + 3 <= KT; kt += 3) {
+        step(kt, wr1, wr0, sr0);      // W(kt+1) in R1, W(kt+3) -> R0
+        step(kt + 1, wr2, wr1, sr1);  // W(kt+2) in R2, W(kt+4) -> R1
+        step(kt + 2, wr0, wr2, sr2);  // W(kt+3) in R0, W(kt+5) -> R2
     }
+    if (kt < KT) step(kt, wr1, wr0, sr0);
+    if (kt + 1 < KT) step(kt + 1, wr2, wr1, sr1);
 
     // ---- epilogue ----
 #pragma unroll
@@ -235,7 +278,7 @@ __global__ void __launch_bounds__(128 * WN) gemm_big(const BigParams p) {
             const float v0 = __fmul_rn(acc[i][0][r], e[0]), v1 = __fmul_rn(acc[i][1][r], e[1]);
             if constexpr (EP == SEPAL_HIP_SWIGLU) {
                 const int f = n0 / 2 + 64 * ib + 32 * hh + lane % 32;
-                if (2 * f < p.n) store_out<YT>(p.y, static_cast<std::size_t>(row) * p.ld_y + f, swiglu_libm(v0, v1));
+                if (2 * f < p.n) store_out<YT>(p.y, static_cast<std::size_t>(row) * p.ld_y + f, swiglu_fast(v0, v1));
             } else {
                 float* y = static_cast<float*>(p.y);
                 if (col[0] < p.n) put_plain<EP>(y, static_cast<std::size_t>(row) * p.ld_y + col[0], v0);
@@ -245,7 +288,29 @@ __global__ void __launch_bounds__(128 * WN) gemm_big(const BigParams p) {
     }
 }
 
+template <int WN>
+constexpr std::size_t lds_bytes() {
+    return static_cast<std::size_t>(STAGES) * ((BM / 32) * (BK / 16) + (64 * WN / 32) * (BK / 16)) * 1024;
+}
+
+} // namespace v2
+
 // ---- launch ----------------------------------------------------------------------------------------------------------
+
+template <int XT, int EP, int YT, int WN>
+void launch_big2(const BigParams& p, hipStream_t stream) {
+    const auto kernel = v2::gemm_big2<XT, EP, YT, WN>;
+    const std::size_t lds = v2::lds_bytes<WN>();
+    static_assert(v2::lds_bytes<WN>() <= (160u << 10), "LDS of one CU");
+    static std::size_t raised = 0;
+    if (lds > raised) {
+        if (hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                static_cast<int>(lds)) != hipSuccess)
+            throw LaunchError("gemm_w8g large-M: hipFuncSetAttribute(MaxDynamicSharedMemorySize) failed");
+        raised = lds;
+    }
+    kernel<<<dim3(p.tiles_m * p.tiles_n), dim3(128 * WN), lds, stream>>>(p);
+}
 
 template <int XT, int EP, int YT>
 void launch_big(const GemmArgs& a, hipStream_t stream) {
@@ -258,10 +323,10 @@ void launch_big(const GemmArgs& a, hipStream_t stream) {
     p.tiles_m = tiles_m;
     if (wide) {
         p.tiles_n = tn256;
-        gemm_big<XT, EP, YT, 4, 64><<<dim3(tiles_m * p.tiles_n), dim3(512), 0, stream>>>(p);
+        launch_big2<XT, EP, YT, 4>(p, stream);
     } else {
         p.tiles_n = static_cast<int>((a.n + 127) / 128);
-        gemm_big<XT, EP, YT, 2, 32><<<dim3(tiles_m * p.tiles_n), dim3(256), 0, stream>>>(p);
+        launch_big2<XT, EP, YT, 2>(p, stream);
     }
     check_launch("gemm_w8g large-M kernel launch");
 }
@@ -295,3 +360,4 @@ void launch_gemm_w8g(const GemmArgs& a, hipStream_t stream) {
 }
 
 } // namespace sepal::hip
+

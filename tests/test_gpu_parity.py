@@ -149,7 +149,8 @@ def test_float_to_bf16(sm):
 
 # ---- w8g ---------------------------------------------------------------------------------------------------------------
 
-W8G_CASES = [(37, 256, 256), (130, 128, 512), (300, 512, 1280), (1, 256, 2560), (64, 384, 640), (600, 96, 384)]
+# (70, 64, 16640): a long K (130 groups)
+W8G_CASES = [(37, 256, 256), (130, 128, 512), (300, 512, 1280), (1, 256, 2560), (64, 384, 640), (600, 96, 384), (70, 64, 16640)]
 
 
 def _w8g_problem(rng, t, n, k, xdt):
