@@ -102,7 +102,7 @@ __device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int& 
 // loads.
 namespace v2 {
 
-constexpr int BM = 256, BK = 32, STAGES = 4;
+constexpr int BM = 256, BK = 32, STAGES = 2;
 
 typedef __attribute__((address_space(3))) unsigned char lds_byte;
 typedef const __attribute__((address_space(1))) void global_void;
@@ -116,11 +116,12 @@ __device__ __forceinline__ void wait_vmcnt() {
 }
 
 template <int XT, int EP, int YT, int WN>
-__global__ void __launch_bounds__(128 * WN) gemm_big2(const BigParams p) {
-    constexpr int NT = 128 * WN, NW = NT / 64;   // threads, waves (2 along M, WN along N)
+__global__ void __launch_bounds__(128 * WN) __attribute__((amdgpu_waves_per_eu(2))) gemm_big2(const BigParams p) {
+    constexpr int NT = 128 * WN, NW = NT / 64;   // threads, waves (2 along M, WN along N; each 128 x 64 outputs)
     constexpr int BN = 64 * WN;
+    constexpr int SPG = 128 / BK;                 // steps per scale group
     constexpr int XF = (BM / 32) * (BK / 16);     // X fragments per stage (16)
-    constexpr int WF = (BN / 32) * (BK / 16);     // W fragments per stage
+    constexpr int WF = (BN / 32) * (BK / 16);     // W fragments per stage (4 WN)
     constexpr int XFPW = XF / NW;                 // X fragments each wave loads per stage
     constexpr int XSTAGE = XF * 1024, WSTAGE = WF * 1024;
     static_assert(WF == 2 * NW, "one W chunk per thread per stage");
@@ -136,52 +137,56 @@ __global__ void __launch_bounds__(128 * WN) gemm_big2(const BigParams p) {
     const int m0 = tm * BM, n0 = tn * BN;
     const int KT = p.k / BK;
 
-    // ---- per-lane global sources (clamped: rows past T repeat row T-1, never stored) ----
-    const unsigned char* xsrc[XFPW];
+    // ---- per-lane global sources (clamped: rows past T or N repeat the last row, never stored) ----
+    const u32x4* xsrc[XFPW];
 #pragma unroll
     for (int i = 0; i < XFPW; ++i) {
         const int f = wave * XFPW + i, mb = f / (BK / 16), st = f % (BK / 16);
         const int row = min(m0 + mb * 32 + lane % 32, p.t - 1);
-        xsrc[i] = reinterpret_cast<const unsigned char*>(p.x + static_cast<std::size_t>(row) * p.ld_x + 16 * st + 8 * (lane / 32));
+        xsrc[i] = reinterpret_cast<const u32x4*>(p.x + static_cast<std::size_t>(row) * p.ld_x + 16 * st + 8 * (lane / 32));
     }
     const int wrow_n = min(n0 + 32 * wave + lane % 32, p.n - 1);
     const signed char* wsrc = p.w + static_cast<std::size_t>(wrow_n) * p.ld_w + 16 * (lane / 32);
-    // LDS destinations: X fragments (wave-uniform bases), the W fragment halves of this lane
-    const int wfrag = wave * 2 + lane / 32;  // W fragment (nb = wave, st = lane / 32)
+    const int wfrag = wave * 2 + lane / 32;  // the W fragment this lane widens (n-block = wave, substep = lane / 32)
 
-    // this lane's output columns: n-block j = 0 (gate half for SwiGLU) and 1 (the matching up half)
+    // this lane's output columns: n-block j = 0 (gate half for SwiGLU) and 1 (the matching up half; gate and up
+    // alternate every 64 columns)
     const int ib = wn / 2, hh = wn % 2;
     const int nbj[2] = {4 * ib + hh, 4 * ib + 2 + hh};
     int col[2];
-    const float* ssrc[2];  // scale rows of the two columns (past N: row N-1, never stored)
+    const float* ssrc[2];  // scale rows of the two columns
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
         col[j] = n0 + 32 * nbj[j] + lane % 32;
         ssrc[j] = p.s + static_cast<std::size_t>(min(col[j], p.n - 1)) * p.ld_s;
     }
 
-    // one step's loads: X fragments straight into LDS, the W chunk into registers and, on a group's first step, the
-    // two column scales of the group (XFPW + 1 vector loads, + 2 on a group's first step, in this order)
-    const auto issue = [&](int kt, u32x4& wreg, float2& sreg) {
-        const int stage = kt % STAGES;
-#pragma unroll
-        for (int i = 0; i < XFPW; ++i) {
-            const int f = wave * XFPW + i;
-            __builtin_amdgcn_global_load_lds((global_void*)(xsrc[i] + static_cast<std::size_t>(kt) * BK * 2),
-                                             xs_base + stage * XSTAGE + f * 1024, 16, 0, 0);
-        }
-        wreg = *reinterpret_cast<const u32x4*>(wsrc + static_cast<std::size_t>(kt) * BK);
-        if (kt % (128 / BK) == 0) {
-            sreg.x = ssrc[0][kt / (128 / BK)];
-            sreg.y = ssrc[1][kt / (128 / BK)];
-        }
+    // one step's operands, loaded into registers: the lane's X fragment chunks and W chunk
+    struct Regs {
+        u32x4 x[XFPW];
+        u32x4 w;
     };
-    const auto convert = [&](int kt, const u32x4 wreg) {
+    float snext[2];  // the next group's scales, loaded ahead of its first step's operands
+    const auto issue = [&](int kt, Regs& r) {
+#pragma unroll
+        for (int i = 0; i < XFPW; ++i) r.x[i] = xsrc[i][static_cast<std::size_t>(kt) * (BK * 2 / 16)];
+        r.w = *reinterpret_cast<const u32x4*>(wsrc + static_cast<std::size_t>(kt) * BK);
+    };
+    const auto issue_scales = [&](int g) {
+        snext[0] = ssrc[0][g];
+        snext[1] = ssrc[1][g];
+    };
+    // the step's operands into its LDS stage, in fragment order, the weights widened exactly to the MFMA type
+    const auto stage = [&](int kt, const Regs& r) {
+        lds_byte* xd = xs_base + (kt % STAGES) * XSTAGE + 16 * lane;
+#pragma unroll
+        for (int i = 0; i < XFPW; ++i)
+            *reinterpret_cast<__attribute__((address_space(3))) u32x4*>(xd + (wave * XFPW + i) * 1024) = r.x[i];
         unsigned o[8];
-        widen16<XT>(wreg, o);
-        lds_byte* d = ws_base + (kt % STAGES) * WSTAGE + wfrag * 1024;
-        *reinterpret_cast<__attribute__((address_space(3))) u32x4*>(d + 16 * (lane % 32)) = u32x4{o[0], o[1], o[2], o[3]};
-        *reinterpret_cast<__attribute__((address_space(3))) u32x4*>(d + 16 * (32 + lane % 32)) = u32x4{o[4], o[5], o[6], o[7]};
+        widen16<XT>(r.w, o);
+        lds_byte* wd = ws_base + (kt % STAGES) * WSTAGE + wfrag * 1024 + 16 * (lane % 32);
+        *reinterpret_cast<__attribute__((address_space(3))) u32x4*>(wd) = u32x4{o[0], o[1], o[2], o[3]};
+        *reinterpret_cast<__attribute__((address_space(3))) u32x4*>(wd + 512) = u32x4{o[4], o[5], o[6], o[7]};
     };
 
     f32x16 acc[4][2];
@@ -192,39 +197,38 @@ __global__ void __launch_bounds__(128 * WN) gemm_big2(const BigParams p) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-    // ---- prologue: steps 0, 1, 2 in flight; step 0 published ----
-    u32x4 wr0, wr1, wr2;
-    float2 sr0, sr1, sr2;
-    issue(0, wr0, sr0);
-    if (KT > 1) issue(1, wr1, sr1);
-    if (KT > 2) issue(2, wr2, sr2);
-    convert(0, wr0);
-    wait_vmcnt<0>();
+    // ---- prologue: group 0's scales, steps 0, 1, 2 in flight; step 0 staged ----
+    Regs r0, r1, r2, r3;
+    issue_scales(0);
+    issue(0, r0);
+    issue(1, r1);
+    issue(2, r2);
+    stage(0, r0);
     __syncthreads();
-    float e[2] = {sr0.x > 0.0f ? sr0.x : 1.0f, sr0.y > 0.0f ? sr0.y : 1.0f};
+    float e[2] = {snext[0] > 0.0f ? snext[0] : 1.0f, snext[1] > 0.0f ? snext[1] : 1.0f};
 
-    // The weight registers rotate through three names, W(s) in R[s % 3]; the loop is unrolled by three so the rotation
-    // is a renaming (a register copy would wait for the load in flight into it).
-    const auto step = [&](int kt, u32x4& r_next, u32x4& r_free, float2& s_free) {
-        // (a) widen step kt + 1's weights (loaded two steps ago) into their stage
-        if (kt + 1 < KT) convert(kt + 1, r_next);
-        // the scales of step kt's group when kt starts one (loaded before step kt + 1's weights, so already here),
-        // read before (b) reuses their registers
-        const float sk[2] = {s_free.x, s_free.y};
-        // (b) loads of step kt + 3 into the registers step kt used (its stage was last read by step kt - 1)
-        if (kt + 3 < KT) issue(kt + 3, r_free, s_free);
-        // (c) Horner step at a group boundary, then the multiply of step kt
-        if (kt > 0 && kt % (128 / BK) == 0) {
+    // One step: stage step kt + 1's operands (loaded two steps ago; the stage was last read by step kt - 1) and issue
+    // step kt + 3's loads into the registers they leave (the next group's scales first when kt + 3 starts a group); at a
+    // group's first step the Horner rescale; the multiply of step kt; one barrier. The load registers rotate through
+    // four names, step s in R[s % 4], and the loop runs one group (four steps) per iteration, so the rotation is a
+    // renaming and the group boundary is known at compile time.
+    const auto step = [&](int kt, const Regs& r_next, Regs& r_free, auto first_t) {
+        constexpr bool first = decltype(first_t)::value;
+        if (kt + 1 < KT) stage(kt + 1, r_next);
+        if (kt + 3 < KT) {
+            if ((kt + 3) % SPG == 0) issue_scales((kt + 3) / SPG);
+            issue(kt + 3, r_free);
+        }
+        if constexpr (first) {
+            if (kt > 0) {
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const float sg = sk[j];
-                const float en = sg > 0.0f ? sg : e[j];
-                const float ratio = __fmul_rn(e[j], __builtin_amdgcn_rcpf(en));
-                e[j] = en;
+                for (int j = 0; j < 2; ++j) {
+                    const float en = snext[j] > 0.0f ? snext[j] : e[j];
+                    const float ratio = __fmul_rn(e[j], __builtin_amdgcn_rcpf(en));
+                    e[j] = en;
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) acc[i][j][r] = __fmul_rn(acc[i][j][r], ratio);
+                    for (int i = 0; i < 4; ++i) acc[i][j] = acc[i][j] * ratio;
+                }
             }
         }
         const lds_byte* xs = xs_base + (kt % STAGES) * XSTAGE + 16 * lane;
@@ -243,30 +247,15 @@ __global__ void __launch_bounds__(128 * WN) gemm_big2(const BigParams p) {
 #pragma unroll
                 for (int j = 0; j < 2; ++j) acc[i][j] = mfma32<XT>(a[i], b[j], acc[i][j]);
         }
-        // (d) step kt + 1's X fragments have landed (its weights were waited for in (a), and those were issued after
-        // them), then publish
-        // (loads issued after them, at least: steps kt + 2 and kt + 3, the scale pair on a group's first step)
-        constexpr int SPG = 128 / BK;
-        if (kt + 3 < KT) {
-            if ((kt + 2) % SPG == 0 || (kt + 3) % SPG == 0) wait_vmcnt<2 * (XFPW + 1) + 2>();
-            else wait_vmcnt<2 * (XFPW + 1)>();
-        } else if (kt + 2 < KT) {
-            if ((kt + 2) % SPG == 0) wait_vmcnt<XFPW + 3>();
-            else wait_vmcnt<XFPW + 1>();
-        } else {
-            wait_vmcnt<0>();
-        }
         __syncthreads();
     };
-    // R0 = wr0 held W(0) (converted in the prologue), R1 = W(1), R2 = W(2)
-    int kt = 0;
-    for (; kt + 3 <= KT; kt += 3) {
-        step(kt, wr1, wr0, sr0);      // W(kt+1) in R1, W(kt+3) -> R0
-        step(kt + 1, wr2, wr1, sr1);  // W(kt+2) in R2, W(kt+4) -> R1
-        step(kt + 2, wr0, wr2, sr2);  // W(kt+3) in R0, W(kt+5) -> R2
+    static_assert(SPG == 4, "four steps per group");
+    for (int kt = 0; kt < KT; kt += 4) {
+        step(kt, r1, r3, std::true_type{});        // R1 holds step kt+1, step kt+3 -> R3
+        step(kt + 1, r2, r0, std::false_type{});   // R2 holds kt+2, kt+4 -> R0
+        step(kt + 2, r3, r1, std::false_type{});   // R3 holds kt+3, kt+5 -> R1
+        step(kt + 3, r0, r2, std::false_type{});   // R0 holds kt+4, kt+6 -> R2
     }
-    if (kt < KT) step(kt, wr1, wr0, sr0);
-    if (kt + 1 < KT) step(kt + 1, wr2, wr1, sr1);
 
     // ---- epilogue ----
 #pragma unroll
