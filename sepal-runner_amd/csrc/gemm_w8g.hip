@@ -211,24 +211,23 @@ __global__ void __launch_bounds__(128 * WN) __attribute__((amdgpu_waves_per_eu(2
     // step kt + 3's loads into the registers they leave (the next group's scales first when kt + 3 starts a group); at a
     // group's first step the Horner rescale; the multiply of step kt; one barrier. The load registers rotate through
     // four names, step s in R[s % 4], and the loop runs one group (four steps) per iteration, so the rotation is a
-    // renaming and the group boundary is known at compile time.
+    // renaming and the group boundary is known at compile time. The body has no branches, so the compiler's load
+    // counting stays exact: near the end the loads repeat the last step (clamped) and the extra stage written at the
+    // last step lands in a buffer nothing reads again. At step 0 the rescale multiplies zero accumulators.
+    const int groups = KT / SPG;
     const auto step = [&](int kt, const Regs& r_next, Regs& r_free, auto first_t) {
         constexpr bool first = decltype(first_t)::value;
-        if (kt + 1 < KT) stage(kt + 1, r_next);
-        if (kt + 3 < KT) {
-            if ((kt + 3) % SPG == 0) issue_scales((kt + 3) / SPG);
-            issue(kt + 3, r_free);
-        }
+        stage(kt + 1, r_next);
+        if ((kt + 3) % SPG == 0) issue_scales(min((kt + 3) / SPG, groups - 1));
+        issue(min(kt + 3, KT - 1), r_free);
         if constexpr (first) {
-            if (kt > 0) {
 #pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    const float en = snext[j] > 0.0f ? snext[j] : e[j];
-                    const float ratio = __fmul_rn(e[j], __builtin_amdgcn_rcpf(en));
-                    e[j] = en;
+            for (int j = 0; j < 2; ++j) {
+                const float en = snext[j] > 0.0f ? snext[j] : e[j];
+                const float ratio = __fmul_rn(e[j], __builtin_amdgcn_rcpf(en));
+                e[j] = en;
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) acc[i][j] = acc[i][j] * ratio;
-                }
+                for (int i = 0; i < 4; ++i) acc[i][j] = acc[i][j] * ratio;
             }
         }
         const lds_byte* xs = xs_base + (kt % STAGES) * XSTAGE + 16 * lane;
