@@ -116,7 +116,8 @@ SEPAL_HIP_API int32_t sepal_hip_q8_group_sums(const int8_t* xq, size_t ld_x, con
 
 /* RMSNorm of rows with the cpu-q8 summation order (runner/src/cpu/elementwise.cpp:22-59): y = (x * inv) * w1 with
  * inv = (float)(1 / sqrt(mean(x^2) + eps)); w1 NULL means ones. x float32 [rows, ld_x]; y of y_type [rows, ld_y].
- * cols a multiple of 8. Glue of the layer stack (the MLP input norm, cuda_engine.cpp:1915-1918). */
+ * cols a multiple of 8; x 16-byte aligned, ld_x a multiple of 4. Glue of the layer stack (the MLP input norm,
+ * cuda_engine.cpp:1915-1918). */
 SEPAL_HIP_API int32_t sepal_hip_rmsnorm_rows(const float* x, size_t ld_x, void* y, int32_t y_type, size_t ld_y, const float* w1,
                                size_t rows, size_t cols, double eps, void* stream);
 

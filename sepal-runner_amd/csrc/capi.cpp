@@ -260,6 +260,7 @@ int32_t sepal_hip_rmsnorm_rows(const float* x, size_t ld_x, void* y, int32_t y_t
         if (rows == 0 || cols == 0) return;
         require(x != nullptr && y != nullptr, "rmsnorm_rows: null pointer");
         require(ld_x >= cols && ld_y >= cols, "rmsnorm_rows: strides below cols");
+        require(ld_x % 4 == 0 && aligned16(x), "rmsnorm_rows: x must be 16-byte aligned with a stride that is a multiple of 4");
         require(eps > 0.0, "rmsnorm_rows: eps must be positive");
         launch_rmsnorm(x, ld_x, y, y_type, ld_y, w1, rows, cols, eps, as_stream(stream));
     });
@@ -292,6 +293,16 @@ int32_t sepal_hip_mlp_stack(int32_t kind, size_t layers, size_t t, size_t hidden
         const std::size_t off_h = kScratchOffset;
         const std::size_t off_q = off_h + (h_bytes + 255) / 256 * 256;
         const std::size_t off_s = off_q + (q_bytes + 255) / 256 * 256;
+        SmallStackPlan plan{};
+        if (kind == 0 && small_stack_plan(t, hidden, inter, plan)) {
+            // M <= 16: three launches per layer (stack_small.hip); H binary16, the down pass's partial sums float32
+            const std::size_t off_p = off_h + (h_bytes + 255) / 256 * 256;
+            char* wsp = static_cast<char*>(workspace(off_p + static_cast<std::size_t>(plan.parts) * t * hidden * 4, st));
+            for (std::size_t l = 0; l < layers; ++l)
+                launch_small_layer(plan, t, hidden, inter, x, w_gate_up[l], s_gate_up[l], w_down[l], s_down[l], wsp + off_h,
+                                   reinterpret_cast<float*>(wsp + off_p), y, l + 1 < layers ? x : nullptr, eps, st);
+            return;
+        }
         char* ws = static_cast<char*>(workspace(off_s + s_bytes, st));
         void* h = ws + off_h;
         std::int8_t* xq = reinterpret_cast<std::int8_t*>(ws + off_q);

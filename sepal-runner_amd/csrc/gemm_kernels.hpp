@@ -45,4 +45,18 @@ void launch_rmsnorm(const float* x, std::size_t ld_x, void* y, int y_type, std::
                     std::size_t rows, std::size_t cols, double eps, hipStream_t stream);
 void launch_f32_to_bf16(const float* src, std::uint16_t* dst, std::size_t count, hipStream_t stream);
 
+// The M <= 16 w8g layer of the MLP stack (stack_small.hip): a launch plan for one shape and device, and one layer.
+struct SmallStackPlan {
+    int blocks;           // blocks of the gate/up pass grid (one per CU)
+    int tiles_per_block;  // gate/up weight tiles (8 features) per block
+    int parts;            // K-parts of the down pass
+    int units_per_block;  // (K-part, column tile) units per block of the down pass
+};
+bool small_stack_plan(std::size_t t, std::size_t hidden, std::size_t inter, SmallStackPlan& plan);
+// x bf16 [t, hidden] -> h binary16 [t, inter] -> part float32 [parts][t][hidden] -> y float32 [t, hidden] and, when
+// xn is set, xn bf16 [t, hidden] = RMSNorm(y) (cpu-q8 order, identity weight).
+void launch_small_layer(const SmallStackPlan& plan, std::size_t t, std::size_t hidden, std::size_t inter, const void* x,
+                        const std::int8_t* w_gu, const float* s_gu, const std::int8_t* w_d, const float* s_d, void* h,
+                        float* part, float* y, void* xn, double eps, hipStream_t stream);
+
 } // namespace sepal::hip

@@ -15,6 +15,8 @@
 //     epilogue, so the result does not depend on which block finishes last. With one split the chain is whole and
 //     the q8 result equals cpu-q8 bit for bit.
 #include <cstdlib>
+#include <mutex>
+#include <vector>
 
 #include "common.hpp"
 #include "gemm_kernels.hpp"
@@ -294,25 +296,47 @@ __global__ void __launch_bounds__(256) gemm_stream(const Params p) {
 
 // ---- launch ----------------------------------------------------------------------------------------------------------
 
-// Groups per split: the most groups (fewest partials) that still give about two blocks per CU, capped so that the X
-// slice fits the LDS. SEPAL_HIP_STREAM_GPS overrides it (tuning).
-// Groups per split: the most groups (the fewest partial sums) that still give about four blocks per CU, at most kGMax
+// Blocks of a kernel that the device holds at once (occupancy x CUs) with `lds` bytes of dynamic LDS; asked once per
+// kernel, device and size.
+inline int resident_blocks(const void* kernel, std::size_t lds) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) throw LaunchError("small-M multiply: hipGetDevice failed");
+    struct Entry {
+        const void* kernel;
+        int dev;
+        std::size_t lds;
+        int blocks;
+    };
+    static std::mutex mu;
+    static std::vector<Entry> cache;
+    std::lock_guard<std::mutex> lock(mu);
+    for (const Entry& e : cache)
+        if (e.kernel == kernel && e.dev == dev && e.lds == lds) return e.blocks;
+    int per_cu = 0, cus = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 256, lds) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        throw LaunchError("small-M multiply: occupancy query failed");
+    const int blocks = (per_cu > 0 ? per_cu : 1) * cus;
+    cache.push_back({kernel, dev, lds, blocks});
+    return blocks;
+}
+
+// Groups per split: the fewest splits (fewest partial sums) that still fill the blocks the device holds at once,
+// without passing that number (a second round of blocks would wait for the first to drain), at most kGMax groups
 // (every weight load of a split is issued at once) and an X slice within 64 KB of LDS. SEPAL_HIP_STREAM_GPS
 // overrides it (tuning).
-inline int pick_gps(int spans, int groups, int mt, int xbytes, int force_splits) {
+inline int pick_gps(int spans, int groups, int mt, int xbytes, int force_splits, int resident) {
     const int lds_cap = ((64 << 10) / (16 * mt) - 16) / (128 * xbytes);
     static const int env = [] {
         const char* v = std::getenv("SEPAL_HIP_STREAM_GPS");
         return v != nullptr ? std::atoi(v) : 0;
     }();
-    int gps;
     if (force_splits == 1) return groups;  // the caller's LDS check refuses what does not fit
-    if (env > 0) gps = env;
-    else {
-        const int want_splits = (4 * 256 + spans - 1) / spans;
-        gps = (groups + want_splits - 1) / want_splits;
-    }
-    return max(1, min(gps, min(groups, min(lds_cap, kGMax))));
+    const int cap = max(1, min(groups, min(lds_cap, kGMax)));
+    if (env > 0) return max(1, min(env, cap));
+    const int max_splits = max(1, resident / max(1, spans));   // splits that fit in one round
+    int gps = (groups + max_splits - 1) / max_splits;          // fewest groups per split within that
+    return max(1, min(gps < 1 ? 1 : gps, cap));
 }
 
 template <int KIND, int EP, int YT, int MT>
@@ -337,14 +361,21 @@ void launch_mt(const GemmArgs& a, hipStream_t stream) {
     p.k = static_cast<int>(a.k);
     p.spans = static_cast<int>((a.n + kSpan - 1) / kSpan);
     const int groups = p.k / 128;
-    p.gps = pick_gps(p.spans, groups, MT, K::xbytes, a.force_splits);
+    const auto kernel = gemm_stream<KIND, EP, YT, MT>;
+    const std::size_t rows = 16 * MT;
+    const auto lds_of = [&](int gps) {
+        const std::size_t x_bytes = rows * (static_cast<std::size_t>(gps) * 128 * K::xbytes + 16) +
+                                    (K::q8 ? rows * gps * sizeof(float) : 0);
+        const std::size_t tile_bytes = rows * (kSpan + 4) * sizeof(float);
+        return x_bytes > tile_bytes ? x_bytes : tile_bytes;
+    };
+    // occupancy at the largest slice this instance may take
+    const int lds_cap = ((64 << 10) / (16 * MT) - 16) / (128 * K::xbytes);  // as pick_gps
+    const int resident = resident_blocks(reinterpret_cast<const void*>(kernel), lds_of(max(1, min(kGMax, min(groups, lds_cap)))));
+    p.gps = pick_gps(p.spans, groups, MT, K::xbytes, a.force_splits, resident);
     p.splits = (groups + p.gps - 1) / p.gps;
     require(a.force_splits != 1 || p.gps <= kGMax, "small-M multiply without a K split (config 2) takes K <= 1280");
-    const std::size_t rows = 16 * MT;
-    const std::size_t x_bytes = rows * (static_cast<std::size_t>(p.gps) * 128 * K::xbytes + 16) +
-                                (K::q8 ? rows * p.gps * sizeof(float) : 0);
-    const std::size_t tile_bytes = rows * (kSpan + 4) * sizeof(float);
-    const std::size_t lds = x_bytes > tile_bytes ? x_bytes : tile_bytes;
+    const std::size_t lds = lds_of(p.gps);
     require(lds <= (160u << 10) - 1024, "small-M multiply: K too long for one split (use config 1)");
     if (p.splits > 1) {
         const std::size_t part = static_cast<std::size_t>(p.splits) * rows * p.spans * kSpan * sizeof(float);
@@ -354,7 +385,6 @@ void launch_mt(const GemmArgs& a, hipStream_t stream) {
         p.counters = reinterpret_cast<unsigned*>(ws);
         p.partial = reinterpret_cast<float*>(ws + kCounterBytes);
     }
-    const auto kernel = gemm_stream<KIND, EP, YT, MT>;
     if (lds > (64u << 10)) {
         static std::size_t raised = 0;  // per kernel instance: the largest dynamic LDS size allowed so far
         if (lds > raised) {

@@ -138,6 +138,16 @@ def test_rmsnorm_matches_reference(sm, golden):
         assert same_bits(host(ob), orc.bf16_round(y))
 
 
+@pytest.mark.parametrize("rows,cols", [(37, 2056), (3, 4104), (9, 2048), (5, 24)])
+def test_rmsnorm_segment_edges(sm, rows, cols):
+    """Rows longer than one LDS segment, with the 8-wide tail starting at a segment boundary (exact order vs oracle)."""
+    say("rmsnorm segments", rows, cols)
+    rng = np.random.default_rng(rows * cols)
+    x = (rng.standard_normal((rows, cols)) * 3).astype(np.float32)
+    out = sm.rmsnorm_rows(dev(x), y_dtype=torch.float32)
+    assert same_bits(host(out), orc.rmsnorm_rows(x))
+
+
 def test_float_to_bf16(sm):
     say("float_to_bf16")
     rng = np.random.default_rng(4)
@@ -378,6 +388,43 @@ def test_mlp_stack(sm, kind, act, t):
         # through 3 layers the bf16 rounding of each layer's input turns ulp-level differences into whole bf16
         # steps on a few activations; the stack stays within a few bf16 steps of the oracle
         assert rel_rms(y, ref) < 2e-3, rel_rms(y, ref)
+
+
+@pytest.mark.parametrize("t", [1, 5, 16])
+def test_mlp_stack_small_path(sm, t):
+    """M <= 16 w8g stack (three launches per layer: whole-K gate/up tiles per CU, K-part partial sums for down, a
+    reduce + RMSNorm pass) against the oracle and against the stack's steps called one by one (same math, other
+    summation order: within tolerance, not bit for bit)."""
+    say("mlp stack small path t", t)
+    rng = np.random.default_rng(77 + t)
+    hidden, inter, nl = 512, 1024, 3
+    layers = _stack_weights(sm, rng, nl, hidden, inter, rule=0)
+    x = bf16_inputs(rng, (t, hidden))
+    xt = dev(x, torch.bfloat16)
+    y = host(sm.mlp_stack(0, xt, layers))
+    ref = _oracle_stack(0, x, layers, 128)
+    assert rel_rms(y, ref) < 2e-3, rel_rms(y, ref)
+    comp = _gpu_composition(sm, 0, x, layers, 128)
+    assert rel_rms(y, comp) < 2e-3, rel_rms(y, comp)
+    # x now holds the last layer's input, bf16(RMSNorm(y of layer nl - 2))
+    y2 = _oracle_stack(0, x, layers[:2], 128)
+    assert rel_rms(host(xt).astype(np.float32), orc.bf16_round(orc.rmsnorm_rows(y2))) < 2e-3
+    y1 = host(sm.mlp_stack(0, dev(x, torch.bfloat16), layers[:1]))
+    ref1 = _oracle_stack(0, x, layers[:1], 128)
+    assert max_rel_over_rms(y1, ref1) < 2e-3, max_rel_over_rms(y1, ref1)
+
+
+def test_mlp_stack_small_path_full_size(sm):
+    """The M = 16 stack at the model's shape (H 2560, I 9728), two layers, against the oracle."""
+    say("mlp stack small path full size")
+    rng = np.random.default_rng(5)
+    layers = _stack_weights(sm, rng, 2, 2560, 9728, rule=0)
+    x = bf16_inputs(rng, (16, 2560))
+    y1 = host(sm.mlp_stack(0, dev(x, torch.bfloat16), layers[:1]))
+    ref1 = _oracle_stack(0, x, layers[:1], 128)
+    assert max_rel_over_rms(y1, ref1) < 2e-3, max_rel_over_rms(y1, ref1)
+    y = host(sm.mlp_stack(0, dev(x, torch.bfloat16), layers))
+    assert rel_rms(y, _oracle_stack(0, x, layers, 128)) < 2e-3
 
 
 # ---- BASELINE shapes (H 2560, I 9728) on sampled rows ------------------------------------------------------------------
