@@ -52,6 +52,9 @@ def parse():
     ap.add_argument("--no-extra", action="store_true", help="only the headline C3 measurement")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-rows", type=int, default=4096, help="rows of the CPU baseline sample")
+    ap.add_argument("--profile-kernels", action="store_true",
+                    help="for rocprofv3 --pmc runs: a plain copy of COPY_BYTES (the counters' calibration), then three "
+                         "launches each of the C3 gate/up and down kernels; no timing, no JSON line")
     return ap.parse_args()
 
 
@@ -159,8 +162,43 @@ def load_traffic():
         return None
 
 
+COPY_BYTES = 1 << 30  # the calibration copy: 1 GiB read and 1 GiB written
+
+
+def profile_kernels():
+    """Launches for counter collection (FETCH_SIZE / WRITE_SIZE): the copy's counters per byte scale the kernels'."""
+    import torch
+
+    import sepal_mlp as sm
+
+    src = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    g = torch.Generator(device="cuda").manual_seed(1000)
+    gate = (torch.randn(I, H, generator=g, device="cuda") * 0.02).half()
+    up = (torch.randn(I, H, generator=g, device="cuda") * 0.02).half()
+    down = (torch.randn(H, I, generator=g, device="cuda") * 0.02).half()
+    wgu, sgu = sm.quantize_gate_up_s8(gate, up)
+    wd, sd = sm.quantize_group_s8(down)
+    x = bf16_x(torch, M_BIG, 0)
+    h = torch.empty(M_BIG, I, dtype=torch.float16, device="cuda")
+    y = torch.empty(M_BIG, H, dtype=torch.float32, device="cuda")
+    for _ in range(3):
+        sm.gemm_w8g(x, wgu, sgu, y=h, epilogue=sm.SWIGLU)
+    for _ in range(3):
+        sm.gemm_w8g(h, wd, sd, y=y)
+    torch.cuda.synchronize()
+    log("profile-kernels: done")
+
+
 def main():
     args = parse()
+    if args.profile_kernels:
+        profile_kernels()
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(f"bench.py: this build measures one GPU only (asked for {args.gpus}); the path shards by rows across GPUs "
               "with no exchange, so the aggregate is N x the one-GPU value", file=sys.stderr)
@@ -202,11 +240,11 @@ def main():
     dn_tflops = dn_flop / (ms_dn * 1e-3) / 1e12
     log(f"gate/up kernel {ms_gu:.3f} ms ({gu_tflops:.0f} TFLOP/s), down kernel {ms_dn:.3f} ms ({dn_tflops:.0f} TFLOP/s)")
     traffic = load_traffic()
-    roofline = {"bound": "mfma", "kernel": "gemm_big<bf16, SwiGLU> (C3 gate/up, M 15872, N 19456, K 2560)",
+    roofline = {"bound": "mfma", "kernel": "w8g::v2::gemm_big2<bf16, SwiGLU, f16> (C3 gate/up, M 15872, N 19456, K 2560)",
                 "achieved": round(gu_tflops, 1), "peak": PEAK["bf16_tflops"], "unit": "TFLOP/s",
                 "frac": round(gu_tflops / PEAK["bf16_tflops"], 4), "ms_per_launch": round(ms_gu, 4),
                 "algorithmic_flop_per_launch": gu_flop,
-                "traffic": traffic.get("gate_up_c3_bytes") if traffic else None}
+                "traffic": traffic.get("gate_up_c3", {}).get("bytes_per_launch") if traffic else None}
 
     extra = {"c3_down_kernel": {"ms": round(ms_dn, 4), "tflops": round(dn_tflops, 1),
                                 "frac_bf16_peak": round(dn_tflops / PEAK["bf16_tflops"], 4)}}

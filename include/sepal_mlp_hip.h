@@ -76,7 +76,7 @@ SEPAL_HIP_API int32_t sepal_hip_quantize_gate_up_s8(const void* gate, const void
  * ld_w multiples of 16; ld_y a multiple of 4; 16-byte aligned pointers. `config` -1 picks a path by T (small-M at T <= 64);
  * 0 forces the large-M tiled path, 1 the small-M weight-streaming path, 2 the small-M path without a split of K (the
  * whole K of a column block in one block; K at most 1280).
- * Replaces launch_gemm_simt with SimtWeight::Int8Group (runner/cuda/src/gemm_simt_kernels.hpp:53-56, .cu:312-332). */
+ * Replaces launch_gemm_simt with SimtWeight::Int8Group (runner/cuda/src/gemm_simt_kernels.hpp:55-57, .cu:312-332). */
 SEPAL_HIP_API int32_t sepal_hip_gemm_w8g(const void* x, int32_t x_type, size_t ld_x, const int8_t* w, size_t ld_w, const float* s,
                            size_t ld_s, void* y, int32_t y_type, size_t ld_y, size_t t, size_t n, size_t k,
                            int32_t epilogue, int32_t config, void* stream);
@@ -130,7 +130,10 @@ SEPAL_HIP_API int32_t sepal_hip_float_to_bf16(const float* src, uint16_t* dst, s
  * kind 0 = w8g (x bf16 [T, hidden]; H binary16), kind 1 = q8 (x bf16; activations quantised per act_block before each
  * multiply; H float32). Weight arrays hold `layers` device pointers each: gate_up int8 [2*inter, hidden] + scales
  * [2*inter, hidden/128]; down int8 [hidden, inter] + scales [hidden, inter/128]. x is overwritten with the last layer's
- * input. Scratch (H, quantised activations) comes from the library's per-device workspace. */
+ * input. Scratch (H, quantised activations, partial sums) comes from the library's per-device workspace.
+ * For kind 0 with T <= 16 (and hidden <= 3072, both multiples of 128 with at least 512 for hidden) the layer runs as
+ * three launches: whole-K gate/up tiles per CU, the down multiply in K-parts, and a pass that adds the parts in order
+ * and applies the RMSNorm; the float32 sums there are rounded in another order than gemm_w8g's (within tolerance). */
 SEPAL_HIP_API int32_t sepal_hip_mlp_stack(int32_t kind, size_t layers, size_t t, size_t hidden, size_t inter, void* x,
                             const int8_t* const* w_gate_up, const float* const* s_gate_up, const int8_t* const* w_down,
                             const float* const* s_down, float* y, size_t act_block, double eps, void* stream);
