@@ -207,17 +207,17 @@ __global__ void __launch_bounds__(128 * WN) __attribute__((amdgpu_waves_per_eu(2
     __syncthreads();
     float e[2] = {snext[0] > 0.0f ? snext[0] : 1.0f, snext[1] > 0.0f ? snext[1] : 1.0f};
 
-    // One step: stage step kt + 1's operands (loaded two steps ago; the stage was last read by step kt - 1) and issue
-    // step kt + 3's loads into the registers they leave (the next group's scales first when kt + 3 starts a group); at a
-    // group's first step the Horner rescale; the multiply of step kt; one barrier. The load registers rotate through
-    // four names, step s in R[s % 4], and the loop runs one group (four steps) per iteration, so the rotation is a
-    // renaming and the group boundary is known at compile time. The body has no branches, so the compiler's load
-    // counting stays exact: near the end the loads repeat the last step (clamped) and the extra stage written at the
-    // last step lands in a buffer nothing reads again. At step 0 the rescale multiplies zero accumulators.
+    // One step: issue step kt + 3's loads into the registers of step kt - 1 (the next group's scales first when
+    // kt + 3 starts a group); at a group's first step the Horner rescale; the multiply of step kt; then stage step
+    // kt + 1's operands (loaded two steps ago; the stage was last read by step kt - 1); one barrier. The load registers
+    // rotate through four names, step s in R[s % 4], and the loop runs one group (four steps) per iteration, so the
+    // rotation is a renaming and the group boundary is known at compile time. The body has no branches, so the
+    // compiler's load counting stays exact: near the end the loads repeat the last step (clamped) and the extra stage
+    // written at the last step lands in a buffer nothing reads again. At step 0 the rescale multiplies zero
+    // accumulators.
     const int groups = KT / SPG;
     const auto step = [&](int kt, const Regs& r_next, Regs& r_free, auto first_t) {
         constexpr bool first = decltype(first_t)::value;
-        stage(kt + 1, r_next);
         if ((kt + 3) % SPG == 0) issue_scales(min((kt + 3) / SPG, groups - 1));
         issue(min(kt + 3, KT - 1), r_free);
         if constexpr (first) {
@@ -246,6 +246,9 @@ __global__ void __launch_bounds__(128 * WN) __attribute__((amdgpu_waves_per_eu(2
 #pragma unroll
                 for (int j = 0; j < 2; ++j) acc[i][j] = mfma32<XT>(a[i], b[j], acc[i][j]);
         }
+        // step kt + 1's operands into their stage after this step's fragment reads, so that the writes overlap the
+        // MFMAs instead of delaying their operands
+        stage(kt + 1, r_next);
         __syncthreads();
     };
     static_assert(SPG == 4, "four steps per group");
