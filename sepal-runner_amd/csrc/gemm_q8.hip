@@ -9,8 +9,9 @@
 // Every step is one IEEE operation in the reference's order, so the large-M path equals cpu-q8 bit for bit.
 //
 // Large-M path: 128 x 256 tiles of 8 waves, each 64 x 64 outputs (2 x 2 blocks of MFMA 32x32x32 i8); K in steps of
-// one group (128 bytes) through a double-buffered LDS tile; the int32 sums of a group are turned into the float chain
-// in registers before the next group starts (a second set of accumulators holds the chain).
+// one group (128 bytes) through a double-buffered LDS tile, the loads of a group issued two groups ahead into three
+// rotating register sets; the int32 sums of a group are turned into the float chain in registers before the next
+// group starts (a second set of accumulators holds the chain).
 // Small-M path: stream.hip (MFMA 16x16x64 i8; a split of K keeps the sums exact but adds the splits' partial chains in
 // split order, within tolerance, not bit for bit).
 #include "common.hpp"
@@ -85,7 +86,7 @@ __device__ __forceinline__ int sw8(int r) { return r & 7; }
 template <int EP, int YT, bool PER_TOKEN, int MODE>
 __global__ void __launch_bounds__(512) gemm_big(const Params p) {
     constexpr int BM = 128, BN = 256, NT = 512;
-    constexpr int XCH = BM * 8 / NT;   // 2
+    constexpr int XCH = BM * 8 / NT;   // 2 chunks of 16 bytes per thread and group
     constexpr int WCH = BN * 8 / NT;   // 4
     __shared__ __align__(16) u32x4 lds_x[2][BM * 8];
     __shared__ __align__(16) u32x4 lds_w[2][BN * 8];
@@ -98,40 +99,23 @@ __global__ void __launch_bounds__(512) gemm_big(const Params p) {
     const int m0 = tm * BM, n0 = tn * BN;
     const int groups = p.k / 128;
 
-    u32x4 xr[XCH], wr[WCH];
-    float xsr = 0.0f;
-    const auto gload = [&](int g) {
-        const int k0 = g * 128;
+    // ---- per-thread sources (clamped: rows past T or N repeat the last row; their outputs are never stored) ----
+    const signed char* xsrc[XCH];
+    const signed char* wsrc[WCH];
+    int xdst[XCH], wdst[WCH];
 #pragma unroll
-        for (int e = 0; e < XCH; ++e) {
-            const int id = tid + e * NT, row = id / 8, c = id % 8;
-            const int m = m0 + row;
-            xr[e] = m < p.t ? *reinterpret_cast<const u32x4*>(p.x + static_cast<std::size_t>(m) * p.ld_x + k0 + 16 * c) : u32x4{0u, 0u, 0u, 0u};
-        }
+    for (int e = 0; e < XCH; ++e) {
+        const int id = tid + e * NT, row = id / 8, c = id % 8;
+        xsrc[e] = p.x + static_cast<std::size_t>(min(m0 + row, p.t - 1)) * p.ld_x + 16 * c;
+        xdst[e] = row * 8 + (c ^ sw8(row));
+    }
 #pragma unroll
-        for (int e = 0; e < WCH; ++e) {
-            const int id = tid + e * NT, row = id / 8, c = id % 8;
-            const int nn = n0 + row;
-            wr[e] = nn < p.n ? *reinterpret_cast<const u32x4*>(p.w + static_cast<std::size_t>(nn) * p.ld_w + k0 + 16 * c) : u32x4{0u, 0u, 0u, 0u};
-        }
-        if (!PER_TOKEN && MODE == MODE_CHAIN && tid < BM) {
-            const int m = m0 + tid;
-            xsr = m < p.t ? p.xs[static_cast<std::size_t>(m) * p.ld_xs + (g >> p.act_shift)] : 0.0f;
-        }
-    };
-    const auto lstore = [&](int buf) {
-#pragma unroll
-        for (int e = 0; e < XCH; ++e) {
-            const int id = tid + e * NT, row = id / 8, c = id % 8;
-            lds_x[buf][row * 8 + (c ^ sw8(row))] = xr[e];
-        }
-#pragma unroll
-        for (int e = 0; e < WCH; ++e) {
-            const int id = tid + e * NT, row = id / 8, c = id % 8;
-            lds_w[buf][row * 8 + (c ^ sw8(row))] = wr[e];
-        }
-        if (!PER_TOKEN && MODE == MODE_CHAIN && tid < BM) lds_xs[buf][tid] = xsr;
-    };
+    for (int e = 0; e < WCH; ++e) {
+        const int id = tid + e * NT, row = id / 8, c = id % 8;
+        wsrc[e] = p.w + static_cast<std::size_t>(min(n0 + row, p.n - 1)) * p.ld_w + 16 * c;
+        wdst[e] = row * 8 + (c ^ sw8(row));
+    }
+    const float* xs_row = p.xs + static_cast<std::size_t>(min(m0 + (tid % BM), p.t - 1)) * p.ld_xs;
 
     const int ib = wn / 2, hh = wn % 2;
     const int colrel[2] = {128 * ib + 32 * hh + lane % 32, 128 * ib + 64 + 32 * hh + lane % 32};
@@ -140,78 +124,124 @@ __global__ void __launch_bounds__(512) gemm_big(const Params p) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
         col[j] = n0 + colrel[j];
-        wsrow[j] = col[j] < p.n ? p.ws + static_cast<std::size_t>(col[j]) * p.ld_ws : nullptr;
+        wsrow[j] = p.ws + static_cast<std::size_t>(min(col[j], p.n - 1)) * p.ld_ws;
     }
 
+    // one group's operands and scales, in registers; the sets rotate (the loads of group g + 2, or g + 1, are issued
+    // while group g is multiplied)
+    struct Set {
+        u32x4 x[XCH], w[WCH];
+        float xs, ws[2];
+    };
+    const auto issue = [&](int g, Set& s) {
+        const std::size_t k0 = static_cast<std::size_t>(g) * 128;
+#pragma unroll
+        for (int e = 0; e < XCH; ++e) s.x[e] = *reinterpret_cast<const u32x4*>(xsrc[e] + k0);
+#pragma unroll
+        for (int e = 0; e < WCH; ++e) s.w[e] = *reinterpret_cast<const u32x4*>(wsrc[e] + k0);
+        if constexpr (!PER_TOKEN && MODE == MODE_CHAIN) s.xs = xs_row[g >> p.act_shift];
+        if constexpr (MODE == MODE_CHAIN) {
+            s.ws[0] = wsrow[0][g];
+            s.ws[1] = wsrow[1][g];
+        }
+    };
+    const auto stage = [&](int buf, const Set& s) {
+#pragma unroll
+        for (int e = 0; e < XCH; ++e) lds_x[buf][xdst[e]] = s.x[e];
+#pragma unroll
+        for (int e = 0; e < WCH; ++e) lds_w[buf][wdst[e]] = s.w[e];
+        if constexpr (!PER_TOKEN && MODE == MODE_CHAIN)
+            if (tid < BM) lds_xs[buf][tid] = s.xs;
+    };
+
     float acc[2][2][16];
-    i32x16 sacc[2][2];
-    const i32x16 zero16 = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+    const i32x16 zero16 = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
 
-    float wsn[2];
+    // One group: issue group g + ahead's loads (clamped; the set they go to was staged and its scales used at earlier
+    // steps); the exact int32 sums of group g; its link of the scale chain (or the sums out); stage group g + 1 into the
+    // other LDS buffer; one barrier. The loop body has no branches around loads, so the compiler's load counting stays
+    // exact; a step past the last group only repeats loads.
+    const auto step = [&](int g, const Set& cur, const Set& next, Set& free_, int ahead) {
+        issue(min(g + ahead, groups - 1), free_);
+        if (g < groups) {
+            const int buf = g & 1;
+            const u32x4* tx = lds_x[buf];
+            const u32x4* tw = lds_w[buf];
+            i32x16 sacc[2][2];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) wsn[j] = wsrow[j] != nullptr ? wsrow[j][0] : 0.0f;
-
-    gload(0);
-    lstore(0);
-    __syncthreads();
-    for (int g = 0; g < groups; ++g) {
-        const int buf = g & 1;
-        if (g + 1 < groups) gload(g + 1);
-        float wsc[2] = {wsn[0], wsn[1]};
-        if (g + 1 < groups)
+            for (int st = 0; st < 4; ++st) {
+                const int c = 2 * st + lane / 32;
+                u32x4 a[2], b[2];
 #pragma unroll
-            for (int j = 0; j < 2; ++j) wsn[j] = wsrow[j] != nullptr ? wsrow[j][g + 1] : 0.0f;
-        const u32x4* tx = lds_x[buf];
-        const u32x4* tw = lds_w[buf];
-#pragma unroll
-        for (int st = 0; st < 4; ++st) {
-            const int c = 2 * st + lane / 32;
-            u32x4 a[2], b[2];
-#pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const int row = wm * 64 + i * 32 + lane % 32;
-                a[i] = tx[row * 8 + (c ^ sw8(row))];
-            }
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const int row = colrel[j];
-                b[j] = tw[row * 8 + (c ^ sw8(row))];
-            }
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-#pragma unroll
-                for (int j = 0; j < 2; ++j) sacc[i][j] = mfma_i8_32(a[i], b[j], st == 0 ? zero16 : sacc[i][j]);
-        }
-        if constexpr (MODE == MODE_SUMS) {
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int row = m0 + wm * 64 + i * 32 + 8 * (r / 4) + 4 * (lane / 32) + (r % 4);
-                    if (row >= p.t) continue;
-#pragma unroll
-                    for (int j = 0; j < 2; ++j)
-                        if (col[j] < p.n) p.sums[(static_cast<std::size_t>(g) * p.t + row) * p.n + col[j]] = sacc[i][j][r];
+                for (int i = 0; i < 2; ++i) {
+                    const int row = wm * 64 + i * 32 + lane % 32;
+                    a[i] = tx[row * 8 + (c ^ sw8(row))];
                 }
-        } else {
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int rl = wm * 64 + i * 32 + 8 * (r / 4) + 4 * (lane / 32) + (r % 4);
-                    const float xsv = PER_TOKEN ? 1.0f : lds_xs[buf][rl];
-#pragma unroll
-                    for (int j = 0; j < 2; ++j) acc[i][j][r] = chain<PER_TOKEN>(acc[i][j][r], sacc[i][j][r], wsc[j], xsv, g == 0);
+                for (int j = 0; j < 2; ++j) {
+                    const int row = colrel[j];
+                    b[j] = tw[row * 8 + (c ^ sw8(row))];
                 }
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) sacc[i][j] = mfma_i8_32(a[i], b[j], st == 0 ? zero16 : sacc[i][j]);
+            }
+            if constexpr (MODE == MODE_SUMS) {
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int row = m0 + wm * 64 + i * 32 + 8 * (r / 4) + 4 * (lane / 32) + (r % 4);
+                        if (row >= p.t) continue;
+#pragma unroll
+                        for (int j = 0; j < 2; ++j)
+                            if (col[j] < p.n) p.sums[(static_cast<std::size_t>(g) * p.t + row) * p.n + col[j]] = sacc[i][j][r];
+                    }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int rl = wm * 64 + i * 32 + 8 * (r / 4) + 4 * (lane / 32) + (r % 4);
+                        const float xsv = PER_TOKEN ? 1.0f : lds_xs[buf][rl];
+#pragma unroll
+                        for (int j = 0; j < 2; ++j) acc[i][j][r] = chain<PER_TOKEN>(acc[i][j][r], sacc[i][j][r], cur.ws[j], xsv, g == 0);
+                    }
+            }
+            if (g + 1 < groups) stage(buf ^ 1, next);
         }
-        if (g + 1 < groups) lstore(buf ^ 1);
         __syncthreads();
+    };
+
+    if constexpr (PER_TOKEN) {
+        // three sets: group g + 2 loads while g multiplies
+        Set s0, s1, s2;
+        issue(0, s0);
+        issue(min(1, groups - 1), s1);
+        stage(0, s0);
+        __syncthreads();
+        for (int g = 0; g < groups; g += 3) {
+            step(g, s0, s1, s2, 2);      // group g in s0, g + 1 in s1; g + 2 -> s2
+            step(g + 1, s1, s2, s0, 2);  // g + 3 -> s0
+            step(g + 2, s2, s0, s1, 2);  // g + 4 -> s1
+        }
+    } else {
+        // per-128 activation scales need more registers in the chain: two sets, group g + 1 loads while g multiplies
+        Set s0, s1;
+        issue(0, s0);
+        stage(0, s0);
+        __syncthreads();
+        for (int g = 0; g < groups; g += 2) {
+            step(g, s0, s1, s1, 1);      // group g in s0; g + 1 -> s1 (staged at the end of this step)
+            step(g + 1, s1, s0, s0, 1);  // g + 2 -> s0
+        }
     }
     if constexpr (MODE == MODE_SUMS) return;
 
