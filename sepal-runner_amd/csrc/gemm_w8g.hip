@@ -12,9 +12,10 @@
 //
 // Two paths:
 //   large M: 256 x BN tiles (BN 128 or 256), 4 or 8 waves of 128 x 64 outputs (4 x 2 blocks of 32 x 32, MFMA
-//            32x32x16), K in steps of BK through a double-buffered LDS tile; the weights are widened once per tile
-//            when staged; 1-D grid with an XCD-aware tile order (a block's id modulo 8 is its XCD; consecutive logical
-//            tiles are kept on one XCD so they share its L2).
+//            32x32x16), K through a double-buffered LDS tile; the weights are widened once per tile when staged; 1-D
+//            grid with an XCD-aware tile order (a block's id modulo 8 is its XCD; consecutive logical tiles are kept
+//            on one XCD so they share its L2). 256 x 256 tiles (gemm_big3) step K by 64 with whole-cache-line loads;
+//            256 x 128 tiles (gemm_big2) step K by 32.
 //   small M: stream.hip (the weights streamed once, HBM-bound).
 #include "common.hpp"
 #include "gemm_kernels.hpp"
@@ -73,6 +74,7 @@ struct BigParams {
     std::size_t ld_y;
     int t, n, k;
     int tiles_m, tiles_n;
+    std::size_t x_bytes, w_bytes;  // extents of X and W (buffer range checks of gemm_big3)
 };
 
 // Logical tile of block `bid` (XCD-aware: the hardware places block b on XCD b % 8).
@@ -279,6 +281,193 @@ __global__ void __launch_bounds__(128 * WN) __attribute__((amdgpu_waves_per_eu(2
     }
 }
 
+
+// ---- large-M kernel, 64-wide k steps with whole-line loads ----------------------------------------------------------
+//
+// The tile, waves and Horner scaling of gemm_big2, with K in steps of 64 and the global loads shaped for the memory
+// pipeline: one X load instruction of a wave covers 8 rows x 128 bytes (whole cache lines) and one W load 16 rows x 64
+// bytes, where 32-wide steps touched 32 rows x 32 bytes per instruction. The writing lane scatters its chunk into the
+// fragment-ordered LDS tile. Within a fragment, lane L's 16 bytes sit at slot L ^ ((2 st + L / 32) & 7), st the 16-wide
+// k substep, and each load instruction's lanes take rows such that every 16 lanes of a write, like every 16 lanes of
+// a fragment read, cover 16 different 16-byte bank groups. Two stages of 64 KB; the loads of step kt + 2 are issued
+// while step kt is multiplied.
+template <int XT, int EP, int YT>
+__global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) gemm_big3(const BigParams p) {
+    constexpr int NW = 8, BN = 256, K3 = 64, SUB = K3 / 16, SPG = 128 / K3;
+    constexpr int XSTAGE = (BM / 32) * SUB * 1024, WSTAGE = (BN / 32) * SUB * 1024;
+    constexpr int XLD = BM * K3 * 2 / 16 / (64 * NW);  // X 16-byte chunks per thread per step (4)
+    constexpr int WLD = BN * K3 / 16 / (64 * NW);      // W 16-byte chunks per thread per step (2)
+    extern __shared__ __align__(16) unsigned char smem[];
+    lds_byte* lds = (lds_byte*)smem;
+    lds_byte* xs_base = lds;
+    lds_byte* ws_base = lds + 2 * XSTAGE;
+
+    const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
+    const int wm = wave % 2, wn = wave / 2;
+    int tm, tn;
+    tile_of(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int KT = p.k / K3;
+
+    // Loads go through buffer descriptors: 32-bit lane offsets, the step and the instruction in the scalar offset, and
+    // rows past T or N read as zero (past num_records); the launcher checks that every offset fits.
+    const __amdgpu_buffer_rsrc_t xres = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<unsigned short*>(p.x), 0, static_cast<int>(p.x_bytes), 0x00020000);
+    const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<signed char*>(p.w), 0, static_cast<int>(p.w_bytes), 0x00020000);
+    // X: instruction i of wave w fills m-block mb = 2 i + w / 4, rows rs(w % 4) = 16 (rs / 2) + 4 (rs % 2) + {0..3} +
+    // {0, 8}; a lane loads 8 values (part) of one row
+    int xoff, xdst;
+    {
+        const int rs = wave % 4, part = lane % 8;
+        const int r = 16 * (rs / 2) + 4 * (rs % 2) + lane / 16 + 8 * ((lane / 8) % 2);  // row within the m-block
+        xoff = (m0 + 32 * (wave / 4) + r) * static_cast<int>(p.ld_x) * 2 + 16 * part;
+        const int L = r + 32 * (part % 2);
+        xdst = ((wave / 4) * SUB + part / 2) * 1024 + 16 * (L ^ part);  // + 2 i SUB KB for instruction i
+    }
+    // W: instruction i of wave w covers rows 32 w + 16 i + {0, 1, 8, 9} + 2 (lane / 16) (n-block w); a lane loads one
+    // substep's 16 bytes and writes them widened as the fragment's two halves (slots L and L + 32)
+    int woff, wdst0, wdst1;
+    {
+        const int q = lane % 4, u = (lane / 4) % 4;
+        const int L = (u & 1) + 8 * (u >> 1) + 2 * (lane / 16);  // row within the n-block for i = 0 (+16 i)
+        woff = (n0 + 32 * wave + L) * static_cast<int>(p.ld_w) + 16 * q;
+        const int frag = (wave * SUB + q) * 1024;
+        wdst0 = frag + 16 * (L ^ (2 * q));             // + 256 i
+        wdst1 = frag + 16 * ((L + 32) ^ (2 * q + 1));  // + 256 i
+    }
+    int rd[SUB];  // this lane's slot in a fragment of substep st
+#pragma unroll
+    for (int st = 0; st < SUB; ++st) rd[st] = 16 * (lane ^ ((2 * st + lane / 32) & 7));
+
+    const int ib = wn / 2, hh = wn % 2;
+    const int nbj[2] = {4 * ib + hh, 4 * ib + 2 + hh};
+    int col[2];
+    const float* ssrc[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        col[j] = n0 + 32 * nbj[j] + lane % 32;
+        ssrc[j] = p.s + static_cast<std::size_t>(min(col[j], p.n - 1)) * p.ld_s;
+    }
+
+    struct Regs {
+        u32x4 x[XLD];
+        u32x4 w[WLD];
+    };
+    float snext[2];
+    const int xstride = 64 * static_cast<int>(p.ld_x) * 2, wstride = 16 * static_cast<int>(p.ld_w);
+    const auto issue = [&](int kt, Regs& r) {
+#pragma unroll
+        for (int i = 0; i < XLD; ++i)
+            r.x[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xres, xoff, kt * K3 * 2 + i * xstride, 0));
+#pragma unroll
+        for (int i = 0; i < WLD; ++i)
+            r.w[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wres, woff, kt * K3 + i * wstride, 0));
+    };
+    const auto issue_scales = [&](int g) {
+        snext[0] = ssrc[0][g];
+        snext[1] = ssrc[1][g];
+    };
+    const auto stage = [&](int kt, const Regs& r) {
+        lds_byte* xd = xs_base + (kt % 2) * XSTAGE;
+#pragma unroll
+        for (int i = 0; i < XLD; ++i)
+            *reinterpret_cast<__attribute__((address_space(3))) u32x4*>(xd + xdst + i * 2 * SUB * 1024) = r.x[i];
+        lds_byte* wd = ws_base + (kt % 2) * WSTAGE;
+#pragma unroll
+        for (int i = 0; i < WLD; ++i) {
+            unsigned o[8];
+            widen16<XT>(r.w[i], o);
+            *reinterpret_cast<__attribute__((address_space(3))) u32x4*>(wd + wdst0 + 256 * i) = u32x4{o[0], o[1], o[2], o[3]};
+            *reinterpret_cast<__attribute__((address_space(3))) u32x4*>(wd + wdst1 + 256 * i) = u32x4{o[4], o[5], o[6], o[7]};
+        }
+    };
+
+    f32x16 acc[4][2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    const int groups = KT / SPG;
+    Regs r0, r1;
+    issue_scales(0);
+    issue(0, r0);
+    issue(min(1, KT - 1), r1);
+    stage(0, r0);
+    __syncthreads();
+    float e[2] = {snext[0] > 0.0f ? snext[0] : 1.0f, snext[1] > 0.0f ? snext[1] : 1.0f};
+
+    // One step: at a group's first step the Horner rescale with the group's scales (loaded one group ahead), then the
+    // next group's scales are issued; the loads of step kt + 2 into the registers freed by step kt; the multiply of
+    // step kt; step kt + 1's operands into their stage; one barrier. Two register sets alternate, so the loop runs one
+    // group (two steps) per iteration. Loads past the end repeat the last step (clamped) and land in a stage nothing
+    // reads again.
+    const auto step = [&](int kt, const Regs& r_next, Regs& r_free, auto first_t) {
+        constexpr bool first = decltype(first_t)::value;
+        if constexpr (first) {
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const float en = snext[j] > 0.0f ? snext[j] : e[j];
+                const float ratio = __fmul_rn(e[j], __builtin_amdgcn_rcpf(en));
+                e[j] = en;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[i][j] = acc[i][j] * ratio;
+            }
+            issue_scales(min(kt / SPG + 1, groups - 1));
+        }
+        issue(min(kt + 2, KT - 1), r_free);
+        // keep the loads at the top of the step, in this order: the wait for a step's operands then leaves the later
+        // steps' loads in flight
+        __builtin_amdgcn_sched_barrier(0);
+        const lds_byte* xs = xs_base + (kt % 2) * XSTAGE;
+        const lds_byte* ws = ws_base + (kt % 2) * WSTAGE;
+#pragma unroll
+        for (int st = 0; st < SUB; ++st) {
+            u32x4 a[4], b[2];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                a[i] = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(xs + ((wm * 4 + i) * SUB + st) * 1024 + rd[st]);
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                b[j] = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(ws + (nbj[j] * SUB + st) * 1024 + rd[st]);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) acc[i][j] = mfma32<XT>(a[i], b[j], acc[i][j]);
+        }
+        stage(kt + 1, r_next);
+        __syncthreads();
+    };
+    static_assert(SPG == 2, "two steps per group");
+    for (int kt = 0; kt < KT; kt += 2) {
+        step(kt, r1, r0, std::true_type{});        // R1 holds step kt+1, step kt+2 -> R0
+        step(kt + 1, r0, r1, std::false_type{});   // R0 holds kt+2, kt+3 -> R1
+    }
+
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int row = m0 + wm * 128 + i * 32 + 8 * (r / 4) + 4 * (lane / 32) + (r % 4);
+            if (row >= p.t) continue;
+            const float v0 = __fmul_rn(acc[i][0][r], e[0]), v1 = __fmul_rn(acc[i][1][r], e[1]);
+            if constexpr (EP == SEPAL_HIP_SWIGLU) {
+                const int f = n0 / 2 + 64 * ib + 32 * hh + lane % 32;
+                if (2 * f < p.n) store_out<YT>(p.y, static_cast<std::size_t>(row) * p.ld_y + f, swiglu_fast(v0, v1));
+            } else {
+                float* y = static_cast<float*>(p.y);
+                if (col[0] < p.n) put_plain<EP>(y, static_cast<std::size_t>(row) * p.ld_y + col[0], v0);
+                if (col[1] < p.n) put_plain<EP>(y, static_cast<std::size_t>(row) * p.ld_y + col[1], v1);
+            }
+        }
+    }
+}
+
+constexpr std::size_t lds_bytes3() { return 2 * static_cast<std::size_t>((BM / 32) * 4 + (256 / 32) * 4) * 1024; }
+
 template <int WN>
 constexpr std::size_t lds_bytes() {
     return static_cast<std::size_t>(STAGES) * ((BM / 32) * (BK / 16) + (64 * WN / 32) * (BK / 16)) * 1024;
@@ -304,15 +493,36 @@ void launch_big2(const BigParams& p, hipStream_t stream) {
 }
 
 template <int XT, int EP, int YT>
+void launch_big3(const BigParams& p, hipStream_t stream) {
+    const auto kernel = v2::gemm_big3<XT, EP, YT>;
+    constexpr std::size_t lds = v2::lds_bytes3();
+    static_assert(lds <= (160u << 10), "LDS of one CU");
+    static bool raised = false;
+    if (!raised) {
+        if (hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                static_cast<int>(lds)) != hipSuccess)
+            throw LaunchError("gemm_w8g large-M: hipFuncSetAttribute(MaxDynamicSharedMemorySize) failed");
+        raised = true;
+    }
+    kernel<<<dim3(p.tiles_m * p.tiles_n), dim3(512), lds, stream>>>(p);
+}
+
+template <int XT, int EP, int YT>
 void launch_big(const GemmArgs& a, hipStream_t stream) {
     BigParams p{static_cast<const unsigned short*>(a.x), a.ld_x, reinterpret_cast<const signed char*>(a.w), a.ld_w, a.s, a.ld_s,
-                a.y, a.ld_y, static_cast<int>(a.t), static_cast<int>(a.n), static_cast<int>(a.k), 0, 0};
+                a.y, a.ld_y, static_cast<int>(a.t), static_cast<int>(a.n), static_cast<int>(a.k), 0, 0,
+                ((a.t - 1) * a.ld_x + a.k) * 2, (a.n - 1) * a.ld_w + a.k};
     // 256 x 256 tiles when there are enough of them to fill the chip twice, else 256 x 128
     const int tiles_m = static_cast<int>((a.t + 255) / 256);
     const int tn256 = static_cast<int>((a.n + 255) / 256);
     const bool wide = static_cast<long>(tiles_m) * tn256 >= 2 * 256 && (EP != SEPAL_HIP_SWIGLU || a.n % 256 == 0);
     p.tiles_m = tiles_m;
-    if (wide) {
+    // gemm_big3 addresses X and W with 32-bit offsets, rows up to one tile past the end included
+    const bool offsets32 = (a.t + 256) * a.ld_x * 2 < (std::size_t{1} << 31) && (a.n + 256) * a.ld_w < (std::size_t{1} << 31);
+    if (wide && offsets32) {
+        p.tiles_n = tn256;
+        launch_big3<XT, EP, YT>(p, stream);
+    } else if (wide) {
         p.tiles_n = tn256;
         launch_big2<XT, EP, YT, 4>(p, stream);
     } else {

@@ -228,6 +228,41 @@ def test_w8g_large_path_rows_are_batch_invariant(sm):
         assert same_bits(part, full[r0:r0 + rows])
 
 
+def _deq_ref(xt, qt, st, k):
+    """float64 X * dequant(W)^T on the GPU: a check of the large tiles at sizes the scalar oracle is slow on."""
+    n = qt.shape[0]
+    deq = (qt.double().view(n, k // 128, 128) * st.double()[:, :, None]).view(n, k)
+    return xt.double() @ deq.T
+
+
+@pytest.mark.parametrize("epilogue", ["store", "add", "swiglu"])
+def test_w8g_wide_tiles_every_element(sm, epilogue):
+    # at least 512 tiles of 256 x 256 select the two-group (ping-pong) kernel; 4000 rows leave a ragged last row tile
+    # and, for store/add, 8000 columns a ragged last column tile
+    t, n, k = (4000, 8192, 384) if epilogue == "swiglu" else (4000, 8000, 384)
+    rng = np.random.default_rng(4242 + len(epilogue))
+    x, q, s = _w8g_problem(rng, t, n, k, torch.bfloat16)
+    xt, qt, st = dev(x, torch.bfloat16), dev(q), dev(s)
+    ref = _deq_ref(xt, qt, st, k)
+    say("w8g wide tiles", epilogue, t, n, k)
+    if epilogue == "swiglu":
+        f = torch.arange(n // 2, device=ref.device)
+        g = ref[:, 128 * (f // 64) + f % 64]
+        u = ref[:, 128 * (f // 64) + 64 + f % 64]
+        href = host(g * torch.sigmoid(g) * u)
+        y = host(sm.gemm_w8g(xt, qt, st, epilogue=sm.SWIGLU, y_dtype=torch.float16).float())
+        assert max_rel_over_rms(y, href) < 2e-3, max_rel_over_rms(y, href)
+    elif epilogue == "store":
+        y = host(sm.gemm_w8g(xt, qt, st))
+        assert max_rel_over_rms(y, host(ref)) < 2e-3 and rel_rms(y, host(ref)) < 1e-5
+    else:
+        base = torch.from_numpy(rng.standard_normal((t, n)).astype(np.float32)).cuda()
+        ya = base.clone()
+        sm.gemm_w8g(xt, qt, st, y=ya, epilogue=sm.ADD)
+        refa = host(base.double() + ref)
+        assert max_rel_over_rms(host(ya), refa) < 2e-3 and rel_rms(host(ya), refa) < 1e-5
+
+
 # ---- q8 ----------------------------------------------------------------------------------------------------------------
 
 Q8_CASES = [(37, 256, 256), (130, 128, 512), (300, 512, 1280), (16, 256, 2560), (64, 384, 640)]
