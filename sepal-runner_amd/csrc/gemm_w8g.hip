@@ -492,6 +492,19 @@ void launch_big2(const BigParams& p, hipStream_t stream) {
     kernel<<<dim3(p.tiles_m * p.tiles_n), dim3(128 * WN), lds, stream>>>(p);
 }
 
+// Compute units of the current device (cached per device).
+inline int device_cus() {
+    static int cached[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0) throw LaunchError("gemm_w8g: hipGetDevice failed");
+    if (dev < 64 && cached[dev] > 0) return cached[dev];
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+        throw LaunchError("gemm_w8g: device query failed");
+    if (dev < 64) cached[dev] = cus;
+    return cus;
+}
+
 template <int XT, int EP, int YT>
 void launch_big3(const BigParams& p, hipStream_t stream) {
     const auto kernel = v2::gemm_big3<XT, EP, YT>;
@@ -520,8 +533,29 @@ void launch_big(const GemmArgs& a, hipStream_t stream) {
     // gemm_big3 addresses X and W with 32-bit offsets, rows up to one tile past the end included
     const bool offsets32 = (a.t + 256) * a.ld_x * 2 < (std::size_t{1} << 31) && (a.n + 256) * a.ld_w < (std::size_t{1} << 31);
     if (wide && offsets32) {
+        // The last, partial round of 256 x 256 tiles is the idle tail of the launch. When the row tiles past the full
+        // rounds fit one round as 256 x 128 tiles, those rows go to a second launch of half-width tiles. Both kernels
+        // run the same k order and Horner chain per output, so a row's bits do not depend on which one computed it.
+        const int cus = device_cus();
+        const long total = static_cast<long>(tiles_m) * tn256;
+        const long full = total / cus * cus;
+        const int m1 = static_cast<int>(full / tn256);
+        const bool split = total % cus > cus / 4 && m1 > 0 && static_cast<long>(tiles_m - m1) * 2 * tn256 <= cus;
         p.tiles_n = tn256;
-        launch_big3<XT, EP, YT>(p, stream);
+        if (!split) {
+            launch_big3<XT, EP, YT>(p, stream);
+        } else {
+            p.tiles_m = m1;
+            launch_big3<XT, EP, YT>(p, stream);
+            BigParams q = p;
+            const std::size_t r0 = static_cast<std::size_t>(m1) * 256;
+            q.x = p.x + r0 * a.ld_x;
+            q.y = static_cast<char*>(a.y) + r0 * a.ld_y * elem_bytes(YT);
+            q.t = static_cast<int>(a.t - r0);
+            q.tiles_m = tiles_m - m1;
+            q.tiles_n = static_cast<int>((a.n + 127) / 128);
+            launch_big2<XT, EP, YT, 2>(q, stream);
+        }
     } else if (wide) {
         p.tiles_n = tn256;
         launch_big2<XT, EP, YT, 4>(p, stream);

@@ -263,6 +263,24 @@ def test_w8g_wide_tiles_every_element(sm, epilogue):
         assert max_rel_over_rms(host(ya), refa) < 2e-3 and rel_rms(host(ya), refa) < 1e-5
 
 
+def test_w8g_wide_tail_split_and_batch_invariance(sm):
+    # 62 x 10 tiles of 256 x 256 on 256 CUs leave a 108-tile last round: rows past the 51st row tile run as 256 x 128
+    # tiles in a second launch. Every element is checked, and rows from both launches match, bit for bit, the same rows
+    # computed in a small batch (the 256 x 128 kernel), as runner/cuda/tests/test_gemm_simt_kernels.cpp:193-211 asks.
+    t, n, k = 15800, 2560, 384
+    rng = np.random.default_rng(777)
+    x, q, s = _w8g_problem(rng, t, n, k, torch.bfloat16)
+    xt, qt, st = dev(x, torch.bfloat16), dev(q), dev(s)
+    say("w8g wide tail split", t, n, k)
+    y = sm.gemm_w8g(xt, qt, st)
+    ref = _deq_ref(xt, qt, st, k)
+    yh = host(y)
+    assert max_rel_over_rms(yh, host(ref)) < 2e-3 and rel_rms(yh, host(ref)) < 1e-5
+    for r0, rows in [(0, 100), (13000, 120), (13056, 77), (15700, 100)]:
+        part = host(sm.gemm_w8g(xt[r0:r0 + rows], qt, st, config=0))
+        assert same_bits(part, yh[r0:r0 + rows]), r0
+
+
 # ---- q8 ----------------------------------------------------------------------------------------------------------------
 
 Q8_CASES = [(37, 256, 256), (130, 128, 512), (300, 512, 1280), (16, 256, 2560), (64, 384, 640)]
