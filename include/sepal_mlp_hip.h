@@ -109,6 +109,19 @@ SEPAL_HIP_API int32_t sepal_hip_gemm_q8(const int8_t* xq, size_t ld_x, const flo
                           const int8_t* w, size_t ld_w, const float* ws, size_t ld_ws, void* y, int32_t y_type,
                           size_t ld_y, size_t t, size_t n, size_t k, int32_t epilogue, int32_t config, void* stream);
 
+/* gate/up of the q8 MLP with the down multiply's input made in the same pass: H = SwiGLU of sepal_hip_gemm_q8 (gate
+ * and up rows in the 64-row interleave), quantized per row and 128 columns by the activation quantizer's rule. hq int8
+ * [T, ld_hq] (N/2 columns), hs float32 [T, ld_hs] (N/256 used); equal, bit for bit, to sepal_hip_gemm_q8 (SWIGLU,
+ * float32 H) followed by sepal_hip_quantize_rows_s8 (block 128) on the same path. N a multiple of 256; other rules and
+ * `config` as sepal_hip_gemm_q8. The large-M kernel quantizes in its epilogue (one tile holds one 128-column block);
+ * the small-M path computes H into the workspace first. No single reference function: it fuses finish_tile's SwiGLU
+ * (runner/src/cpu/gemm.cpp:417-447) with pack_acts (gemm.cpp:285-306), the SwiGLU -> int8 fusion the reference lists
+ * as not done (runner/cuda/README.md:1513-1515). */
+SEPAL_HIP_API int32_t sepal_hip_gemm_q8_swiglu_quantize(const int8_t* xq, size_t ld_x, const float* xs, size_t ld_xs,
+                                          size_t act_block, const int8_t* w, size_t ld_w, const float* ws, size_t ld_ws,
+                                          int8_t* hq, size_t ld_hq, float* hs, size_t ld_hs, size_t t, size_t n,
+                                          size_t k, int32_t config, void* stream);
+
 /* The exact int32 per-group sums of the q8 multiply, sums[g][t][n] = sum over k in group g of xq[t,k] * w[n,k]
  * (int8 MFMA, the same kernel body as sepal_hip_gemm_q8's large-M path). For checking the integer part bit for bit. */
 SEPAL_HIP_API int32_t sepal_hip_q8_group_sums(const int8_t* xq, size_t ld_x, const int8_t* w, size_t ld_w, int32_t* sums, size_t t,
@@ -120,6 +133,17 @@ SEPAL_HIP_API int32_t sepal_hip_q8_group_sums(const int8_t* xq, size_t ld_x, con
  * cuda_engine.cpp:1915-1918). */
 SEPAL_HIP_API int32_t sepal_hip_rmsnorm_rows(const float* x, size_t ld_x, void* y, int32_t y_type, size_t ld_y, const float* w1,
                                size_t rows, size_t cols, double eps, void* stream);
+
+/* The q8 layer input in one pass: RMSNorm as sepal_hip_rmsnorm_rows, each value rounded to bfloat16, then the
+ * activation quantizer of sepal_hip_quantize_rows_s8 on the rounded values (block 128, or cols for one scale per row).
+ * q int8 [rows, ld_q] and scales [rows, ld_s] equal, bit for bit, rmsnorm_rows to bf16 followed by quantize_rows_s8;
+ * y_bf16 (may be NULL) receives the bf16 values. cols a multiple of 128; x, q 16-byte aligned; ld_x, ld_q multiples
+ * of 16. No single reference function: it fuses the MLP input norm (runner/src/cpu/elementwise.cpp:43-59, bf16 store
+ * as in cuda_engine.cpp:1915-1918) with launch_quantize_rows_s8 / pack_acts (runner/cuda/src/gemm_s8_kernels.hpp:20-27,
+ * runner/src/cpu/gemm.cpp:285-306), the fused producer the reference lists as not done (runner/cuda/README.md:1513-1515). */
+SEPAL_HIP_API int32_t sepal_hip_rmsnorm_quantize_rows(const float* x, size_t ld_x, const float* w1, uint16_t* y_bf16,
+                                        size_t ld_y, int8_t* q, size_t ld_q, float* scales, size_t ld_s, size_t rows,
+                                        size_t cols, size_t block, double eps, void* stream);
 
 /* float32 -> bfloat16, nearest even, NaN stays NaN (launch_float_to_bf16, runner/cuda/src/gemm_simt_kernels.hpp:69-70). */
 SEPAL_HIP_API int32_t sepal_hip_float_to_bf16(const float* src, uint16_t* dst, size_t count, void* stream);

@@ -230,6 +230,58 @@ int32_t sepal_hip_gemm_q8(const int8_t* xq, size_t ld_x, const float* xs, size_t
     });
 }
 
+int32_t sepal_hip_gemm_q8_swiglu_quantize(const int8_t* xq, size_t ld_x, const float* xs, size_t ld_xs, size_t act_block,
+                                          const int8_t* w, size_t ld_w, const float* ws, size_t ld_ws, int8_t* hq,
+                                          size_t ld_hq, float* hs, size_t ld_hs, size_t t, size_t n, size_t k,
+                                          int32_t config, void* stream) {
+    return guarded([&] {
+        require(config >= -1 && config <= 2, "gemm_q8_swiglu_quantize: config must be -1, 0, 1 or 2");
+        check_gemm_common("gemm_q8_swiglu_quantize", xq, ld_x, w, ld_w, ws, ld_ws, hq, ld_hq, n, k, SEPAL_HIP_SWIGLU);
+        require(n % 256 == 0, "gemm_q8_swiglu_quantize: N must be a multiple of 256 (128-column output blocks)");
+        require(act_block == 128 || act_block == k, "gemm_q8_swiglu_quantize: act_block must be 128 or K");
+        require(xs != nullptr && ld_xs >= k / act_block, "gemm_q8_swiglu_quantize: activation scales missing or stride too small");
+        require(hs != nullptr && ld_hs >= n / 256, "gemm_q8_swiglu_quantize: output scales missing or stride too small");
+        require(ld_hq % 16 == 0, "gemm_q8_swiglu_quantize: ld_hq must be a multiple of 16");
+        if (t == 0) return;
+        require(t < 0x7FFFFFFFu, "gemm_q8_swiglu_quantize: dimension beyond 2^31");
+        if (config >= 1) require(t <= kSmallM, "gemm_q8_swiglu_quantize: the small-M path takes at most 64 rows");
+        const hipStream_t st = as_stream(stream);
+        GemmArgs a;
+        a.x = xq;
+        a.ld_x = ld_x;
+        a.xs = xs;
+        a.ld_xs = ld_xs;
+        a.act_block = act_block;
+        a.w = w;
+        a.ld_w = ld_w;
+        a.s = ws;
+        a.ld_s = ld_ws;
+        a.t = t;
+        a.n = n;
+        a.k = k;
+        const bool large = config == 0 || (config < 0 && t > kSmallM);
+        if (large) {
+            a.y = hq;
+            a.ld_y = ld_hq;
+            a.ys = hs;
+            a.ld_ys = ld_hs;
+            launch_gemm_q8_swiglu_q8(a, st);
+            return;
+        }
+        // small M: the float32 H through the workspace, then the activation quantizer (the same values and rule)
+        const std::size_t cols = n / 2;
+        float* h = reinterpret_cast<float*>(static_cast<char*>(workspace(kScratchOffset + t * cols * 4, st)) + kScratchOffset);
+        a.y = h;
+        a.y_type = SEPAL_HIP_F32;
+        a.ld_y = cols;
+        a.epilogue = SEPAL_HIP_SWIGLU;
+        a.config = config == 2 ? 1 : config;
+        a.force_splits = config == 2 ? 1 : 0;
+        launch_gemm_q8(a, st);
+        launch_quantize_rows(h, SEPAL_HIP_F32, cols, hq, ld_hq, hs, ld_hs, t, cols, 128, st);
+    });
+}
+
 int32_t sepal_hip_q8_group_sums(const int8_t* xq, size_t ld_x, const int8_t* w, size_t ld_w, int32_t* sums, size_t t,
                                 size_t n, size_t k, void* stream) {
     return guarded([&] {
@@ -266,6 +318,23 @@ int32_t sepal_hip_rmsnorm_rows(const float* x, size_t ld_x, void* y, int32_t y_t
     });
 }
 
+int32_t sepal_hip_rmsnorm_quantize_rows(const float* x, size_t ld_x, const float* w1, uint16_t* y_bf16, size_t ld_y,
+                                        int8_t* q, size_t ld_q, float* scales, size_t ld_s, size_t rows, size_t cols,
+                                        size_t block, double eps, void* stream) {
+    return guarded([&] {
+        require(block == 128 || block == cols, "rmsnorm_quantize_rows: block must be 128 or cols");
+        if (rows == 0 || cols == 0) return;
+        require(x != nullptr && q != nullptr && scales != nullptr, "rmsnorm_quantize_rows: null pointer");
+        require(cols % 128 == 0, "rmsnorm_quantize_rows: cols must be a multiple of 128");
+        require(ld_x >= cols && ld_q >= cols && ld_s >= cols / block && (y_bf16 == nullptr || ld_y >= cols),
+                "rmsnorm_quantize_rows: strides below the row");
+        require(ld_x % 16 == 0 && ld_q % 16 == 0 && aligned16(x) && aligned16(q),
+                "rmsnorm_quantize_rows: x and q must be 16-byte aligned with strides that are multiples of 16");
+        require(eps > 0.0, "rmsnorm_quantize_rows: eps must be positive");
+        launch_rmsnorm_quantize(x, ld_x, y_bf16, ld_y, w1, q, ld_q, scales, ld_s, rows, cols, block, eps, as_stream(stream));
+    });
+}
+
 int32_t sepal_hip_float_to_bf16(const float* src, uint16_t* dst, size_t count, void* stream) {
     return guarded([&] {
         if (count == 0) return;
@@ -285,28 +354,34 @@ int32_t sepal_hip_mlp_stack(int32_t kind, size_t layers, size_t t, size_t hidden
         require(kind == 0 || act_block == 128 || act_block == 0, "mlp_stack: act_block must be 128 or 0 (one scale per token)");
         if (layers == 0 || t == 0) return;
         const hipStream_t st = as_stream(stream);
-        // workspace: H [t, inter] (binary16 for w8g, float32 for q8); q8 also xq [t, max(h, i)] int8 and scales
-        const std::size_t h_bytes = t * inter * (kind == 0 ? 2 : 4);
-        const std::size_t kmax = hidden > inter ? hidden : inter;
-        const std::size_t q_bytes = kind == 1 ? t * kmax : 0;
-        const std::size_t s_bytes = kind == 1 ? t * (kmax / 128) * 4 : 0;
+        // workspace: H [t, inter] (binary16 for w8g; float32 for q8 unless the gate/up epilogue quantizes it); q8 also
+        // the int8 layer input and int8 H with their scales
+        const std::size_t ab_h = act_block == 0 ? hidden : 128, ab_i = act_block == 0 ? inter : 128;
+        const bool fused_h = kind == 1 && ab_i == 128 && t > kSmallM;
+        const auto up256 = [](std::size_t b) { return (b + 255) / 256 * 256; };
+        const std::size_t h_bytes = kind == 0 ? t * inter * 2 : (fused_h ? 0 : t * inter * 4);
         const std::size_t off_h = kScratchOffset;
-        const std::size_t off_q = off_h + (h_bytes + 255) / 256 * 256;
-        const std::size_t off_s = off_q + (q_bytes + 255) / 256 * 256;
         SmallStackPlan plan{};
         if (kind == 0 && small_stack_plan(t, hidden, inter, plan)) {
             // M <= 16: three launches per layer (stack_small.hip); H binary16, the down pass's partial sums float32
-            const std::size_t off_p = off_h + (h_bytes + 255) / 256 * 256;
+            const std::size_t off_p = off_h + up256(h_bytes);
             char* wsp = static_cast<char*>(workspace(off_p + static_cast<std::size_t>(plan.parts) * t * hidden * 4, st));
             for (std::size_t l = 0; l < layers; ++l)
                 launch_small_layer(plan, t, hidden, inter, x, w_gate_up[l], s_gate_up[l], w_down[l], s_down[l], wsp + off_h,
                                    reinterpret_cast<float*>(wsp + off_p), y, l + 1 < layers ? x : nullptr, eps, st);
             return;
         }
-        char* ws = static_cast<char*>(workspace(off_s + s_bytes, st));
+        const std::size_t off_qx = off_h + up256(h_bytes);
+        const std::size_t off_sx = off_qx + (kind == 1 ? up256(t * hidden) : 0);
+        const std::size_t off_qh = off_sx + (kind == 1 ? up256(t * (hidden / ab_h) * 4) : 0);
+        const std::size_t off_sh = off_qh + (kind == 1 ? up256(t * inter) : 0);
+        const std::size_t end = off_sh + (kind == 1 ? up256(t * (inter / ab_i) * 4) : 0);
+        char* ws = static_cast<char*>(workspace(end, st));
         void* h = ws + off_h;
-        std::int8_t* xq = reinterpret_cast<std::int8_t*>(ws + off_q);
-        float* xsc = reinterpret_cast<float*>(ws + off_s);
+        std::int8_t* qx = reinterpret_cast<std::int8_t*>(ws + off_qx);
+        float* sx = reinterpret_cast<float*>(ws + off_sx);
+        std::int8_t* qh = reinterpret_cast<std::int8_t*>(ws + off_qh);
+        float* sh = reinterpret_cast<float*>(ws + off_sh);
         for (std::size_t l = 0; l < layers; ++l) {
             GemmArgs gu;
             gu.t = t;
@@ -341,26 +416,40 @@ int32_t sepal_hip_mlp_stack(int32_t kind, size_t layers, size_t t, size_t hidden
                 dn.ld_x = inter;
                 dn.y_type = SEPAL_HIP_F32;
                 launch_gemm_w8g(dn, st);
-            } else {
-                const std::size_t ab_h = act_block == 0 ? hidden : 128, ab_i = act_block == 0 ? inter : 128;
-                launch_quantize_rows(x, SEPAL_HIP_BF16, hidden, xq, hidden, xsc, hidden / ab_h, t, hidden, ab_h, st);
-                gu.x = xq;
-                gu.ld_x = hidden;
-                gu.xs = xsc;
-                gu.ld_xs = hidden / ab_h;
-                gu.act_block = ab_h;
-                gu.y_type = SEPAL_HIP_F32;
-                launch_gemm_q8(gu, st);
-                launch_quantize_rows(h, SEPAL_HIP_F32, inter, xq, inter, xsc, inter / ab_i, t, inter, ab_i, st);
-                dn.x = xq;
-                dn.ld_x = inter;
-                dn.xs = xsc;
-                dn.ld_xs = inter / ab_i;
-                dn.act_block = ab_i;
-                dn.y_type = SEPAL_HIP_F32;
-                launch_gemm_q8(dn, st);
+                if (l + 1 < layers) launch_rmsnorm(y, hidden, x, SEPAL_HIP_BF16, hidden, nullptr, t, hidden, eps, st);
+                continue;
             }
-            if (l + 1 < layers) launch_rmsnorm(y, hidden, x, SEPAL_HIP_BF16, hidden, nullptr, t, hidden, eps, st);
+            // q8: the first layer's input is quantized here; later ones come quantized out of the fused RMSNorm
+            if (l == 0) launch_quantize_rows(x, SEPAL_HIP_BF16, hidden, qx, hidden, sx, hidden / ab_h, t, hidden, ab_h, st);
+            gu.x = qx;
+            gu.ld_x = hidden;
+            gu.xs = sx;
+            gu.ld_xs = hidden / ab_h;
+            gu.act_block = ab_h;
+            gu.y_type = SEPAL_HIP_F32;
+            if (fused_h) {
+                // SwiGLU and the int8 re-quantization of H in the gate/up epilogue
+                gu.y = qh;
+                gu.ld_y = inter;
+                gu.ys = sh;
+                gu.ld_ys = inter / 128;
+                launch_gemm_q8_swiglu_q8(gu, st);
+            } else {
+                launch_gemm_q8(gu, st);
+                launch_quantize_rows(h, SEPAL_HIP_F32, inter, qh, inter, sh, inter / ab_i, t, inter, ab_i, st);
+            }
+            dn.x = qh;
+            dn.ld_x = inter;
+            dn.xs = sh;
+            dn.ld_xs = inter / ab_i;
+            dn.act_block = ab_i;
+            dn.y_type = SEPAL_HIP_F32;
+            launch_gemm_q8(dn, st);
+            // the next layer's input: RMSNorm, bf16 and the int8 quantization in one pass (x keeps the bf16 input of
+            // the last layer)
+            if (l + 1 < layers)
+                launch_rmsnorm_quantize(y, hidden, l + 2 == layers ? static_cast<std::uint16_t*>(x) : nullptr, hidden, nullptr,
+                                        qx, hidden, sx, hidden / ab_h, t, hidden, ab_h, eps, st);
         }
     });
 }

@@ -28,13 +28,20 @@ struct GemmArgs {
     std::size_t ld_xs = 0;
     std::size_t act_block = 128;
     std::int32_t* sums = nullptr;  // group-sum mode
+    float* ys = nullptr;           // kSwigluQ8: output scales [t, ld_ys], one per 128 columns of y
+    std::size_t ld_ys = 0;
 };
+
+// q8 epilogue (internal, not in the public enum): SwiGLU, then the output quantized to int8 per row and 128 columns
+// (rule RECIPROCAL); y is int8 [t, ld_y], the scales go to ys.
+constexpr int kSwigluQ8 = 16;
 
 void launch_gemm_w8g(const GemmArgs& a, hipStream_t stream);
 void launch_stream_w8g(const GemmArgs& a, hipStream_t stream);
 void launch_stream_q8(const GemmArgs& a, hipStream_t stream);
 void launch_gemm_q8(const GemmArgs& a, hipStream_t stream);
 void launch_q8_group_sums(const GemmArgs& a, hipStream_t stream);
+void launch_gemm_q8_swiglu_q8(const GemmArgs& a, hipStream_t stream);  // large-M kernel only
 
 void launch_quantize_group(const void* src, int src_type, std::size_t ld_src, const void* src_up, std::int8_t* q,
                            std::size_t ld_q, float* s, std::size_t ld_s, std::size_t rows, std::size_t k, int rule,
@@ -43,6 +50,9 @@ void launch_quantize_rows(const void* x, int x_type, std::size_t ld_x, std::int8
                           std::size_t ld_s, std::size_t rows, std::size_t cols, std::size_t block, hipStream_t stream);
 void launch_rmsnorm(const float* x, std::size_t ld_x, void* y, int y_type, std::size_t ld_y, const float* w1,
                     std::size_t rows, std::size_t cols, double eps, hipStream_t stream);
+void launch_rmsnorm_quantize(const float* x, std::size_t ld_x, std::uint16_t* y_bf16, std::size_t ld_y, const float* w1,
+                             std::int8_t* q, std::size_t ld_q, float* scales, std::size_t ld_s, std::size_t rows,
+                             std::size_t cols, std::size_t block, double eps, hipStream_t stream);
 void launch_f32_to_bf16(const float* src, std::uint16_t* dst, std::size_t count, hipStream_t stream);
 
 // The M <= 16 w8g layer of the MLP stack (stack_small.hip): a launch plan for one shape and device, and one layer.

@@ -60,6 +60,8 @@ struct Params {
     int t, n, k;
     int tiles_m, tiles_n;
     std::int32_t* sums;     // MODE_SUMS: [groups][T][N]
+    float* ys;              // kSwigluQ8: [T, ld_ys]
+    std::size_t ld_ys;
     // small-M
     int splits, groups_per_split, col_blocks;
     float* partial;
@@ -245,6 +247,53 @@ __global__ void __launch_bounds__(512) gemm_big(const Params p) {
     }
     if constexpr (MODE == MODE_SUMS) return;
 
+    if constexpr (EP == kSwigluQ8) {
+        // The tile's 128 output columns are one quantization block. Each wave reduces |h| over its 32 columns per row
+        // (lanes sharing lane / 32), the four waves of a row half combine through LDS, then every lane quantizes its
+        // values with the block's scale. max is exact in any order, so this equals quantize_rows on the float32 H.
+        __shared__ float lds_amax[4][BM];
+        float h[2][16];
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row = min(m0 + wm * 64 + i * 32 + 8 * (r / 4) + 4 * (lane / 32) + (r % 4), p.t - 1);
+                float v0 = acc[i][0][r], v1 = acc[i][1][r];
+                if constexpr (PER_TOKEN) {
+                    const float xs = p.xs[static_cast<std::size_t>(row) * p.ld_xs];
+                    v0 = __fmul_rn(v0, xs);
+                    v1 = __fmul_rn(v1, xs);
+                }
+                h[i][r] = swiglu_cephes(v0, v1);
+                float m = fabsf(h[i][r]);
+#pragma unroll
+                for (int o = 16; o > 0; o >>= 1) {
+                    const float other = __shfl_xor(m, o, 32);
+                    m = other > m ? other : m;
+                }
+                if (lane % 32 == 0) lds_amax[wn][wm * 64 + i * 32 + 8 * (r / 4) + 4 * (lane / 32) + (r % 4)] = m;
+            }
+        __syncthreads();
+        const int f = n0 / 2 + 64 * ib + 32 * hh + lane % 32;
+        signed char* hq = static_cast<signed char*>(p.y);
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int rl = wm * 64 + i * 32 + 8 * (r / 4) + 4 * (lane / 32) + (r % 4), row = m0 + rl;
+                float m = lds_amax[0][rl];
+#pragma unroll
+                for (int w = 1; w < 4; ++w) m = lds_amax[w][rl] > m ? lds_amax[w][rl] : m;
+                const float scale = m > 0.0f ? __fdiv_rn(m, 127.0f) : 1.0f;
+                const float inverse = __fdiv_rn(1.0f, scale);
+                if (row >= p.t) continue;
+                float qv = __builtin_rintf(__fmul_rn(h[i][r], inverse));
+                qv = qv < -127.0f ? -127.0f : (qv > 127.0f ? 127.0f : qv);
+                if (2 * f < p.n) hq[static_cast<std::size_t>(row) * p.ld_y + f] = static_cast<signed char>(static_cast<int>(qv));
+                if (wn == 0 && lane % 32 == 0) p.ys[static_cast<std::size_t>(row) * p.ld_ys + n0 / 256] = scale;
+            }
+        return;
+    } else {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
 #pragma unroll
@@ -265,6 +314,7 @@ __global__ void __launch_bounds__(512) gemm_big(const Params p) {
                 if (col[1] < p.n) put<EP, YT>(p.y, p.ld_y, row, col[1], v1);
             }
         }
+    }
     }
 }
 
@@ -289,6 +339,8 @@ inline Params make_params(const GemmArgs& a) {
     p.n = static_cast<int>(a.n);
     p.k = static_cast<int>(a.k);
     p.sums = a.sums;
+    p.ys = a.ys;
+    p.ld_ys = a.ld_ys;
     return p;
 }
 
@@ -327,6 +379,11 @@ void dispatch_ep(const GemmArgs& a, hipStream_t stream) {
 void launch_gemm_q8(const GemmArgs& a, hipStream_t stream) {
     if (a.act_block == a.k && a.k != 128) q8::dispatch_ep<true>(a, stream);
     else q8::dispatch_ep<false>(a, stream);
+}
+
+void launch_gemm_q8_swiglu_q8(const GemmArgs& a, hipStream_t stream) {
+    if (a.act_block == a.k && a.k != 128) q8::launch_big<kSwigluQ8, SEPAL_HIP_F32, true, q8::MODE_CHAIN>(a, stream);
+    else q8::launch_big<kSwigluQ8, SEPAL_HIP_F32, false, q8::MODE_CHAIN>(a, stream);
 }
 
 void launch_q8_group_sums(const GemmArgs& a, hipStream_t stream) {

@@ -8,7 +8,8 @@
 //     (gemm_simt_kernels.hpp:72-77).
 //   quantize_rows_token: one scale per row (block = cols), rule RECIPROCAL; a block of 256 threads per row.
 //   rmsnorm: the cpu-q8 RMSNorm with its exact summation order (runner/src/cpu/elementwise.cpp:22-59): 32 lanes stand
-//     for the reference's 4 x 8 accumulator lanes, then the same combining order.
+//     for the reference's 4 x 8 accumulator lanes, then the same combining order. Its fused variant rounds the output to
+//     bfloat16 and quantizes it in the same pass (the layer input of the q8 stack: RMSNorm, bf16, quantize_rows).
 #include "common.hpp"
 #include "gemm_kernels.hpp"
 
@@ -150,10 +151,15 @@ __global__ void __launch_bounds__(256) quantize_rows_token_kernel(const void* __
 // take the remaining groups of 8). The combine and the normalising pass follow the reference.
 constexpr int kNormSeg = 2048;  // columns per LDS segment and wave
 
-template <int YT>
+// OUT: NORM_STORE writes y (YT); NORM_Q_TOKEN and NORM_Q_128 round each value to bfloat16 (y, when not null, gets those
+// bits) and quantize the rounded values as quantize_rows does (one scale per row, or per 128 columns).
+enum { NORM_STORE = 0, NORM_Q_TOKEN = 1, NORM_Q_128 = 2 };
+
+template <int YT, int OUT>
 __global__ void __launch_bounds__(256) rmsnorm_kernel(const float* __restrict__ x, std::size_t ld_x, void* __restrict__ y,
                                                       std::size_t ld_y, const float* __restrict__ w1, int rows, int cols,
-                                                      double eps) {
+                                                      double eps, std::int8_t* __restrict__ q, std::size_t ld_q,
+                                                      float* __restrict__ qs, std::size_t ld_qs) {
     __shared__ __align__(16) float seg[4][kNormSeg];
     const int wave = threadIdx.x / 64, lane = threadIdx.x % 64, L = lane % 32;
     const int row = blockIdx.x * 4 + wave;
@@ -210,14 +216,92 @@ __global__ void __launch_bounds__(256) rmsnorm_kernel(const float* __restrict__ 
     if (!live) return;
     const double mean = static_cast<double>(sum) / static_cast<double>(cols);
     const float inv = static_cast<float>(1.0 / __builtin_sqrt(mean + eps));
-    for (int c = 4 * lane; c < cols; c += 256) {
-        const float4 v = *reinterpret_cast<const float4*>(xr + c);
-        const float vv[4] = {v.x, v.y, v.z, v.w};
+    if constexpr (OUT == NORM_STORE) {
+        for (int c = 4 * lane; c < cols; c += 256) {
+            const float4 v = *reinterpret_cast<const float4*>(xr + c);
+            const float vv[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-            if (c + q < cols)
-                store_out<YT>(y, static_cast<std::size_t>(row) * ld_y + c + q,
-                              __fmul_rn(__fmul_rn(vv[q], inv), w1 != nullptr ? w1[c + q] : 1.0f));
+            for (int j = 0; j < 4; ++j)
+                if (c + j < cols)
+                    store_out<YT>(y, static_cast<std::size_t>(row) * ld_y + c + j,
+                                  __fmul_rn(__fmul_rn(vv[j], inv), w1 != nullptr ? w1[c + j] : 1.0f));
+        }
+    } else {
+        // four normalised columns c .. c + 3 rounded to bfloat16 (zero past cols)
+        const auto norm4 = [&](int c, float (&b)[4]) {
+            if (c < cols) {
+                const float4 v = *reinterpret_cast<const float4*>(xr + c);
+                const float vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const float n = __fmul_rn(__fmul_rn(vv[j], inv), w1 != nullptr ? w1[c + j] : 1.0f);
+                    b[j] = bf16_bits_to_f32(f32_to_bf16_bits(n));
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) b[j] = 0.0f;
+            }
+        };
+        const auto amax4 = [](const float (&b)[4], float m) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float a = fabsf(b[j]);
+                m = a > m ? a : m;
+            }
+            return m;
+        };
+        const auto put4 = [&](int c, const float (&b)[4], float scale, float inverse) {
+            unsigned packed = 0u;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                packed |= (static_cast<unsigned>(quantize_value<SEPAL_HIP_RULE_RECIPROCAL>(b[j], scale, inverse)) & 0xFFu) << (8 * j);
+            *reinterpret_cast<unsigned*>(q + static_cast<std::size_t>(row) * ld_q + c) = packed;
+            if (y != nullptr) {
+                unsigned short* yb = static_cast<unsigned short*>(y) + static_cast<std::size_t>(row) * ld_y + c;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) yb[j] = f32_to_bf16_bits(b[j]);
+            }
+        };
+        if constexpr (OUT == NORM_Q_128) {
+            // lanes 0..31 hold one 128-column block, lanes 32..63 the next (cols is a multiple of 128)
+            for (int c0 = 0; c0 < cols; c0 += 256) {
+                const int c = c0 + 4 * lane;
+                float b[4];
+                norm4(c, b);
+                float m = amax4(b, 0.0f);
+#pragma unroll
+                for (int o = 16; o > 0; o >>= 1) {
+                    const float other = __shfl_xor(m, o, 32);
+                    m = other > m ? other : m;
+                }
+                const float scale = m > 0.0f ? __fdiv_rn(m, 127.0f) : 1.0f;
+                const float inverse = __fdiv_rn(1.0f, scale);
+                if (c < cols) {
+                    put4(c, b, scale, inverse);
+                    if (lane % 32 == 0) qs[static_cast<std::size_t>(row) * ld_qs + c / 128] = scale;
+                }
+            }
+        } else {
+            float m = 0.0f;
+            for (int c = 4 * lane; c < cols; c += 256) {
+                float b[4];
+                norm4(c, b);
+                m = amax4(b, m);
+            }
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) {
+                const float other = __shfl_xor(m, o, 64);
+                m = other > m ? other : m;
+            }
+            const float scale = m > 0.0f ? __fdiv_rn(m, 127.0f) : 1.0f;
+            const float inverse = __fdiv_rn(1.0f, scale);
+            if (lane == 0) qs[static_cast<std::size_t>(row) * ld_qs] = scale;
+            for (int c = 4 * lane; c < cols; c += 256) {
+                float b[4];
+                norm4(c, b);
+                put4(c, b, scale, inverse);
+            }
+        }
     }
 }
 
@@ -271,12 +355,25 @@ void launch_rmsnorm(const float* x, std::size_t ld_x, void* y, int y_type, std::
                     std::size_t rows, std::size_t cols, double eps, hipStream_t stream) {
     const dim3 grid(static_cast<unsigned>((rows + 3) / 4));  // one row per wave
     const int r = static_cast<int>(rows), c = static_cast<int>(cols);
+    using quant::NORM_STORE;
     switch (y_type) {
-    case SEPAL_HIP_F32: quant::rmsnorm_kernel<SEPAL_HIP_F32><<<grid, dim3(256), 0, stream>>>(x, ld_x, y, ld_y, w1, r, c, eps); break;
-    case SEPAL_HIP_BF16: quant::rmsnorm_kernel<SEPAL_HIP_BF16><<<grid, dim3(256), 0, stream>>>(x, ld_x, y, ld_y, w1, r, c, eps); break;
-    default: quant::rmsnorm_kernel<SEPAL_HIP_F16><<<grid, dim3(256), 0, stream>>>(x, ld_x, y, ld_y, w1, r, c, eps); break;
+    case SEPAL_HIP_F32: quant::rmsnorm_kernel<SEPAL_HIP_F32, NORM_STORE><<<grid, dim3(256), 0, stream>>>(x, ld_x, y, ld_y, w1, r, c, eps, nullptr, 0, nullptr, 0); break;
+    case SEPAL_HIP_BF16: quant::rmsnorm_kernel<SEPAL_HIP_BF16, NORM_STORE><<<grid, dim3(256), 0, stream>>>(x, ld_x, y, ld_y, w1, r, c, eps, nullptr, 0, nullptr, 0); break;
+    default: quant::rmsnorm_kernel<SEPAL_HIP_F16, NORM_STORE><<<grid, dim3(256), 0, stream>>>(x, ld_x, y, ld_y, w1, r, c, eps, nullptr, 0, nullptr, 0); break;
     }
     check_launch("rmsnorm kernel launch");
+}
+
+void launch_rmsnorm_quantize(const float* x, std::size_t ld_x, std::uint16_t* y_bf16, std::size_t ld_y, const float* w1,
+                             std::int8_t* q, std::size_t ld_q, float* scales, std::size_t ld_s, std::size_t rows,
+                             std::size_t cols, std::size_t block, double eps, hipStream_t stream) {
+    const dim3 grid(static_cast<unsigned>((rows + 3) / 4));
+    const int r = static_cast<int>(rows), c = static_cast<int>(cols);
+    if (block == 128)
+        quant::rmsnorm_kernel<SEPAL_HIP_BF16, quant::NORM_Q_128><<<grid, dim3(256), 0, stream>>>(x, ld_x, y_bf16, ld_y, w1, r, c, eps, q, ld_q, scales, ld_s);
+    else
+        quant::rmsnorm_kernel<SEPAL_HIP_BF16, quant::NORM_Q_TOKEN><<<grid, dim3(256), 0, stream>>>(x, ld_x, y_bf16, ld_y, w1, r, c, eps, q, ld_q, scales, ld_s);
+    check_launch("rmsnorm_quantize kernel launch");
 }
 
 void launch_f32_to_bf16(const float* src, std::uint16_t* dst, std::size_t count, hipStream_t stream) {

@@ -54,10 +54,14 @@ def library() -> C.CDLL:
         L.sepal_hip_q8_group_sums.argtypes = [vp, sz, vp, sz, vp, sz, sz, sz, vp]
         L.sepal_hip_rmsnorm_rows.argtypes = [vp, sz, vp, i32, sz, vp, sz, sz, d, vp]
         L.sepal_hip_float_to_bf16.argtypes = [vp, vp, sz, vp]
+        L.sepal_hip_rmsnorm_quantize_rows.argtypes = [vp, sz, vp, vp, sz, vp, sz, vp, sz, sz, sz, sz, d, vp]
+        L.sepal_hip_gemm_q8_swiglu_quantize.argtypes = [vp, sz, vp, sz, sz, vp, sz, vp, sz, vp, sz, vp, sz, sz, sz, sz,
+                                                        i32, vp]
         L.sepal_hip_mlp_stack.argtypes = [i32, sz, sz, sz, sz, vp, vp, vp, vp, vp, vp, sz, d, vp]
         for name in ("sepal_hip_quantize_group_s8", "sepal_hip_quantize_gate_up_s8", "sepal_hip_gemm_w8g",
                      "sepal_hip_quantize_rows_s8", "sepal_hip_gemm_q8", "sepal_hip_q8_group_sums",
-                     "sepal_hip_rmsnorm_rows", "sepal_hip_float_to_bf16", "sepal_hip_mlp_stack"):
+                     "sepal_hip_rmsnorm_rows", "sepal_hip_float_to_bf16", "sepal_hip_mlp_stack",
+                     "sepal_hip_rmsnorm_quantize_rows", "sepal_hip_gemm_q8_swiglu_quantize"):
             getattr(L, name).restype = i32
         L.sepal_hip_gemm_w8g_supports.restype = i32
         _lib = L
@@ -189,6 +193,19 @@ def q8_group_sums(xq, w, stream=None):
     return out
 
 
+def gemm_q8_swiglu_quantize(xq, xs, w, ws, act_block: int = 128, config: int = -1, stream=None):
+    """q8 gate/up with SwiGLU and the output quantized per 128 columns: (hq int8 [T, N/2], hs [T, N/256])."""
+    torch = _torch()
+    t, k = xq.shape
+    n = w.shape[0]
+    hq = torch.empty(t, n // 2, dtype=torch.int8, device=xq.device)
+    hs = torch.empty(t, max(n // 256, 1), dtype=torch.float32, device=xq.device)
+    _check(library().sepal_hip_gemm_q8_swiglu_quantize(_ptr(xq), _ld(xq), _ptr(xs), _ld(xs), act_block, _ptr(w), _ld(w),
+                                                       _ptr(ws), _ld(ws), _ptr(hq), _ld(hq), _ptr(hs), _ld(hs), t, n, k,
+                                                       config, _stream(stream)))
+    return hq, hs
+
+
 def rmsnorm_rows(x, y_dtype=None, w1=None, eps: float = 1e-6, stream=None):
     torch = _torch()
     rows, cols = x.shape
@@ -196,6 +213,19 @@ def rmsnorm_rows(x, y_dtype=None, w1=None, eps: float = 1e-6, stream=None):
     _check(library().sepal_hip_rmsnorm_rows(_ptr(x), _ld(x), _ptr(y), _type_of(y), _ld(y), _ptr(w1), rows, cols, eps,
                                             _stream(stream)))
     return y
+
+
+def rmsnorm_quantize_rows(x, block: int = 128, w1=None, eps: float = 1e-6, with_bf16: bool = False, stream=None):
+    """RMSNorm -> bf16 -> int8 activation quantizer in one pass: (q, scales) or (q, scales, y_bf16)."""
+    torch = _torch()
+    rows, cols = x.shape
+    q = torch.empty(rows, cols, dtype=torch.int8, device=x.device)
+    sc = torch.empty(rows, max(cols // block, 1), dtype=torch.float32, device=x.device)
+    y = torch.empty(rows, cols, dtype=torch.bfloat16, device=x.device) if with_bf16 else None
+    _check(library().sepal_hip_rmsnorm_quantize_rows(_ptr(x), _ld(x), _ptr(w1), _ptr(y), _ld(y) if y is not None else 0,
+                                                     _ptr(q), _ld(q), _ptr(sc), _ld(sc), rows, cols, block, eps,
+                                                     _stream(stream)))
+    return (q, sc, y) if with_bf16 else (q, sc)
 
 
 def float_to_bf16(x, stream=None):

@@ -148,6 +148,28 @@ def test_rmsnorm_segment_edges(sm, rows, cols):
     assert same_bits(host(out), orc.rmsnorm_rows(x))
 
 
+@pytest.mark.parametrize("block", [128, 0])
+@pytest.mark.parametrize("rows,cols", [(37, 2560), (5, 384), (130, 9728), (4, 128)])
+def test_rmsnorm_quantize_fused(sm, rows, cols, block):
+    """The fused q8 layer input equals RMSNorm (exact order) -> bf16 -> the cpu-q8 quantizer, bit for bit."""
+    say("rmsnorm_quantize", rows, cols, block)
+    rng = np.random.default_rng(rows + cols + block)
+    x = (rng.standard_normal((rows, cols)) * 3).astype(np.float32)
+    x[1 % rows, : min(cols, 256)] = 0.0  # a zero block (scale 1) where the row allows
+    x[0, 7] = 400.0                         # an outlier sets its block's scale
+    w1 = (rng.standard_normal(cols) * 0.5 + 1).astype(np.float32) if rows == 37 else None
+    b = cols if block == 0 else 128
+    q, s, yb = sm.rmsnorm_quantize_rows(dev(x), block=b, w1=dev(w1) if w1 is not None else None, with_bf16=True)
+    xn = orc.bf16_round(orc.rmsnorm_rows(x, w1=w1))
+    qo, so = orc.quantize_block_r2(xn, block=b)
+    assert same_bits(host(yb), xn)
+    assert same_bits(host(q), qo) and same_bits(host(s), so)
+    # and the same as the two GPU passes it replaces
+    q2, s2 = sm.quantize_rows_s8(sm.rmsnorm_rows(dev(x), y_dtype=torch.bfloat16, w1=dev(w1) if w1 is not None else None),
+                                 block=b)
+    assert same_bits(host(q), host(q2)) and same_bits(host(s), host(s2))
+
+
 def test_float_to_bf16(sm):
     say("float_to_bf16")
     rng = np.random.default_rng(4)
@@ -237,7 +259,7 @@ def _deq_ref(xt, qt, st, k):
 
 @pytest.mark.parametrize("epilogue", ["store", "add", "swiglu"])
 def test_w8g_wide_tiles_every_element(sm, epilogue):
-    # at least 512 tiles of 256 x 256 select the two-group (ping-pong) kernel; 4000 rows leave a ragged last row tile
+    # at least 512 tiles of 256 x 256 select the 64-wide-step kernel; 4000 rows leave a ragged last row tile
     # and, for store/add, 8000 columns a ragged last column tile
     t, n, k = (4000, 8192, 384) if epilogue == "swiglu" else (4000, 8000, 384)
     rng = np.random.default_rng(4242 + len(epilogue))
@@ -329,6 +351,33 @@ def test_q8_swiglu_bit_exact(sm, case):
         say("q8 swiglu", case, "config", cfg)
         y = host(sm.gemm_q8(xq, xs, wq, ws, epilogue=sm.SWIGLU, config=cfg))
         assert same_bits(y, ref)
+
+
+@pytest.mark.parametrize("case", [(130, 512, 256), (300, 1024, 1280), (16, 512, 384), (64, 256, 640)])
+@pytest.mark.parametrize("act", ["128", "token"])
+def test_q8_swiglu_quantize_fused(sm, case, act):
+    """gate/up with the int8 re-quantization of H in the epilogue equals gemm_q8 (SwiGLU, float32 H) followed by the
+    activation quantizer (block 128), bit for bit, on both paths; the large path also equals the oracle chain."""
+    t, n, k = case
+    rng = np.random.default_rng(11 * t + n + k)
+    x = bf16_inputs(rng, (t, k), outlier_frac=0.01)
+    gate = (rng.standard_normal((n // 2, k)) * 0.02).astype(np.float32)
+    up = (rng.standard_normal((n // 2, k)) * 0.02).astype(np.float32)
+    gate[3] = 0.0
+    up[3] = 0.0  # an all-zero H column
+    wq, ws = sm.quantize_gate_up_s8(dev(gate), dev(up), rule=1)
+    ab = 128 if act == "128" else k
+    xq, xs = sm.quantize_rows_s8(dev(x, torch.bfloat16), block=ab)
+    for cfg in ([-1, 0] if t <= 64 else [-1]):
+        say("q8 swiglu quantize", case, act, "config", cfg)
+        h = sm.gemm_q8(xq, xs, wq, ws, epilogue=sm.SWIGLU, act_block=ab, config=cfg)
+        hq_ref, hs_ref = sm.quantize_rows_s8(h, block=128)
+        hq, hs = sm.gemm_q8_swiglu_quantize(xq, xs, wq, ws, act_block=ab, config=cfg)
+        assert same_bits(host(hq), host(hq_ref)) and same_bits(host(hs), host(hs_ref))
+        if cfg == 0 or t > 64:
+            href = orc.gemm_q8(host(xq), host(xs), host(wq), host(ws), epilogue=orc.SWIGLU, act_block=ab)
+            qo, so = orc.quantize_block_r2(href, block=128)
+            assert same_bits(host(hq), qo) and same_bits(host(hs), so)
 
 
 def test_q8_matches_reference_outputs(sm, golden):
@@ -427,9 +476,13 @@ def test_mlp_stack(sm, kind, act, t):
     hidden, inter, nl = 256, 512, 3
     layers = _stack_weights(sm, rng, nl, hidden, inter, rule=0 if kind == 0 else 1)
     x = bf16_inputs(rng, (t, hidden))
-    y = host(sm.mlp_stack(kind, dev(x, torch.bfloat16), layers, act_block=act))
+    xt = dev(x, torch.bfloat16)
+    y = host(sm.mlp_stack(kind, xt, layers, act_block=act))
     # the one-call stack is exactly its steps called one by one
     assert same_bits(y, _gpu_composition(sm, kind, x, layers, act))
+    if kind == 1 and t > 64:
+        # x holds the last layer's input (for q8 written by the fused RMSNorm + quantize pass)
+        assert same_bits(host(xt), orc.bf16_round(orc.rmsnorm_rows(_oracle_stack(kind, x, layers[:2], act))))
     # one layer (no rounding of an intermediate activation to bf16) against the oracle at the parity bar
     y1 = host(sm.mlp_stack(kind, dev(x, torch.bfloat16), layers[:1], act_block=act))
     ref1 = _oracle_stack(kind, x, layers[:1], act)
