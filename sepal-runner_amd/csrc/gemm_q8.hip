@@ -248,50 +248,69 @@ __global__ void __launch_bounds__(512) gemm_big(const Params p) {
     if constexpr (MODE == MODE_SUMS) return;
 
     if constexpr (EP == kSwigluQ8) {
-        // The tile's 128 output columns are one quantization block. Each wave reduces |h| over its 32 columns per row
-        // (lanes sharing lane / 32), the four waves of a row half combine through LDS, then every lane quantizes its
-        // values with the block's scale. max is exact in any order, so this equals quantize_rows on the float32 H.
+        // The tile's 128 output columns are one quantization block. H goes through LDS (the W tile's space, free after
+        // the last step's barrier): 128 rows of 512 bytes, 16-byte chunk c of row r at c ^ (r % 16). Thread (row, q)
+        // then takes 32 columns of one row: the max over them, the four quarters combined through LDS, the scale, and
+        // 32 int8 values stored as two 16-byte chunks. max is exact in any order, so this equals quantize_rows on the
+        // float32 H (rule RECIPROCAL).
+        float* hb = reinterpret_cast<float*>(&lds_w[0][0]);
         __shared__ float lds_amax[4][BM];
-        float h[2][16];
+        const int c = 64 * ib + 32 * hh + lane % 32;  // this lane's column within the block
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const int row = min(m0 + wm * 64 + i * 32 + 8 * (r / 4) + 4 * (lane / 32) + (r % 4), p.t - 1);
+                const int rl = wm * 64 + i * 32 + 8 * (r / 4) + 4 * (lane / 32) + (r % 4);
                 float v0 = acc[i][0][r], v1 = acc[i][1][r];
                 if constexpr (PER_TOKEN) {
-                    const float xs = p.xs[static_cast<std::size_t>(row) * p.ld_xs];
+                    const float xs = p.xs[static_cast<std::size_t>(min(m0 + rl, p.t - 1)) * p.ld_xs];
                     v0 = __fmul_rn(v0, xs);
                     v1 = __fmul_rn(v1, xs);
                 }
-                h[i][r] = swiglu_cephes(v0, v1);
-                float m = fabsf(h[i][r]);
-#pragma unroll
-                for (int o = 16; o > 0; o >>= 1) {
-                    const float other = __shfl_xor(m, o, 32);
-                    m = other > m ? other : m;
-                }
-                if (lane % 32 == 0) lds_amax[wn][wm * 64 + i * 32 + 8 * (r / 4) + 4 * (lane / 32) + (r % 4)] = m;
+                hb[rl * 128 + (((c / 4) ^ (rl % 16)) * 4) + c % 4] = swiglu_cephes(v0, v1);
             }
         __syncthreads();
-        const int f = n0 / 2 + 64 * ib + 32 * hh + lane % 32;
-        signed char* hq = static_cast<signed char*>(p.y);
+        const int row_l = tid % BM, quarter = tid / BM;
+        float hv[32];
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int j = 0; j < 8; ++j) {
+            const float4 v = *reinterpret_cast<const float4*>(hb + row_l * 128 + (((8 * quarter + j) ^ (row_l % 16)) * 4));
+            hv[4 * j] = v.x;
+            hv[4 * j + 1] = v.y;
+            hv[4 * j + 2] = v.z;
+            hv[4 * j + 3] = v.w;
+        }
+        float m = 0.0f;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int rl = wm * 64 + i * 32 + 8 * (r / 4) + 4 * (lane / 32) + (r % 4), row = m0 + rl;
-                float m = lds_amax[0][rl];
+        for (int j = 0; j < 32; ++j) {
+            const float a = fabsf(hv[j]);
+            m = a > m ? a : m;
+        }
+        lds_amax[quarter][row_l] = m;
+        __syncthreads();
+        m = lds_amax[0][row_l];
 #pragma unroll
-                for (int w = 1; w < 4; ++w) m = lds_amax[w][rl] > m ? lds_amax[w][rl] : m;
-                const float scale = m > 0.0f ? __fdiv_rn(m, 127.0f) : 1.0f;
-                const float inverse = __fdiv_rn(1.0f, scale);
-                if (row >= p.t) continue;
-                float qv = __builtin_rintf(__fmul_rn(h[i][r], inverse));
-                qv = qv < -127.0f ? -127.0f : (qv > 127.0f ? 127.0f : qv);
-                if (2 * f < p.n) hq[static_cast<std::size_t>(row) * p.ld_y + f] = static_cast<signed char>(static_cast<int>(qv));
-                if (wn == 0 && lane % 32 == 0) p.ys[static_cast<std::size_t>(row) * p.ld_ys + n0 / 256] = scale;
+        for (int w = 1; w < 4; ++w) m = lds_amax[w][row_l] > m ? lds_amax[w][row_l] : m;
+        const float scale = m > 0.0f ? __fdiv_rn(m, 127.0f) : 1.0f;
+        const float inverse = __fdiv_rn(1.0f, scale);
+        const int row = m0 + row_l;
+        if (row < p.t) {
+            unsigned packed[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                packed[j] = 0u;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    float qv = __builtin_rintf(__fmul_rn(hv[4 * j + e], inverse));
+                    qv = qv < -127.0f ? -127.0f : (qv > 127.0f ? 127.0f : qv);
+                    packed[j] |= (static_cast<unsigned>(static_cast<int>(qv)) & 0xFFu) << (8 * e);
+                }
             }
+            signed char* dst = static_cast<signed char*>(p.y) + static_cast<std::size_t>(row) * p.ld_y + n0 / 2 + 32 * quarter;
+            *reinterpret_cast<u32x4*>(dst) = u32x4{packed[0], packed[1], packed[2], packed[3]};
+            *reinterpret_cast<u32x4*>(dst + 16) = u32x4{packed[4], packed[5], packed[6], packed[7]};
+            if (quarter == 0) p.ys[static_cast<std::size_t>(row) * p.ld_ys + n0 / 256] = scale;
+        }
         return;
     } else {
 #pragma unroll

@@ -591,3 +591,32 @@ def test_full_size_block_sampled_rows(sm, big_layer, m):
         assert same_bits(host(hq)[rows], href) and same_bits(yq[rows], yref)
     else:
         assert max_rel_over_rms(yq[rows], yref) < 2e-3
+
+
+# ---- the other int8 weight groups of w8g_int8 (dn_in, attn_in, attn_out) ------------------------------------------------
+
+@pytest.mark.parametrize("n,k", [(12288, 2560), (10240, 2560), (2560, 4096)])
+@pytest.mark.parametrize("m", [16, 896, 4000])
+def test_other_weight_groups_shapes(sm, n, k, m):
+    """The same kernels at the shapes of the model's other int8 groups (runner/cuda/src/gpu_profiles.cpp:21-24,
+    cuda_engine.hpp:200-212): w8g against a float64 product of the dequantised weights (every element), q8 against
+    the cpu-q8 oracle chain on sampled rows (bit for bit on the large-M path)."""
+    say("other groups", m, n, k)
+    rng = np.random.default_rng(n + k + m)
+    x = bf16_inputs(rng, (m, k), outlier_frac=0.01)
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float16)
+    wt = dev(w)
+    q, s = sm.quantize_group_s8(wt, rule=0)
+    xt = dev(x, torch.bfloat16)
+    y = host(sm.gemm_w8g(xt, q, s))
+    ref = host(_deq_ref(xt, q, s, k))
+    assert max_rel_over_rms(y, ref) < 2e-3 and rel_rms(y, ref) < 1e-5
+    qq, qs = sm.quantize_group_s8(wt, rule=1)
+    xq, xs = sm.quantize_rows_s8(xt, block=128)
+    yq = host(sm.gemm_q8(xq, xs, qq, qs))
+    rows = sorted(set([0, m - 1] + list(rng.choice(m, size=min(m, 4), replace=False))))
+    yref = orc.gemm_q8(host(xq)[rows], host(xs)[rows], host(qq), host(qs))
+    if m > 64:
+        assert same_bits(yq[rows], yref)
+    else:
+        assert max_rel_over_rms(yq[rows], yref) < 2e-3
