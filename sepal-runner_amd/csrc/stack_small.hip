@@ -4,9 +4,10 @@
 // every CU streaming its share of weights for the whole kernel:
 //   tiles  (gate/up, SwiGLU): one block of 16 waves per CU, and each block owns whole 16-row weight tiles (8 gate rows
 //          and the 8 up rows of the same features) over the full K, 4 or 5 tiles per CU at the model's shape. The X
-//          rows are staged once per block in LDS; the block's (tile, group) pairs are split evenly over the 16 waves,
-//          every weight load of a wave is issued before X is staged, and the waves' partial tiles are added in LDS in
-//          wave order, then SwiGLU.
+//          rows and the block's scales are staged once per block in LDS before any weight load is issued (loads
+//          complete in order per wave, and small loads issued beside the weight burst wait for all of it); the block's
+//          (tile, group) pairs are split evenly over the 16 waves, every weight load of a wave is in flight at once,
+//          and the waves' partial tiles are added in LDS in wave order, then SwiGLU.
 //   parts  (down): the (K-part, column tile) units are dealt out evenly to the blocks, K-part major so that a
 //          block's units share one slice of H; each unit's sum is written to a partial buffer P[part][row][col].
 //   finish: one block per row adds the K-parts in order (y, float32), then runs the cpu-q8 RMSNorm on it with the
@@ -75,6 +76,7 @@ __global__ void __launch_bounds__(kThreads) pass_kernel(const PassParams p) {
     const int kw = 128 * gpt;                 // staged X columns [128 g_lo, 128 g_hi)
     const int xpitch = 2 * kw + 16;           // bytes per staged row (padded: an operand read's 16 rows hit distinct banks)
     float* red = reinterpret_cast<float*>(lds + 16 * xpitch);  // [kWaves][kSlots][16 x 16]
+    float* scl = red + kWaves * kSlots * 256;                   // [block tile][16 rows][gpt] scales
     // the block's (tile, group) pairs, tile major, dealt to the waves in runs of `per` (the last waves may get none)
     const int total = ntiles * gpt;
     const int per = (total + kWaves - 1) / kWaves;
@@ -83,8 +85,8 @@ __global__ void __launch_bounds__(kThreads) pass_kernel(const PassParams p) {
     const int first_tile = min(q0, total - 1) / gpt;  // block-local
     static_assert(kWaves == 16, "one staged X row per wave");
 
-    // ---- X[0..16)[k range] into registers first, wave w taking row w (rows past T repeat row T-1 and feed only
-    // outputs that are never stored), so that waiting for X never waits for the weights issued after it ----
+    // ---- X[0..16)[k range] into registers, wave w taking row w (rows past T repeat row T-1 and feed only outputs
+    // that are never stored) ----
     const int cpr = kw / 8;  // 16-byte chunks per row
     u32x4 xv[kXChunks];
     {
@@ -93,16 +95,35 @@ __global__ void __launch_bounds__(kThreads) pass_kernel(const PassParams p) {
         for (int e = 0; e < kXChunks; ++e) xv[e] = *reinterpret_cast<const u32x4*>(xrow + 8 * min(lane + 64 * e, cpr - 1));
     }
 
-    // ---- every weight and scale load of this wave's pairs (clamped, unconditional). The wave's pairs touch at most
-    // kSlots consecutive tiles; their row pointers are formed once, and the (tile, group) walk is wave-uniform. ----
+    // ---- the block's scales (row runs of gpt words); with X they are in LDS before any weight load is issued: loads
+    // complete in order per wave, and small loads issued beside the weight burst wait for the whole burst in the
+    // memory queues ----
+    float sv[2];
+    const int nsc = ntiles * 16 * gpt;  // at most kWaves * kPairs * 16 = 2 * kThreads
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+        const int idx = min(tid + e * kThreads, nsc - 1);
+        const int tl = idx / (16 * gpt), rem = idx % (16 * gpt);
+        const int row = min(tile_row<SWIGLU>(tile0 + tl, rem / gpt), p.n - 1);
+        sv[e] = p.s[static_cast<std::size_t>(row) * p.ld_s + g_lo + rem % gpt];
+    }
+#pragma unroll
+    for (int e = 0; e < kXChunks; ++e)
+        if (lane + 64 * e < cpr) *reinterpret_cast<u32x4*>(lds + wave * xpitch + 16 * (lane + 64 * e)) = xv[e];
+#pragma unroll
+    for (int e = 0; e < 2; ++e)
+        if (tid + e * kThreads < nsc) scl[tid + e * kThreads] = sv[e];
+    __syncthreads();
+
+    // ---- then every weight load of this wave's pairs at once (clamped, unconditional). The wave's pairs touch at
+    // most kSlots consecutive tiles; their row pointers are formed once, and the (tile, group) walk is wave-uniform;
+    // past the wave's share it stays on its last pair (the same addresses again, never multiplied). ----
     const signed char* wrow[kSlots];
-    const float* srow[kSlots];
 #pragma unroll
     for (int j = 0; j < kSlots; ++j) {
         const int tile = tile0 + min(first_tile + j, ntiles - 1);
         const std::size_t row = static_cast<std::size_t>(min(tile_row<SWIGLU>(tile, lane % 16), p.n - 1));  // past N: never stored
         wrow[j] = p.w + row * p.ld_w + 16 * (lane / 16);
-        srow[j] = p.s + row * p.ld_s;
     }
     u32x4 wb[kPairs][2];
     float sc[kPairs];
@@ -111,12 +132,10 @@ __global__ void __launch_bounds__(kThreads) pass_kernel(const PassParams p) {
         int slot = qs / gpt - first_tile, g = g_lo + qs % gpt;
 #pragma unroll
         for (int i = 0; i < kPairs; ++i) {
-            // past the wave's share the walk stays on its last pair: the same addresses again, never multiplied
             const signed char* src = (slot == 0 ? wrow[0] : slot == 1 ? wrow[1] : wrow[2]) + 128 * g;
-            const float* ss = (slot == 0 ? srow[0] : slot == 1 ? srow[1] : srow[2]) + g;
             wb[i][0] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src));
             wb[i][1] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + 64));
-            sc[i] = *ss;
+            sc[i] = scl[((first_tile + slot) * 16 + lane % 16) * gpt + (g - g_lo)];
             if (q0 + i + 1 < q1) {
                 if (++g == g_hi) {
                     g = g_lo;
@@ -125,12 +144,6 @@ __global__ void __launch_bounds__(kThreads) pass_kernel(const PassParams p) {
             }
         }
     }
-
-    // ---- X into LDS ----
-#pragma unroll
-    for (int e = 0; e < kXChunks; ++e)
-        if (lane + 64 * e < cpr) *reinterpret_cast<u32x4*>(lds + wave * xpitch + 16 * (lane + 64 * e)) = xv[e];
-    __syncthreads();
 
     // ---- multiply: per pair, four MFMAs over the group's 128 k (lane quarter q holds k 16 q .. 16 q + 15 of each
     // 64-k half: the same permutation on both operands), then cur += s * P; the wave's pairs run tile by tile, and
@@ -279,7 +292,8 @@ int device_cus() {
 }
 
 std::size_t pass_lds(std::size_t kw) {
-    return 16 * (2 * kw + 16) + static_cast<std::size_t>(stack::kWaves) * stack::kSlots * 256 * sizeof(float);
+    return 16 * (2 * kw + 16) + static_cast<std::size_t>(stack::kWaves) * stack::kSlots * 256 * sizeof(float) +
+           static_cast<std::size_t>(stack::kWaves) * stack::kPairs * 16 * sizeof(float);
 }
 
 template <typename Kernel>
