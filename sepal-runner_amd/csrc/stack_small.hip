@@ -4,10 +4,9 @@
 // every CU streaming its share of weights for the whole kernel:
 //   tiles  (gate/up, SwiGLU): one block of 16 waves per CU, and each block owns whole 16-row weight tiles (8 gate rows
 //          and the 8 up rows of the same features) over the full K, 4 or 5 tiles per CU at the model's shape. The X
-//          rows and the block's scales are staged once per block in LDS before any weight load is issued (loads
-//          complete in order per wave, and small loads issued beside the weight burst wait for all of it); the block's
-//          (tile, group) pairs are split evenly over the 16 waves, every weight load of a wave is in flight at once,
-//          and the waves' partial tiles are added in LDS in wave order, then SwiGLU.
+//          rows and the block's scales are staged once per block in LDS by 4 loader waves while the 12 worker waves
+//          already have every weight load of their pairs in flight; the block's (tile, group) pairs are split evenly
+//          over the workers, and their partial tiles are added in LDS in worker order, then SwiGLU.
 //   parts  (down): the (K-part, column tile) units are dealt out evenly to the blocks, K-part major so that a
 //          block's units share one slice of H; each unit's sum is written to a partial buffer P[part][row][col].
 //   finish: one block per row adds the K-parts in order (y, float32), then runs the cpu-q8 RMSNorm on it with the
@@ -22,8 +21,11 @@ namespace sepal::hip {
 namespace stack {
 
 constexpr int kWaves = 16, kThreads = 64 * kWaves;
-constexpr int kPairs = 8;  // (tile or unit, group) pairs one wave holds; all their loads are in flight at once
-constexpr int kSlots = 3;  // tiles or units a wave's pairs may touch
+constexpr int kLoaders = 4;                  // waves that stage X and the scales
+constexpr int kWorkers = kWaves - kLoaders;  // waves that load weights and multiply
+constexpr int kPairs = 9;   // (tile or unit, group) pairs one worker holds; all their loads are in flight at once
+constexpr int kSlots = 3;   // tiles or units a worker's pairs may touch: 1 + ceil((kPairs - 1) / 4) with >= 4 groups per tile
+constexpr int kScaleLoads = (kWorkers * kPairs * 16 + 64 * kLoaders - 1) / (64 * kLoaders);  // per loader thread
 
 __device__ __forceinline__ f32x4 mfma16(int xt, const u32x4 a, const u32x4 b, f32x4 c) {
     if (xt == SEPAL_HIP_BF16)
@@ -59,13 +61,19 @@ __device__ __forceinline__ int tile_row(int tile, int c) {
     }
 }
 
-constexpr int kXChunks = 6;  // 16-byte X chunks per lane: a row of 64 x 6 x 8 = 3072 columns at most
+constexpr int kXChunks = 6;  // 16-byte X chunks per lane of a staged row: 64 x 6 x 8 = 3072 columns at most
 
 // One multiply pass over a block of weight tiles and one K-part (the gate/up pass: SWIGLU, one part covering K, the
 // output H; the down pass: several parts, the output P[part]). XT is the activation type, YT the SwiGLU output type.
+//
+// Waves 0 .. kLoaders - 1 stage the block's X rows and scales in LDS and then raise an LDS flag; waves kLoaders .. 15
+// (the workers) issue every weight load of their pairs at once from the start, wait for the flag, and multiply. The
+// weights are thus in flight while X and the scales arrive, and no worker's load issue (which stalls when the memory
+// queues are full) holds up a barrier.
 template <int XT, bool SWIGLU, int YT>
 __global__ void __launch_bounds__(kThreads) pass_kernel(const PassParams p) {
     extern __shared__ __align__(16) unsigned char lds[];
+    __shared__ unsigned ready;
     const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
     const int groups = p.k / 128;
     const int part = blockIdx.x / p.blocks_per_part;
@@ -75,128 +83,145 @@ __global__ void __launch_bounds__(kThreads) pass_kernel(const PassParams p) {
     const int gpt = g_hi - g_lo;              // groups per tile in this part
     const int kw = 128 * gpt;                 // staged X columns [128 g_lo, 128 g_hi)
     const int xpitch = 2 * kw + 16;           // bytes per staged row (padded: an operand read's 16 rows hit distinct banks)
-    float* red = reinterpret_cast<float*>(lds + 16 * xpitch);  // [kWaves][kSlots][16 x 16]
-    float* scl = red + kWaves * kSlots * 256;                   // [block tile][16 rows][gpt] scales
-    // the block's (tile, group) pairs, tile major, dealt to the waves in runs of `per` (the last waves may get none)
+    float* red = reinterpret_cast<float*>(lds + 16 * xpitch);  // [kWorkers][kSlots][16 x 16]
+    float* scl = red + kWorkers * kSlots * 256;                 // [block tile][16 rows][gpt] scales
+    // the block's (tile, group) pairs, tile major, dealt to the workers in runs of `per` (the last may get none)
     const int total = ntiles * gpt;
-    const int per = (total + kWaves - 1) / kWaves;
-    const int q0 = min(wave * per, total), q1 = min(q0 + per, total);
-    const int n_pairs = q1 - q0;
-    const int first_tile = min(q0, total - 1) / gpt;  // block-local
-    static_assert(kWaves == 16, "one staged X row per wave");
-
-    // ---- X[0..16)[k range] into registers, wave w taking row w (rows past T repeat row T-1 and feed only outputs
-    // that are never stored) ----
-    const int cpr = kw / 8;  // 16-byte chunks per row
-    u32x4 xv[kXChunks];
-    {
-        const unsigned short* xrow = p.x + static_cast<std::size_t>(min(wave, p.t - 1)) * p.ld_x + 128 * g_lo;
-#pragma unroll
-        for (int e = 0; e < kXChunks; ++e) xv[e] = *reinterpret_cast<const u32x4*>(xrow + 8 * min(lane + 64 * e, cpr - 1));
-    }
-
-    // ---- the block's scales (row runs of gpt words); with X they are in LDS before any weight load is issued: loads
-    // complete in order per wave, and small loads issued beside the weight burst wait for the whole burst in the
-    // memory queues ----
-    float sv[2];
-    const int nsc = ntiles * 16 * gpt;  // at most kWaves * kPairs * 16 = 2 * kThreads
-#pragma unroll
-    for (int e = 0; e < 2; ++e) {
-        const int idx = min(tid + e * kThreads, nsc - 1);
-        const int tl = idx / (16 * gpt), rem = idx % (16 * gpt);
-        const int row = min(tile_row<SWIGLU>(tile0 + tl, rem / gpt), p.n - 1);
-        sv[e] = p.s[static_cast<std::size_t>(row) * p.ld_s + g_lo + rem % gpt];
-    }
-#pragma unroll
-    for (int e = 0; e < kXChunks; ++e)
-        if (lane + 64 * e < cpr) *reinterpret_cast<u32x4*>(lds + wave * xpitch + 16 * (lane + 64 * e)) = xv[e];
-#pragma unroll
-    for (int e = 0; e < 2; ++e)
-        if (tid + e * kThreads < nsc) scl[tid + e * kThreads] = sv[e];
+    const int per = (total + kWorkers - 1) / kWorkers;
+    if (tid == 0) ready = 0u;
     __syncthreads();
 
-    // ---- then every weight load of this wave's pairs at once (clamped, unconditional). The wave's pairs touch at
-    // most kSlots consecutive tiles; their row pointers are formed once, and the (tile, group) walk is wave-uniform;
-    // past the wave's share it stays on its last pair (the same addresses again, never multiplied). ----
-    const signed char* wrow[kSlots];
+    if (wave < kLoaders) {
+        // ---- loaders: rows 4 w .. 4 w + 3 of X[0..16)[k range] (rows past T repeat row T-1 and feed only outputs
+        // that are never stored), two rows at a time, and the block's scales (row runs of gpt words) ----
+        const int cpr = kw / 8;  // 16-byte chunks per row
+        const int lt = tid;      // 0 .. 64 kLoaders - 1
+        float sv[kScaleLoads];
 #pragma unroll
-    for (int j = 0; j < kSlots; ++j) {
-        const int tile = tile0 + min(first_tile + j, ntiles - 1);
-        const std::size_t row = static_cast<std::size_t>(min(tile_row<SWIGLU>(tile, lane % 16), p.n - 1));  // past N: never stored
-        wrow[j] = p.w + row * p.ld_w + 16 * (lane / 16);
-    }
-    u32x4 wb[kPairs][2];
-    float sc[kPairs];
-    {
-        const int qs = min(q0, total - 1);
-        int slot = qs / gpt - first_tile, g = g_lo + qs % gpt;
+        for (int e = 0; e < kScaleLoads; ++e) {
+            const int idx = min(lt + e * 64 * kLoaders, total * 16 - 1);
+            const int tl = idx / (16 * gpt), rem = idx % (16 * gpt);
+            const int row = min(tile_row<SWIGLU>(tile0 + tl, rem / gpt), p.n - 1);
+            sv[e] = p.s[static_cast<std::size_t>(row) * p.ld_s + g_lo + rem % gpt];
+        }
 #pragma unroll
-        for (int i = 0; i < kPairs; ++i) {
-            const signed char* src = (slot == 0 ? wrow[0] : slot == 1 ? wrow[1] : wrow[2]) + 128 * g;
-            wb[i][0] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src));
-            wb[i][1] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + 64));
-            sc[i] = scl[((first_tile + slot) * 16 + lane % 16) * gpt + (g - g_lo)];
-            if (q0 + i + 1 < q1) {
-                if (++g == g_hi) {
-                    g = g_lo;
-                    ++slot;
+        for (int rr = 0; rr < 4; rr += 2) {
+            u32x4 xv[2][kXChunks];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int r = 4 * wave + rr + h;
+                const unsigned short* xrow = p.x + static_cast<std::size_t>(min(r, p.t - 1)) * p.ld_x + 128 * g_lo;
+#pragma unroll
+                for (int e = 0; e < kXChunks; ++e) xv[h][e] = *reinterpret_cast<const u32x4*>(xrow + 8 * min(lane + 64 * e, cpr - 1));
+            }
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int e = 0; e < kXChunks; ++e)
+                    if (lane + 64 * e < cpr)
+                        *reinterpret_cast<u32x4*>(lds + (4 * wave + rr + h) * xpitch + 16 * (lane + 64 * e)) = xv[h][e];
+        }
+#pragma unroll
+        for (int e = 0; e < kScaleLoads; ++e)
+            if (lt + e * 64 * kLoaders < total * 16) scl[lt + e * 64 * kLoaders] = sv[e];
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS writes are done
+        if (lane == 0) __hip_atomic_fetch_add(&ready, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+    } else {
+        const int wk = wave - kLoaders;
+        const int q0 = min(wk * per, total), q1 = min(q0 + per, total);
+        const int n_pairs = q1 - q0;
+        const int first_tile = min(q0, total - 1) / gpt;  // block-local
+        // ---- every weight load of this worker's pairs at once (clamped, unconditional). The pairs touch at most
+        // kSlots consecutive tiles; their row pointers are formed once, and the (tile, group) walk is wave-uniform;
+        // past the worker's share it stays on its last pair (the same addresses again, never multiplied). ----
+        const signed char* wrow[kSlots];
+#pragma unroll
+        for (int j = 0; j < kSlots; ++j) {
+            const int tile = tile0 + min(first_tile + j, ntiles - 1);
+            const std::size_t row = static_cast<std::size_t>(min(tile_row<SWIGLU>(tile, lane % 16), p.n - 1));  // past N: never stored
+            wrow[j] = p.w + row * p.ld_w + 16 * (lane / 16);
+        }
+        u32x4 wb[kPairs][2];
+        int pslot[kPairs], pg[kPairs];
+        {
+            const int qs = min(q0, total - 1);
+            int slot = qs / gpt - first_tile, g = g_lo + qs % gpt;
+#pragma unroll
+            for (int i = 0; i < kPairs; ++i) {
+                const signed char* src = wrow[0] + 128 * g;
+#pragma unroll
+                for (int j = 1; j < kSlots; ++j)
+                    if (slot == j) src = wrow[j] + 128 * g;
+                wb[i][0] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src));
+                wb[i][1] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + 64));
+                pslot[i] = slot;
+                pg[i] = g;
+                if (q0 + i + 1 < q1) {
+                    if (++g == g_hi) {
+                        g = g_lo;
+                        ++slot;
+                    }
                 }
             }
         }
-    }
+        // ---- X and the scales are staged ----
+        while (__hip_atomic_load(&ready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < static_cast<unsigned>(kLoaders))
+            __builtin_amdgcn_s_sleep(1);
 
-    // ---- multiply: per pair, four MFMAs over the group's 128 k (lane quarter q holds k 16 q .. 16 q + 15 of each
-    // 64-k half: the same permutation on both operands), then cur += s * P; the wave's pairs run tile by tile, and
-    // each finished tile goes to its LDS slot [wave][slot][row][col] ----
-    f32x4 cur = {0.0f, 0.0f, 0.0f, 0.0f};
-    int cur_slot = 0;
-    const auto flush = [&](int slot_) {
+        // ---- multiply: per pair, four MFMAs over the group's 128 k (lane quarter q holds k 16 q .. 16 q + 15 of each
+        // 64-k half: the same permutation on both operands), then cur += s * P; the worker's pairs run tile by tile,
+        // and each finished tile goes to its LDS slot [worker][slot][row][col] ----
+        f32x4 cur = {0.0f, 0.0f, 0.0f, 0.0f};
+        int cur_slot = 0;
+        const auto flush = [&](int slot_) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) red[(wave * kSlots + slot_) * 256 + (4 * (lane / 16) + r) * 16 + lane % 16] = cur[r];
-    };
+            for (int r = 0; r < 4; ++r) red[(wk * kSlots + slot_) * 256 + (4 * (lane / 16) + r) * 16 + lane % 16] = cur[r];
+        };
 #pragma unroll
-    for (int i = 0; i < kPairs; ++i) {
-        if (i >= n_pairs) continue;
-        const int q = q0 + i;
-        if (i > 0 && q % gpt == 0) {  // a new tile (wave-uniform)
-            flush(cur_slot);
-            ++cur_slot;
-            cur = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-        }
-        const int kofs = 128 * (q % gpt);
-        f32x4 prt = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            unsigned o[8];
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                if constexpr (XT == SEPAL_HIP_BF16) s8x4_to_bf16x4(wb[i][h][c], o[2 * c], o[2 * c + 1]);
-                else s8x4_to_f16x4(wb[i][h][c], o[2 * c], o[2 * c + 1]);
+        for (int i = 0; i < kPairs; ++i) {
+            if (i >= n_pairs) continue;
+            const int q = q0 + i;
+            if (i > 0 && q % gpt == 0) {  // a new tile (wave-uniform)
+                flush(cur_slot);
+                ++cur_slot;
+                cur = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
             }
-            const unsigned char* xr = lds + (lane % 16) * xpitch + 2 * (kofs + 64 * h + 16 * (lane / 16));
-            const u32x4 a0 = *reinterpret_cast<const u32x4*>(xr);
-            const u32x4 a1 = *reinterpret_cast<const u32x4*>(xr + 16);
-            prt = mfma16(XT, a0, u32x4{o[0], o[1], o[2], o[3]}, prt);
-            prt = mfma16(XT, a1, u32x4{o[4], o[5], o[6], o[7]}, prt);
-        }
+            const float sc = scl[((first_tile + pslot[i]) * 16 + lane % 16) * gpt + (pg[i] - g_lo)];
+            const int kofs = 128 * (q % gpt);
+            f32x4 prt = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int r = 0; r < 4; ++r) cur[r] = __builtin_fmaf(prt[r], sc[i], cur[r]);
+            for (int h = 0; h < 2; ++h) {
+                unsigned o[8];
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    if constexpr (XT == SEPAL_HIP_BF16) s8x4_to_bf16x4(wb[i][h][c], o[2 * c], o[2 * c + 1]);
+                    else s8x4_to_f16x4(wb[i][h][c], o[2 * c], o[2 * c + 1]);
+                }
+                const unsigned char* xr = lds + (lane % 16) * xpitch + 2 * (kofs + 64 * h + 16 * (lane / 16));
+                const u32x4 a0 = *reinterpret_cast<const u32x4*>(xr);
+                const u32x4 a1 = *reinterpret_cast<const u32x4*>(xr + 16);
+                prt = mfma16(XT, a0, u32x4{o[0], o[1], o[2], o[3]}, prt);
+                prt = mfma16(XT, a1, u32x4{o[4], o[5], o[6], o[7]}, prt);
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) cur[r] = __builtin_fmaf(prt[r], sc, cur[r]);
+        }
+        if (n_pairs > 0) flush(cur_slot);
     }
-    if (n_pairs > 0) flush(cur_slot);
 
-    // ---- per block-local tile: the waves that cover it, q / per over the tile's pairs; per wave: its first tile ----
-    __shared__ int cover_lo[kWaves], cover_hi[kWaves], wave_first[kWaves];
+    // ---- per block-local tile: the workers that cover it, q / per over the tile's pairs; per worker: its first tile ----
+    __shared__ int cover_lo[kWaves], cover_hi[kWaves], worker_first[kWorkers];
     if (tid < ntiles) {
         cover_lo[tid] = tid * gpt / per;
         cover_hi[tid] = ((tid + 1) * gpt - 1) / per;
     }
-    if (tid < kWaves) wave_first[tid] = min(tid * per, total - 1) / gpt;
+    if (tid < kWorkers) worker_first[tid] = min(tid * per, total - 1) / gpt;
     __syncthreads();
-    // the tile's sum in wave order; tile tl sits in slot tl - (first tile of w) of wave w
+    // the tile's sum in worker order; tile tl sits in slot tl - (first tile of w) of worker w
     const auto sum_tile = [&](int tl, int e) {
         const int lo = cover_lo[tl], hi = cover_hi[tl];
-        float v = red[(lo * kSlots + (tl - wave_first[lo])) * 256 + e];
-        for (int w = lo + 1; w <= hi; ++w) v = __fadd_rn(v, red[(w * kSlots + (tl - wave_first[w])) * 256 + e]);
+        float v = red[(lo * kSlots + (tl - worker_first[lo])) * 256 + e];
+        for (int w = lo + 1; w <= hi; ++w) v = __fadd_rn(v, red[(w * kSlots + (tl - worker_first[w])) * 256 + e]);
         return v;
     };
     if constexpr (SWIGLU) {
@@ -292,8 +317,8 @@ int device_cus() {
 }
 
 std::size_t pass_lds(std::size_t kw) {
-    return 16 * (2 * kw + 16) + static_cast<std::size_t>(stack::kWaves) * stack::kSlots * 256 * sizeof(float) +
-           static_cast<std::size_t>(stack::kWaves) * stack::kPairs * 16 * sizeof(float);
+    return 16 * (2 * kw + 16) + static_cast<std::size_t>(stack::kWorkers) * stack::kSlots * 256 * sizeof(float) +
+           static_cast<std::size_t>(stack::kWorkers) * stack::kPairs * 16 * sizeof(float);
 }
 
 template <typename Kernel>
@@ -310,7 +335,7 @@ void raise_lds(Kernel kernel, std::size_t lds, std::size_t& raised) {
 
 bool small_stack_plan(std::size_t t, std::size_t hidden, std::size_t inter, SmallStackPlan& plan) {
     constexpr std::size_t kLds = 160u << 10;
-    constexpr int kMaxPairs = stack::kWaves * stack::kPairs;    // pairs of one block
+    constexpr int kMaxPairs = stack::kWorkers * stack::kPairs;  // pairs of one block
     constexpr std::size_t kMaxK = stack::kXChunks * stack::kThreads * 16 / (16 * 2);  // staged X columns
     if (t == 0 || t > 16 || hidden % 128 != 0 || inter % 128 != 0) return false;
     const int g = device_cus();
