@@ -71,6 +71,27 @@ def test_q8_and_quantizer_refusals():
     assert L.sepal_hip_q8_group_sums(FAKE, 256, FAKE, 256, FAKE, 0, 128, 256, None) == sm.OK
 
 
+def test_fused_producer_refusals():
+    L = sm.library()
+    # RMSNorm -> int8: block must be 128 or cols; cols a multiple of 128; misaligned q; eps positive
+    assert L.sepal_hip_rmsnorm_quantize_rows(FAKE, 256, None, None, 0, FAKE, 256, FAKE, 2, 3, 256, 64, 1e-6, None) == sm.EINVAL
+    assert "block" in _err()
+    assert L.sepal_hip_rmsnorm_quantize_rows(FAKE, 208, None, None, 0, FAKE, 208, FAKE, 2, 3, 208, 208, 1e-6, None) == sm.EINVAL
+    assert L.sepal_hip_rmsnorm_quantize_rows(FAKE, 256, None, None, 0, FAKE + 4, 256, FAKE, 2, 3, 256, 128, 1e-6, None) == sm.EINVAL
+    assert L.sepal_hip_rmsnorm_quantize_rows(FAKE, 256, None, None, 0, FAKE, 256, FAKE, 2, 3, 256, 128, 0.0, None) == sm.EINVAL
+    assert L.sepal_hip_rmsnorm_quantize_rows(FAKE, 256, None, None, 0, FAKE, 256, FAKE, 2, 0, 256, 128, 1e-6, None) == sm.OK
+    # SwiGLU -> int8: N a multiple of 256, output scales present, act_block 128 or K
+    assert L.sepal_hip_gemm_q8_swiglu_quantize(FAKE, 256, FAKE, 2, 128, FAKE, 256, FAKE, 2, FAKE, 64, FAKE, 1, 4, 128,
+                                               256, -1, None) == sm.EINVAL
+    assert "multiple of 256" in _err()
+    assert L.sepal_hip_gemm_q8_swiglu_quantize(FAKE, 256, FAKE, 2, 128, FAKE, 256, FAKE, 2, FAKE, 128, None, 1, 4, 256,
+                                               256, -1, None) == sm.EINVAL
+    assert L.sepal_hip_gemm_q8_swiglu_quantize(FAKE, 256, FAKE, 2, 64, FAKE, 256, FAKE, 2, FAKE, 128, FAKE, 1, 4, 256,
+                                               256, -1, None) == sm.EINVAL
+    assert L.sepal_hip_gemm_q8_swiglu_quantize(FAKE, 256, FAKE, 2, 128, FAKE, 256, FAKE, 2, FAKE, 128, FAKE, 1, 0, 256,
+                                               256, -1, None) == sm.OK
+
+
 def test_python_front_end_raises_value_error():
     with pytest.raises(sm.SepalHipInvalid):
         sm._check(sm.EINVAL)
