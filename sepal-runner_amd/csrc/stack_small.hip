@@ -6,7 +6,9 @@
 //          and the 8 up rows of the same features) over the full K, 4 or 5 tiles per CU at the model's shape. The X
 //          rows and the block's scales are staged once per block in LDS by 4 loader waves while the 12 worker waves
 //          already have every weight load of their pairs in flight; the block's (tile, group) pairs are split evenly
-//          over the workers, and their partial tiles are added in LDS in worker order, then SwiGLU.
+//          over the workers, and their partial tiles are added in LDS in worker order, then SwiGLU. Weight loads take
+//          whole 128-byte lines (8 rows per instruction) and pass through a per-worker LDS transpose into the MFMA
+//          layout.
 //   parts  (down): the (K-part, column tile) units are dealt out evenly to the blocks, K-part major so that a
 //          block's units share one slice of H; each unit's sum is written to a partial buffer P[part][row][col].
 //   finish: one block per row adds the K-parts in order (y, float32), then runs the cpu-q8 RMSNorm on it with the
@@ -85,6 +87,7 @@ __global__ void __launch_bounds__(kThreads) pass_kernel(const PassParams p) {
     const int xpitch = 2 * kw + 16;           // bytes per staged row (padded: an operand read's 16 rows hit distinct banks)
     float* red = reinterpret_cast<float*>(lds + 16 * xpitch);  // [kWorkers][kSlots][16 x 16]
     float* scl = red + kWorkers * kSlots * 256;                 // [block tile][16 rows][gpt] scales
+    unsigned char* tbuf = reinterpret_cast<unsigned char*>(scl + kWorkers * kPairs * 16);  // [worker][2 KB] transposes
     // the block's (tile, group) pairs, tile major, dealt to the workers in runs of `per` (the last may get none)
     const int total = ntiles * gpt;
     const int per = (total + kWorkers - 1) / kWorkers;
@@ -134,12 +137,15 @@ __global__ void __launch_bounds__(kThreads) pass_kernel(const PassParams p) {
         // ---- every weight load of this worker's pairs at once (clamped, unconditional). The pairs touch at most
         // kSlots consecutive tiles; their row pointers are formed once, and the (tile, group) walk is wave-uniform;
         // past the worker's share it stays on its last pair (the same addresses again, never multiplied). ----
+        // A pair's weights are 16 rows x 128 bytes, loaded as two instructions of 8 rows x 128 bytes (whole cache
+        // lines: lane l takes row l / 8 and 16-byte chunk l % 8); the second 8 rows are kRowStep rows past the first.
+        constexpr int kRowStep = SWIGLU ? 64 : 8;
         const signed char* wrow[kSlots];
 #pragma unroll
         for (int j = 0; j < kSlots; ++j) {
             const int tile = tile0 + min(first_tile + j, ntiles - 1);
-            const std::size_t row = static_cast<std::size_t>(min(tile_row<SWIGLU>(tile, lane % 16), p.n - 1));  // past N: never stored
-            wrow[j] = p.w + row * p.ld_w + 16 * (lane / 16);
+            const std::size_t row = static_cast<std::size_t>(tile_row<SWIGLU>(tile, lane / 8));  // the plan keeps rows < N
+            wrow[j] = p.w + row * p.ld_w + 16 * (lane % 8);
         }
         u32x4 wb[kPairs][2];
         int pslot[kPairs], pg[kPairs];
@@ -153,7 +159,7 @@ __global__ void __launch_bounds__(kThreads) pass_kernel(const PassParams p) {
                 for (int j = 1; j < kSlots; ++j)
                     if (slot == j) src = wrow[j] + 128 * g;
                 wb[i][0] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src));
-                wb[i][1] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + 64));
+                wb[i][1] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + kRowStep * p.ld_w));
                 pslot[i] = slot;
                 pg[i] = g;
                 if (q0 + i + 1 < q1) {
@@ -168,9 +174,14 @@ __global__ void __launch_bounds__(kThreads) pass_kernel(const PassParams p) {
         while (__hip_atomic_load(&ready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < static_cast<unsigned>(kLoaders))
             __builtin_amdgcn_s_sleep(1);
 
-        // ---- multiply: per pair, four MFMAs over the group's 128 k (lane quarter q holds k 16 q .. 16 q + 15 of each
-        // 64-k half: the same permutation on both operands), then cur += s * P; the worker's pairs run tile by tile,
-        // and each finished tile goes to its LDS slot [worker][slot][row][col] ----
+        // ---- multiply: per pair, the weights pass through this worker's 2 KB of LDS into the MFMA layout (row r's
+        // chunk c at r * 128 + ((c + r / 2) % 8) * 16: the writes and the reads hit 16 bank groups per 16 lanes), then
+        // four MFMAs over the group's 128 k (lane quarter q holds k 16 q .. 16 q + 15 of each 64-k half: the same
+        // permutation on both operands), then cur += s * P; the worker's pairs run tile by tile, and each finished tile
+        // goes to its LDS slot [worker][slot][row][col] ----
+        unsigned char* tb = tbuf + wk * 2048;
+        const int wr_lo = (lane / 8) * 128 + ((lane % 8 + lane / 16) % 8) * 16;  // rows 0..7 (r / 2 = lane / 16)
+        const int wr_hi = (8 + lane / 8) * 128 + ((lane % 8 + 4 + lane / 16) % 8) * 16;  // rows 8..15
         f32x4 cur = {0.0f, 0.0f, 0.0f, 0.0f};
         int cur_slot = 0;
         const auto flush = [&](int slot_) {
@@ -189,13 +200,17 @@ __global__ void __launch_bounds__(kThreads) pass_kernel(const PassParams p) {
             const float sc = scl[((first_tile + pslot[i]) * 16 + lane % 16) * gpt + (pg[i] - g_lo)];
             const int kofs = 128 * (q % gpt);
             f32x4 prt = {0.0f, 0.0f, 0.0f, 0.0f};
+            *reinterpret_cast<u32x4*>(tb + wr_lo) = wb[i][0];
+            *reinterpret_cast<u32x4*>(tb + wr_hi) = wb[i][1];
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
+                const int rr = lane % 16, cc = 4 * h + lane / 16;
+                const u32x4 wv = *reinterpret_cast<const u32x4*>(tb + rr * 128 + ((cc + rr / 2) % 8) * 16);
                 unsigned o[8];
 #pragma unroll
                 for (int c = 0; c < 4; ++c) {
-                    if constexpr (XT == SEPAL_HIP_BF16) s8x4_to_bf16x4(wb[i][h][c], o[2 * c], o[2 * c + 1]);
-                    else s8x4_to_f16x4(wb[i][h][c], o[2 * c], o[2 * c + 1]);
+                    if constexpr (XT == SEPAL_HIP_BF16) s8x4_to_bf16x4(wv[c], o[2 * c], o[2 * c + 1]);
+                    else s8x4_to_f16x4(wv[c], o[2 * c], o[2 * c + 1]);
                 }
                 const unsigned char* xr = lds + (lane % 16) * xpitch + 2 * (kofs + 64 * h + 16 * (lane / 16));
                 const u32x4 a0 = *reinterpret_cast<const u32x4*>(xr);
@@ -318,7 +333,8 @@ int device_cus() {
 
 std::size_t pass_lds(std::size_t kw) {
     return 16 * (2 * kw + 16) + static_cast<std::size_t>(stack::kWorkers) * stack::kSlots * 256 * sizeof(float) +
-           static_cast<std::size_t>(stack::kWorkers) * stack::kPairs * 16 * sizeof(float);
+           static_cast<std::size_t>(stack::kWorkers) * stack::kPairs * 16 * sizeof(float) +
+           static_cast<std::size_t>(stack::kWorkers) * 2048;
 }
 
 template <typename Kernel>
