@@ -361,8 +361,8 @@ bool small_stack_plan(std::size_t t, std::size_t hidden, std::size_t inter, Smal
     const int tiles = static_cast<int>(inter / 8);
     const int per_a = (tiles + g - 1) / g;
     if (gh < 4 || per_a > stack::kWaves || per_a * gh > kMaxPairs || hidden > kMaxK || pass_lds(hidden) > kLds) return false;
-    // down: K-parts x blocks of column tiles, at most one block per CU, the fewest pairs per block (then the fewest
-    // parts); every part has >= 4 groups
+    // down: K-parts x blocks of column tiles, at most one block per CU, the fewest pairs per block plus two per part
+    // (each part is read back by the finish pass); every part has >= 4 groups
     const int ntile = static_cast<int>((hidden + 15) / 16);
     int best_kp = 0, best_pb = 0, best_cost = 0;
     for (int kp = 1; kp <= stack::kFinishParts && gi / kp >= 4; ++kp) {
@@ -372,7 +372,7 @@ bool small_stack_plan(std::size_t t, std::size_t hidden, std::size_t inter, Smal
             const int blocks = kp * ((ntile + pb - 1) / pb);
             if (blocks > g) continue;
             if (pb * gpt > kMaxPairs || pb > stack::kWaves) break;
-            const int cost = pb * gpt;
+            const int cost = pb * gpt + 2 * kp;  // the pairs of a block, plus the finish pass's reads of the parts
             if (best_kp == 0 || cost < best_cost) {
                 best_kp = kp;
                 best_pb = pb;
