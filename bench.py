@@ -273,6 +273,29 @@ def main():
         log(f"packer: {ms_pk * 1e3:.1f} us, {gbs_pk:.0f} GB/s")
         extra["packer_fp16_9728x2560"] = {"us": round(ms_pk * 1e3, 2), "gbs": round(gbs_pk, 1),
                                           "frac_hbm": round(gbs_pk / PEAK["hbm_gbs"], 4), "bytes": PACKER_BYTES}
+        # ---- the packed-weight file of that matrix: fingerprint of the fp16 source, save, load (host file system,
+        # page cache warm after the save), against packing it again ----
+        import tempfile
+        ms_fp = timed(torch, lambda: sm.weight_fingerprint(src), 5, 1, stream)
+        src_fp = sm.weight_fingerprint(src)
+        tmpd = tempfile.mkdtemp(prefix="spw_")
+        path = os.path.join(tmpd, "down.spw")
+        t0 = time.time()
+        sm.packed_save(path, qb, sb, src_fp)
+        ms_save = (time.time() - t0) * 1e3
+        q2, s2 = torch.empty_like(qb), torch.empty_like(sb)
+        sm.packed_load(path, q2, s2, src_fp)
+        t0 = time.time()
+        for _ in range(3):
+            assert sm.packed_load(path, q2, s2, src_fp)
+        ms_load = (time.time() - t0) * 1e3 / 3
+        os.remove(path)
+        os.rmdir(tmpd)
+        file_bytes = 64 + I * H + I * (H // 128) * 4
+        extra["packed_file_9728x2560"] = {"fingerprint_ms": round(ms_fp, 3), "save_ms": round(ms_save, 1),
+                                          "load_ms": round(ms_load, 1), "load_gbs": round(file_bytes / (ms_load * 1e-3) / 1e9, 2),
+                                          "bytes": file_bytes, "repack_us": round(ms_pk * 1e3, 2)}
+        log(f"packed file: fingerprint {ms_fp:.3f} ms, save {ms_save:.1f} ms, load {ms_load:.1f} ms")
         del layers, hbuf
         torch.cuda.empty_cache()
         # ---- C4: the q8w stack, per-token activation scales, outliers ----
@@ -307,6 +330,24 @@ def main():
         extra["c5_q8w_m16"] = {"ms_per_pass": round(ms_c4_16, 4), "gbs": round(gbs_q16, 1),
                                "frac_hbm": round(gbs_q16 / PEAK["hbm_gbs"], 4)}
         log(f"C5 q8w M=16 stack: {ms_c4_16:.3f} ms/pass, {gbs_q16:.0f} GB/s")
+        del qlayers
+        torch.cuda.empty_cache()
+        # ---- the model's other int8 weight groups (dn_in / attn_in [12288 or 10240, 2560], attn_out [2560, 4096]):
+        # the same w8g kernels, one Store multiply each at M = 15872 ----
+        others = {}
+        g2 = torch.Generator(device="cuda").manual_seed(11)
+        for n_o, k_o in ((12288, 2560), (10240, 2560), (2560, 4096)):
+            w_o = (torch.randn(n_o, k_o, generator=g2, device="cuda") * 0.02).half()
+            q_o, s_o = sm.quantize_group_s8(w_o)
+            x_o = torch.randn(M_BIG, k_o, generator=g2, device="cuda").bfloat16()
+            y_o = torch.empty(M_BIG, n_o, dtype=torch.float32, device="cuda")
+            ms_o = timed(torch, lambda: sm.gemm_w8g(x_o, q_o, s_o, y=y_o), 10, 2, stream)
+            tf_o = 2.0 * M_BIG * n_o * k_o / (ms_o * 1e-3) / 1e12
+            others[f"{n_o}x{k_o}"] = {"ms": round(ms_o, 4), "tflops": round(tf_o, 1),
+                                      "frac_bf16_peak": round(tf_o / PEAK["bf16_tflops"], 4)}
+            del w_o, q_o, s_o, x_o, y_o
+        extra["other_groups_w8g_m15872"] = others
+        log(f"other int8 groups (w8g, M=15872): {others}")
 
     cpu = None
     if not args.no_cpu:

@@ -33,6 +33,12 @@ int32_t guarded(F&& f) {
     } catch (const std::bad_alloc& e) {
         g_error = std::string("out of memory: ") + e.what();
         return SEPAL_HIP_ENOMEM;
+    } catch (const IoError& e) {
+        g_error = e.what();
+        return SEPAL_HIP_EIO;
+    } catch (const StaleError& e) {
+        g_error = e.what();
+        return SEPAL_HIP_ESTALE;
     } catch (const std::exception& e) {
         g_error = e.what();
         return SEPAL_HIP_ELAUNCH;
@@ -340,6 +346,49 @@ int32_t sepal_hip_float_to_bf16(const float* src, uint16_t* dst, size_t count, v
         if (count == 0) return;
         require(src != nullptr && dst != nullptr, "float_to_bf16: null pointer");
         launch_f32_to_bf16(src, dst, count, as_stream(stream));
+    });
+}
+
+int32_t sepal_hip_weight_fingerprint(const void* data, size_t bytes, uint64_t* out, void* stream) {
+    return guarded([&] {
+        require(data != nullptr && out != nullptr, "weight_fingerprint: null pointer");
+        require(aligned8(data), "weight_fingerprint: data must be 8-byte aligned");
+        const hipStream_t st = as_stream(stream);
+        char* ws = static_cast<char*>(workspace(kScratchOffset + fingerprint_scratch_bytes(), st));
+        launch_fingerprint(data, bytes, out, ws + kScratchOffset, st);
+    });
+}
+
+namespace {
+void check_packed(const char* who, const char* path, const void* q, std::size_t ld_q, const void* s, std::size_t ld_s,
+                  std::size_t rows, std::size_t k, int32_t rule, int32_t layout) {
+    const std::string w = who;
+    require(path != nullptr && q != nullptr && s != nullptr, w + ": null pointer");
+    require(rows != 0 && k != 0 && k % 128 == 0, w + ": rows must be non-zero and k a non-zero multiple of 128");
+    require(ld_q == k && ld_s == k / 128, w + ": q and s must be contiguous (ld_q = k, ld_s = k / 128)");
+    require(rule == SEPAL_HIP_RULE_DIVIDE || rule == SEPAL_HIP_RULE_RECIPROCAL, w + ": unknown quantizer rule");
+    require(layout == 0 || (layout == 1 && rows % 128 == 0), w + ": layout must be 0 (plain rows) or 1 (gate/up interleave, rows a multiple of 128)");
+    require(aligned8(q) && aligned8(s), w + ": q and s must be 8-byte aligned");
+}
+} // namespace
+
+int32_t sepal_hip_packed_save(const char* path, const int8_t* q, size_t ld_q, const float* s, size_t ld_s, size_t rows,
+                              size_t k, int32_t rule, int32_t layout, uint64_t source_fp, void* stream) {
+    return guarded([&] {
+        check_packed("packed_save", path, q, ld_q, s, ld_s, rows, k, rule, layout);
+        const hipStream_t st = as_stream(stream);
+        char* ws = static_cast<char*>(workspace(kScratchOffset + fingerprint_scratch_bytes(), st));
+        packed_save(path, q, ld_q, s, ld_s, rows, k, rule, layout, source_fp, ws + kScratchOffset, st);
+    });
+}
+
+int32_t sepal_hip_packed_load(const char* path, int8_t* q, size_t ld_q, float* s, size_t ld_s, size_t rows, size_t k,
+                              int32_t rule, int32_t layout, uint64_t source_fp, void* stream) {
+    return guarded([&] {
+        check_packed("packed_load", path, q, ld_q, s, ld_s, rows, k, rule, layout);
+        const hipStream_t st = as_stream(stream);
+        char* ws = static_cast<char*>(workspace(kScratchOffset + fingerprint_scratch_bytes(), st));
+        packed_load(path, q, ld_q, s, ld_s, rows, k, rule, layout, source_fp, ws + kScratchOffset, st);
     });
 }
 

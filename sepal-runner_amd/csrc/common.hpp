@@ -20,6 +20,12 @@ struct InvalidArgument : std::invalid_argument {
 struct LaunchError : std::runtime_error {
     using std::runtime_error::runtime_error;
 };
+struct IoError : std::runtime_error {      // a packed-weight file cannot be opened, read or written, or is corrupt
+    using std::runtime_error::runtime_error;
+};
+struct StaleError : std::runtime_error {   // a packed-weight file holds other weights (shape, rule, layout, source)
+    using std::runtime_error::runtime_error;
+};
 
 inline void check_launch(const char* what) {
     const hipError_t e = hipGetLastError();
@@ -31,6 +37,7 @@ inline void require(bool ok, const std::string& message) {
 }
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<std::uintptr_t>(p) & 15u) == 0; }
+inline bool aligned8(const void* p) { return (reinterpret_cast<std::uintptr_t>(p) & 7u) == 0; }
 
 // ---- vector types of the MFMA builtins ------------------------------------------------------------------------------
 

@@ -55,6 +55,16 @@ void launch_rmsnorm_quantize(const float* x, std::size_t ld_x, std::uint16_t* y_
                              std::size_t cols, std::size_t block, double eps, hipStream_t stream);
 void launch_f32_to_bf16(const float* src, std::uint16_t* dst, std::size_t count, hipStream_t stream);
 
+// Packed-weight files (packed_file.hip): the device fingerprint of a byte range (`lanes` holds
+// fingerprint_scratch_bytes()), and the synchronous save / load of one packed matrix.
+void launch_fingerprint(const void* data, std::size_t bytes, std::uint64_t* out, void* lanes, hipStream_t stream);
+std::size_t fingerprint_scratch_bytes();
+void packed_save(const char* path, const std::int8_t* q, std::size_t ld_q, const float* s, std::size_t ld_s,
+                 std::size_t rows, std::size_t k, int rule, int layout, std::uint64_t source_fp, void* scratch,
+                 hipStream_t stream);
+void packed_load(const char* path, std::int8_t* q, std::size_t ld_q, float* s, std::size_t ld_s, std::size_t rows,
+                 std::size_t k, int rule, int layout, std::uint64_t source_fp, void* scratch, hipStream_t stream);
+
 // The M <= 16 w8g layer of the MLP stack (stack_small.hip): a launch plan for one shape and device, and one layer.
 struct SmallStackPlan {
     int blocks;           // blocks of the gate/up pass grid (one per CU)

@@ -18,7 +18,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libsepal_mlp_hip.so")
 HEADER = os.path.join(os.path.dirname(os.path.dirname(HERE)), "include", "sepal_mlp_hip.h")
 
-OK, EINVAL, ELAUNCH, ENOMEM = 0, 1, 2, 3
+OK, EINVAL, ELAUNCH, ENOMEM, EIO, ESTALE = 0, 1, 2, 3, 4, 5
 F32, BF16, F16 = 0, 1, 2
 STORE, ADD, SWIGLU = 0, 1, 2
 RULE_DIVIDE, RULE_RECIPROCAL = 0, 1
@@ -55,13 +55,18 @@ def library() -> C.CDLL:
         L.sepal_hip_rmsnorm_rows.argtypes = [vp, sz, vp, i32, sz, vp, sz, sz, d, vp]
         L.sepal_hip_float_to_bf16.argtypes = [vp, vp, sz, vp]
         L.sepal_hip_rmsnorm_quantize_rows.argtypes = [vp, sz, vp, vp, sz, vp, sz, vp, sz, sz, sz, sz, d, vp]
+        u64 = C.c_uint64
+        L.sepal_hip_weight_fingerprint.argtypes = [vp, sz, vp, vp]
+        L.sepal_hip_packed_save.argtypes = [C.c_char_p, vp, sz, vp, sz, sz, sz, i32, i32, u64, vp]
+        L.sepal_hip_packed_load.argtypes = [C.c_char_p, vp, sz, vp, sz, sz, sz, i32, i32, u64, vp]
         L.sepal_hip_gemm_q8_swiglu_quantize.argtypes = [vp, sz, vp, sz, sz, vp, sz, vp, sz, vp, sz, vp, sz, sz, sz, sz,
                                                         i32, vp]
         L.sepal_hip_mlp_stack.argtypes = [i32, sz, sz, sz, sz, vp, vp, vp, vp, vp, vp, sz, d, vp]
         for name in ("sepal_hip_quantize_group_s8", "sepal_hip_quantize_gate_up_s8", "sepal_hip_gemm_w8g",
                      "sepal_hip_quantize_rows_s8", "sepal_hip_gemm_q8", "sepal_hip_q8_group_sums",
                      "sepal_hip_rmsnorm_rows", "sepal_hip_float_to_bf16", "sepal_hip_mlp_stack",
-                     "sepal_hip_rmsnorm_quantize_rows", "sepal_hip_gemm_q8_swiglu_quantize"):
+                     "sepal_hip_rmsnorm_quantize_rows", "sepal_hip_gemm_q8_swiglu_quantize",
+                     "sepal_hip_weight_fingerprint", "sepal_hip_packed_save", "sepal_hip_packed_load"):
             getattr(L, name).restype = i32
         L.sepal_hip_gemm_w8g_supports.restype = i32
         _lib = L
@@ -81,6 +86,8 @@ def _check(rc: int) -> None:
     msg = library().sepal_hip_last_error().decode()
     if rc == EINVAL:
         raise SepalHipInvalid(msg)
+    if rc == EIO:
+        raise OSError(msg)
     raise SepalHipError(msg)
 
 
@@ -226,6 +233,32 @@ def rmsnorm_quantize_rows(x, block: int = 128, w1=None, eps: float = 1e-6, with_
                                                      _ptr(q), _ld(q), _ptr(sc), _ld(sc), rows, cols, block, eps,
                                                      _stream(stream)))
     return (q, sc, y) if with_bf16 else (q, sc)
+
+
+def weight_fingerprint(t, stream=None) -> int:
+    """64-bit fingerprint of a device tensor's bytes (waits for the stream)."""
+    torch = _torch()
+    out = torch.zeros(1, dtype=torch.int64, device=t.device)
+    _check(library().sepal_hip_weight_fingerprint(_ptr(t), t.numel() * t.element_size(), _ptr(out), _stream(stream)))
+    return int(out.cpu().view(torch.int64).item()) & 0xFFFFFFFFFFFFFFFF
+
+
+def packed_save(path: str, q, s, source_fp: int, rule: int = RULE_DIVIDE, layout: int = 0, stream=None) -> None:
+    """Write one packed matrix (q int8 [rows, k], s float32 [rows, k/128]) with the source weights' fingerprint."""
+    rows, k = q.shape
+    _check(library().sepal_hip_packed_save(path.encode(), _ptr(q), _ld(q), _ptr(s), _ld(s), rows, k, rule, layout,
+                                           source_fp, _stream(stream)))
+
+
+def packed_load(path: str, q, s, source_fp: int, rule: int = RULE_DIVIDE, layout: int = 0, stream=None) -> bool:
+    """Fill q and s from a packed-weight file; False when the file holds other weights (then pack instead)."""
+    rows, k = q.shape
+    rc = library().sepal_hip_packed_load(path.encode(), _ptr(q), _ld(q), _ptr(s), _ld(s), rows, k, rule, layout,
+                                         source_fp, _stream(stream))
+    if rc == ESTALE:
+        return False
+    _check(rc)
+    return True
 
 
 def float_to_bf16(x, stream=None):

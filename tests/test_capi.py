@@ -92,6 +92,18 @@ def test_fused_producer_refusals():
                                                256, -1, None) == sm.OK
 
 
+def test_packed_file_refusals():
+    L = sm.library()
+    # null path, strided buffers, k not a multiple of 128, unknown rule, interleave with rows not a multiple of 128
+    assert L.sepal_hip_packed_save(None, FAKE, 256, FAKE, 2, 4, 256, 0, 0, 1, None) == sm.EINVAL
+    assert L.sepal_hip_packed_save(b"/tmp/x", FAKE, 512, FAKE, 2, 4, 256, 0, 0, 1, None) == sm.EINVAL
+    assert "contiguous" in _err()
+    assert L.sepal_hip_packed_load(b"/tmp/x", FAKE, 200, FAKE, 1, 4, 200, 0, 0, 1, None) == sm.EINVAL
+    assert L.sepal_hip_packed_load(b"/tmp/x", FAKE, 256, FAKE, 2, 4, 256, 7, 0, 1, None) == sm.EINVAL
+    assert L.sepal_hip_packed_load(b"/tmp/x", FAKE, 256, FAKE, 2, 100, 256, 0, 1, 1, None) == sm.EINVAL
+    assert L.sepal_hip_weight_fingerprint(FAKE + 4, 64, FAKE, None) == sm.EINVAL
+
+
 def test_python_front_end_raises_value_error():
     with pytest.raises(sm.SepalHipInvalid):
         sm._check(sm.EINVAL)

@@ -620,3 +620,89 @@ def test_other_weight_groups_shapes(sm, n, k, m):
         assert same_bits(yq[rows], yref)
     else:
         assert max_rel_over_rms(yq[rows], yref) < 2e-3
+
+
+# ---- packed-weight files (the cache of the load-time packer) --------------------------------------------------------
+
+_M64 = (1 << 64) - 1
+
+
+def _mix64(z):
+    z = np.asarray(z, dtype=np.uint64)
+    with np.errstate(over="ignore"):
+        z = (z ^ (z >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
+        z = (z ^ (z >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
+        return z ^ (z >> np.uint64(31))
+
+
+def _fingerprint_np(data: bytes) -> int:
+    """The fingerprint's definition restated in numpy: 8-byte little-endian words (tail zero-padded), word i folded into
+    lane i mod 65536 by splitmix64's finalizer over (word + golden * (i + 1)), the lanes folded in order in 256 runs of
+    256, the runs folded in order, then the byte count."""
+    lanes_n = 65536
+    n = len(data)
+    words = np.frombuffer(data + b"\0" * (-n % 8), dtype="<u8")
+    h = _mix64(np.arange(1, lanes_n + 1, dtype=np.uint64))
+    golden = np.uint64(0x9E3779B97F4A7C15)
+    with np.errstate(over="ignore"):
+        for r0 in range(0, len(words), lanes_n):
+            w = words[r0:r0 + lanes_n]
+            idx = np.arange(r0, r0 + len(w), dtype=np.uint64)
+            h[: len(w)] = _mix64(h[: len(w)] ^ (w + golden * (idx + np.uint64(1))))
+    part = np.zeros(256, dtype=np.uint64)
+    for t in range(256):
+        acc = np.uint64(0)
+        for j in range(256):
+            acc = _mix64(acc ^ h[t * 256 + j])
+        part[t] = acc
+    r = np.uint64(0)
+    for t in range(256):
+        r = _mix64(r ^ part[t])
+    return int(_mix64(r ^ np.uint64(n)))
+
+
+def test_weight_fingerprint_definition_and_sensitivity(sm):
+    say("weight fingerprint")
+    rng = np.random.default_rng(91)
+    raw = rng.integers(0, 256, size=(1 << 20) + 13, dtype=np.uint8)
+    t = torch.from_numpy(raw).cuda()
+    fp = sm.weight_fingerprint(t)
+    assert fp == _fingerprint_np(raw.tobytes())
+    assert sm.weight_fingerprint(t.clone()) == fp  # the bytes, not the address
+    flipped = t.clone()
+    flipped[123457] ^= 1
+    assert sm.weight_fingerprint(flipped) != fp
+    assert sm.weight_fingerprint(t[:-1]) != fp
+    small = torch.from_numpy(raw[:5].copy()).cuda()
+    assert sm.weight_fingerprint(small) == _fingerprint_np(raw[:5].tobytes())
+
+
+def test_packed_file_round_trip_and_refusals(sm, tmp_path):
+    say("packed file")
+    rng = np.random.default_rng(92)
+    inter, hidden = 256, 384
+    gate = torch.from_numpy((rng.standard_normal((inter, hidden)) * 0.02).astype(np.float16)).cuda()
+    up = torch.from_numpy((rng.standard_normal((inter, hidden)) * 0.02).astype(np.float16)).cuda()
+    q, s = sm.quantize_gate_up_s8(gate, up, rule=sm.RULE_DIVIDE)
+    src_fp = sm.weight_fingerprint(torch.cat([gate, up]))
+    path = str(tmp_path / "gate_up.spw")
+    sm.packed_save(path, q, s, src_fp, rule=sm.RULE_DIVIDE, layout=1)
+    q2, s2 = torch.empty_like(q), torch.empty_like(s)
+    assert sm.packed_load(path, q2, s2, src_fp, rule=sm.RULE_DIVIDE, layout=1)
+    assert same_bits(host(q2), host(q)) and same_bits(host(s2), host(s))
+    # other weights, rule or layout: stale (the caller packs instead)
+    assert not sm.packed_load(path, q2, s2, src_fp ^ 1, rule=sm.RULE_DIVIDE, layout=1)
+    assert not sm.packed_load(path, q2, s2, src_fp, rule=sm.RULE_RECIPROCAL, layout=1)
+    assert not sm.packed_load(path, q2, s2, src_fp, rule=sm.RULE_DIVIDE, layout=0)
+    # a corrupted payload byte and a truncated file are read errors; so is a missing file
+    data = bytearray(open(path, "rb").read())
+    data[64 + 1000] ^= 0x40
+    bad = str(tmp_path / "bad.spw")
+    open(bad, "wb").write(bytes(data))
+    with pytest.raises(OSError):
+        sm.packed_load(bad, q2, s2, src_fp, rule=sm.RULE_DIVIDE, layout=1)
+    open(bad, "wb").write(bytes(data[: len(data) // 2]))
+    with pytest.raises(OSError):
+        sm.packed_load(bad, q2, s2, src_fp, rule=sm.RULE_DIVIDE, layout=1)
+    with pytest.raises(OSError):
+        sm.packed_load(str(tmp_path / "missing.spw"), q2, s2, src_fp, rule=sm.RULE_DIVIDE, layout=1)
