@@ -177,7 +177,10 @@ SEPAL_HIP_API int32_t sepal_hip_packed_load(const char* path, int8_t* q, size_t 
  * input. Scratch (H, quantised activations, partial sums) comes from the library's per-device workspace.
  * For kind 0 with T <= 16 (and hidden <= 3072, both multiples of 128 with at least 512 for hidden) the layer runs as
  * three launches: whole-K gate/up tiles per CU, the down multiply in K-parts, and a pass that adds the parts in order
- * and applies the RMSNorm; the float32 sums there are rounded in another order than gemm_w8g's (within tolerance). */
+ * and applies the RMSNorm; the float32 sums there are rounded in another order than gemm_w8g's (within tolerance).
+ * The environment variable SEPAL_HIP_SMALL_STACK = "persistent" (or "persistent-late") runs those layers instead as one
+ * cooperative launch per 64 layers with grid barriers between the phases; same bits, slower on MI355X (the default,
+ * "layers", is the three launches). */
 SEPAL_HIP_API int32_t sepal_hip_mlp_stack(int32_t kind, size_t layers, size_t t, size_t hidden, size_t inter, void* x,
                             const int8_t* const* w_gate_up, const float* const* s_gate_up, const int8_t* const* w_down,
                             const float* const* s_down, float* y, size_t act_block, double eps, void* stream);

@@ -8,6 +8,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstring>
+#include <cstdlib>
 #include <mutex>
 #include <new>
 #include <string>
@@ -412,9 +413,21 @@ int32_t sepal_hip_mlp_stack(int32_t kind, size_t layers, size_t t, size_t hidden
         const std::size_t off_h = kScratchOffset;
         SmallStackPlan plan{};
         if (kind == 0 && small_stack_plan(t, hidden, inter, plan)) {
-            // M <= 16: three launches per layer (stack_small.hip); H binary16, the down pass's partial sums float32
+            // M <= 16 (stack_small.hip): three launches per layer, or every layer in one cooperative launch; H
+            // binary16, the down pass's partial sums float32. SEPAL_HIP_SMALL_STACK selects the form: "layers"
+            // (default, the faster), "persistent" or "persistent-late" (weights issued only once a phase has started);
+            // all three give the same bits.
             const std::size_t off_p = off_h + up256(h_bytes);
             char* wsp = static_cast<char*>(workspace(off_p + static_cast<std::size_t>(plan.parts) * t * hidden * 4, st));
+            const char* mode = std::getenv("SEPAL_HIP_SMALL_STACK");
+            const std::string m = mode != nullptr ? mode : "layers";
+            require(m == "persistent" || m == "persistent-late" || m == "layers",
+                    "mlp_stack: SEPAL_HIP_SMALL_STACK must be persistent, persistent-late or layers");
+            if (m != "layers" &&
+                launch_small_stack(plan, layers, t, hidden, inter, x, w_gate_up, s_gate_up, w_down, s_down, wsp + off_h,
+                                   reinterpret_cast<float*>(wsp + off_p), y, reinterpret_cast<unsigned*>(wsp), eps,
+                                   m == "persistent", st))
+                return;
             for (std::size_t l = 0; l < layers; ++l)
                 launch_small_layer(plan, t, hidden, inter, x, w_gate_up[l], s_gate_up[l], w_down[l], s_down[l], wsp + off_h,
                                    reinterpret_cast<float*>(wsp + off_p), y, l + 1 < layers ? x : nullptr, eps, st);

@@ -78,5 +78,12 @@ bool small_stack_plan(std::size_t t, std::size_t hidden, std::size_t inter, Smal
 void launch_small_layer(const SmallStackPlan& plan, std::size_t t, std::size_t hidden, std::size_t inter, const void* x,
                         const std::int8_t* w_gu, const float* s_gu, const std::int8_t* w_d, const float* s_d, void* h,
                         float* part, float* y, void* xn, double eps, hipStream_t stream);
+// Every layer in one cooperative launch per 64 layers (one block per CU), the same results as launch_small_layer per
+// layer. counters: the library's zero-at-rest counter words (hidden / 16 tile counters at the start, the grid barrier's
+// at word 4096). Returns false, launching nothing, when the device cannot keep the grid resident.
+bool launch_small_stack(const SmallStackPlan& plan, std::size_t layers, std::size_t t, std::size_t hidden, std::size_t inter,
+                        void* x, const std::int8_t* const* w_gu, const float* const* s_gu, const std::int8_t* const* w_d,
+                        const float* const* s_d, void* h, float* part, float* y, unsigned* counters, double eps,
+                        bool early, hipStream_t stream);
 
 } // namespace sepal::hip

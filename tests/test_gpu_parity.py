@@ -520,6 +520,29 @@ def test_mlp_stack_small_path(sm, t):
     assert max_rel_over_rms(y1, ref1) < 2e-3, max_rel_over_rms(y1, ref1)
 
 
+@pytest.mark.parametrize("t,nl,hidden,inter", [(1, 3, 512, 1024), (5, 3, 512, 1024), (16, 3, 512, 1024),
+                                                (16, 66, 512, 1024), (16, 2, 2560, 9728)])
+def test_mlp_stack_small_persistent_same_bits(sm, monkeypatch, t, nl, hidden, inter):
+    """The one-launch (cooperative, grid barriers) form of the M <= 16 stack, with the weights issued before or after
+    each phase's barrier, gives the same bits as three launches per layer: same plan, same summation orders. 66 layers
+    take two launches (64 layers each at most) with the part sum and RMSNorm between them."""
+    say("mlp stack persistent t", t, "layers", nl, "hidden", hidden, "inter", inter)
+    rng = np.random.default_rng(300 + t + nl)
+    layers = _stack_weights(sm, rng, nl, hidden, inter, rule=0)
+    x = bf16_inputs(rng, (t, hidden))
+    out = {}
+    for mode in ("layers", "persistent", "persistent-late"):
+        monkeypatch.setenv("SEPAL_HIP_SMALL_STACK", mode)
+        xt = dev(x, torch.bfloat16)
+        y = host(sm.mlp_stack(0, xt, layers))
+        out[mode] = (y, host(xt))
+    for mode in ("persistent", "persistent-late"):
+        assert same_bits(out[mode][0], out["layers"][0]), mode
+        assert same_bits(out[mode][1], out["layers"][1]), mode
+    if nl <= 3:
+        assert rel_rms(out["layers"][0], _oracle_stack(0, x, layers, 128)) < 2e-3
+
+
 def test_mlp_stack_small_path_full_size(sm):
     """The M = 16 stack at the model's shape (H 2560, I 9728), two layers, against the oracle."""
     say("mlp stack small path full size")
