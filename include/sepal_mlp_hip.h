@@ -178,6 +178,10 @@ SEPAL_HIP_API int32_t sepal_hip_packed_load(const char* path, int8_t* q, size_t 
  * For kind 0 with T <= 16 (and hidden <= 3072, both multiples of 128 with at least 512 for hidden) the layer runs as
  * three launches: whole-K gate/up tiles per CU, the down multiply in K-parts, and a pass that adds the parts in order
  * and applies the RMSNorm; the float32 sums there are rounded in another order than gemm_w8g's (within tolerance).
+ * For kind 1 with T <= 16 (same shape limits) the layer runs the same three-launch scheme on int8 MFMAs: the gate/up
+ * pass writes H in float32 (with, per token, its partial row maxima), the down pass quantizes its slice of H while
+ * staging it, and the finish pass quantizes the next layer's input; the int8 products are exact, the float sums
+ * are rounded in another order than gemm_q8's (within tolerance).
  * The environment variable SEPAL_HIP_SMALL_STACK = "persistent" (or "persistent-late") runs those layers instead as one
  * cooperative launch per 64 layers with grid barriers between the phases; same bits, slower on MI355X (the default,
  * "layers", is the three launches). */

@@ -433,6 +433,29 @@ int32_t sepal_hip_mlp_stack(int32_t kind, size_t layers, size_t t, size_t hidden
                                    reinterpret_cast<float*>(wsp + off_p), y, l + 1 < layers ? x : nullptr, eps, st);
             return;
         }
+        // (per token, the down pass reads the gate/up grid's partial row maxima: at most 256 blocks)
+        if (kind == 1 && small_stack_plan(t, hidden, inter, plan) &&
+            (act_block != 0 || (inter / 8 + plan.tiles_per_block - 1) / plan.tiles_per_block <= 256)) {
+            // M <= 16 gpu-q8w (stack_small.hip): three launches per layer on int8 MFMAs; H float32 with, per token,
+            // its partial row maxima; the down pass quantizes H while staging it; the finish pass quantizes the next
+            // layer's input
+            const bool per_token = act_block == 0;
+            const std::size_t ab = per_token ? hidden : 128;
+            const std::size_t q_h = off_h, q_hmax = q_h + up256(t * inter * 4);
+            const std::size_t q_p = q_hmax + up256(t * static_cast<std::size_t>(plan.blocks) * 4);
+            const std::size_t q_x = q_p + up256(static_cast<std::size_t>(plan.parts) * t * hidden * 4);
+            const std::size_t q_s = q_x + up256(t * hidden);
+            char* wsq = static_cast<char*>(workspace(q_s + up256(t * (hidden / ab) * 4), st));
+            auto* qx = reinterpret_cast<std::int8_t*>(wsq + q_x);
+            auto* sx = reinterpret_cast<float*>(wsq + q_s);
+            launch_quantize_rows(x, SEPAL_HIP_BF16, hidden, qx, hidden, sx, hidden / ab, t, hidden, ab, st);
+            for (std::size_t l = 0; l < layers; ++l)
+                launch_small_layer_q8(plan, t, hidden, inter, qx, sx, per_token, w_gate_up[l], s_gate_up[l], w_down[l], s_down[l],
+                                      reinterpret_cast<float*>(wsq + q_h), reinterpret_cast<float*>(wsq + q_hmax),
+                                      reinterpret_cast<float*>(wsq + q_p), y, l + 1 < layers ? qx : nullptr, sx,
+                                      l + 1 < layers ? x : nullptr, eps, st);
+            return;
+        }
         const std::size_t off_qx = off_h + up256(h_bytes);
         const std::size_t off_sx = off_qx + (kind == 1 ? up256(t * hidden) : 0);
         const std::size_t off_qh = off_sx + (kind == 1 ? up256(t * (hidden / ab_h) * 4) : 0);

@@ -78,6 +78,13 @@ bool small_stack_plan(std::size_t t, std::size_t hidden, std::size_t inter, Smal
 void launch_small_layer(const SmallStackPlan& plan, std::size_t t, std::size_t hidden, std::size_t inter, const void* x,
                         const std::int8_t* w_gu, const float* s_gu, const std::int8_t* w_d, const float* s_d, void* h,
                         float* part, float* y, void* xn, double eps, hipStream_t stream);
+// The gpu-q8w form: int8 x [t, hidden] with its scales (one per token, or per 128 columns) -> H float32 [t, inter]
+// (per token also hmax [t, ceil(inter / 8 / tiles_per_block)], the partial row maxima of |H|) -> part -> y; when xq_next is
+// set, the next layer's input bf16(RMSNorm(y)) goes to xn (bf16) and, quantized, to xq_next / xs_next.
+void launch_small_layer_q8(const SmallStackPlan& plan, std::size_t t, std::size_t hidden, std::size_t inter,
+                           const std::int8_t* xq, const float* xs, bool per_token, const std::int8_t* w_gu, const float* s_gu,
+                           const std::int8_t* w_d, const float* s_d, float* h, float* hmax, float* part, float* y,
+                           std::int8_t* xq_next, float* xs_next, void* xn, double eps, hipStream_t stream);
 // Every layer in one cooperative launch per 64 layers (one block per CU), the same results as launch_small_layer per
 // layer. counters: the library's zero-at-rest counter words (hidden / 16 tile counters at the start, the grid barrier's
 // at word 4096). Returns false, launching nothing, when the device cannot keep the grid resident.

@@ -37,8 +37,19 @@ __device__ __forceinline__ f32x4 mfma16(int xt, const u32x4 a, const u32x4 b, f3
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
 }
 
+// Activation type of the gpu-q8w stack: int8 X (and int8 H, quantized by the down pass's loaders) on int8 MFMAs.
+constexpr int kActI8 = 8;
+
+// The activation quantizer's rounding (rule RECIPROCAL: rint(v / scale) as v * (1 / scale), clamped to +-127), as
+// quantize_rows applies it (runner/src/cpu/gemm.cpp pack_acts).
+__device__ __forceinline__ int quantize_act(float v, float inverse) {
+    float r = __builtin_rintf(__fmul_rn(v, inverse));
+    r = r < -127.0f ? -127.0f : (r > 127.0f ? 127.0f : r);
+    return static_cast<int>(r);
+}
+
 struct PassParams {
-    const unsigned short* x;  // [T, ld_x] bf16 / binary16
+    const unsigned short* x;  // [T, ld_x] bf16 / binary16; q8 gate/up: int8 [T, ld_x]
     std::size_t ld_x;
     const signed char* w;     // [N, ld_w]
     std::size_t ld_w;
@@ -51,6 +62,14 @@ struct PassParams {
     int parts;                // K-parts (1 for the tiles pass)
     int per_block;            // tiles per block; a block's tiles share one K-part
     int blocks_per_part;      // ceil(tiles / per_block)
+    // q8 only
+    const float* xs;          // gate/up: X scales [T, ld_xs], one per token or per 128 columns
+    std::size_t ld_xs;
+    int per_token;            // 1: one activation scale per token; 0: one per 128 columns
+    const float* xf;          // down: H float32 [T, ld_x], quantized here
+    const float* hmax;        // down, per token: the gate/up pass's partial row maxima of |H| [T, hmax_blocks]
+    int hmax_blocks;
+    float* pmax;              // gate/up, per token: this pass's partial row maxima [T, gridDim.x]
 };
 
 // Weight row of column c (0..15) of a tile. SwiGLU tiles take 8 gate rows and the 8 up rows of the same features in the
@@ -66,6 +85,66 @@ __device__ __forceinline__ int tile_row(int tile, int c) {
 }
 
 constexpr int kXChunks = 6;  // 16-byte X chunks per lane of a staged row: 64 x 6 x 8 = 3072 columns at most
+
+// The q8 down pass's staging of H rows 4 w .. 4 w + 3 (w = loader wave), ROWS rows per round trip: NQ float4 loads
+// per lane and row cover 2 NQ blocks of 128 columns (NQ = ceil(gpt / 2) rounded up to an instantiated size).
+template <int NQ, int ROWS>
+__device__ __forceinline__ void stage_h_q8(const PassParams& p, unsigned char* lds, float* xsc, int xpitch, int g_lo, int gpt,
+                                           int wave, int lane) {
+    constexpr int kMaxPartials = 4;  // 64 lanes x 4: the gate/up grid has at most 256 blocks
+#pragma unroll 1
+    for (int rr = 0; rr < 4; rr += ROWS) {
+        float4 hv[ROWS][NQ];
+        float pm[ROWS][kMaxPartials];
+#pragma unroll
+        for (int h = 0; h < ROWS; ++h) {
+            const int rs = min(4 * wave + rr + h, p.t - 1);
+            const float* hrow = p.xf + static_cast<std::size_t>(rs) * p.ld_x + 128 * g_lo;
+#pragma unroll
+            for (int e = 0; e < NQ; ++e)
+                hv[h][e] = *reinterpret_cast<const float4*>(hrow + 128 * min(2 * e + lane / 32, gpt - 1) + 4 * (lane % 32));
+            if (p.per_token) {
+#pragma unroll
+                for (int i = 0; i < kMaxPartials; ++i)
+                    pm[h][i] = p.hmax[static_cast<std::size_t>(rs) * p.hmax_blocks + min(lane + 64 * i, p.hmax_blocks - 1)];
+            }
+        }
+#pragma unroll
+        for (int h = 0; h < ROWS; ++h) {
+            const int r = 4 * wave + rr + h;
+            float rscale = 1.0f, rinv = 1.0f;
+            if (p.per_token) {
+                float m = fmaxf(fmaxf(pm[h][0], pm[h][1]), fmaxf(pm[h][2], pm[h][3]));
+#pragma unroll
+                for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+                rscale = m > 0.0f ? __fdiv_rn(m, 127.0f) : 1.0f;
+                rinv = __fdiv_rn(1.0f, rscale);
+                if (lane == 0) xsc[r] = rscale;
+            }
+#pragma unroll
+            for (int e = 0; e < NQ; ++e) {
+                if (2 * e >= gpt) break;  // uniform
+                const int g = 2 * e + lane / 32;
+                const float v[4] = {hv[h][e].x, hv[h][e].y, hv[h][e].z, hv[h][e].w};
+                float scale = rscale, inv = rinv;
+                if (!p.per_token) {
+                    float m = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+#pragma unroll
+                    for (int o = 16; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 32));
+                    scale = m > 0.0f ? __fdiv_rn(m, 127.0f) : 1.0f;
+                    inv = __fdiv_rn(1.0f, scale);
+                }
+                unsigned packed = 0u;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) packed |= (static_cast<unsigned>(quantize_act(v[j], inv)) & 0xFFu) << (8 * j);
+                if (g < gpt) {
+                    *reinterpret_cast<unsigned*>(lds + r * xpitch + 128 * g + 4 * (lane % 32)) = packed;
+                    if (!p.per_token && lane % 32 == 0) xsc[r * gpt + g] = scale;
+                }
+            }
+        }
+    }
+}
 
 // One multiply pass over a block of weight tiles and one K-part (the gate/up pass: SWIGLU, one part covering K, the
 // output H; the down pass: several parts, the output P[part]). XT is the activation type, YT the SwiGLU output type.
@@ -86,14 +165,18 @@ __global__ void __launch_bounds__(kThreads) pass_kernel(const PassParams p) {
     const int g_lo = part * groups / p.parts, g_hi = (part + 1) * groups / p.parts;
     const int gpt = g_hi - g_lo;              // groups per tile in this part
     const int kw = 128 * gpt;                 // staged X columns [128 g_lo, 128 g_hi)
-    const int xpitch = 2 * kw + 16;           // bytes per staged row (padded: an operand read's 16 rows hit distinct banks)
+    constexpr bool Q8 = XT == kActI8;
+    const int xpitch = (Q8 ? kw : 2 * kw) + 16;  // bytes per staged row (padded: an operand read's 16 rows hit distinct banks)
     float* red = reinterpret_cast<float*>(lds + 16 * xpitch);  // [kWorkers][kSlots][16 x 16]
     float* scl = red + kWorkers * kSlots * 256;                 // [block tile][16 rows][gpt] scales
     unsigned char* tbuf = reinterpret_cast<unsigned char*>(scl + kWorkers * kPairs * 16);  // [worker][2 KB] transposes
+    float* xsc = reinterpret_cast<float*>(tbuf + kWorkers * 2048);  // q8: activation scales [16 rows][gpt] (per token [16])
     // the block's (tile, group) pairs, tile major, dealt to the workers in runs of `per` (the last may get none)
     const int total = ntiles * gpt;
     const int per = (total + kWorkers - 1) / kWorkers;
+    __shared__ unsigned row_max[16];  // q8 gate/up, per token: |H| maxima of this block's outputs (float bits)
     if (tid == 0) ready = 0u;
+    if (tid < 16) row_max[tid] = 0u;
     __syncthreads();
 
     if (wave < kLoaders) {
@@ -109,22 +192,56 @@ __global__ void __launch_bounds__(kThreads) pass_kernel(const PassParams p) {
             const int row = min(tile_row<SWIGLU>(tile0 + tl, rem / gpt), p.n - 1);
             sv[e] = p.s[static_cast<std::size_t>(row) * p.ld_s + g_lo + rem % gpt];
         }
+        if constexpr (Q8 && SWIGLU) {
+            // int8 rows: 16-byte chunks of 16 columns, and the rows' activation scales
+            const int cq = kw / 16;
 #pragma unroll
-        for (int rr = 0; rr < 4; rr += 2) {
-            u32x4 xv[2][kXChunks];
+            for (int rr = 0; rr < 4; rr += 2) {
+                u32x4 xv[2][kXChunks / 2];
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const int r = 4 * wave + rr + h;
-                const unsigned short* xrow = p.x + static_cast<std::size_t>(min(r, p.t - 1)) * p.ld_x + 128 * g_lo;
+                for (int h = 0; h < 2; ++h) {
+                    const unsigned char* xrow = reinterpret_cast<const unsigned char*>(p.x) +
+                                                static_cast<std::size_t>(min(4 * wave + rr + h, p.t - 1)) * p.ld_x + 128 * g_lo;
 #pragma unroll
-                for (int e = 0; e < kXChunks; ++e) xv[h][e] = *reinterpret_cast<const u32x4*>(xrow + 8 * min(lane + 64 * e, cpr - 1));
+                    for (int e = 0; e < kXChunks / 2; ++e)
+                        xv[h][e] = *reinterpret_cast<const u32x4*>(xrow + 16 * min(lane + 64 * e, cq - 1));
+                }
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+#pragma unroll
+                    for (int e = 0; e < kXChunks / 2; ++e)
+                        if (lane + 64 * e < cq)
+                            *reinterpret_cast<u32x4*>(lds + (4 * wave + rr + h) * xpitch + 16 * (lane + 64 * e)) = xv[h][e];
             }
-#pragma unroll
-            for (int h = 0; h < 2; ++h)
-#pragma unroll
-                for (int e = 0; e < kXChunks; ++e)
-                    if (lane + 64 * e < cpr)
-                        *reinterpret_cast<u32x4*>(lds + (4 * wave + rr + h) * xpitch + 16 * (lane + 64 * e)) = xv[h][e];
+            const int nsc = p.per_token ? 16 : 16 * gpt;
+            for (int i = lt; i < nsc; i += 64 * kLoaders) {
+                const int r = p.per_token ? i : i / gpt, j = p.per_token ? 0 : i % gpt;
+                xsc[i] = p.xs[static_cast<std::size_t>(min(r, p.t - 1)) * p.ld_xs + (p.per_token ? 0 : g_lo + j)];
+            }
+        } else if constexpr (Q8) {
+            // down: H float32 quantized as the activation quantizer does (rule RECIPROCAL, scale = max / 127): per
+            // 128-column block (lanes 0..31 one block, lanes 32..63 the next), or with the row maximum of the gate/up
+            // pass's partial maxima (per token). Up to 28 groups of a row: two rows at a time; more: one.
+            if (gpt <= 14) stage_h_q8<7, 2>(p, lds, xsc, xpitch, g_lo, gpt, wave, lane);
+            else stage_h_q8<12, 1>(p, lds, xsc, xpitch, g_lo, gpt, wave, lane);
+        } else {
+    #pragma unroll
+            for (int rr = 0; rr < 4; rr += 2) {
+                u32x4 xv[2][kXChunks];
+    #pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const int r = 4 * wave + rr + h;
+                    const unsigned short* xrow = p.x + static_cast<std::size_t>(min(r, p.t - 1)) * p.ld_x + 128 * g_lo;
+    #pragma unroll
+                    for (int e = 0; e < kXChunks; ++e) xv[h][e] = *reinterpret_cast<const u32x4*>(xrow + 8 * min(lane + 64 * e, cpr - 1));
+                }
+    #pragma unroll
+                for (int h = 0; h < 2; ++h)
+    #pragma unroll
+                    for (int e = 0; e < kXChunks; ++e)
+                        if (lane + 64 * e < cpr)
+                            *reinterpret_cast<u32x4*>(lds + (4 * wave + rr + h) * xpitch + 16 * (lane + 64 * e)) = xv[h][e];
+            }
         }
 #pragma unroll
         for (int e = 0; e < kScaleLoads; ++e)
@@ -204,6 +321,25 @@ __global__ void __launch_bounds__(kThreads) pass_kernel(const PassParams p) {
             f32x4 prt = {0.0f, 0.0f, 0.0f, 0.0f};
             *reinterpret_cast<u32x4*>(tb + wr_lo) = wb[i][0];
             *reinterpret_cast<u32x4*>(tb + wr_hi) = wb[i][1];
+            if constexpr (Q8) {
+                // the int8 weights go to the MFMA as they are: the exact int32 group sum, then the cpu-q8 float chain
+                // (runner/src/cpu/gemm_kernels_avx512.cpp:67-115): t = fma(f_g, ws_g, t) with one scale per token
+                // (applied after the sum), fma(f_g, ws_g * xs_g, t) with one per 128 columns
+                i32x4 acc = {0, 0, 0, 0};
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const int rr = lane % 16, cc = 4 * h + lane / 16;
+                    const u32x4 wv = *reinterpret_cast<const u32x4*>(tb + rr * 128 + ((cc + rr / 2) % 8) * 16);
+                    const u32x4 a = *reinterpret_cast<const u32x4*>(lds + (lane % 16) * xpitch + kofs + 64 * h + 16 * (lane / 16));
+                    acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i32x4, a), __builtin_bit_cast(i32x4, wv), acc, 0, 0, 0);
+                }
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float s_r = p.per_token ? sc : __fmul_rn(sc, xsc[(4 * (lane / 16) + r) * gpt + q % gpt]);
+                    cur[r] = __builtin_fmaf(static_cast<float>(acc[r]), s_r, cur[r]);
+                }
+                continue;
+            }
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
                 const int rr = lane % 16, cc = 4 * h + lane / 16;
@@ -241,7 +377,37 @@ __global__ void __launch_bounds__(kThreads) pass_kernel(const PassParams p) {
         for (int w = lo + 1; w <= hi; ++w) v = __fadd_rn(v, red[(w * kSlots + (tl - worker_first[w])) * 256 + e]);
         return v;
     };
-    if constexpr (SWIGLU) {
+    if constexpr (Q8 && SWIGLU) {
+        // H = swiglu_cephes(gate, up) in float32 (the gpu-q8w epilogue), and, per token, this block's row maxima of |H|
+        float* hy = static_cast<float*>(p.y);
+        for (int id = tid; id < ntiles * 16 * 8; id += kThreads) {
+            const int tl = id / 128, r = (id / 8) % 16, i = id % 8;
+            const int tile = tile0 + tl;
+            const int f = 64 * (tile / 8) + 8 * (tile % 8) + i;
+            if (r >= p.t || 2 * f >= p.n) continue;
+            float g = sum_tile(tl, r * 16 + i), u = sum_tile(tl, r * 16 + 8 + i);
+            if (p.per_token) {
+                g = __fmul_rn(g, xsc[r]);
+                u = __fmul_rn(u, xsc[r]);
+            }
+            const float hv = swiglu_cephes(g, u);
+            hy[static_cast<std::size_t>(r) * p.ld_y + f] = hv;
+            if (p.per_token) atomicMax(&row_max[r], __float_as_uint(fabsf(hv)));
+        }
+        if (p.per_token) {
+            __syncthreads();
+            if (tid < p.t) p.pmax[static_cast<std::size_t>(tid) * gridDim.x + blockIdx.x] = __uint_as_float(row_max[tid]);
+        }
+    } else if constexpr (Q8) {
+        float* y = static_cast<float*>(p.y);
+        for (int id = tid; id < ntiles * 256; id += kThreads) {
+            const int tl = id / 256, r = (id / 16) % 16, c = id % 16;
+            const int col = 16 * (tile0 + tl) + c;
+            if (r >= p.t || col >= p.n) continue;
+            const float v = sum_tile(tl, r * 16 + c);
+            y[(static_cast<std::size_t>(part) * p.t + r) * p.ld_y + col] = p.per_token ? __fmul_rn(v, xsc[r]) : v;
+        }
+    } else if constexpr (SWIGLU) {
         // output (tile, row, feature i < 8) = swiglu(col i, col 8 + i)
         for (int id = tid; id < ntiles * 16 * 8; id += kThreads) {
             const int tl = id / 128, r = (id / 8) % 16, i = id % 8;
@@ -267,8 +433,11 @@ __global__ void __launch_bounds__(kThreads) pass_kernel(const PassParams p) {
 // thread's partial loads (up to kFinishParts) are all in flight at once.
 constexpr int kFinishParts = 16;
 
+// With q set (the gpu-q8w stack), the bf16 values are also quantized as quantize_rows does (rule RECIPROCAL), with
+// one scale per row (qblock = n) or per 128 columns (qblock = 128), into q [t, n] and qs [t, n / qblock].
 __global__ void __launch_bounds__(1024) finish_kernel(const float* __restrict__ part, int parts, int t, int n, float* __restrict__ y,
-                                                      std::uint16_t* __restrict__ xn, double eps) {
+                                                      std::uint16_t* __restrict__ xn, double eps, std::int8_t* __restrict__ q,
+                                                      float* __restrict__ qs, int qblock) {
     extern __shared__ __align__(16) float row_buf[];  // [n]
     const int r = blockIdx.x, tid = threadIdx.x;
     for (int c4 = tid; c4 < n / 4; c4 += 1024) {
@@ -288,7 +457,7 @@ __global__ void __launch_bounds__(1024) finish_kernel(const float* __restrict__ 
         *reinterpret_cast<float4*>(row_buf + 4 * c4) = a;
         *reinterpret_cast<float4*>(y + static_cast<std::size_t>(r) * n + 4 * c4) = a;
     }
-    if (xn == nullptr) return;  // uniform over the block
+    if (xn == nullptr && q == nullptr) return;  // uniform over the block
     __syncthreads();
     // lanes 0..31 of wave 0 are the reference's 4 x 8 accumulator lanes: lane L adds c = L, L + 32, ..., then the
     // 8-wide tail on lanes 0..7
@@ -316,7 +485,51 @@ __global__ void __launch_bounds__(1024) finish_kernel(const float* __restrict__ 
     }
     __syncthreads();
     const float inv = inv_s;
-    for (int c = tid; c < n; c += 1024) xn[static_cast<std::size_t>(r) * n + c] = f32_to_bf16_bits(__fmul_rn(row_buf[c], inv));
+    if (xn != nullptr)
+        for (int c = tid; c < n; c += 1024) xn[static_cast<std::size_t>(r) * n + c] = f32_to_bf16_bits(__fmul_rn(row_buf[c], inv));
+    if (q == nullptr) return;
+    // the bf16-rounded values, their maxima (per row, or per 128 columns: two waves per block of 128), the int8 values
+    __shared__ float wmax[16];
+    __shared__ float rmax_s;
+    const int wave = tid / 64, lane = tid % 64;
+    if (qblock != 128) {
+        float m = 0.0f;
+        for (int c = tid; c < n; c += 1024) m = fmaxf(m, fabsf(bf16_bits_to_f32(f32_to_bf16_bits(__fmul_rn(row_buf[c], inv)))));
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+        if (lane == 0) wmax[wave] = m;
+        __syncthreads();
+        if (tid == 0) {
+            float a = wmax[0];
+            for (int w = 1; w < 16; ++w) a = fmaxf(a, wmax[w]);
+            rmax_s = a;
+        }
+        __syncthreads();
+        const float scale = rmax_s > 0.0f ? __fdiv_rn(rmax_s, 127.0f) : 1.0f;
+        const float inverse = __fdiv_rn(1.0f, scale);
+        if (tid == 0) qs[r] = scale;
+        for (int c = tid; c < n; c += 1024)
+            q[static_cast<std::size_t>(r) * n + c] =
+                static_cast<std::int8_t>(quantize_act(bf16_bits_to_f32(f32_to_bf16_bits(__fmul_rn(row_buf[c], inv))), inverse));
+        return;
+    }
+    for (int c0 = 0; c0 < n; c0 += 1024) {  // n is a multiple of 128
+        const int c = c0 + tid;
+        const float b = c < n ? bf16_bits_to_f32(f32_to_bf16_bits(__fmul_rn(row_buf[c], inv))) : 0.0f;
+        float m = fabsf(b);
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+        if (lane == 0) wmax[wave] = m;
+        __syncthreads();
+        const float bm = fmaxf(wmax[wave & ~1], wmax[wave | 1]);
+        const float scale = bm > 0.0f ? __fdiv_rn(bm, 127.0f) : 1.0f;
+        const float inverse = __fdiv_rn(1.0f, scale);
+        if (c < n) {
+            q[static_cast<std::size_t>(r) * n + c] = static_cast<std::int8_t>(quantize_act(b, inverse));
+            if (c % 128 == 0) qs[static_cast<std::size_t>(r) * (n / 128) + c / 128] = scale;
+        }
+        __syncthreads();
+    }
 }
 
 
@@ -742,10 +955,12 @@ int device_cus() {
     return cus;
 }
 
-std::size_t pass_lds(std::size_t kw) {
-    return 16 * (2 * kw + 16) + static_cast<std::size_t>(stack::kWorkers) * stack::kSlots * 256 * sizeof(float) +
+// LDS of one pass: 16 staged rows of row_bytes (+16 padding), the workers' tile slots, the block's scales, the
+// workers' transpose buffers, and the q8 activation scales (16 rows x 24 groups at most)
+std::size_t pass_lds(std::size_t row_bytes) {
+    return 16 * (row_bytes + 16) + static_cast<std::size_t>(stack::kWorkers) * stack::kSlots * 256 * sizeof(float) +
            static_cast<std::size_t>(stack::kWorkers) * stack::kPairs * 16 * sizeof(float) +
-           static_cast<std::size_t>(stack::kWorkers) * 2048;
+           static_cast<std::size_t>(stack::kWorkers) * 2048 + 16 * 24 * sizeof(float);
 }
 
 template <typename Kernel>
@@ -771,14 +986,14 @@ bool small_stack_plan(std::size_t t, std::size_t hidden, std::size_t inter, Smal
     // tile has >= 4 groups
     const int tiles = static_cast<int>(inter / 8);
     const int per_a = (tiles + g - 1) / g;
-    if (gh < 4 || per_a > stack::kWaves || per_a * gh > kMaxPairs || hidden > kMaxK || pass_lds(hidden) > kLds) return false;
+    if (gh < 4 || per_a > stack::kWaves || per_a * gh > kMaxPairs || hidden > kMaxK || pass_lds(2 * hidden) > kLds) return false;
     // down: K-parts x blocks of column tiles, at most one block per CU, the fewest pairs per block plus two per part
     // (each part is read back by the finish pass); every part has >= 4 groups
     const int ntile = static_cast<int>((hidden + 15) / 16);
     int best_kp = 0, best_pb = 0, best_cost = 0;
     for (int kp = 1; kp <= stack::kFinishParts && gi / kp >= 4; ++kp) {
         const int gpt = (gi + kp - 1) / kp;
-        if (static_cast<std::size_t>(gpt) * 128 > kMaxK || pass_lds(static_cast<std::size_t>(gpt) * 128) > kLds) continue;
+        if (static_cast<std::size_t>(gpt) * 128 > kMaxK || pass_lds(static_cast<std::size_t>(gpt) * 256) > kLds) continue;
         for (int pb = 1; pb <= ntile; ++pb) {
             const int blocks = kp * ((ntile + pb - 1) / pb);
             if (blocks > g) continue;
@@ -823,7 +1038,7 @@ void launch_small_layer(const SmallStackPlan& plan, std::size_t t, std::size_t h
     a.blocks_per_part = (a.tiles + a.per_block - 1) / a.per_block;
     const auto ka = pass_kernel<SEPAL_HIP_BF16, true, SEPAL_HIP_F16>;
     static std::size_t raised_a = 0;
-    const std::size_t lds_a = pass_lds(hidden);
+    const std::size_t lds_a = pass_lds(2 * hidden);
     raise_lds(ka, lds_a, raised_a);
     ka<<<dim3(a.blocks_per_part), dim3(kThreads), lds_a, stream>>>(a);
     check_launch("small-M stack gate/up launch");
@@ -847,16 +1062,83 @@ void launch_small_layer(const SmallStackPlan& plan, std::size_t t, std::size_t h
     const auto kd = pass_kernel<SEPAL_HIP_F16, false, SEPAL_HIP_F32>;
     static std::size_t raised_d = 0;
     const std::size_t gpt = (inter / 128 + plan.parts - 1) / plan.parts;
-    const std::size_t lds_d = pass_lds(gpt * 128);
+    const std::size_t lds_d = pass_lds(gpt * 256);
     raise_lds(kd, lds_d, raised_d);
     kd<<<dim3(d.parts * d.blocks_per_part), dim3(kThreads), lds_d, stream>>>(d);
     check_launch("small-M stack down launch");
     // y = sum of the parts; next layer's input
     finish_kernel<<<dim3(static_cast<unsigned>(t)), dim3(1024), hidden * sizeof(float), stream>>>(
-        part, plan.parts, static_cast<int>(t), static_cast<int>(hidden), y, static_cast<std::uint16_t*>(xn), eps);
+        part, plan.parts, static_cast<int>(t), static_cast<int>(hidden), y, static_cast<std::uint16_t*>(xn), eps, nullptr,
+        nullptr, 0);
     check_launch("small-M stack finish launch");
 }
 
+
+void launch_small_layer_q8(const SmallStackPlan& plan, std::size_t t, std::size_t hidden, std::size_t inter,
+                           const std::int8_t* xq, const float* xs, bool per_token, const std::int8_t* w_gu, const float* s_gu,
+                           const std::int8_t* w_d, const float* s_d, float* h, float* hmax, float* part, float* y,
+                           std::int8_t* xq_next, float* xs_next, void* xn, double eps, hipStream_t stream) {
+    using namespace stack;
+    // gate/up: int8 X [t, hidden] (+ scales) -> H float32 [t, inter] (+ per token: partial row maxima of |H|)
+    PassParams a{};
+    a.x = reinterpret_cast<const unsigned short*>(xq);
+    a.ld_x = hidden;  // bytes
+    a.w = reinterpret_cast<const signed char*>(w_gu);
+    a.ld_w = hidden;
+    a.s = s_gu;
+    a.ld_s = hidden / 128;
+    a.y = h;
+    a.ld_y = inter;
+    a.t = static_cast<int>(t);
+    a.n = static_cast<int>(2 * inter);
+    a.k = static_cast<int>(hidden);
+    a.tiles = static_cast<int>(inter / 8);
+    a.parts = 1;
+    a.per_block = plan.tiles_per_block;
+    a.blocks_per_part = (a.tiles + a.per_block - 1) / a.per_block;
+    a.xs = xs;
+    a.ld_xs = per_token ? 1 : hidden / 128;
+    a.per_token = per_token ? 1 : 0;
+    a.pmax = hmax;
+    const auto ka = pass_kernel<kActI8, true, SEPAL_HIP_F32>;
+    static std::size_t raised_a = 0;
+    const std::size_t lds_a = pass_lds(hidden);
+    raise_lds(ka, lds_a, raised_a);
+    ka<<<dim3(a.blocks_per_part), dim3(kThreads), lds_a, stream>>>(a);
+    check_launch("small-M q8 stack gate/up launch");
+    // down: H quantized per block of 128 or per token while staged -> P [parts][t][hidden]
+    PassParams d{};
+    d.xf = h;
+    d.ld_x = inter;
+    d.w = reinterpret_cast<const signed char*>(w_d);
+    d.ld_w = inter;
+    d.s = s_d;
+    d.ld_s = inter / 128;
+    d.y = part;
+    d.ld_y = hidden;
+    d.t = static_cast<int>(t);
+    d.n = static_cast<int>(hidden);
+    d.k = static_cast<int>(inter);
+    d.tiles = static_cast<int>((hidden + 15) / 16);
+    d.parts = plan.parts;
+    d.per_block = plan.units_per_block;
+    d.blocks_per_part = (d.tiles + d.per_block - 1) / d.per_block;
+    d.per_token = per_token ? 1 : 0;
+    d.hmax = hmax;
+    d.hmax_blocks = a.blocks_per_part;
+    const auto kd = pass_kernel<kActI8, false, SEPAL_HIP_F32>;
+    static std::size_t raised_d = 0;
+    const std::size_t gpt = (inter / 128 + plan.parts - 1) / plan.parts;
+    const std::size_t lds_d = pass_lds(gpt * 128);
+    raise_lds(kd, lds_d, raised_d);
+    kd<<<dim3(d.parts * d.blocks_per_part), dim3(kThreads), lds_d, stream>>>(d);
+    check_launch("small-M q8 stack down launch");
+    // y = sum of the parts; the next layer's bf16 input (xn) and its int8 form
+    finish_kernel<<<dim3(static_cast<unsigned>(t)), dim3(1024), hidden * sizeof(float), stream>>>(
+        part, plan.parts, static_cast<int>(t), static_cast<int>(hidden), y, static_cast<std::uint16_t*>(xn), eps, xq_next,
+        xs_next, per_token ? static_cast<int>(hidden) : 128);
+    check_launch("small-M q8 stack finish launch");
+}
 
 bool launch_small_stack(const SmallStackPlan& plan, std::size_t layers, std::size_t t, std::size_t hidden, std::size_t inter,
                         void* x, const std::int8_t* const* w_gu, const float* const* s_gu, const std::int8_t* const* w_d,
@@ -897,7 +1179,8 @@ bool launch_small_stack(const SmallStackPlan& plan, std::size_t layers, std::siz
         if (l0 > 0) {
             // the previous launch ended after its last down pass: its y and parts are final; make this launch's input
             finish_kernel<<<dim3(static_cast<unsigned>(t)), dim3(1024), hidden * sizeof(float), stream>>>(
-                part, plan.parts, static_cast<int>(t), static_cast<int>(hidden), y, static_cast<std::uint16_t*>(x), eps);
+                part, plan.parts, static_cast<int>(t), static_cast<int>(hidden), y, static_cast<std::uint16_t*>(x), eps,
+                nullptr, nullptr, 0);
             check_launch("small-M stack finish launch");
         }
         p.layers = static_cast<int>(n);

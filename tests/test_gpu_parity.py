@@ -543,6 +543,42 @@ def test_mlp_stack_small_persistent_same_bits(sm, monkeypatch, t, nl, hidden, in
         assert rel_rms(out["layers"][0], _oracle_stack(0, x, layers, 128)) < 2e-3
 
 
+@pytest.mark.parametrize("t,act", [(1, 0), (5, 128), (16, 0), (16, 128)])
+def test_mlp_stack_small_q8(sm, t, act):
+    """M <= 16 gpu-q8w stack (int8 MFMAs, H quantized by the down pass while staged, the next layer's input quantized
+    by the finish pass) against the oracle's q8 chain: same int8 products, float sums in another order (tolerance)."""
+    say("mlp stack small q8 t", t, "act", act)
+    rng = np.random.default_rng(91 + t + act)
+    hidden, inter, nl = 512, 1024, 3
+    layers = _stack_weights(sm, rng, nl, hidden, inter, rule=1)
+    x = bf16_inputs(rng, (t, hidden))
+    x[:, ::97] *= 20.0  # outlier channels, as the q8 benchmark's activations
+    x = orc.bf16_round(x)
+    xt = dev(x, torch.bfloat16)
+    y = host(sm.mlp_stack(1, xt, layers, act_block=act))
+    ref = _oracle_stack(1, x, layers, act)
+    assert rel_rms(y, ref) < 2e-3, rel_rms(y, ref)
+    y2 = _oracle_stack(1, x, layers[:2], act)
+    assert rel_rms(host(xt).astype(np.float32), orc.bf16_round(orc.rmsnorm_rows(y2))) < 2e-3
+    y1 = host(sm.mlp_stack(1, dev(x, torch.bfloat16), layers[:1], act_block=act))
+    ref1 = _oracle_stack(1, x, layers[:1], act)
+    assert max_rel_over_rms(y1, ref1) < 2e-3, max_rel_over_rms(y1, ref1)
+
+
+@pytest.mark.parametrize("act", [0, 128])
+def test_mlp_stack_small_q8_full_size(sm, act):
+    """The M = 16 q8 stack at the model's shape (H 2560, I 9728), two layers, against the oracle."""
+    say("mlp stack small q8 full size act", act)
+    rng = np.random.default_rng(6 + act)
+    layers = _stack_weights(sm, rng, 2, 2560, 9728, rule=1)
+    x = bf16_inputs(rng, (16, 2560))
+    y1 = host(sm.mlp_stack(1, dev(x, torch.bfloat16), layers[:1], act_block=act))
+    ref1 = _oracle_stack(1, x, layers[:1], act)
+    assert max_rel_over_rms(y1, ref1) < 2e-3, max_rel_over_rms(y1, ref1)
+    y = host(sm.mlp_stack(1, dev(x, torch.bfloat16), layers, act_block=act))
+    assert rel_rms(y, _oracle_stack(1, x, layers, act)) < 2e-3
+
+
 def test_mlp_stack_small_path_full_size(sm):
     """The M = 16 stack at the model's shape (H 2560, I 9728), two layers, against the oracle."""
     say("mlp stack small path full size")
