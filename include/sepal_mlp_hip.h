@@ -103,11 +103,37 @@ SEPAL_HIP_API int32_t sepal_hip_quantize_rows_s8(const void* x, int32_t x_type, 
  * [T, ld_y], or y_type for SWIGLU. K a multiple of 128; strides multiples of 16; 16-byte aligned pointers. `config` as
  * sepal_hip_gemm_w8g; the small-M path splits K across blocks when N is narrow, which keeps the sums exact but adds
  * the splits' partial chains (within tolerance, not bit for bit); config 2 keeps the chain whole (bit for bit).
- * Replaces kernel_i8_z + finish_tile (runner/src/cpu/gemm_kernels_avx512.cpp:67-115, gemm.cpp:417-447, 545-569) and
- * launch_gemm_s8 (runner/cuda/src/gemm_s8_kernels.hpp:43-49) with per-group scales. */
+ * Replaces kernel_i8_z + finish_tile (runner/src/cpu/gemm_kernels_avx512.cpp:67-115, gemm.cpp:417-447, 545-569)
+ * with per-group scales (the per-channel launch_gemm_s8 is sepal_hip_gemm_s8). */
 SEPAL_HIP_API int32_t sepal_hip_gemm_q8(const int8_t* xq, size_t ld_x, const float* xs, size_t ld_xs, size_t act_block,
                           const int8_t* w, size_t ld_w, const float* ws, size_t ld_ws, void* y, int32_t y_type,
                           size_t ld_y, size_t t, size_t n, size_t k, int32_t epilogue, int32_t config, void* stream);
+
+/* The GPU int8 path's per-row quantizer: for each row v = x * smooth[c] (float32; smooth null: x as it is), amax =
+ * max |v|, scales[row] = amax / 127 (0 for an all-zero row), q = clamp(rint(v * (127 / amax)), -127, 127) (0 when amax
+ * is 0). x float32 / bf16 / binary16 [rows, ld_x], q int8 [rows, ld_q]. cols a multiple of 16, strides multiples of 16,
+ * 16-byte aligned x, q and smooth. Replaces launch_quantize_rows_s8 (runner/cuda/src/gemm_s8_kernels.hpp:20-27,
+ * activations with their smoothing factors) and launch_quantize_weights_s8 in its Plain layout (:29-34: weights
+ * [n, k] per output channel, smooth = col_scale); the Fp16Pairs layout is an NVIDIA fragment order this library does
+ * not use. */
+SEPAL_HIP_API int32_t sepal_hip_s8_quantize_rows(const void* x, int32_t x_type, size_t ld_x, const float* smooth, int8_t* q,
+                                                 size_t ld_q, float* scales, size_t rows, size_t cols, void* stream);
+
+/* The int8-activation multiply with per-channel scales: Y[t, n] = (float(sum over K of xq[t,k] * wq[n,k]) * sx[t]) *
+ * sw[n], the sum exact in int32 (int8 MFMA over the whole K), then two float32 products in that order. Y float32 or
+ * binary16 (y_type; round to nearest even) [T, ld_y]. K a multiple of 128 (the reference allows 16), strides of X and W
+ * multiples of 16, 16-byte aligned X and W. Replaces launch_gemm_s8 (runner/cuda/src/gemm_s8_kernels.hpp:43-49). */
+SEPAL_HIP_API int32_t sepal_hip_gemm_s8(const int8_t* xq, size_t ld_x, const float* sx, const int8_t* wq, size_t ld_w,
+                                        const float* sw, void* y, int32_t y_type, size_t ld_y, size_t t, size_t n, size_t k,
+                                        void* stream);
+
+/* binary16 activations times int8 weights with per-channel scales: Y[t, n] = sw[n] * sum over K of x[t,k] * wq[n,k],
+ * the weights widened exactly and multiplied with float32 accumulation (the gpu-w8g kernels with the channel's scale
+ * in every group: within float32 rounding of one accumulator times sw). Y float32 or binary16 [T, ld_y] (binary16 goes
+ * through float32 row chunks of at most 64 MB of workspace). Shape rules as sepal_hip_gemm_s8; wq in the Plain layout.
+ * Replaces launch_gemm_w8a16 (runner/cuda/src/gemm_s8_kernels.hpp:51-57), the reference's gpu-q8w profile multiply. */
+SEPAL_HIP_API int32_t sepal_hip_gemm_w8a16(const void* x, size_t ld_x, const int8_t* wq, size_t ld_w, const float* sw, void* y,
+                                           int32_t y_type, size_t ld_y, size_t t, size_t n, size_t k, void* stream);
 
 /* gate/up of the q8 MLP with the down multiply's input made in the same pass: H = SwiGLU of sepal_hip_gemm_q8 (gate
  * and up rows in the 64-row interleave), quantized per row and 128 columns by the activation quantizer's rule. hq int8

@@ -55,6 +55,8 @@ def lib():
         L.orc_swiglu_libm.restype = f32
         L.orc_gate_up_source.argtypes = [sz, sz]
         L.orc_gate_up_source.restype = sz
+        L.orc_s8_quantize_rows.argtypes = [vp, sz, vp, sz, sz, vp, sz, vp]
+        L.orc_gemm_s8.argtypes = [vp, sz, vp, vp, sz, vp, vp, sz, sz, sz, sz]
         _orc = L
     return _orc
 
@@ -146,6 +148,27 @@ def gemm_q8(xq, xs, wq, ws, epilogue=STORE, act_block=128, y=None):
     y = np.zeros((t, ncols), np.float32) if y is None else _f32(y).copy()
     lib().orc_gemm_q8(_p(xq), k, _p(xs), xs.shape[1], act_block, _p(wq), k, _p(ws), ws.shape[1], _p(y), ncols, t, n, k,
                       epilogue)
+    return y
+
+
+def s8_quantize_rows(x, smooth=None):
+    """GPU int8 path's per-row quantizer (127 / amax rule, zero rows scale 0): int8 q and scales [rows]."""
+    x = _f32(x)
+    rows, cols = x.shape
+    q = np.zeros((rows, cols), np.int8)
+    s = np.zeros(rows, np.float32)
+    sm = None if smooth is None else _f32(smooth)
+    lib().orc_s8_quantize_rows(_p(x), cols, None if sm is None else _p(sm), rows, cols, _p(q), cols, _p(s))
+    return q, s
+
+
+def gemm_s8(xq, sx, wq, sw):
+    """y = ((float)S * sx[t]) * sw[n] with S the exact integer sum, float32 [T, N]."""
+    xq, wq = _i8(xq), _i8(wq)
+    t, k = xq.shape
+    n = wq.shape[0]
+    y = np.zeros((t, n), np.float32)
+    lib().orc_gemm_s8(_p(xq), k, _p(_f32(sx)), _p(wq), k, _p(_f32(sw)), _p(y), n, t, n, k)
     return y
 
 

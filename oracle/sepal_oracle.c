@@ -244,3 +244,37 @@ void orc_rmsnorm_rows(const float* x, size_t ld_x, float* y, size_t ld_y, size_t
         }
     }
 }
+
+void orc_s8_quantize_rows(const float* x, size_t ld_x, const float* smooth, size_t rows, size_t cols, int8_t* q, size_t ld_q,
+                          float* scales) {
+    for (size_t r = 0; r < rows; ++r) {
+        const float* xr = x + r * ld_x;
+        float amax = 0.0f;
+        for (size_t c = 0; c < cols; ++c) {
+            const float v = smooth != NULL ? xr[c] * smooth[c] : xr[c];
+            const float a = fabsf(v);
+            if (a > amax) amax = a;
+        }
+        const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
+        scales[r] = amax / 127.0f;
+        for (size_t c = 0; c < cols; ++c) {
+            const float v = smooth != NULL ? xr[c] * smooth[c] : xr[c];
+            float t = rintf(v * inv);
+            if (t > 127.0f) t = 127.0f;
+            if (t < -127.0f) t = -127.0f;
+            q[r * ld_q + c] = (int8_t)t;
+        }
+    }
+}
+
+void orc_gemm_s8(const int8_t* xq, size_t ld_x, const float* sx, const int8_t* wq, size_t ld_w, const float* sw, float* y,
+                 size_t ld_y, size_t t, size_t n, size_t k) {
+    for (size_t r = 0; r < t; ++r)
+        for (size_t c = 0; c < n; ++c) {
+            int64_t acc = 0;
+            for (size_t i = 0; i < k; ++i) acc += (int64_t)xq[r * ld_x + i] * (int64_t)wq[c * ld_w + i];
+            const float f = (float)(int32_t)acc;
+            const float a = f * sx[r];
+            y[r * ld_y + c] = a * sw[c];
+        }
+}

@@ -18,6 +18,10 @@
  *   orc_swiglu_libm         "parity unpinned" at the ulp level: the reference GPU path calls CUDA expf/log1pf; pinned by
  *                           tolerance against float64 silu(g)*u only.
  *   orc_rmsnorm_rows        bit-exact against the compiled reference rmsnorm_rows fixtures.
+ *   orc_s8_quantize_rows    the rule's closed-form cases: zero rows (scale 0, q 0), the row maximum at +-127, ties
+ *                           rounded to even where 127 / amax is exactly 1, the half-step bound, smoothing as a
+ *                           pre-multiplied input (the reference CUDA quantizer cannot be built here).
+ *   orc_gemm_s8             the integer sum against numpy int64 products; the float32 order by hand-checked cases.
  */
 #ifndef SEPAL_ORACLE_H
 #define SEPAL_ORACLE_H
@@ -93,6 +97,20 @@ float orc_swiglu_libm(float g, float u);
  * (runner/src/cpu/elementwise.cpp:22-39 sum_squares, :43-59 rmsnorm_rows; vmath.hpp:52-59 hsum_ps.) */
 void orc_rmsnorm_rows(const float* x, size_t ld_x, float* y, size_t ld_y, size_t rows, size_t cols, const float* w1,
                       double eps);
+
+/* The GPU int8 path's per-row quantizer (launch_quantize_rows_s8, and launch_quantize_weights_s8's Plain layout): per
+ * row v = x * smooth[c] in float32 (smooth NULL: x), amax = max |v|, inv = amax > 0 ? 127 / amax : 0, scale =
+ * amax / 127, q = clamp(rint(v * inv), -127, 127).
+ * (runner/cuda/src/gemm_s8_kernels.cu:29-32 quantize_one, :50-79 rows, :82-110 weights; host form
+ *  runner/cuda/tests/test_gemm_s8_kernels.cpp:58-68.) */
+void orc_s8_quantize_rows(const float* x, size_t ld_x, const float* smooth, size_t rows, size_t cols, int8_t* q, size_t ld_q,
+                          float* scales);
+
+/* The int8-activation multiply with per-channel scales: S = exact integer sum over k of xq[t,k] * wq[n,k] (int32),
+ * y = ((float)S * sx[t]) * sw[n] in float32 (runner/cuda/src/gemm_s8_kernels.cu:255-266; closed form
+ * runner/cuda/tests/test_gemm_s8_kernels.cpp:208-213). */
+void orc_gemm_s8(const int8_t* xq, size_t ld_x, const float* sx, const int8_t* wq, size_t ld_w, const float* sw, float* y,
+                 size_t ld_y, size_t t, size_t n, size_t k);
 
 #ifdef __cplusplus
 }

@@ -7,6 +7,7 @@
 // launch_gemm_s8, runner/cuda/src/gemm_s8_kernels.cu:472-546) for the shapes this library takes.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstring>
 #include <cstdlib>
 #include <mutex>
@@ -234,6 +235,103 @@ int32_t sepal_hip_gemm_q8(const int8_t* xq, size_t ld_x, const float* xs, size_t
         a.config = config == 2 ? 1 : config;
         a.force_splits = config == 2 ? 1 : 0;
         launch_gemm_q8(a, as_stream(stream));
+    });
+}
+
+int32_t sepal_hip_s8_quantize_rows(const void* x, int32_t x_type, size_t ld_x, const float* smooth, int8_t* q, size_t ld_q,
+                                   float* scales, size_t rows, size_t cols, void* stream) {
+    return guarded([&] {
+        require(x != nullptr && q != nullptr && scales != nullptr, "s8_quantize_rows: null pointer");
+        require(valid_type(x_type), "s8_quantize_rows: unknown input type");
+        require(cols != 0 && cols % 16 == 0, "s8_quantize_rows: cols must be a non-zero multiple of 16");
+        require(ld_x >= cols && ld_q >= cols && ld_x % 16 == 0 && ld_q % 16 == 0,
+                "s8_quantize_rows: row strides must be multiples of 16 and at least cols");
+        require(aligned16(x) && aligned16(q) && (smooth == nullptr || aligned16(smooth)),
+                "s8_quantize_rows: x, q and smooth must be 16-byte aligned");
+        if (rows == 0) return;
+        require(rows < 0x7FFFFFFFu, "s8_quantize_rows: dimension beyond 2^31");
+        launch_s8_quantize_rows(x, x_type, ld_x, smooth, q, ld_q, scales, rows, cols, as_stream(stream));
+    });
+}
+
+namespace {
+void check_s8_family(const char* who, const void* x, size_t ld_x, const void* w, size_t ld_w, const float* sw, const void* y,
+                     int32_t y_type, size_t ld_y, size_t n, size_t k) {
+    const std::string w_ = who;
+    require(x != nullptr && w != nullptr && sw != nullptr && y != nullptr, w_ + ": null pointer");
+    require(y_type == SEPAL_HIP_F32 || y_type == SEPAL_HIP_F16, w_ + ": the output is float32 or binary16");
+    require(n != 0 && k != 0 && k % 128 == 0, w_ + ": K must be a non-zero multiple of 128 (this library's group step) and N non-zero");
+    require(ld_x >= k && ld_w >= k && ld_x % 16 == 0 && ld_w % 16 == 0, w_ + ": row strides of X and W must be multiples of 16 and at least K");
+    require(ld_y >= n, w_ + ": ld_y must be at least N");
+    require(aligned16(x) && aligned16(w) && aligned8(y), w_ + ": X and W must be 16-byte aligned, Y 8-byte aligned");
+}
+} // namespace
+
+int32_t sepal_hip_gemm_s8(const int8_t* xq, size_t ld_x, const float* sx, const int8_t* wq, size_t ld_w, const float* sw,
+                          void* y, int32_t y_type, size_t ld_y, size_t t, size_t n, size_t k, void* stream) {
+    return guarded([&] {
+        check_s8_family("gemm_s8", xq, ld_x, wq, ld_w, sw, y, y_type, ld_y, n, k);
+        require(sx != nullptr, "gemm_s8: null pointer");
+        if (t == 0) return;
+        require(t < 0x7FFFFFFFu && n < 0x7FFFFFFFu, "gemm_s8: dimension beyond 2^31");
+        GemmArgs a;
+        a.x = xq;
+        a.ld_x = ld_x;
+        a.xs = sx;
+        a.ld_xs = 1;
+        a.act_block = k;
+        a.w = wq;
+        a.ld_w = ld_w;
+        a.s = sw;
+        a.ld_s = 1;
+        a.y = y;
+        a.y_type = y_type;
+        a.ld_y = ld_y;
+        a.t = t;
+        a.n = n;
+        a.k = k;
+        a.epilogue = SEPAL_HIP_STORE;
+        launch_gemm_s8(a, as_stream(stream));
+    });
+}
+
+int32_t sepal_hip_gemm_w8a16(const void* x, size_t ld_x, const int8_t* wq, size_t ld_w, const float* sw, void* y,
+                             int32_t y_type, size_t ld_y, size_t t, size_t n, size_t k, void* stream) {
+    return guarded([&] {
+        check_s8_family("gemm_w8a16", x, ld_x, wq, ld_w, sw, y, y_type, ld_y, n, k);
+        if (t == 0) return;
+        require(t < 0x7FFFFFFFu && n < 0x7FFFFFFFu, "gemm_w8a16: dimension beyond 2^31");
+        const hipStream_t st = as_stream(stream);
+        // the per-channel scale as per-group scales in the workspace, then the w8g multiply (binary16 X, Store); a
+        // binary16 output goes through float32 row chunks of at most 64 MB (a row's bits do not depend on the batch)
+        const std::size_t groups = k / 128, s_bytes = (n * groups * 4 + 255) / 256 * 256;
+        const std::size_t chunk = y_type == SEPAL_HIP_F32 ? t : std::max<std::size_t>(1, (std::size_t{64} << 20) / (n * 4));
+        const std::size_t rows = std::min(t, chunk);
+        char* ws = static_cast<char*>(workspace(kScratchOffset + s_bytes + (y_type == SEPAL_HIP_F32 ? 0 : rows * n * 4), st));
+        float* s = reinterpret_cast<float*>(ws + kScratchOffset);
+        float* tmp = reinterpret_cast<float*>(ws + kScratchOffset + s_bytes);
+        launch_broadcast_scales(sw, s, n, groups, st);
+        for (std::size_t r0 = 0; r0 < t; r0 += rows) {
+            const std::size_t tr = std::min(rows, t - r0);
+            GemmArgs a;
+            a.x = static_cast<const std::uint16_t*>(x) + r0 * ld_x;
+            a.x_type = SEPAL_HIP_F16;
+            a.ld_x = ld_x;
+            a.w = wq;
+            a.ld_w = ld_w;
+            a.s = s;
+            a.ld_s = groups;
+            a.y = y_type == SEPAL_HIP_F32 ? static_cast<void*>(static_cast<float*>(y) + r0 * ld_y) : static_cast<void*>(tmp);
+            a.y_type = SEPAL_HIP_F32;
+            a.ld_y = y_type == SEPAL_HIP_F32 ? ld_y : n;
+            a.t = tr;
+            a.n = n;
+            a.k = k;
+            a.epilogue = SEPAL_HIP_STORE;
+            launch_gemm_w8g(a, st);
+            if (y_type == SEPAL_HIP_F16)
+                launch_f32_to_f16(tmp, n, static_cast<std::uint16_t*>(y) + r0 * ld_y, ld_y, tr, n, st);
+        }
     });
 }
 

@@ -64,8 +64,11 @@ __device__ __forceinline__ unsigned short f32_to_bf16_bits(float f) {
     return static_cast<unsigned short>((bits + 0x7FFFu + ((bits >> 16) & 1u)) >> 16);
 }
 
-// float32 -> binary16 bits, round to nearest even (the hardware conversion).
+// float32 -> binary16 bits, round to nearest even (the hardware conversion) of the float32 value. The empty asm keeps
+// the value a rounded float32: otherwise the compiler may fold a producing multiply into a mixed-precision instruction
+// that rounds the exact product straight to binary16 (a different result at float32 ties, seen in gemm_s8's output).
 __device__ __forceinline__ unsigned short f32_to_f16_bits(float f) {
+    asm volatile("" : "+v"(f));
     return __builtin_bit_cast(unsigned short, static_cast<_Float16>(f));
 }
 

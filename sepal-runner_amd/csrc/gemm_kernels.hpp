@@ -40,6 +40,15 @@ void launch_gemm_w8g(const GemmArgs& a, hipStream_t stream);
 void launch_stream_w8g(const GemmArgs& a, hipStream_t stream);
 void launch_stream_q8(const GemmArgs& a, hipStream_t stream);
 void launch_gemm_q8(const GemmArgs& a, hipStream_t stream);
+// The int8-activation multiply with per-channel weight scales: y = (float(sum over K of xq * wq) * xs[t]) * s[n] (a.s
+// holds one scale per row, a.ld_s = 1); y float32 or binary16 (a.y_type).
+void launch_gemm_s8(const GemmArgs& a, hipStream_t stream);
+// The GPU int8 path's per-row quantizer (rule 127 / amax, zero rows scale 0), with an optional per-column factor.
+void launch_s8_quantize_rows(const void* x, int x_type, std::size_t ld_x, const float* smooth, std::int8_t* q, std::size_t ld_q,
+                             float* scales, std::size_t rows, std::size_t cols, hipStream_t stream);
+void launch_broadcast_scales(const float* sw, float* s, std::size_t n, std::size_t groups, hipStream_t stream);
+void launch_f32_to_f16(const float* src, std::size_t ld_src, std::uint16_t* dst, std::size_t ld_dst, std::size_t rows,
+                       std::size_t cols, hipStream_t stream);
 void launch_q8_group_sums(const GemmArgs& a, hipStream_t stream);
 void launch_gemm_q8_swiglu_q8(const GemmArgs& a, hipStream_t stream);  // large-M kernel only
 

@@ -20,7 +20,9 @@
 namespace sepal::hip {
 namespace q8 {
 
-enum { MODE_CHAIN = 0, MODE_SUMS = 1 };
+// MODE_CHAIN: the per-group float chain; MODE_SUMS: the int32 group sums out; MODE_WHOLE: one int32 sum over the whole
+// K (per-channel weight scales), then (float(S) * sx) * sw (runner/cuda/src/gemm_s8_kernels.cu:255-266)
+enum { MODE_CHAIN = 0, MODE_SUMS = 1, MODE_WHOLE = 2 };
 
 __device__ __forceinline__ i32x16 mfma_i8_32(const u32x4 a, const u32x4 b, i32x16 c) {
     return __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(i32x4, a), __builtin_bit_cast(i32x4, b), c, 0, 0, 0);
@@ -164,6 +166,7 @@ __global__ void __launch_bounds__(512) gemm_big(const Params p) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
     const i32x16 zero16 = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+    i32x16 tot[2][2] = {{zero16, zero16}, {zero16, zero16}};  // MODE_WHOLE: the running int32 sums
 
     // One group: issue group g + ahead's loads (clamped; the set they go to was staged and its scales used at earlier
     // steps); the exact int32 sums of group g; its link of the scale chain (or the sums out); stage group g + 1 into the
@@ -193,9 +196,13 @@ __global__ void __launch_bounds__(512) gemm_big(const Params p) {
 #pragma unroll
                 for (int i = 0; i < 2; ++i)
 #pragma unroll
-                    for (int j = 0; j < 2; ++j) sacc[i][j] = mfma_i8_32(a[i], b[j], st == 0 ? zero16 : sacc[i][j]);
+                    for (int j = 0; j < 2; ++j) {
+                        if constexpr (MODE == MODE_WHOLE) tot[i][j] = mfma_i8_32(a[i], b[j], tot[i][j]);
+                        else sacc[i][j] = mfma_i8_32(a[i], b[j], st == 0 ? zero16 : sacc[i][j]);
+                    }
             }
-            if constexpr (MODE == MODE_SUMS) {
+            if constexpr (MODE == MODE_WHOLE) {
+            } else if constexpr (MODE == MODE_SUMS) {
 #pragma unroll
                 for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -246,6 +253,26 @@ __global__ void __launch_bounds__(512) gemm_big(const Params p) {
         }
     }
     if constexpr (MODE == MODE_SUMS) return;
+    if constexpr (MODE == MODE_WHOLE) {
+        // y = (float(S) * sx[t]) * sw[n], float32 or binary16 (round to nearest even)
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row = m0 + wm * 64 + i * 32 + 8 * (r / 4) + 4 * (lane / 32) + (r % 4);
+                if (row >= p.t) continue;
+                const float sx = p.xs[static_cast<std::size_t>(row) * p.ld_xs];
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    if (col[j] < p.n) {
+                        const float v = __fmul_rn(__fmul_rn(static_cast<float>(tot[i][j][r]), sx), wsrow[j][0]);
+                        const std::size_t idx = static_cast<std::size_t>(row) * p.ld_y + col[j];
+                        if constexpr (YT == SEPAL_HIP_F16) static_cast<unsigned short*>(p.y)[idx] = f32_to_f16_bits(v);
+                        else static_cast<float*>(p.y)[idx] = v;
+                    }
+            }
+        return;
+    }
 
     if constexpr (EP == kSwigluQ8) {
         // The tile's 128 output columns are one quantization block. H goes through LDS (the W tile's space, free after
@@ -403,6 +430,11 @@ void launch_gemm_q8(const GemmArgs& a, hipStream_t stream) {
 void launch_gemm_q8_swiglu_q8(const GemmArgs& a, hipStream_t stream) {
     if (a.act_block == a.k && a.k != 128) q8::launch_big<kSwigluQ8, SEPAL_HIP_F32, true, q8::MODE_CHAIN>(a, stream);
     else q8::launch_big<kSwigluQ8, SEPAL_HIP_F32, false, q8::MODE_CHAIN>(a, stream);
+}
+
+void launch_gemm_s8(const GemmArgs& a, hipStream_t stream) {
+    if (a.y_type == SEPAL_HIP_F16) q8::launch_big<SEPAL_HIP_STORE, SEPAL_HIP_F16, true, q8::MODE_WHOLE>(a, stream);
+    else q8::launch_big<SEPAL_HIP_STORE, SEPAL_HIP_F32, true, q8::MODE_WHOLE>(a, stream);
 }
 
 void launch_q8_group_sums(const GemmArgs& a, hipStream_t stream) {

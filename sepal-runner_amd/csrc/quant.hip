@@ -310,6 +310,64 @@ __global__ void f32_to_bf16_kernel(const float* __restrict__ src, std::uint16_t*
     if (i < count) dst[i] = f32_to_bf16_bits(src[i]);
 }
 
+// The GPU int8 path's per-row quantizer (the int8-activation multiply's rows, and per-output-channel weights):
+// v = x * smooth[c] in float32 when smooth is set; amax = max |v| over the row; scale = amax / 127 (0 for an all-zero
+// row); q = clamp(rint(v * (127 / amax)), -127, 127), 0 when amax is 0. One block per row: the maximum (order-free),
+// then the values (runner/cuda/src/gemm_s8_kernels.cu:29-32, 50-79, 82-110; host form
+// runner/cuda/tests/test_gemm_s8_kernels.cpp:58-68).
+template <int ST>
+__global__ void __launch_bounds__(256) s8_rows_kernel(const void* __restrict__ x, std::size_t ld_x, const float* __restrict__ smooth,
+                                                      std::int8_t* __restrict__ q, std::size_t ld_q, float* __restrict__ scales,
+                                                      int cols) {
+    __shared__ float red[4];
+    const std::size_t row = blockIdx.x;
+    const int chunks = cols / 8;
+    const auto values = [&](int c, float (&v)[8]) {
+        load8<ST>(x, row * ld_x + 8 * c, v);
+        if (smooth != nullptr)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] = __fmul_rn(v[i], smooth[8 * c + i]);
+    };
+    float m = 0.0f;
+    for (int c = threadIdx.x; c < chunks; c += 256) {
+        float v[8];
+        values(c, v);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(v[i]));
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+    if (threadIdx.x % 64 == 0) red[threadIdx.x / 64] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    const float inv = m > 0.0f ? __fdiv_rn(127.0f, m) : 0.0f;
+    if (threadIdx.x == 0) scales[row] = __fdiv_rn(m, 127.0f);
+    for (int c = threadIdx.x; c < chunks; c += 256) {
+        float v[8];
+        values(c, v);
+        unsigned packed[2] = {0u, 0u};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            float r = __builtin_rintf(__fmul_rn(v[i], inv));
+            r = r < -127.0f ? -127.0f : (r > 127.0f ? 127.0f : r);
+            packed[i / 4] |= (static_cast<unsigned>(static_cast<int>(r)) & 0xFFu) << (8 * (i % 4));
+        }
+        *reinterpret_cast<uint2*>(q + row * ld_q + 8 * c) = make_uint2(packed[0], packed[1]);
+    }
+}
+
+// s[r][g] = sw[r] for g < groups: a per-channel scale as per-group scales
+__global__ void broadcast_scales_kernel(const float* __restrict__ sw, float* __restrict__ s, std::size_t n, std::size_t groups) {
+    const std::size_t i = static_cast<std::size_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (i < n * groups) s[i] = sw[i / groups];
+}
+
+__global__ void f32_to_f16_kernel(const float* __restrict__ src, std::size_t ld_src, std::uint16_t* __restrict__ dst,
+                                  std::size_t ld_dst, std::size_t rows, std::size_t cols) {
+    const std::size_t i = static_cast<std::size_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (i < rows * cols) dst[(i / cols) * ld_dst + i % cols] = f32_to_f16_bits(src[(i / cols) * ld_src + i % cols]);
+}
+
 template <int ST>
 void launch_group(const void* src, std::size_t ld_src, const void* src_up, std::int8_t* q, std::size_t ld_q, float* s,
                   std::size_t ld_s, std::size_t rows, std::size_t k, int rule, std::size_t inter, hipStream_t stream) {
@@ -374,6 +432,30 @@ void launch_rmsnorm_quantize(const float* x, std::size_t ld_x, std::uint16_t* y_
     else
         quant::rmsnorm_kernel<SEPAL_HIP_BF16, quant::NORM_Q_TOKEN><<<grid, dim3(256), 0, stream>>>(x, ld_x, y_bf16, ld_y, w1, r, c, eps, q, ld_q, scales, ld_s);
     check_launch("rmsnorm_quantize kernel launch");
+}
+
+void launch_s8_quantize_rows(const void* x, int x_type, std::size_t ld_x, const float* smooth, std::int8_t* q, std::size_t ld_q,
+                             float* scales, std::size_t rows, std::size_t cols, hipStream_t stream) {
+    const dim3 grid(static_cast<unsigned>(rows)), block(256);
+    const int c = static_cast<int>(cols);
+    switch (x_type) {
+    case SEPAL_HIP_F32: quant::s8_rows_kernel<SEPAL_HIP_F32><<<grid, block, 0, stream>>>(x, ld_x, smooth, q, ld_q, scales, c); break;
+    case SEPAL_HIP_BF16: quant::s8_rows_kernel<SEPAL_HIP_BF16><<<grid, block, 0, stream>>>(x, ld_x, smooth, q, ld_q, scales, c); break;
+    default: quant::s8_rows_kernel<SEPAL_HIP_F16><<<grid, block, 0, stream>>>(x, ld_x, smooth, q, ld_q, scales, c); break;
+    }
+    check_launch("s8 row quantizer launch");
+}
+
+void launch_broadcast_scales(const float* sw, float* s, std::size_t n, std::size_t groups, hipStream_t stream) {
+    quant::broadcast_scales_kernel<<<dim3(static_cast<unsigned>((n * groups + 255) / 256)), dim3(256), 0, stream>>>(sw, s, n, groups);
+    check_launch("scale broadcast launch");
+}
+
+void launch_f32_to_f16(const float* src, std::size_t ld_src, std::uint16_t* dst, std::size_t ld_dst, std::size_t rows,
+                       std::size_t cols, hipStream_t stream) {
+    quant::f32_to_f16_kernel<<<dim3(static_cast<unsigned>((rows * cols + 255) / 256)), dim3(256), 0, stream>>>(src, ld_src, dst,
+                                                                                                             ld_dst, rows, cols);
+    check_launch("float32 to binary16 launch");
 }
 
 void launch_f32_to_bf16(const float* src, std::uint16_t* dst, std::size_t count, hipStream_t stream) {

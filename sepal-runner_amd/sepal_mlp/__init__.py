@@ -62,11 +62,15 @@ def library() -> C.CDLL:
         L.sepal_hip_gemm_q8_swiglu_quantize.argtypes = [vp, sz, vp, sz, sz, vp, sz, vp, sz, vp, sz, vp, sz, sz, sz, sz,
                                                         i32, vp]
         L.sepal_hip_mlp_stack.argtypes = [i32, sz, sz, sz, sz, vp, vp, vp, vp, vp, vp, sz, d, vp]
+        L.sepal_hip_s8_quantize_rows.argtypes = [vp, i32, sz, vp, vp, sz, vp, sz, sz, vp]
+        L.sepal_hip_gemm_s8.argtypes = [vp, sz, vp, vp, sz, vp, vp, i32, sz, sz, sz, sz, vp]
+        L.sepal_hip_gemm_w8a16.argtypes = [vp, sz, vp, sz, vp, vp, i32, sz, sz, sz, sz, vp]
         for name in ("sepal_hip_quantize_group_s8", "sepal_hip_quantize_gate_up_s8", "sepal_hip_gemm_w8g",
                      "sepal_hip_quantize_rows_s8", "sepal_hip_gemm_q8", "sepal_hip_q8_group_sums",
                      "sepal_hip_rmsnorm_rows", "sepal_hip_float_to_bf16", "sepal_hip_mlp_stack",
                      "sepal_hip_rmsnorm_quantize_rows", "sepal_hip_gemm_q8_swiglu_quantize",
-                     "sepal_hip_weight_fingerprint", "sepal_hip_packed_save", "sepal_hip_packed_load"):
+                     "sepal_hip_weight_fingerprint", "sepal_hip_packed_save", "sepal_hip_packed_load",
+                     "sepal_hip_s8_quantize_rows", "sepal_hip_gemm_s8", "sepal_hip_gemm_w8a16"):
             getattr(L, name).restype = i32
         L.sepal_hip_gemm_w8g_supports.restype = i32
         _lib = L
@@ -173,6 +177,40 @@ def quantize_rows_s8(x, block: int = 128, stream=None):
     _check(library().sepal_hip_quantize_rows_s8(_ptr(x), _type_of(x), _ld(x), _ptr(q), _ld(q), _ptr(sc), _ld(sc), rows,
                                                 cols, block, _stream(stream)))
     return q, sc
+
+
+def s8_quantize_rows(x, smooth=None, stream=None):
+    """The GPU int8 path's per-row quantizer (127 / amax, zero rows scale 0): int8 q [rows, cols] and scales [rows].
+    Serves activations (smooth: per-column factors) and per-channel weights alike."""
+    torch = _torch()
+    rows, cols = x.shape
+    q = torch.empty(rows, cols, dtype=torch.int8, device=x.device)
+    sc = torch.empty(rows, dtype=torch.float32, device=x.device)
+    _check(library().sepal_hip_s8_quantize_rows(_ptr(x), _type_of(x), _ld(x), _ptr(smooth) if smooth is not None else None,
+                                                _ptr(q), _ld(q), _ptr(sc), rows, cols, _stream(stream)))
+    return q, sc
+
+
+def gemm_s8(xq, sx, wq, sw, y_dtype=None, stream=None):
+    """Y = (float(sum xq * wq) * sx[t]) * sw[n], per-channel scales; float32 or binary16 out."""
+    torch = _torch()
+    t, k = xq.shape
+    n = wq.shape[0]
+    y = torch.empty(t, n, dtype=y_dtype or torch.float32, device=xq.device)
+    _check(library().sepal_hip_gemm_s8(_ptr(xq), _ld(xq), _ptr(sx), _ptr(wq), _ld(wq), _ptr(sw), _ptr(y), _type_of(y),
+                                       _ld(y), t, n, k, _stream(stream)))
+    return y
+
+
+def gemm_w8a16(x, wq, sw, y_dtype=None, stream=None):
+    """Y = sw[n] * sum x * wq: binary16 x, int8 weights with per-channel scales; float32 or binary16 out."""
+    torch = _torch()
+    t, k = x.shape
+    n = wq.shape[0]
+    y = torch.empty(t, n, dtype=y_dtype or torch.float32, device=x.device)
+    _check(library().sepal_hip_gemm_w8a16(_ptr(x), _ld(x), _ptr(wq), _ld(wq), _ptr(sw), _ptr(y), _type_of(y), _ld(y), t, n,
+                                          k, _stream(stream)))
+    return y
 
 
 def gemm_q8(xq, xs, w, ws, y=None, epilogue: int = STORE, act_block: int = 128, y_dtype=None, config: int = -1,

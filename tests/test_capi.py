@@ -92,6 +92,27 @@ def test_fused_producer_refusals():
                                                256, -1, None) == sm.OK
 
 
+def test_s8_family_refusals():
+    L = sm.library()
+    # row quantizer: cols a multiple of 16, strides, alignment, unknown type; zero rows is a no-op
+    assert L.sepal_hip_s8_quantize_rows(FAKE, 2, 256, None, FAKE, 256, FAKE, 4, 200, None) == sm.EINVAL
+    assert "multiple of 16" in _err()
+    assert L.sepal_hip_s8_quantize_rows(FAKE, 2, 200, None, FAKE, 256, FAKE, 4, 256, None) == sm.EINVAL
+    assert L.sepal_hip_s8_quantize_rows(FAKE, 2, 256, FAKE + 4, FAKE, 256, FAKE, 4, 256, None) == sm.EINVAL
+    assert L.sepal_hip_s8_quantize_rows(FAKE, 9, 256, None, FAKE, 256, FAKE, 4, 256, None) == sm.EINVAL
+    assert L.sepal_hip_s8_quantize_rows(FAKE, 2, 256, None, FAKE, 256, FAKE, 0, 256, None) == sm.OK
+    # gemm_s8 / gemm_w8a16: K a multiple of 128, output float32 or binary16, ld_y >= N, null scales; T = 0 is a no-op
+    assert L.sepal_hip_gemm_s8(FAKE, 272, FAKE, FAKE, 272, FAKE, FAKE, 0, 64, 4, 64, 272, None) == sm.EINVAL
+    assert "multiple of 128" in _err()
+    assert L.sepal_hip_gemm_s8(FAKE, 256, FAKE, FAKE, 256, FAKE, FAKE, 1, 64, 4, 64, 256, None) == sm.EINVAL
+    assert L.sepal_hip_gemm_s8(FAKE, 256, FAKE, FAKE, 256, FAKE, FAKE, 0, 32, 4, 64, 256, None) == sm.EINVAL
+    assert L.sepal_hip_gemm_s8(FAKE, 256, None, FAKE, 256, FAKE, FAKE, 0, 64, 4, 64, 256, None) == sm.EINVAL
+    assert L.sepal_hip_gemm_s8(FAKE, 256, FAKE, FAKE, 256, FAKE, FAKE, 2, 64, 0, 64, 256, None) == sm.OK
+    assert L.sepal_hip_gemm_w8a16(FAKE, 256, FAKE, 256, None, FAKE, 0, 64, 4, 64, 256, None) == sm.EINVAL
+    assert L.sepal_hip_gemm_w8a16(FAKE + 4, 256, FAKE, 256, FAKE, FAKE, 0, 64, 4, 64, 256, None) == sm.EINVAL
+    assert L.sepal_hip_gemm_w8a16(FAKE, 256, FAKE, 256, FAKE, FAKE, 2, 64, 0, 64, 256, None) == sm.OK
+
+
 def test_packed_file_refusals():
     L = sm.library()
     # null path, strided buffers, k not a multiple of 128, unknown rule, interleave with rows not a multiple of 128

@@ -592,6 +592,75 @@ def test_mlp_stack_small_path_full_size(sm):
     assert rel_rms(y, _oracle_stack(0, x, layers, 128)) < 2e-3
 
 
+# ---- the GPU int8 path with per-channel scales (launch_quantize_rows_s8 / launch_gemm_s8 / launch_gemm_w8a16) ------------
+
+_TORCH_TYPES = {"f16": torch.float16, "bf16": torch.bfloat16, "f32": torch.float32}
+
+
+@pytest.mark.parametrize("src", ["f16", "bf16", "f32"])
+def test_s8_quantize_rows_bit_exact(sm, src):
+    """Rows (zero row, outlier channels x20, smoothing factors) and per-channel weights, bit for bit against the
+    oracle of the 127 / amax rule."""
+    say("s8 quantize rows", src)
+    rng = np.random.default_rng(21)
+    for rows, cols, smooth in ((37, 3584, False), (21, 1040, True), (3, 16, False)):
+        x = rng.standard_normal((rows, cols)).astype(np.float32)
+        x[:, ::97] *= 20.0
+        x[min(1, rows - 1)] = 0.0
+        xt = dev(x, _TORCH_TYPES[src])
+        xv = host(xt.float())
+        sm_ = rng.uniform(0.25, 4.0, cols).astype(np.float32) if smooth else None
+        q, s = sm.s8_quantize_rows(xt, smooth=dev(sm_) if smooth else None)
+        qr, sr = orc.s8_quantize_rows(xv, smooth=sm_)
+        assert same_bits(host(q), qr) and same_bits(host(s), sr), (rows, cols, smooth)
+
+
+@pytest.mark.parametrize("t,n,k", [(100, 200, 1024), (37, 66, 3584), (5, 40, 6144), (300, 130, 2048), (1, 8, 128)])
+def test_gemm_s8_bit_exact(sm, t, n, k):
+    """y = (float(S) * sx) * sw bit for bit against the oracle (the reference test's shapes with K a multiple of 128),
+    and the binary16 result is the float32 one rounded."""
+    say("gemm s8", t, n, k)
+    rng = np.random.default_rng(t + n + k)
+    xq, sx = sm.s8_quantize_rows(dev((rng.standard_normal((t, k)) * 3.0).astype(np.float16)))
+    wq, sw = sm.s8_quantize_rows(dev(rng.standard_normal((n, k)).astype(np.float16)))
+    ref = orc.gemm_s8(host(xq), host(sx), host(wq), host(sw))
+    assert same_bits(host(sm.gemm_s8(xq, sx, wq, sw)), ref)
+    assert same_bits(host(sm.gemm_s8(xq, sx, wq, sw, y_dtype=torch.float16)), ref.astype(np.float16))
+
+
+def test_gemm_s8_full_size_sampled_rows(sm):
+    """M = 15872 x N 2560 x K 9728 (the down shape): every row computed, 48 sampled rows against the oracle."""
+    say("gemm s8 full size")
+    rng = np.random.default_rng(8)
+    t, n, k = 15872, 2560, 9728
+    x = torch.randn(t, k, generator=torch.Generator(device="cuda").manual_seed(8), device="cuda").half()
+    xq, sx = sm.s8_quantize_rows(x)
+    wq, sw = sm.s8_quantize_rows(dev((rng.standard_normal((n, k)) * 0.02).astype(np.float16)))
+    y = sm.gemm_s8(xq, sx, wq, sw)
+    rows = np.sort(rng.choice(t, 48, replace=False))
+    ref = orc.gemm_s8(host(xq[rows]), host(sx[rows]), host(wq), host(sw))
+    assert same_bits(host(y[rows]), ref)
+
+
+@pytest.mark.parametrize("t,n,k", [(100, 256, 1024), (16, 384, 2560), (5000, 4096, 256)])
+def test_gemm_w8a16_against_float64(sm, t, n, k):
+    """binary16 x times per-channel int8 weights, against float64 of the dequantised weights (the reference test's
+    check) at the parity bar; the binary16 output (row chunks through float32 at 5000 x 4096) is the float32 one
+    rounded."""
+    say("gemm w8a16", t, n, k)
+    rng = np.random.default_rng(t + k)
+    x = rng.standard_normal((t, k)).astype(np.float16)
+    wq, sw = sm.s8_quantize_rows(dev((rng.standard_normal((n, k)) * 0.02).astype(np.float16)))
+    xt = dev(x)
+    y = host(sm.gemm_w8a16(xt, wq, sw))
+    rows = np.arange(t) if t <= 128 else np.sort(rng.choice(t, 64, replace=False))
+    wd = host(wq).astype(np.float64) * host(sw).astype(np.float64)[:, None]
+    ref = x[rows].astype(np.float64) @ wd.T
+    assert max_rel_over_rms(y[rows], ref) < 2e-3, max_rel_over_rms(y[rows], ref)
+    y16 = host(sm.gemm_w8a16(xt, wq, sw, y_dtype=torch.float16))
+    assert same_bits(y16, y.astype(np.float16))
+
+
 # ---- BASELINE shapes (H 2560, I 9728) on sampled rows ------------------------------------------------------------------
 
 H, I = 2560, 9728

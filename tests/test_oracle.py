@@ -109,6 +109,51 @@ def test_r1_quantizer_closed_form_and_special_cases():
     assert err.max() <= 0.5 + 1e-6
 
 
+def test_s8_row_quantizer_rule():
+    """The GPU int8 path's rule (127 / amax, zero rows scale 0), by its closed-form cases: where 127 / amax is exactly
+    1 the values round half to even; the row maximum maps to +-127; a zero row gets scale 0 and zeros; every value is
+    within half a step; the smoothing factor acts as a pre-multiplied input; a plausible mix-up with the cpu-q8 rule
+    (1 / (amax / 127), scale 1 on zero rows) differs on the zero row's scale and on real data."""
+    x = np.array([[0, 0, 0, 0], [127, 2.5, 3.5, -2.5], [-127, 0.5, 1.5, -0.5]], np.float32)
+    q, s = orc.s8_quantize_rows(x)
+    assert q[0].tolist() == [0, 0, 0, 0] and s[0] == 0.0
+    assert q[1].tolist() == [127, 2, 4, -2] and s[1] == 1.0
+    assert q[2].tolist() == [-127, 0, 2, 0] and s[2] == 1.0
+    rng = np.random.default_rng(3)
+    x = (rng.standard_normal((64, 512)) * rng.uniform(0.01, 30, (64, 1))).astype(np.float32)
+    x[5] = 0.0
+    q, s = orc.s8_quantize_rows(x)
+    amax = np.abs(x).max(1)
+    assert np.array_equal(np.abs(q).max(1)[amax > 0], np.full((amax > 0).sum(), 127))
+    assert s[5] == 0.0 and not q[5].any()
+    assert np.all(np.abs(q.astype(np.float64) * s[:, None] - x) <= s[:, None] * (0.5 + 1e-5) + 1e-30)
+    sm = rng.uniform(0.5, 2.0, 512).astype(np.float32)
+    q2, s2 = orc.s8_quantize_rows(x, smooth=sm)
+    q3, s3 = orc.s8_quantize_rows((x * sm).astype(np.float32))
+    assert same_bits(q2, q3) and same_bits(s2, s3)
+    qr, sr = orc.quantize_block_r2(x, block=512)
+    assert sr[5, 0] == 1.0
+    xh = rng.standard_normal((512, 2048)).astype(np.float16).astype(np.float32)
+    assert (orc.s8_quantize_rows(xh)[0] != orc.quantize_block_r2(xh, block=2048)[0]).any()  # 127 / amax vs 1 / (amax / 127)
+
+
+def test_gemm_s8_closed_form():
+    """The exact integer sum against numpy int64 products (a different implementation), and the two float32 products
+    in the stated order: (f * sx) * sw differs from f * (sx * sw) on some elements, so the order is pinned."""
+    rng = np.random.default_rng(4)
+    t, n, k = 13, 37, 640
+    xq = rng.integers(-127, 128, (t, k)).astype(np.int8)
+    wq = rng.integers(-127, 128, (n, k)).astype(np.int8)
+    sx = rng.uniform(1e-3, 1e-1, t).astype(np.float32)
+    sw = rng.uniform(1e-3, 1e-1, n).astype(np.float32)
+    y = orc.gemm_s8(xq, sx, wq, sw)
+    f = (xq.astype(np.int64) @ wq.T.astype(np.int64)).astype(np.float32)
+    assert same_bits(orc.gemm_s8(xq, np.ones(t, np.float32), wq, np.ones(n, np.float32)), f)
+    left = (f * sx[:, None]).astype(np.float32) * sw[None, :]
+    other = f * (sx[:, None] * sw[None, :]).astype(np.float32)
+    assert same_bits(y, left.astype(np.float32)) and (other != left).any()
+
+
 def test_r1_and_r2_differ_on_fp16_weights():
     # the two rules disagree on real data (rounding of w / s against w * (1 / s)): the packer must keep them apart
     rng = np.random.default_rng(0)
