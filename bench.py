@@ -348,6 +348,26 @@ def main():
             del w_o, q_o, s_o, x_o, y_o
         extra["other_groups_w8g_m15872"] = others
         log(f"other int8 groups (w8g, M=15872): {others}")
+        # ---- the per-channel int8 family (the reference's launch_gemm_s8 / launch_gemm_w8a16) at the MLP shapes ----
+        s8 = {}
+        for n_o, k_o in ((2 * I, H), (H, I)):
+            w_o = (torch.randn(n_o, k_o, generator=g2, device="cuda") * 0.02).half()
+            wq_o, sw_o = sm.s8_quantize_rows(w_o)
+            x_o = torch.randn(M_BIG, k_o, generator=g2, device="cuda").half()
+            xq_o, sx_o = sm.s8_quantize_rows(x_o)
+            ms_q = timed(torch, lambda: sm.s8_quantize_rows(x_o), 10, 2, stream)
+            ms_s8 = timed(torch, lambda: sm.gemm_s8(xq_o, sx_o, wq_o, sw_o), 10, 2, stream)
+            ms_a16 = timed(torch, lambda: sm.gemm_w8a16(x_o, wq_o, sw_o), 10, 2, stream)
+            ops = 2.0 * M_BIG * n_o * k_o
+            s8[f"{n_o}x{k_o}"] = {"gemm_s8_ms": round(ms_s8, 4), "gemm_s8_tops": round(ops / (ms_s8 * 1e-3) / 1e12, 1),
+                                  "gemm_s8_frac_int8_peak": round(ops / (ms_s8 * 1e-3) / 1e12 / PEAK["int8_tops"], 4),
+                                  "gemm_w8a16_ms": round(ms_a16, 4),
+                                  "gemm_w8a16_tflops": round(ops / (ms_a16 * 1e-3) / 1e12, 1),
+                                  "quantize_rows_us": round(ms_q * 1e3, 1),
+                                  "quantize_rows_gbs": round(M_BIG * k_o * 3 / (ms_q * 1e-3) / 1e9, 1)}
+            del w_o, wq_o, sw_o, x_o, xq_o, sx_o
+        extra["per_channel_int8_m15872"] = s8
+        log(f"per-channel int8 family (M=15872): {s8}")
 
     cpu = None
     if not args.no_cpu:
