@@ -407,14 +407,13 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
     // reads again.
     const auto step = [&](int kt, const Regs& r_next, Regs& r_free, auto first_t) {
         constexpr bool first = decltype(first_t)::value;
+        float ratio[2] = {1.0f, 1.0f};
         if constexpr (first) {
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
                 const float en = snext[j] > 0.0f ? snext[j] : e[j];
-                const float ratio = __fmul_rn(e[j], __builtin_amdgcn_rcpf(en));
+                ratio[j] = __fmul_rn(e[j], __builtin_amdgcn_rcpf(en));
                 e[j] = en;
-#pragma unroll
-                for (int i = 0; i < 4; ++i) acc[i][j] = acc[i][j] * ratio;
             }
             issue_scales(min(kt / SPG + 1, groups - 1));
         }
@@ -436,7 +435,22 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
-                for (int j = 0; j < 2; ++j) acc[i][j] = mfma32<XT>(a[i], b[j], acc[i][j]);
+                for (int j = 0; j < 2; ++j) {
+                    // a group's Horner rescale of each accumulator block right before its first MFMA of the group:
+                    // the multiplies of one block overlap the MFMA of the previous one
+                    if constexpr (first)
+                        if (st == 0) acc[i][j] = acc[i][j] * ratio[j];
+                    acc[i][j] = mfma32<XT>(a[i], b[j], acc[i][j]);
+                }
+        }
+        if constexpr (first) {
+            // the first substep's fragment reads, then each block's 16 rescale multiplies and its MFMA, in turn
+            __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            }
         }
         stage(kt + 1, r_next);
         __syncthreads();
