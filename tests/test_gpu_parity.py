@@ -642,6 +642,39 @@ def test_gemm_s8_full_size_sampled_rows(sm):
     assert same_bits(host(y[rows]), ref)
 
 
+def test_s8_family_row_invariance(sm):
+    """A row's bits depend only on that row, the weights and K (runner/cuda/tests/test_gemm_s8_kernels.cpp:281-304):
+    for gemm_s8 (float32 and binary16) the same rows computed in a batch of 700, in a slice of 37 at an offset and
+    one at a time give the same bits. gemm_w8a16 runs the w8g kernels, whose small-M path (T <= 64) rounds in another
+    order than the large-M kernels: slices of more than 64 rows give the same bits, smaller ones agree within the
+    parity bar. Zero activation rows give zeros."""
+    say("s8 family row invariance")
+    rng = np.random.default_rng(31)
+    t, n, k = 700, 320, 1280
+    x = rng.standard_normal((t, k)).astype(np.float16)
+    x[3] = 0
+    xt = dev(x)
+    xq, sx = sm.s8_quantize_rows(xt)
+    wq, sw = sm.s8_quantize_rows(dev((rng.standard_normal((n, k)) * 0.02).astype(np.float16)))
+    full = host(sm.gemm_s8(xq, sx, wq, sw))
+    full16 = host(sm.gemm_s8(xq, sx, wq, sw, y_dtype=torch.float16))
+    fa = host(sm.gemm_w8a16(xt, wq, sw))
+    assert not full[3].any() and not fa[3].any()
+    for lo, hi in ((300, 337), (699, 700), (0, 1)):
+        assert same_bits(host(sm.gemm_s8(xq[lo:hi], sx[lo:hi], wq, sw)), full[lo:hi]), (lo, hi)
+        assert same_bits(host(sm.gemm_s8(xq[lo:hi], sx[lo:hi], wq, sw, y_dtype=torch.float16)), full16[lo:hi]), (lo, hi)
+        ys = host(sm.gemm_w8a16(xt[lo:hi], wq, sw))
+        assert max_rel_over_rms(ys, fa[lo:hi].astype(np.float64)) < 2e-3, (lo, hi)
+    for lo, hi in ((0, 65), (300, 451), (635, 700)):
+        assert same_bits(host(sm.gemm_w8a16(xt[lo:hi], wq, sw)), fa[lo:hi]), (lo, hi)
+    # the remedy for callers that need the same bits at any batch size: config 0 forces the large-M w8g kernels
+    wg, sg = sm.quantize_group_s8(dev((rng.standard_normal((n, k)) * 0.02).astype(np.float16)))
+    xb = dev(x, torch.bfloat16)
+    big = host(sm.gemm_w8g(xb, wg, sg, config=0))
+    for lo, hi in ((300, 337), (699, 700), (0, 1)):
+        assert same_bits(host(sm.gemm_w8g(xb[lo:hi], wg, sg, config=0)), big[lo:hi]), (lo, hi)
+
+
 @pytest.mark.parametrize("t,n,k", [(100, 256, 1024), (16, 384, 2560), (5000, 4096, 256)])
 def test_gemm_w8a16_against_float64(sm, t, n, k):
     """binary16 x times per-channel int8 weights, against float64 of the dequantised weights (the reference test's
