@@ -119,6 +119,15 @@ SEPAL_HIP_API int32_t sepal_hip_gemm_q8(const int8_t* xq, size_t ld_x, const flo
 SEPAL_HIP_API int32_t sepal_hip_s8_quantize_rows(const void* x, int32_t x_type, size_t ld_x, const float* smooth, int8_t* q,
                                                  size_t ld_q, float* scales, size_t rows, size_t cols, void* stream);
 
+/* Calibration statistics of binary16 activations x [rows, ld_x] (one thread per column, rows in order: the same bits
+ * on every run). column_absmax: out[c] = max over the rows of |x[r, c]|. channel_stats adds into what is there:
+ * amax[c] = max(amax[c], max |x[r, c]|), sums[c] += sum |x[r, c]|, sums[cols + c] += sum x[r, c]^2, the sums in double.
+ * Replace launch_column_absmax / launch_channel_stats (runner/cuda/src/gemm_s8_kernels.hpp:36-41), the statistics the
+ * smoothing factors of sepal_hip_s8_quantize_rows come from. */
+SEPAL_HIP_API int32_t sepal_hip_column_absmax(const void* x, size_t ld_x, float* out, size_t rows, size_t cols, void* stream);
+SEPAL_HIP_API int32_t sepal_hip_channel_stats(const void* x, size_t ld_x, size_t rows, size_t cols, float* amax, double* sums,
+                                              void* stream);
+
 /* The int8-activation multiply with per-channel scales: Y[t, n] = (float(sum over K of xq[t,k] * wq[n,k]) * sx[t]) *
  * sw[n], the sum exact in int32 (int8 MFMA over the whole K), then two float32 products in that order. Y float32 or
  * binary16 (y_type; round to nearest even) [T, ld_y]. K a multiple of 128 (the reference allows 16), strides of X and W

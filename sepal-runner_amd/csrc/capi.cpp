@@ -254,6 +254,25 @@ int32_t sepal_hip_s8_quantize_rows(const void* x, int32_t x_type, size_t ld_x, c
     });
 }
 
+int32_t sepal_hip_column_absmax(const void* x, size_t ld_x, float* out, size_t rows, size_t cols, void* stream) {
+    return guarded([&] {
+        require(x != nullptr && out != nullptr, "column_absmax: null pointer");
+        require(ld_x >= cols && cols < 0x7FFFFFFFu, "column_absmax: stride below the column count");
+        if (cols == 0) return;
+        launch_column_stats(x, ld_x, rows, cols, out, nullptr, as_stream(stream));
+    });
+}
+
+int32_t sepal_hip_channel_stats(const void* x, size_t ld_x, size_t rows, size_t cols, float* amax, double* sums,
+                                void* stream) {
+    return guarded([&] {
+        require(x != nullptr && amax != nullptr && sums != nullptr, "channel_stats: null pointer");
+        require(ld_x >= cols && cols < 0x7FFFFFFFu, "channel_stats: stride below the column count");
+        if (cols == 0) return;
+        launch_column_stats(x, ld_x, rows, cols, amax, sums, as_stream(stream));
+    });
+}
+
 namespace {
 void check_s8_family(const char* who, const void* x, size_t ld_x, const void* w, size_t ld_w, const float* sw, const void* y,
                      int32_t y_type, size_t ld_y, size_t n, size_t k) {

@@ -47,6 +47,10 @@ void launch_gemm_s8(const GemmArgs& a, hipStream_t stream);
 void launch_s8_quantize_rows(const void* x, int x_type, std::size_t ld_x, const float* smooth, std::int8_t* q, std::size_t ld_q,
                              float* scales, std::size_t rows, std::size_t cols, hipStream_t stream);
 void launch_broadcast_scales(const float* sw, float* s, std::size_t n, std::size_t groups, hipStream_t stream);
+// Column statistics of binary16 x: sums null -> amax[c] = max |x[:, c]|; else amax[c] = max(amax[c], ...), sums[c] +=
+// sum |x|, sums[cols + c] += sum x^2 (double, rows in order).
+void launch_column_stats(const void* x, std::size_t ld_x, std::size_t rows, std::size_t cols, float* amax, double* sums,
+                         hipStream_t stream);
 void launch_f32_to_f16(const float* src, std::size_t ld_src, std::uint16_t* dst, std::size_t ld_dst, std::size_t rows,
                        std::size_t cols, hipStream_t stream);
 void launch_q8_group_sums(const GemmArgs& a, hipStream_t stream);

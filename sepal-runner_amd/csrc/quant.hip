@@ -356,6 +356,33 @@ __global__ void __launch_bounds__(256) s8_rows_kernel(const void* __restrict__ x
     }
 }
 
+// Calibration statistics of binary16 activations, one thread per column, the rows in order (so every run gives the
+// same bits): m = max |x[r, c]|; with STATS also a = sum |x[r, c]| and q = sum x[r, c]^2 in double, added into what
+// is there (runner/cuda/src/gemm_s8_kernels.cu:121-149).
+template <bool STATS>
+__global__ void __launch_bounds__(256) column_stats_kernel(const std::uint16_t* __restrict__ x, std::size_t ld_x, std::size_t rows,
+                                                           int cols, float* __restrict__ amax, double* __restrict__ sums) {
+    const int c = blockIdx.x * 256 + threadIdx.x;
+    if (c >= cols) return;
+    float m = 0.0f;
+    double a = 0.0, q = 0.0;
+    for (std::size_t r = 0; r < rows; ++r) {
+        const float v = f16_bits_to_f32(x[r * ld_x + c]);
+        m = fmaxf(m, fabsf(v));
+        if constexpr (STATS) {
+            a = __dadd_rn(a, static_cast<double>(fabsf(v)));
+            q = __dadd_rn(q, __dmul_rn(static_cast<double>(v), static_cast<double>(v)));
+        }
+    }
+    if constexpr (STATS) {
+        amax[c] = fmaxf(amax[c], m);
+        sums[c] = __dadd_rn(sums[c], a);
+        sums[cols + c] = __dadd_rn(sums[cols + c], q);
+    } else {
+        amax[c] = m;
+    }
+}
+
 // s[r][g] = sw[r] for g < groups: a per-channel scale as per-group scales
 __global__ void broadcast_scales_kernel(const float* __restrict__ sw, float* __restrict__ s, std::size_t n, std::size_t groups) {
     const std::size_t i = static_cast<std::size_t>(blockIdx.x) * 256 + threadIdx.x;
@@ -444,6 +471,15 @@ void launch_s8_quantize_rows(const void* x, int x_type, std::size_t ld_x, const 
     default: quant::s8_rows_kernel<SEPAL_HIP_F16><<<grid, block, 0, stream>>>(x, ld_x, smooth, q, ld_q, scales, c); break;
     }
     check_launch("s8 row quantizer launch");
+}
+
+void launch_column_stats(const void* x, std::size_t ld_x, std::size_t rows, std::size_t cols, float* amax, double* sums,
+                         hipStream_t stream) {
+    const dim3 grid(static_cast<unsigned>((cols + 255) / 256)), block(256);
+    const auto* xp = static_cast<const std::uint16_t*>(x);
+    if (sums == nullptr) quant::column_stats_kernel<false><<<grid, block, 0, stream>>>(xp, ld_x, rows, static_cast<int>(cols), amax, nullptr);
+    else quant::column_stats_kernel<true><<<grid, block, 0, stream>>>(xp, ld_x, rows, static_cast<int>(cols), amax, sums);
+    check_launch("column statistics launch");
 }
 
 void launch_broadcast_scales(const float* sw, float* s, std::size_t n, std::size_t groups, hipStream_t stream) {

@@ -65,12 +65,15 @@ def library() -> C.CDLL:
         L.sepal_hip_s8_quantize_rows.argtypes = [vp, i32, sz, vp, vp, sz, vp, sz, sz, vp]
         L.sepal_hip_gemm_s8.argtypes = [vp, sz, vp, vp, sz, vp, vp, i32, sz, sz, sz, sz, vp]
         L.sepal_hip_gemm_w8a16.argtypes = [vp, sz, vp, sz, vp, vp, i32, sz, sz, sz, sz, vp]
+        L.sepal_hip_column_absmax.argtypes = [vp, sz, vp, sz, sz, vp]
+        L.sepal_hip_channel_stats.argtypes = [vp, sz, sz, sz, vp, vp, vp]
         for name in ("sepal_hip_quantize_group_s8", "sepal_hip_quantize_gate_up_s8", "sepal_hip_gemm_w8g",
                      "sepal_hip_quantize_rows_s8", "sepal_hip_gemm_q8", "sepal_hip_q8_group_sums",
                      "sepal_hip_rmsnorm_rows", "sepal_hip_float_to_bf16", "sepal_hip_mlp_stack",
                      "sepal_hip_rmsnorm_quantize_rows", "sepal_hip_gemm_q8_swiglu_quantize",
                      "sepal_hip_weight_fingerprint", "sepal_hip_packed_save", "sepal_hip_packed_load",
-                     "sepal_hip_s8_quantize_rows", "sepal_hip_gemm_s8", "sepal_hip_gemm_w8a16"):
+                     "sepal_hip_s8_quantize_rows", "sepal_hip_gemm_s8", "sepal_hip_gemm_w8a16",
+                     "sepal_hip_column_absmax", "sepal_hip_channel_stats"):
             getattr(L, name).restype = i32
         L.sepal_hip_gemm_w8g_supports.restype = i32
         _lib = L
@@ -189,6 +192,21 @@ def s8_quantize_rows(x, smooth=None, stream=None):
     _check(library().sepal_hip_s8_quantize_rows(_ptr(x), _type_of(x), _ld(x), _ptr(smooth) if smooth is not None else None,
                                                 _ptr(q), _ld(q), _ptr(sc), rows, cols, _stream(stream)))
     return q, sc
+
+
+def column_absmax(x, stream=None):
+    """out[c] = max over the rows of |x[r, c]| for binary16 x [rows, cols]."""
+    torch = _torch()
+    rows, cols = x.shape
+    out = torch.empty(cols, dtype=torch.float32, device=x.device)
+    _check(library().sepal_hip_column_absmax(_ptr(x), _ld(x), _ptr(out), rows, cols, _stream(stream)))
+    return out
+
+
+def channel_stats(x, amax, sums, stream=None):
+    """Adds the statistics of binary16 x [rows, cols] into amax (float32 [cols]) and sums (float64 [2 cols])."""
+    rows, cols = x.shape
+    _check(library().sepal_hip_channel_stats(_ptr(x), _ld(x), rows, cols, _ptr(amax), _ptr(sums), _stream(stream)))
 
 
 def gemm_s8(xq, sx, wq, sw, y_dtype=None, stream=None):

@@ -111,6 +111,10 @@ def test_s8_family_refusals():
     assert L.sepal_hip_gemm_w8a16(FAKE, 256, FAKE, 256, None, FAKE, 0, 64, 4, 64, 256, None) == sm.EINVAL
     assert L.sepal_hip_gemm_w8a16(FAKE + 4, 256, FAKE, 256, FAKE, FAKE, 0, 64, 4, 64, 256, None) == sm.EINVAL
     assert L.sepal_hip_gemm_w8a16(FAKE, 256, FAKE, 256, FAKE, FAKE, 2, 64, 0, 64, 256, None) == sm.OK
+    # calibration statistics: stride below the columns, null buffers; zero columns is a no-op
+    assert L.sepal_hip_column_absmax(FAKE, 100, FAKE, 4, 200, None) == sm.EINVAL
+    assert L.sepal_hip_channel_stats(FAKE, 256, 4, 256, FAKE, None, None) == sm.EINVAL
+    assert L.sepal_hip_channel_stats(FAKE, 256, 4, 0, FAKE, FAKE, None) == sm.OK
 
 
 def test_packed_file_refusals():

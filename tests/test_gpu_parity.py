@@ -615,6 +615,27 @@ def test_s8_quantize_rows_bit_exact(sm, src):
         assert same_bits(host(q), qr) and same_bits(host(s), sr), (rows, cols, smooth)
 
 
+def test_calibration_statistics(sm):
+    """column_absmax and channel_stats against numpy: the maxima exactly, the double sums in row order (a sequential
+    cumulative sum) bit for bit, added into what the buffers held (runner/cuda/src/gemm_s8_kernels.cu:121-149)."""
+    say("calibration statistics")
+    rng = np.random.default_rng(41)
+    rows, cols = 1000, 300
+    x = rng.standard_normal((rows, cols)).astype(np.float16)
+    x[:, ::37] *= 40
+    xt = dev(x)
+    xf = x.astype(np.float32)
+    assert same_bits(host(sm.column_absmax(xt)), np.abs(xf).max(0))
+    prior_a = rng.uniform(0, 50, cols).astype(np.float32)
+    prior_s = rng.uniform(0, 10, 2 * cols)
+    amax, sums = dev(prior_a), torch.from_numpy(prior_s.copy()).cuda()
+    sm.channel_stats(xt, amax, sums)
+    x64 = xf.astype(np.float64)
+    want_a = np.maximum(prior_a, np.abs(xf).max(0))
+    want_s = prior_s + np.concatenate([np.cumsum(np.abs(x64), 0)[-1], np.cumsum(x64 * x64, 0)[-1]])
+    assert same_bits(host(amax), want_a) and same_bits(host(sums), want_s)
+
+
 @pytest.mark.parametrize("t,n,k", [(100, 200, 1024), (37, 66, 3584), (5, 40, 6144), (300, 130, 2048), (1, 8, 128)])
 def test_gemm_s8_bit_exact(sm, t, n, k):
     """y = (float(S) * sx) * sw bit for bit against the oracle (the reference test's shapes with K a multiple of 128),
