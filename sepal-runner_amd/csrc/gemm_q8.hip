@@ -84,8 +84,11 @@ __device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int& 
     tn = in_group / gm;
 }
 
-// 128-byte LDS rows of 8 chunks; chunk c of row r stored at c ^ (r & 7).
-__device__ __forceinline__ int sw8(int r) { return r & 7; }
+// 128-byte LDS rows of 8 chunks; chunk c of row r stored at c ^ ((r / 2) & 7). A 16-byte read is served 16 lanes at a
+// time, and a fragment read's 16 lanes take 16 consecutive rows: two rows share a 256-byte bank line, so (r & 1) picks
+// the half and (r / 2) & 7 the chunk, and the 16 lanes hit 16 different bank groups (with c ^ (r & 7), rows r and r + 8
+// collided: 2-way conflicts on every fragment read).
+__device__ __forceinline__ int sw8(int r) { return (r >> 1) & 7; }
 
 template <int EP, int YT, bool PER_TOKEN, int MODE>
 __global__ void __launch_bounds__(512) gemm_big(const Params p) {
