@@ -176,6 +176,8 @@ __global__ void __launch_bounds__(512) gemm_big(const Params p) {
     // other LDS buffer; one barrier. The loop body has no branches around loads, so the compiler's load counting stays
     // exact; a step past the last group only repeats loads.
     const auto step = [&](int g, const Set& cur, const Set& next, Set& free_, int ahead) {
+        // group g's weight scales, read before the issue below may reuse cur's registers (free_ == cur)
+        const float cur_ws[2] = {cur.ws[0], cur.ws[1]};
         issue(min(g + ahead, groups - 1), free_);
         if (g < groups) {
             const int buf = g & 1;
@@ -224,7 +226,7 @@ __global__ void __launch_bounds__(512) gemm_big(const Params p) {
                         const int rl = wm * 64 + i * 32 + 8 * (r / 4) + 4 * (lane / 32) + (r % 4);
                         const float xsv = PER_TOKEN ? 1.0f : lds_xs[buf][rl];
 #pragma unroll
-                        for (int j = 0; j < 2; ++j) acc[i][j][r] = chain<PER_TOKEN>(acc[i][j][r], sacc[i][j][r], cur.ws[j], xsv, g == 0);
+                        for (int j = 0; j < 2; ++j) acc[i][j][r] = chain<PER_TOKEN>(acc[i][j][r], sacc[i][j][r], cur_ws[j], xsv, g == 0);
                     }
             }
             if (g + 1 < groups) stage(buf ^ 1, next);
@@ -245,14 +247,16 @@ __global__ void __launch_bounds__(512) gemm_big(const Params p) {
             step(g + 2, s2, s0, s1, 2);  // g + 4 -> s1
         }
     } else {
-        // per-128 activation scales need more registers in the chain: two sets, group g + 1 loads while g multiplies
+        // per-128 activation scales need more registers in the chain: two sets. Group g's set is free once staged (at
+        // the end of step g - 1), so group g + 2 loads into it while g multiplies and g + 1 waits in the other set
         Set s0, s1;
         issue(0, s0);
+        issue(min(1, groups - 1), s1);
         stage(0, s0);
         __syncthreads();
         for (int g = 0; g < groups; g += 2) {
-            step(g, s0, s1, s1, 1);      // group g in s0; g + 1 -> s1 (staged at the end of this step)
-            step(g + 1, s1, s0, s0, 1);  // g + 2 -> s0
+            step(g, s0, s1, s0, 2);      // group g in s0 (scales kept), g + 1 in s1; g + 2 -> s0
+            step(g + 1, s1, s0, s1, 2);  // g + 1 in s1, g + 2 in s0; g + 3 -> s1
         }
     }
     if constexpr (MODE == MODE_SUMS) return;
