@@ -282,25 +282,43 @@ __global__ void __launch_bounds__(128 * WN) __attribute__((amdgpu_waves_per_eu(2
 }
 
 
-// ---- large-M kernel, 64-wide k steps with whole-line loads ----------------------------------------------------------
+// ---- large-M kernel, 64-wide k steps, X straight into LDS -----------------------------------------------------------
 //
-// The tile, waves and Horner scaling of gemm_big2, with K in steps of 64 and the global loads shaped for the memory
-// pipeline: one X load instruction of a wave covers 8 rows x 128 bytes (whole cache lines) and one W load 16 rows x 64
-// bytes, where 32-wide steps touched 32 rows x 32 bytes per instruction. The writing lane scatters its chunk into the
-// fragment-ordered LDS tile. Within a fragment, lane L's 16 bytes sit at slot L ^ ((2 st + L / 32) & 7), st the 16-wide
-// k substep, and each load instruction's lanes take rows such that every 16 lanes of a write, like every 16 lanes of
-// a fragment read, cover 16 different 16-byte bank groups. Two stages of 64 KB; the loads of step kt + 2 are issued
-// while step kt is multiplied.
+// The tile, waves and Horner scaling of gemm_big2, with K in steps of 64.
+//   X: buffer_load ... lds (16 bytes a lane) writes the step's 256 x 64 tile straight into LDS, row-major with 128-byte
+//      rows, chunk c of row r at slot c ^ ((r / 2) & 7): each 8 lanes of a load instruction read one whole cache line,
+//      and every 16 lanes of an MFMA fragment read (16 rows, one chunk) cover the 16 bank groups. Three X stages; the
+//      loads of step kt + 2 are issued while step kt is multiplied.
+//   W: the int8 bytes come to registers two steps ahead (16 rows x 64 bytes per instruction) and are widened into a
+//      fragment-ordered stage (lane L's 16 bytes at slot L ^ ((2 st + L / 32) & 7), st the 16-wide substep). Two
+//      stages.
+// The five stages are separate LDS arrays and the loop is unrolled over six steps, so that the compiler sees which
+// array each direct load writes: a fragment read waits only for loads into the array it reads. Each step publishes
+// its successor with a bare s_barrier after an explicit wait, since a workgroup release fence waits for every direct
+// load in flight, including the ones two steps ahead.
+template <int N>
+__device__ __forceinline__ void wait_vm_lgkm0() {
+    static_assert(N >= 0 && N < 64, "vmcnt");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4));  // vmcnt(N) lgkmcnt(0)
+}
+
 template <int XT, int EP, int YT>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) gemm_big3(const BigParams p) {
     constexpr int NW = 8, BN = 256, K3 = 64, SUB = K3 / 16, SPG = 128 / K3;
-    constexpr int XSTAGE = (BM / 32) * SUB * 1024, WSTAGE = (BN / 32) * SUB * 1024;
-    constexpr int XLD = BM * K3 * 2 / 16 / (64 * NW);  // X 16-byte chunks per thread per step (4)
+    constexpr int XSTAGE = BM * K3 * 2, WSTAGE = (BN / 32) * SUB * 1024;
+    constexpr int XLD = XSTAGE / 16 / (64 * NW);       // X direct loads per thread per step (4)
     constexpr int WLD = BN * K3 / 16 / (64 * NW);      // W 16-byte chunks per thread per step (2)
-    extern __shared__ __align__(16) unsigned char smem[];
-    lds_byte* lds = (lds_byte*)smem;
-    lds_byte* xs_base = lds;
-    lds_byte* ws_base = lds + 2 * XSTAGE;
+    __shared__ __align__(1024) unsigned char xs0[XSTAGE], xs1[XSTAGE], xs2[XSTAGE], ws0[WSTAGE], ws1[WSTAGE];
+    const auto xstage = [&](auto it) -> lds_byte* {
+        constexpr int i = decltype(it)::value;
+        if constexpr (i == 0) return (lds_byte*)xs0;
+        else if constexpr (i == 1) return (lds_byte*)xs1;
+        else return (lds_byte*)xs2;
+    };
+    const auto wstage = [&](auto it) -> lds_byte* {
+        if constexpr (decltype(it)::value == 0) return (lds_byte*)ws0;
+        else return (lds_byte*)ws1;
+    };
 
     const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
     const int wm = wave % 2, wn = wave / 2;
@@ -315,16 +333,17 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
         const_cast<unsigned short*>(p.x), 0, static_cast<int>(p.x_bytes), 0x00020000);
     const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<signed char*>(p.w), 0, static_cast<int>(p.w_bytes), 0x00020000);
-    // X: instruction i of wave w fills m-block mb = 2 i + w / 4, rows rs(w % 4) = 16 (rs / 2) + 4 (rs % 2) + {0..3} +
-    // {0, 8}; a lane loads 8 values (part) of one row
-    int xoff, xdst;
+    // X: direct load i of wave w fills LDS kilobyte w + 8 i = rows 8 w + 64 i + {0..7}; lane l writes slot l % 8 of row
+    // 8 w + 64 i + l / 8, which holds chunk (l % 8) ^ ((row / 2) & 7) = (l % 8) ^ ((4 w + l / 16) & 7)
+    int xoff;
     {
-        const int rs = wave % 4, part = lane % 8;
-        const int r = 16 * (rs / 2) + 4 * (rs % 2) + lane / 16 + 8 * ((lane / 8) % 2);  // row within the m-block
-        xoff = (m0 + 32 * (wave / 4) + r) * static_cast<int>(p.ld_x) * 2 + 16 * part;
-        const int L = r + 32 * (part % 2);
-        xdst = ((wave / 4) * SUB + part / 2) * 1024 + 16 * (L ^ part);  // + 2 i SUB KB for instruction i
+        const int r = 8 * wave + lane / 8, c = (lane % 8) ^ ((4 * wave + lane / 16) & 7);
+        xoff = (m0 + r) * static_cast<int>(p.ld_x) * 2 + 16 * c;
     }
+    // X fragment reads: lane l of m-block mb, substep st reads row 32 mb + l % 32, chunk 2 st + l / 32
+    int rx[SUB];
+#pragma unroll
+    for (int st = 0; st < SUB; ++st) rx[st] = (lane % 32) * 128 + 16 * ((2 * st + lane / 32) ^ ((lane / 2) & 7));
     // W: instruction i of wave w covers rows 32 w + 16 i + {0, 1, 8, 9} + 2 (lane / 16) (n-block w); a lane loads one
     // substep's 16 bytes and writes them widened as the fragment's two halves (slots L and L + 32)
     int woff, wdst0, wdst1;
@@ -336,7 +355,7 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
         wdst0 = frag + 16 * (L ^ (2 * q));             // + 256 i
         wdst1 = frag + 16 * ((L + 32) ^ (2 * q + 1));  // + 256 i
     }
-    int rd[SUB];  // this lane's slot in a fragment of substep st
+    int rd[SUB];  // this lane's slot in a W fragment of substep st
 #pragma unroll
     for (int st = 0; st < SUB; ++st) rd[st] = 16 * (lane ^ ((2 * st + lane / 32) & 7));
 
@@ -351,15 +370,17 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
     }
 
     struct Regs {
-        u32x4 x[XLD];
         u32x4 w[WLD];
     };
     float snext[2];
     const int xstride = 64 * static_cast<int>(p.ld_x) * 2, wstride = 16 * static_cast<int>(p.ld_w);
-    const auto issue = [&](int kt, Regs& r) {
+    const auto issue_x = [&](int kt, lds_byte* xd) {
 #pragma unroll
         for (int i = 0; i < XLD; ++i)
-            r.x[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xres, xoff, kt * K3 * 2 + i * xstride, 0));
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(xres, (__attribute__((address_space(3))) void*)(xd + (wave + 8 * i) * 1024), 16,
+                                                     xoff, kt * K3 * 2 + i * xstride, 0, 0);
+    };
+    const auto issue_w = [&](int kt, Regs& r) {
 #pragma unroll
         for (int i = 0; i < WLD; ++i)
             r.w[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wres, woff, kt * K3 + i * wstride, 0));
@@ -368,12 +389,7 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
         snext[0] = ssrc[0][g];
         snext[1] = ssrc[1][g];
     };
-    const auto stage = [&](int kt, const Regs& r) {
-        lds_byte* xd = xs_base + (kt % 2) * XSTAGE;
-#pragma unroll
-        for (int i = 0; i < XLD; ++i)
-            *reinterpret_cast<__attribute__((address_space(3))) u32x4*>(xd + xdst + i * 2 * SUB * 1024) = r.x[i];
-        lds_byte* wd = ws_base + (kt % 2) * WSTAGE;
+    const auto stage_w = [&](lds_byte* wd, const Regs& r) {
 #pragma unroll
         for (int i = 0; i < WLD; ++i) {
             unsigned o[8];
@@ -381,6 +397,14 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
             *reinterpret_cast<__attribute__((address_space(3))) u32x4*>(wd + wdst0 + 256 * i) = u32x4{o[0], o[1], o[2], o[3]};
             *reinterpret_cast<__attribute__((address_space(3))) u32x4*>(wd + wdst1 + 256 * i) = u32x4{o[4], o[5], o[6], o[7]};
         }
+    };
+    // the wait leaves the loads issued by the current step in flight (at most 2 scales, XLD X, WLD W) and covers every
+    // earlier one, among them the next step's X
+    const auto barrier = [&]() {
+        asm volatile("" ::: "memory");
+        wait_vm_lgkm0<2 + XLD + WLD>();
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
     };
 
     f32x16 acc[4][2];
@@ -392,55 +416,69 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
     const int groups = KT / SPG;
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
     Regs r0, r1;
     issue_scales(0);
-    issue(0, r0);
-    issue(min(1, KT - 1), r1);
-    stage(0, r0);
-    __syncthreads();
+    issue_x(0, xstage(I0{}));
+    issue_x(min(1, KT - 1), xstage(I1{}));
+    __builtin_amdgcn_sched_barrier(0);
+    issue_w(0, r0);
+    issue_w(min(1, KT - 1), r1);
+    __builtin_amdgcn_sched_barrier(0);
+    stage_w(wstage(I0{}), r0);
+    asm volatile("" ::: "memory");
+    wait_vm_lgkm0<WLD>();  // everything but step 1's W (X of steps 0 and 1 included)
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
     float e[2] = {snext[0] > 0.0f ? snext[0] : 1.0f, snext[1] > 0.0f ? snext[1] : 1.0f};
 
-    // One step: at a group's first step the Horner rescale with the group's scales (loaded one group ahead), then the
-    // next group's scales are issued; the loads of step kt + 2 into the registers freed by step kt; the multiply of
-    // step kt; step kt + 1's operands into their stage; one barrier. Two register sets alternate, so the loop runs one
-    // group (two steps) per iteration. Loads past the end repeat the last step (clamped) and land in a stage nothing
-    // reads again.
-    const auto step = [&](int kt, const Regs& r_next, Regs& r_free, auto first_t) {
-        constexpr bool first = decltype(first_t)::value;
+    // Step kt (j = kt mod 6): at a group's first step the Horner rescale with the group's scales (loaded one group
+    // ahead), then the next group's scales are issued; the direct X loads of step kt + 2 into X stage (j + 2) mod 3 (last
+    // read by step kt - 1); step kt + 2's W into the registers freed by step kt; the multiply of step kt from X stage
+    // j mod 3 and W stage j mod 2; step kt + 1's W into its stage; one barrier. Loads past the end repeat the last step
+    // (clamped) and land in stages nothing reads again.
+    const auto step = [&](int kt, auto jt) {
+        constexpr int j = decltype(jt)::value;
+        constexpr bool first = j % 2 == 0;
+        Regs& r_next = j % 2 == 0 ? r1 : r0;
+        Regs& r_free = j % 2 == 0 ? r0 : r1;
+        const lds_byte* xs = xstage(std::integral_constant<int, j % 3>{});
+        const lds_byte* ws = wstage(std::integral_constant<int, j % 2>{});
         float ratio[2] = {1.0f, 1.0f};
         if constexpr (first) {
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const float en = snext[j] > 0.0f ? snext[j] : e[j];
-                ratio[j] = __fmul_rn(e[j], __builtin_amdgcn_rcpf(en));
-                e[j] = en;
+            for (int q = 0; q < 2; ++q) {
+                const float en = snext[q] > 0.0f ? snext[q] : e[q];
+                ratio[q] = __fmul_rn(e[q], __builtin_amdgcn_rcpf(en));
+                e[q] = en;
             }
             issue_scales(min(kt / SPG + 1, groups - 1));
         }
-        issue(min(kt + 2, KT - 1), r_free);
+        issue_x(min(kt + 2, KT - 1), xstage(std::integral_constant<int, (j + 2) % 3>{}));
+        __builtin_amdgcn_sched_barrier(0);
+        issue_w(min(kt + 2, KT - 1), r_free);
         // keep the loads at the top of the step, in this order: the wait for a step's operands then leaves the later
         // steps' loads in flight
         __builtin_amdgcn_sched_barrier(0);
-        const lds_byte* xs = xs_base + (kt % 2) * XSTAGE;
-        const lds_byte* ws = ws_base + (kt % 2) * WSTAGE;
 #pragma unroll
         for (int st = 0; st < SUB; ++st) {
             u32x4 a[4], b[2];
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-                a[i] = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(xs + ((wm * 4 + i) * SUB + st) * 1024 + rd[st]);
+                a[i] = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(xs + (wm * 4 + i) * 4096 + rx[st]);
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
-                b[j] = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(ws + (nbj[j] * SUB + st) * 1024 + rd[st]);
+            for (int q = 0; q < 2; ++q)
+                b[q] = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(ws + (nbj[q] * SUB + st) * 1024 + rd[st]);
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
-                for (int j = 0; j < 2; ++j) {
+                for (int q = 0; q < 2; ++q) {
                     // a group's Horner rescale of each accumulator block right before its first MFMA of the group:
                     // the multiplies of one block overlap the MFMA of the previous one
                     if constexpr (first)
-                        if (st == 0) acc[i][j] = acc[i][j] * ratio[j];
-                    acc[i][j] = mfma32<XT>(a[i], b[j], acc[i][j]);
+                        if (st == 0) acc[i][q] = acc[i][q] * ratio[q];
+                    acc[i][q] = mfma32<XT>(a[i], b[q], acc[i][q]);
                 }
         }
         if constexpr (first) {
@@ -452,14 +490,29 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
             }
         }
-        stage(kt + 1, r_next);
-        __syncthreads();
+        stage_w(wstage(std::integral_constant<int, (j + 1) % 2>{}), r_next);
+        barrier();
     };
     static_assert(SPG == 2, "two steps per group");
-    for (int kt = 0; kt < KT; kt += 2) {
-        step(kt, r1, r0, std::true_type{});        // R1 holds step kt+1, step kt+2 -> R0
-        step(kt + 1, r0, r1, std::false_type{});   // R0 holds kt+2, kt+3 -> R1
+    int kt = 0;
+    for (; kt + 6 <= KT; kt += 6) {
+        step(kt, std::integral_constant<int, 0>{});
+        step(kt + 1, std::integral_constant<int, 1>{});
+        step(kt + 2, std::integral_constant<int, 2>{});
+        step(kt + 3, std::integral_constant<int, 3>{});
+        step(kt + 4, std::integral_constant<int, 4>{});
+        step(kt + 5, std::integral_constant<int, 5>{});
     }
+    if (kt + 2 <= KT) {
+        step(kt, std::integral_constant<int, 0>{});
+        step(kt + 1, std::integral_constant<int, 1>{});
+        if (kt + 4 <= KT) {
+            step(kt + 2, std::integral_constant<int, 2>{});
+            step(kt + 3, std::integral_constant<int, 3>{});
+        }
+    }
+    // no direct load may still be writing LDS when the block ends
+    wait_vmcnt<0>();
 
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -479,8 +532,6 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
         }
     }
 }
-
-constexpr std::size_t lds_bytes3() { return 2 * static_cast<std::size_t>((BM / 32) * 4 + (256 / 32) * 4) * 1024; }
 
 template <int WN>
 constexpr std::size_t lds_bytes() {
@@ -521,17 +572,7 @@ inline int device_cus() {
 
 template <int XT, int EP, int YT>
 void launch_big3(const BigParams& p, hipStream_t stream) {
-    const auto kernel = v2::gemm_big3<XT, EP, YT>;
-    constexpr std::size_t lds = v2::lds_bytes3();
-    static_assert(lds <= (160u << 10), "LDS of one CU");
-    static bool raised = false;
-    if (!raised) {
-        if (hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                static_cast<int>(lds)) != hipSuccess)
-            throw LaunchError("gemm_w8g large-M: hipFuncSetAttribute(MaxDynamicSharedMemorySize) failed");
-        raised = true;
-    }
-    kernel<<<dim3(p.tiles_m * p.tiles_n), dim3(512), lds, stream>>>(p);
+    v2::gemm_big3<XT, EP, YT><<<dim3(p.tiles_m * p.tiles_n), dim3(512), 0, stream>>>(p);
 }
 
 template <int XT, int EP, int YT>
