@@ -9,9 +9,9 @@
 // Every step is one IEEE operation in the reference's order, so the large-M path equals cpu-q8 bit for bit.
 //
 // Large-M path: 128 x 256 tiles of 8 waves, each 64 x 64 outputs (2 x 2 blocks of MFMA 32x32x32 i8); K in steps of
-// one group (128 bytes) through a double-buffered LDS tile, the loads of a group issued two groups ahead into three
-// rotating register sets; the int32 sums of a group are turned into the float chain in registers before the next
-// group starts (a second set of accumulators holds the chain).
+// one group (128 bytes) through three LDS stages, filled straight from global memory (global_load_lds, whole 128-byte
+// rows per 8 lanes) two groups ahead; the int32 sums of a group are turned into the float chain in registers before
+// the next group starts (a second set of accumulators holds the chain).
 // Small-M path: stream.hip (MFMA 16x16x64 i8; a split of K keeps the sums exact but adds the splits' partial chains in
 // split order, within tolerance, not bit for bit).
 #include "common.hpp"
@@ -90,14 +90,39 @@ __device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int& 
 // collided: 2-way conflicts on every fragment read).
 __device__ __forceinline__ int sw8(int r) { return (r >> 1) & 7; }
 
+// s_waitcnt with the vector memory counter at N and the LDS counter at 0 (gfx9 encoding: vmcnt[3:0] bits 3:0,
+// vmcnt[5:4] bits 15:14, expcnt bits 6:4 left at its maximum, lgkmcnt bits 11:8).
+template <int N>
+__device__ __forceinline__ void wait_vm_lgkm0() {
+    static_assert(N >= 0 && N < 64, "vmcnt");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4));
+}
+
+typedef __attribute__((address_space(3))) void lds_void;
+typedef const __attribute__((address_space(1))) void global_void;
+
 template <int EP, int YT, bool PER_TOKEN, int MODE>
 __global__ void __launch_bounds__(512) gemm_big(const Params p) {
-    constexpr int BM = 128, BN = 256, NT = 512;
-    constexpr int XCH = BM * 8 / NT;   // 2 chunks of 16 bytes per thread and group
-    constexpr int WCH = BN * 8 / NT;   // 4
-    __shared__ __align__(16) u32x4 lds_x[2][BM * 8];
-    __shared__ __align__(16) u32x4 lds_w[2][BN * 8];
+    constexpr int BM = 128, BN = 256;
+    constexpr int XDMA = BM / 64, WDMA = BN / 64;  // direct loads per thread and group (8 rows of 128 bytes each)
+    constexpr int NSC = MODE == MODE_CHAIN ? (PER_TOKEN ? 2 : 3) : 0;  // scale loads per thread and group
+    // Three stages of each operand, each its own LDS array: the compiler then knows which array a direct load writes,
+    // and a fragment read waits only for loads into the array it reads.
+    __shared__ __align__(1024) u32x4 lx0[BM * 8], lx1[BM * 8], lx2[BM * 8];
+    __shared__ __align__(1024) u32x4 lw0[BN * 8], lw1[BN * 8], lw2[BN * 8];
     __shared__ float lds_xs[2][BM];
+    const auto xstage = [&](auto it) -> u32x4* {
+        constexpr int i = decltype(it)::value;
+        if constexpr (i == 0) return lx0;
+        else if constexpr (i == 1) return lx1;
+        else return lx2;
+    };
+    const auto wstage = [&](auto it) -> u32x4* {
+        constexpr int i = decltype(it)::value;
+        if constexpr (i == 0) return lw0;
+        else if constexpr (i == 1) return lw1;
+        else return lw2;
+    };
 
     const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
     const int wm = wave % 2, wn = wave / 2;
@@ -106,22 +131,18 @@ __global__ void __launch_bounds__(512) gemm_big(const Params p) {
     const int m0 = tm * BM, n0 = tn * BN;
     const int groups = p.k / 128;
 
-    // ---- per-thread sources (clamped: rows past T or N repeat the last row; their outputs are never stored) ----
-    const signed char* xsrc[XCH];
-    const signed char* wsrc[WCH];
-    int xdst[XCH], wdst[WCH];
+    // ---- direct loads: load e of wave w fills LDS kilobyte w + 8 e = rows 8 w + 64 e + {0..7} of the stage; lane l
+    // writes slot l % 8 of row 8 w + 64 e + l / 8, which holds chunk (l % 8) ^ sw8(row) = (l % 8) ^ ((4 w + l / 16) & 7).
+    // Sources are clamped: rows past T or N repeat the last row; their outputs are never stored.
+    const int chunk = (lane % 8) ^ ((4 * wave + lane / 16) & 7);
+    const signed char* xsrc[XDMA];
+    const signed char* wsrc[WDMA];
 #pragma unroll
-    for (int e = 0; e < XCH; ++e) {
-        const int id = tid + e * NT, row = id / 8, c = id % 8;
-        xsrc[e] = p.x + static_cast<std::size_t>(min(m0 + row, p.t - 1)) * p.ld_x + 16 * c;
-        xdst[e] = row * 8 + (c ^ sw8(row));
-    }
+    for (int e = 0; e < XDMA; ++e)
+        xsrc[e] = p.x + static_cast<std::size_t>(min(m0 + 8 * wave + 64 * e + lane / 8, p.t - 1)) * p.ld_x + 16 * chunk;
 #pragma unroll
-    for (int e = 0; e < WCH; ++e) {
-        const int id = tid + e * NT, row = id / 8, c = id % 8;
-        wsrc[e] = p.w + static_cast<std::size_t>(min(n0 + row, p.n - 1)) * p.ld_w + 16 * c;
-        wdst[e] = row * 8 + (c ^ sw8(row));
-    }
+    for (int e = 0; e < WDMA; ++e)
+        wsrc[e] = p.w + static_cast<std::size_t>(min(n0 + 8 * wave + 64 * e + lane / 8, p.n - 1)) * p.ld_w + 16 * chunk;
     const float* xs_row = p.xs + static_cast<std::size_t>(min(m0 + (tid % BM), p.t - 1)) * p.ld_xs;
 
     const int ib = wn / 2, hh = wn % 2;
@@ -134,31 +155,36 @@ __global__ void __launch_bounds__(512) gemm_big(const Params p) {
         wsrow[j] = p.ws + static_cast<std::size_t>(min(col[j], p.n - 1)) * p.ld_ws;
     }
 
-    // one group's operands and scales, in registers; the sets rotate (the loads of group g + 2, or g + 1, are issued
-    // while group g is multiplied)
+    // one group's scales, in registers; three sets rotate with the stages (group g's in set g mod 3)
     struct Set {
-        u32x4 x[XCH], w[WCH];
         float xs, ws[2];
     };
-    const auto issue = [&](int g, Set& s) {
+    const auto issue = [&](int g, u32x4* xd, u32x4* wd, Set& s) {
         const std::size_t k0 = static_cast<std::size_t>(g) * 128;
 #pragma unroll
-        for (int e = 0; e < XCH; ++e) s.x[e] = *reinterpret_cast<const u32x4*>(xsrc[e] + k0);
+        for (int e = 0; e < XDMA; ++e)
+            __builtin_amdgcn_global_load_lds((global_void*)(xsrc[e] + k0), (lds_void*)(xd + (wave + 8 * e) * 64), 16, 0, 0);
 #pragma unroll
-        for (int e = 0; e < WCH; ++e) s.w[e] = *reinterpret_cast<const u32x4*>(wsrc[e] + k0);
+        for (int e = 0; e < WDMA; ++e)
+            __builtin_amdgcn_global_load_lds((global_void*)(wsrc[e] + k0), (lds_void*)(wd + (wave + 8 * e) * 64), 16, 0, 0);
         if constexpr (!PER_TOKEN && MODE == MODE_CHAIN) s.xs = xs_row[g >> p.act_shift];
         if constexpr (MODE == MODE_CHAIN) {
             s.ws[0] = wsrow[0][g];
             s.ws[1] = wsrow[1][g];
         }
     };
-    const auto stage = [&](int buf, const Set& s) {
-#pragma unroll
-        for (int e = 0; e < XCH; ++e) lds_x[buf][xdst[e]] = s.x[e];
-#pragma unroll
-        for (int e = 0; e < WCH; ++e) lds_w[buf][wdst[e]] = s.w[e];
+    // per-128 activation scales of the next group into their LDS buffer
+    const auto stage_xs = [&](int buf, const Set& s) {
         if constexpr (!PER_TOKEN && MODE == MODE_CHAIN)
             if (tid < BM) lds_xs[buf][tid] = s.xs;
+    };
+    // the wait leaves the loads issued by the current step in flight and covers every earlier one, among them the next
+    // group's operands; a workgroup release fence would also wait for the loads two groups ahead
+    const auto barrier = [&]() {
+        asm volatile("" ::: "memory");
+        wait_vm_lgkm0<XDMA + WDMA + NSC>();
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
     };
 
     float acc[2][2][16];
@@ -171,18 +197,23 @@ __global__ void __launch_bounds__(512) gemm_big(const Params p) {
     const i32x16 zero16 = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
     i32x16 tot[2][2] = {{zero16, zero16}, {zero16, zero16}};  // MODE_WHOLE: the running int32 sums
 
-    // One group: issue group g + ahead's loads (clamped; the set they go to was staged and its scales used at earlier
-    // steps); the exact int32 sums of group g; its link of the scale chain (or the sums out); stage group g + 1 into the
-    // other LDS buffer; one barrier. The loop body has no branches around loads, so the compiler's load counting stays
-    // exact; a step past the last group only repeats loads.
-    const auto step = [&](int g, const Set& cur, const Set& next, Set& free_, int ahead) {
-        // group g's weight scales, read before the issue below may reuse cur's registers (free_ == cur)
-        const float cur_ws[2] = {cur.ws[0], cur.ws[1]};
-        issue(min(g + ahead, groups - 1), free_);
+    // Group g (j = g mod 3): issue group g + 2's loads (clamped) into stage (j + 2) mod 3, last read by group g - 1; the
+    // exact int32 sums of group g from stage j; its link of the scale chain (or the sums out); group g + 1's per-128
+    // activation scales into LDS; one barrier. The loads are issued at every step, past the last group too (repeats
+    // into stages nothing reads again), so the wait count of the barrier stays exact.
+    Set s0, s1, s2;
+    const auto step = [&](int g, auto jt) {
+        constexpr int j = decltype(jt)::value;
+        Set& cur = j == 0 ? s0 : (j == 1 ? s1 : s2);
+        Set& next = j == 0 ? s1 : (j == 1 ? s2 : s0);
+        Set& free_ = j == 0 ? s2 : (j == 1 ? s0 : s1);
+        issue(min(g + 2, groups - 1), xstage(std::integral_constant<int, (j + 2) % 3>{}),
+              wstage(std::integral_constant<int, (j + 2) % 3>{}), free_);
+        __builtin_amdgcn_sched_barrier(0);
         if (g < groups) {
             const int buf = g & 1;
-            const u32x4* tx = lds_x[buf];
-            const u32x4* tw = lds_w[buf];
+            const u32x4* tx = xstage(std::integral_constant<int, j>{});
+            const u32x4* tw = wstage(std::integral_constant<int, j>{});
             i32x16 sacc[2][2];
 #pragma unroll
             for (int st = 0; st < 4; ++st) {
@@ -194,29 +225,32 @@ __global__ void __launch_bounds__(512) gemm_big(const Params p) {
                     a[i] = tx[row * 8 + (c ^ sw8(row))];
                 }
 #pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    const int row = colrel[j];
-                    b[j] = tw[row * 8 + (c ^ sw8(row))];
+                for (int q = 0; q < 2; ++q) {
+                    const int row = colrel[q];
+                    b[q] = tw[row * 8 + (c ^ sw8(row))];
                 }
 #pragma unroll
                 for (int i = 0; i < 2; ++i)
 #pragma unroll
-                    for (int j = 0; j < 2; ++j) {
-                        if constexpr (MODE == MODE_WHOLE) tot[i][j] = mfma_i8_32(a[i], b[j], tot[i][j]);
-                        else sacc[i][j] = mfma_i8_32(a[i], b[j], st == 0 ? zero16 : sacc[i][j]);
+                    for (int q = 0; q < 2; ++q) {
+                        if constexpr (MODE == MODE_WHOLE) tot[i][q] = mfma_i8_32(a[i], b[q], tot[i][q]);
+                        else sacc[i][q] = mfma_i8_32(a[i], b[q], st == 0 ? zero16 : sacc[i][q]);
                     }
             }
             if constexpr (MODE == MODE_WHOLE) {
             } else if constexpr (MODE == MODE_SUMS) {
+                // the row base is opaque here, so that the 64 store addresses are not hoisted out of the loop (spills)
+                int mb = m0;
+                asm volatile("" : "+s"(mb));
 #pragma unroll
                 for (int i = 0; i < 2; ++i)
 #pragma unroll
                     for (int r = 0; r < 16; ++r) {
-                        const int row = m0 + wm * 64 + i * 32 + 8 * (r / 4) + 4 * (lane / 32) + (r % 4);
+                        const int row = mb + wm * 64 + i * 32 + 8 * (r / 4) + 4 * (lane / 32) + (r % 4);
                         if (row >= p.t) continue;
 #pragma unroll
-                        for (int j = 0; j < 2; ++j)
-                            if (col[j] < p.n) p.sums[(static_cast<std::size_t>(g) * p.t + row) * p.n + col[j]] = sacc[i][j][r];
+                        for (int q = 0; q < 2; ++q)
+                            if (col[q] < p.n) p.sums[(static_cast<std::size_t>(g) * p.t + row) * p.n + col[q]] = sacc[i][q][r];
                     }
             } else {
 #pragma unroll
@@ -226,39 +260,30 @@ __global__ void __launch_bounds__(512) gemm_big(const Params p) {
                         const int rl = wm * 64 + i * 32 + 8 * (r / 4) + 4 * (lane / 32) + (r % 4);
                         const float xsv = PER_TOKEN ? 1.0f : lds_xs[buf][rl];
 #pragma unroll
-                        for (int j = 0; j < 2; ++j) acc[i][j][r] = chain<PER_TOKEN>(acc[i][j][r], sacc[i][j][r], cur_ws[j], xsv, g == 0);
+                        for (int q = 0; q < 2; ++q) acc[i][q][r] = chain<PER_TOKEN>(acc[i][q][r], sacc[i][q][r], cur.ws[q], xsv, g == 0);
                     }
             }
-            if (g + 1 < groups) stage(buf ^ 1, next);
+            if (g + 1 < groups) stage_xs(buf ^ 1, next);
         }
-        __syncthreads();
+        barrier();
     };
 
-    if constexpr (PER_TOKEN) {
-        // three sets: group g + 2 loads while g multiplies
-        Set s0, s1, s2;
-        issue(0, s0);
-        issue(min(1, groups - 1), s1);
-        stage(0, s0);
-        __syncthreads();
-        for (int g = 0; g < groups; g += 3) {
-            step(g, s0, s1, s2, 2);      // group g in s0, g + 1 in s1; g + 2 -> s2
-            step(g + 1, s1, s2, s0, 2);  // g + 3 -> s0
-            step(g + 2, s2, s0, s1, 2);  // g + 4 -> s1
-        }
-    } else {
-        // per-128 activation scales need more registers in the chain: two sets. Group g's set is free once staged (at
-        // the end of step g - 1), so group g + 2 loads into it while g multiplies and g + 1 waits in the other set
-        Set s0, s1;
-        issue(0, s0);
-        issue(min(1, groups - 1), s1);
-        stage(0, s0);
-        __syncthreads();
-        for (int g = 0; g < groups; g += 2) {
-            step(g, s0, s1, s0, 2);      // group g in s0 (scales kept), g + 1 in s1; g + 2 -> s0
-            step(g + 1, s1, s0, s1, 2);  // g + 1 in s1, g + 2 in s0; g + 3 -> s1
-        }
+    issue(0, lx0, lw0, s0);
+    issue(min(1, groups - 1), lx1, lw1, s1);
+    __builtin_amdgcn_sched_barrier(0);
+    stage_xs(0, s0);
+    asm volatile("" ::: "memory");
+    wait_vm_lgkm0<XDMA + WDMA + NSC>();  // group 0's loads
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    for (int g = 0; g < groups; g += 3) {
+        step(g, std::integral_constant<int, 0>{});
+        step(g + 1, std::integral_constant<int, 1>{});
+        step(g + 2, std::integral_constant<int, 2>{});
     }
+    // the repeated loads of the last steps may still be writing LDS: drain them before the block reuses or leaves it
+    wait_vm_lgkm0<0>();
+    __syncthreads();
     if constexpr (MODE == MODE_SUMS) return;
     if constexpr (MODE == MODE_WHOLE) {
         // y = (float(S) * sx[t]) * sw[n], float32 or binary16 (round to nearest even)
@@ -282,37 +307,43 @@ __global__ void __launch_bounds__(512) gemm_big(const Params p) {
     }
 
     if constexpr (EP == kSwigluQ8) {
-        // The tile's 128 output columns are one quantization block. H goes through LDS (the W tile's space, free after
-        // the last step's barrier): 128 rows of 512 bytes, 16-byte chunk c of row r at c ^ (r % 16). Thread (row, q)
-        // then takes 32 columns of one row: the max over them, the four quarters combined through LDS, the scale, and
-        // 32 int8 values stored as two 16-byte chunks. max is exact in any order, so this equals quantize_rows on the
-        // float32 H (rule RECIPROCAL).
-        float* hb = reinterpret_cast<float*>(&lds_w[0][0]);
+        // The tile's 128 output columns are one quantization block. H goes through LDS (the first W stage, free after
+        // the loop) in two halves of 64 columns: 128 rows of 256 bytes, 16-byte chunk c of row r at c ^ (r % 16). Thread
+        // (row, q) takes 16 columns of one row from each half: the max over them, the four quarters combined through
+        // LDS, the scale, and 32 int8 values stored as two 16-byte chunks. max is exact in any order, so this equals
+        // quantize_rows on the float32 H (rule RECIPROCAL).
+        float* hb = reinterpret_cast<float*>(lw0);
         __shared__ float lds_amax[4][BM];
-        const int c = 64 * ib + 32 * hh + lane % 32;  // this lane's column within the block
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int rl = wm * 64 + i * 32 + 8 * (r / 4) + 4 * (lane / 32) + (r % 4);
-                float v0 = acc[i][0][r], v1 = acc[i][1][r];
-                if constexpr (PER_TOKEN) {
-                    const float xs = p.xs[static_cast<std::size_t>(min(m0 + rl, p.t - 1)) * p.ld_xs];
-                    v0 = __fmul_rn(v0, xs);
-                    v1 = __fmul_rn(v1, xs);
-                }
-                hb[rl * 128 + (((c / 4) ^ (rl % 16)) * 4) + c % 4] = swiglu_cephes(v0, v1);
-            }
-        __syncthreads();
+        const int c = 32 * hh + lane % 32;  // this lane's column within its half (half ib)
         const int row_l = tid % BM, quarter = tid / BM;
         float hv[32];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const float4 v = *reinterpret_cast<const float4*>(hb + row_l * 128 + (((8 * quarter + j) ^ (row_l % 16)) * 4));
-            hv[4 * j] = v.x;
-            hv[4 * j + 1] = v.y;
-            hv[4 * j + 2] = v.z;
-            hv[4 * j + 3] = v.w;
+        for (int half = 0; half < 2; ++half) {
+            if (ib == half) {
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int rl = wm * 64 + i * 32 + 8 * (r / 4) + 4 * (lane / 32) + (r % 4);
+                        float v0 = acc[i][0][r], v1 = acc[i][1][r];
+                        if constexpr (PER_TOKEN) {
+                            const float xs = p.xs[static_cast<std::size_t>(min(m0 + rl, p.t - 1)) * p.ld_xs];
+                            v0 = __fmul_rn(v0, xs);
+                            v1 = __fmul_rn(v1, xs);
+                        }
+                        hb[rl * 64 + (((c / 4) ^ (rl % 16)) * 4) + c % 4] = swiglu_cephes(v0, v1);
+                    }
+            }
+            __syncthreads();
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float4 v = *reinterpret_cast<const float4*>(hb + row_l * 64 + (((4 * quarter + j) ^ (row_l % 16)) * 4));
+                hv[16 * half + 4 * j] = v.x;
+                hv[16 * half + 4 * j + 1] = v.y;
+                hv[16 * half + 4 * j + 2] = v.z;
+                hv[16 * half + 4 * j + 3] = v.w;
+            }
+            __syncthreads();
         }
         float m = 0.0f;
 #pragma unroll
@@ -340,9 +371,9 @@ __global__ void __launch_bounds__(512) gemm_big(const Params p) {
                     packed[j] |= (static_cast<unsigned>(static_cast<int>(qv)) & 0xFFu) << (8 * e);
                 }
             }
-            signed char* dst = static_cast<signed char*>(p.y) + static_cast<std::size_t>(row) * p.ld_y + n0 / 2 + 32 * quarter;
+            signed char* dst = static_cast<signed char*>(p.y) + static_cast<std::size_t>(row) * p.ld_y + n0 / 2 + 16 * quarter;
             *reinterpret_cast<u32x4*>(dst) = u32x4{packed[0], packed[1], packed[2], packed[3]};
-            *reinterpret_cast<u32x4*>(dst + 16) = u32x4{packed[4], packed[5], packed[6], packed[7]};
+            *reinterpret_cast<u32x4*>(dst + 64) = u32x4{packed[4], packed[5], packed[6], packed[7]};
             if (quarter == 0) p.ys[static_cast<std::size_t>(row) * p.ld_ys + n0 / 256] = scale;
         }
         return;
