@@ -149,7 +149,7 @@ __global__ void __launch_bounds__(256) quantize_rows_token_kernel(const void* __
 // at once) into LDS, then lanes 0..31 run the reference's 32 accumulator chains from LDS: lane L is accumulator register
 // L / 8, lane L % 8, and adds x[c]^2 for c = L, L + 32, ... in order (then, for a tail of 8 to 31 columns, lanes 0..7
 // take the remaining groups of 8). The combine and the normalising pass follow the reference.
-constexpr int kNormSeg = 2048;  // columns per LDS segment and wave
+constexpr int kNormSeg = 2560;  // columns per LDS segment and wave (a whole row of the MLP width)
 
 // OUT: NORM_STORE writes y (YT); NORM_Q_TOKEN and NORM_Q_128 round each value to bfloat16 (y, when not null, gets those
 // bits) and quantize the rounded values as quantize_rows does (one scale per row, or per 128 columns).
@@ -168,11 +168,12 @@ __global__ void __launch_bounds__(256) rmsnorm_kernel(const float* __restrict__ 
     float* buf = seg[wave];
     float a = 0.0f;
     const int full = cols / 32 * 32;  // columns taken by the 32-wide loop
+    // len is a multiple of 8: 8-column pieces, one per lane and round, loads first. When the row is one segment, v
+    // still holds it for the normalising pass.
+    constexpr int R = kNormSeg / 8 / 64;
+    float4 v[R][2];
     for (int s0 = 0; s0 < cols; s0 += kNormSeg) {
         const int len = min(kNormSeg, cols - s0);
-        // len is a multiple of 8: 8-column pieces, one per lane and round, loads first
-        constexpr int R = kNormSeg / 8 / 64;
-        float4 v[R][2];
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             const int c = 8 * (lane + 64 * r);
@@ -217,6 +218,42 @@ __global__ void __launch_bounds__(256) rmsnorm_kernel(const float* __restrict__ 
     const double mean = static_cast<double>(sum) / static_cast<double>(cols);
     const float inv = static_cast<float>(1.0 / __builtin_sqrt(mean + eps));
     if constexpr (OUT == NORM_STORE) {
+        const bool vec_out = reinterpret_cast<std::uintptr_t>(y) % 16 == 0 && ld_y * (YT == SEPAL_HIP_F32 ? 4 : 2) % 16 == 0 &&
+                             (w1 == nullptr || reinterpret_cast<std::uintptr_t>(w1) % 16 == 0);
+        if (cols <= kNormSeg && vec_out) {
+            // from the registers: lane l holds columns 8 (l + 64 r) .. + 7; one 16-byte (or two, float32) store each
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const int c = 8 * (lane + 64 * r);
+                if (c >= cols) continue;
+                const float vv[8] = {v[r][0].x, v[r][0].y, v[r][0].z, v[r][0].w, v[r][1].x, v[r][1].y, v[r][1].z, v[r][1].w};
+                float g[8] = {1.0f, 1.0f, 1.0f, 1.0f, 1.0f, 1.0f, 1.0f, 1.0f};
+                if (w1 != nullptr) {
+                    const float4 g0 = *reinterpret_cast<const float4*>(w1 + c), g1 = *reinterpret_cast<const float4*>(w1 + c + 4);
+                    g[0] = g0.x; g[1] = g0.y; g[2] = g0.z; g[3] = g0.w;
+                    g[4] = g1.x; g[5] = g1.y; g[6] = g1.z; g[7] = g1.w;
+                }
+                float n[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) n[j] = __fmul_rn(__fmul_rn(vv[j], inv), g[j]);
+                if constexpr (YT == SEPAL_HIP_F32) {
+                    float* yr = static_cast<float*>(y) + static_cast<std::size_t>(row) * ld_y + c;
+                    *reinterpret_cast<float4*>(yr) = make_float4(n[0], n[1], n[2], n[3]);
+                    *reinterpret_cast<float4*>(yr + 4) = make_float4(n[4], n[5], n[6], n[7]);
+                } else {
+                    unsigned u[4];
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const unsigned lo = YT == SEPAL_HIP_BF16 ? f32_to_bf16_bits(n[2 * j]) : f32_to_f16_bits(n[2 * j]);
+                        const unsigned hi = YT == SEPAL_HIP_BF16 ? f32_to_bf16_bits(n[2 * j + 1]) : f32_to_f16_bits(n[2 * j + 1]);
+                        u[j] = lo | (hi << 16);
+                    }
+                    *reinterpret_cast<u32x4*>(static_cast<unsigned short*>(y) + static_cast<std::size_t>(row) * ld_y + c) =
+                        u32x4{u[0], u[1], u[2], u[3]};
+                }
+            }
+            return;
+        }
         for (int c = 4 * lane; c < cols; c += 256) {
             const float4 v = *reinterpret_cast<const float4*>(xr + c);
             const float vv[4] = {v.x, v.y, v.z, v.w};
@@ -262,6 +299,85 @@ __global__ void __launch_bounds__(256) rmsnorm_kernel(const float* __restrict__ 
                 for (int j = 0; j < 4; ++j) yb[j] = f32_to_bf16_bits(b[j]);
             }
         };
+        const bool vec_q = reinterpret_cast<std::uintptr_t>(q) % 8 == 0 && ld_q % 8 == 0 &&
+                           (y == nullptr || (reinterpret_cast<std::uintptr_t>(y) % 16 == 0 && ld_y % 8 == 0)) &&
+                           (w1 == nullptr || reinterpret_cast<std::uintptr_t>(w1) % 16 == 0);
+        if (cols <= kNormSeg && vec_q) {
+            // from the registers: lane l holds columns 8 (l + 64 r) .. + 7, a 128-column block is 16 lanes of one r
+            float nb[R][8];
+            float m = 0.0f;
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const int c = 8 * (lane + 64 * r);
+                const float vv[8] = {v[r][0].x, v[r][0].y, v[r][0].z, v[r][0].w, v[r][1].x, v[r][1].y, v[r][1].z, v[r][1].w};
+                float g[8] = {1.0f, 1.0f, 1.0f, 1.0f, 1.0f, 1.0f, 1.0f, 1.0f};
+                if (w1 != nullptr && c < cols) {
+                    const float4 g0 = *reinterpret_cast<const float4*>(w1 + c), g1 = *reinterpret_cast<const float4*>(w1 + c + 4);
+                    g[0] = g0.x; g[1] = g0.y; g[2] = g0.z; g[3] = g0.w;
+                    g[4] = g1.x; g[5] = g1.y; g[6] = g1.z; g[7] = g1.w;
+                }
+                float mr = 0.0f;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    nb[r][j] = c < cols ? bf16_bits_to_f32(f32_to_bf16_bits(__fmul_rn(__fmul_rn(vv[j], inv), g[j]))) : 0.0f;
+                    const float a = fabsf(nb[r][j]);
+                    mr = a > mr ? a : mr;
+                }
+                if constexpr (OUT == NORM_Q_128) {
+#pragma unroll
+                    for (int o = 8; o > 0; o >>= 1) {
+                        const float other = __shfl_xor(mr, o, 16);
+                        mr = other > mr ? other : mr;
+                    }
+                    const float scale = mr > 0.0f ? __fdiv_rn(mr, 127.0f) : 1.0f;
+                    const float inverse = __fdiv_rn(1.0f, scale);
+                    if (c < cols) {
+                        unsigned packed[2] = {0u, 0u};
+#pragma unroll
+                        for (int j = 0; j < 8; ++j)
+                            packed[j / 4] |= (static_cast<unsigned>(quantize_value<SEPAL_HIP_RULE_RECIPROCAL>(nb[r][j], scale, inverse)) & 0xFFu)
+                                             << (8 * (j % 4));
+                        *reinterpret_cast<uint2*>(q + static_cast<std::size_t>(row) * ld_q + c) = make_uint2(packed[0], packed[1]);
+                        if (lane % 16 == 0) qs[static_cast<std::size_t>(row) * ld_qs + c / 128] = scale;
+                    }
+                } else {
+                    m = mr > m ? mr : m;
+                }
+            }
+            float scale = 1.0f, inverse = 1.0f;
+            if constexpr (OUT == NORM_Q_TOKEN) {
+#pragma unroll
+                for (int o = 32; o > 0; o >>= 1) {
+                    const float other = __shfl_xor(m, o, 64);
+                    m = other > m ? other : m;
+                }
+                scale = m > 0.0f ? __fdiv_rn(m, 127.0f) : 1.0f;
+                inverse = __fdiv_rn(1.0f, scale);
+                if (lane == 0) qs[static_cast<std::size_t>(row) * ld_qs] = scale;
+            }
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const int c = 8 * (lane + 64 * r);
+                if (c >= cols) continue;
+                if constexpr (OUT == NORM_Q_TOKEN) {
+                    unsigned packed[2] = {0u, 0u};
+#pragma unroll
+                    for (int j = 0; j < 8; ++j)
+                        packed[j / 4] |= (static_cast<unsigned>(quantize_value<SEPAL_HIP_RULE_RECIPROCAL>(nb[r][j], scale, inverse)) & 0xFFu)
+                                         << (8 * (j % 4));
+                    *reinterpret_cast<uint2*>(q + static_cast<std::size_t>(row) * ld_q + c) = make_uint2(packed[0], packed[1]);
+                }
+                if (y != nullptr) {
+                    unsigned u[4];
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        u[j] = static_cast<unsigned>(f32_to_bf16_bits(nb[r][2 * j])) | (static_cast<unsigned>(f32_to_bf16_bits(nb[r][2 * j + 1])) << 16);
+                    *reinterpret_cast<u32x4*>(static_cast<unsigned short*>(y) + static_cast<std::size_t>(row) * ld_y + c) =
+                        u32x4{u[0], u[1], u[2], u[3]};
+                }
+            }
+            return;
+        }
         if constexpr (OUT == NORM_Q_128) {
             // lanes 0..31 hold one 128-column block, lanes 32..63 the next (cols is a multiple of 128)
             for (int c0 = 0; c0 < cols; c0 += 256) {

@@ -138,14 +138,21 @@ def test_rmsnorm_matches_reference(sm, golden):
         assert same_bits(host(ob), orc.bf16_round(y))
 
 
-@pytest.mark.parametrize("rows,cols", [(37, 2056), (3, 4104), (9, 2048), (5, 24)])
+@pytest.mark.parametrize("rows,cols", [(37, 2056), (3, 4104), (9, 2048), (5, 24), (6, 2560), (7, 2568), (3, 5128)])
 def test_rmsnorm_segment_edges(sm, rows, cols):
-    """Rows longer than one LDS segment, with the 8-wide tail starting at a segment boundary (exact order vs oracle)."""
+    """Rows of one LDS segment (normalised from registers) and longer ones (re-read), with the 8-wide tail starting at a
+    segment boundary (2568 = 2560 + 8): exact order vs oracle, with and without the gain vector, every output type."""
     say("rmsnorm segments", rows, cols)
     rng = np.random.default_rng(rows * cols)
     x = (rng.standard_normal((rows, cols)) * 3).astype(np.float32)
+    w1 = (rng.standard_normal(cols) * 0.5 + 1).astype(np.float32)
     out = sm.rmsnorm_rows(dev(x), y_dtype=torch.float32)
     assert same_bits(host(out), orc.rmsnorm_rows(x))
+    ref = orc.rmsnorm_rows(x, w1=w1)
+    assert same_bits(host(sm.rmsnorm_rows(dev(x), y_dtype=torch.float32, w1=dev(w1))), ref)
+    assert same_bits(host(sm.rmsnorm_rows(dev(x), y_dtype=torch.bfloat16, w1=dev(w1))), orc.bf16_round(ref))
+    assert same_bits(host(sm.rmsnorm_rows(dev(x), y_dtype=torch.float16, w1=dev(w1))).astype(np.float32),
+                     ref.astype(np.float16).astype(np.float32))
 
 
 @pytest.mark.parametrize("block", [128, 0])
