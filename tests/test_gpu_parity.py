@@ -110,17 +110,19 @@ def test_packer_and_act_quantizer_match_reference_fixtures(sm, golden):
         assert same_bits(host(xq), g[f"c{i}_xq"]) and same_bits(host(xs), g[f"c{i}_xs"])
 
 
+@pytest.mark.parametrize("cols", [1280, 9728, 16512])
 @pytest.mark.parametrize("src", ["f32", "bf16", "f16"])
 @pytest.mark.parametrize("block", [128, 0])
-def test_activation_quantizer(sm, src, block):
-    say("act quantizer", src, block)
+def test_activation_quantizer(sm, src, block, cols):
+    """Per token, rows up to 16384 columns are held in registers and longer ones read twice (16512)."""
+    say("act quantizer", src, block, cols)
     rng = np.random.default_rng(5)
-    x = bf16_inputs(rng, (70, 1280), outlier_frac=0.01)
+    x = bf16_inputs(rng, (70, cols), outlier_frac=0.01)
     x[3] = 0.0  # a zero row: scale 1, all zeros
     tdt = {"f16": torch.float16, "bf16": torch.bfloat16, "f32": torch.float32}[src]
     xt = dev(x).to(tdt)
     xf = xt.float().cpu().numpy()
-    b = 128 if block == 128 else 1280
+    b = 128 if block == 128 else cols
     q, s = sm.quantize_rows_s8(xt, block=b)
     qo, so = orc.quantize_block_r2(xf, block=b)
     assert same_bits(host(q), qo) and same_bits(host(s), so)
