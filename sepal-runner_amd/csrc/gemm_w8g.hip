@@ -75,21 +75,30 @@ struct BigParams {
     int t, n, k;
     int tiles_m, tiles_n;
     std::size_t x_bytes, w_bytes;  // extents of X and W (buffer range checks of gemm_big3)
+    int id0 = 0, count = 0;        // gemm_big3: the logical 256 x 256 tiles [id0, id0 + count) of this launch
 };
 
-// Logical tile of block `bid` (XCD-aware: the hardware places block b on XCD b % 8).
-__device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int& tm, int& tn) {
-    const int total = tiles_m * tiles_n;
-    const int q = total / 8, r = total % 8;
-    const int xcd = bid % 8, idx = bid / 8;
-    const int id = xcd * q + min(xcd, r) + idx;
-    constexpr int GM = 4;  // M tiles per group: a group sweeps N with the same few X row panels
+// Tile of logical id `id`: groups of GM M tiles sweep N with the same few X row panels.
+__device__ __forceinline__ void tile_from_id(int id, int tiles_m, int tiles_n, int& tm, int& tn) {
+    constexpr int GM = 4;
     const int per_group = GM * tiles_n;
     const int group = id / per_group, first_m = group * GM;
     const int gm = min(tiles_m - first_m, GM);
     const int in_group = id % per_group;
     tm = first_m + in_group % gm;
     tn = in_group / gm;
+}
+
+// Logical id of block `bid` among `total` (XCD-aware: the hardware places block b on XCD b % 8, and each XCD takes a
+// contiguous range of ids, so that consecutive tiles share its L2).
+__device__ __forceinline__ int xcd_id(int bid, int total) {
+    const int q = total / 8, r = total % 8;
+    const int xcd = bid % 8, idx = bid / 8;
+    return xcd * q + min(xcd, r) + idx;
+}
+
+__device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int& tm, int& tn) {
+    tile_from_id(xcd_id(bid, tiles_m * tiles_n), tiles_m, tiles_n, tm, tn);
 }
 
 // ---- large-M kernel: fragment-order LDS, direct global->LDS X tiles, 4-stage pipeline ----------------------------
@@ -302,10 +311,11 @@ __device__ __forceinline__ void wait_vm_lgkm0() {
     __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4));  // vmcnt(N) lgkmcnt(0)
 }
 
-template <int XT, int EP, int YT>
+template <int XT, int EP, int YT, int MB>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) gemm_big3(const BigParams p) {
-    constexpr int NW = 8, BN = 256, K3 = 64, SUB = K3 / 16, SPG = 128 / K3;
-    constexpr int XSTAGE = BM * K3 * 2, WSTAGE = (BN / 32) * SUB * 1024;
+    // MB m-blocks of 32 rows per wave: tiles of BM3 = 64 MB rows (256, or 128 for the tail rows of a launch)
+    constexpr int NW = 8, BN = 256, K3 = 64, SUB = K3 / 16, SPG = 128 / K3, BM3 = 64 * MB;
+    constexpr int XSTAGE = BM3 * K3 * 2, WSTAGE = (BN / 32) * SUB * 1024;
     constexpr int XLD = XSTAGE / 16 / (64 * NW);       // X direct loads per thread per step (4)
     constexpr int WLD = BN * K3 / 16 / (64 * NW);      // W 16-byte chunks per thread per step (2)
     __shared__ __align__(1024) unsigned char xs0[XSTAGE], xs1[XSTAGE], xs2[XSTAGE], ws0[WSTAGE], ws1[WSTAGE];
@@ -322,9 +332,17 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
 
     const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
     const int wm = wave % 2, wn = wave / 2;
-    int tm, tn;
-    tile_of(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
-    const int m0 = tm * BM, n0 = tn * BN;
+    // MB 4: one logical 256 x 256 tile per block; MB 2: block b is half b / count (128 rows) of tile id0 + b % count
+    int tm, tn, m0;
+    if constexpr (MB == 4) {
+        tile_from_id(p.id0 + xcd_id(blockIdx.x, p.count), p.tiles_m, p.tiles_n, tm, tn);
+        m0 = tm * 256;
+    } else {
+        const int b = blockIdx.x;
+        tile_from_id(p.id0 + b % p.count, p.tiles_m, p.tiles_n, tm, tn);
+        m0 = tm * 256 + (b / p.count) * BM3;
+    }
+    const int n0 = tn * BN;
     const int KT = p.k / K3;
 
     // Loads go through buffer descriptors: 32-bit lane offsets, the step and the instruction in the scalar offset, and
@@ -407,9 +425,9 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
         asm volatile("" ::: "memory");
     };
 
-    f32x16 acc[4][2];
+    f32x16 acc[MB][2];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < MB; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
@@ -463,15 +481,15 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int st = 0; st < SUB; ++st) {
-            u32x4 a[4], b[2];
+            u32x4 a[MB], b[2];
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-                a[i] = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(xs + (wm * 4 + i) * 4096 + rx[st]);
+            for (int i = 0; i < MB; ++i)
+                a[i] = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(xs + (wm * MB + i) * 4096 + rx[st]);
 #pragma unroll
             for (int q = 0; q < 2; ++q)
                 b[q] = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(ws + (nbj[q] * SUB + st) * 1024 + rd[st]);
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < MB; ++i)
 #pragma unroll
                 for (int q = 0; q < 2; ++q) {
                     // a group's Horner rescale of each accumulator block right before its first MFMA of the group:
@@ -483,9 +501,9 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
         }
         if constexpr (first) {
             // the first substep's fragment reads, then each block's 16 rescale multiplies and its MFMA, in turn
-            __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, MB + 2, 0);
 #pragma unroll
-            for (int q = 0; q < 8; ++q) {
+            for (int q = 0; q < 2 * MB; ++q) {
                 __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
             }
@@ -515,10 +533,10 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
     wait_vmcnt<0>();
 
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < MB; ++i) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            const int row = m0 + wm * 128 + i * 32 + 8 * (r / 4) + 4 * (lane / 32) + (r % 4);
+            const int row = m0 + wm * 32 * MB + i * 32 + 8 * (r / 4) + 4 * (lane / 32) + (r % 4);
             if (row >= p.t) continue;
             const float v0 = __fmul_rn(acc[i][0][r], e[0]), v1 = __fmul_rn(acc[i][1][r], e[1]);
             if constexpr (EP == SEPAL_HIP_SWIGLU) {
@@ -570,9 +588,9 @@ inline int device_cus() {
     return cus;
 }
 
-template <int XT, int EP, int YT>
+template <int XT, int EP, int YT, int MB>
 void launch_big3(const BigParams& p, hipStream_t stream) {
-    v2::gemm_big3<XT, EP, YT><<<dim3(p.tiles_m * p.tiles_n), dim3(512), 0, stream>>>(p);
+    v2::gemm_big3<XT, EP, YT, MB><<<dim3(p.count * (256 / (64 * MB))), dim3(512), 0, stream>>>(p);
 }
 
 template <int XT, int EP, int YT>
@@ -588,28 +606,23 @@ void launch_big(const GemmArgs& a, hipStream_t stream) {
     // gemm_big3 addresses X and W with 32-bit offsets, rows up to one tile past the end included
     const bool offsets32 = (a.t + 256) * a.ld_x * 2 < (std::size_t{1} << 31) && (a.n + 256) * a.ld_w < (std::size_t{1} << 31);
     if (wide && offsets32) {
-        // The last, partial round of 256 x 256 tiles is the idle tail of the launch. When the row tiles past the full
-        // rounds fit one round as 256 x 128 tiles, those rows go to a second launch of half-width tiles. Both kernels
-        // run the same k order and Horner chain per output, so a row's bits do not depend on which one computed it.
+        // The last, partial round of 256 x 256 tiles is the idle tail of the launch. When it is more than a quarter
+        // full and its tiles fit one round as 128 x 256 halves, they go to a second launch of half-height tiles (the
+        // logical ids past the full rounds, each as two halves). Both launches run the same k order and Horner chain
+        // per output, so a row's bits do not depend on which one computed it.
         const int cus = device_cus();
-        const long total = static_cast<long>(tiles_m) * tn256;
-        const long full = total / cus * cus;
-        const int m1 = static_cast<int>(full / tn256);
-        const bool split = total % cus > cus / 4 && m1 > 0 && static_cast<long>(tiles_m - m1) * 2 * tn256 <= cus;
+        const int total = tiles_m * tn256;
+        const int full = total / cus * cus, rest = total - full;
+        const bool split = rest > cus / 4 && full > 0 && 2 * rest <= cus;
         p.tiles_n = tn256;
-        if (!split) {
-            launch_big3<XT, EP, YT>(p, stream);
-        } else {
-            p.tiles_m = m1;
-            launch_big3<XT, EP, YT>(p, stream);
+        p.id0 = 0;
+        p.count = split ? full : total;
+        launch_big3<XT, EP, YT, 4>(p, stream);
+        if (split) {
             BigParams q = p;
-            const std::size_t r0 = static_cast<std::size_t>(m1) * 256;
-            q.x = p.x + r0 * a.ld_x;
-            q.y = static_cast<char*>(a.y) + r0 * a.ld_y * elem_bytes(YT);
-            q.t = static_cast<int>(a.t - r0);
-            q.tiles_m = tiles_m - m1;
-            q.tiles_n = static_cast<int>((a.n + 127) / 128);
-            launch_big2<XT, EP, YT, 2>(q, stream);
+            q.id0 = full;
+            q.count = rest;
+            launch_big3<XT, EP, YT, 2>(q, stream);
         }
     } else if (wide) {
         p.tiles_n = tn256;

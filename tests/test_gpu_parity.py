@@ -295,9 +295,9 @@ def test_w8g_wide_tiles_every_element(sm, epilogue):
 
 
 def test_w8g_wide_tail_split_and_batch_invariance(sm):
-    # 62 x 10 tiles of 256 x 256 on 256 CUs leave a 108-tile last round: rows past the 51st row tile run as 256 x 128
-    # tiles in a second launch. Every element is checked, and rows from both launches match, bit for bit, the same rows
-    # computed in a small batch (the 256 x 128 kernel), as runner/cuda/tests/test_gemm_simt_kernels.cpp:193-211 asks.
+    # 62 x 10 tiles of 256 x 256 on 256 CUs leave a 108-tile last round: those tiles run as 128 x 256 halves in a second
+    # launch. Every element is checked, and rows from both launches match, bit for bit, the same rows computed in a
+    # small batch (the 256 x 128 kernel), as runner/cuda/tests/test_gemm_simt_kernels.cpp:193-211 asks.
     t, n, k = 15800, 2560, 384
     rng = np.random.default_rng(777)
     x, q, s = _w8g_problem(rng, t, n, k, torch.bfloat16)
@@ -311,6 +311,26 @@ def test_w8g_wide_tail_split_and_batch_invariance(sm):
         part = host(sm.gemm_w8g(xt[r0:r0 + rows], qt, st, config=0))
         assert same_bits(part, yh[r0:r0 + rows]), r0
 
+
+
+def test_w8g_gate_up_tail_split_and_batch_invariance(sm):
+    # the gate/up shape: 62 x 76 tiles leave a 104-tile last round (the last row tiles' right-hand columns), run as
+    # 128 x 256 halves. Sampled rows of both launches against float64, and row slices bit for bit against a small batch.
+    t, n, k = 15800, 19456, 256
+    rng = np.random.default_rng(779)
+    x, q, s = _w8g_problem(rng, t, n, k, torch.bfloat16)
+    xt, qt, st = dev(x, torch.bfloat16), dev(q), dev(s)
+    say("w8g gate/up tail split", t, n, k)
+    y = host(sm.gemm_w8g(xt, qt, st, epilogue=sm.SWIGLU, y_dtype=torch.float16).float())
+    rows = torch.tensor([0, 1, 255, 7000, 15359, 15360, 15423, 15500, 15615, 15616, 15799], device="cuda")
+    ref = _deq_ref(xt[rows], qt, st, k)
+    f = torch.arange(n // 2, device=ref.device)
+    g, u = ref[:, 128 * (f // 64) + f % 64], ref[:, 128 * (f // 64) + 64 + f % 64]
+    href = host(g * torch.sigmoid(g) * u)
+    assert max_rel_over_rms(y[rows.cpu().numpy()], href) < 2e-3
+    for r0, nr in [(0, 100), (15360, 130), (15600, 200)]:
+        part = host(sm.gemm_w8g(xt[r0:r0 + nr], qt, st, epilogue=sm.SWIGLU, y_dtype=torch.float16, config=0).float())
+        assert same_bits(part, y[r0:r0 + nr]), r0
 
 # ---- q8 ----------------------------------------------------------------------------------------------------------------
 
