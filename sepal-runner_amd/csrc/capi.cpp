@@ -321,12 +321,14 @@ int32_t sepal_hip_gemm_w8a16(const void* x, size_t ld_x, const int8_t* wq, size_
         if (t == 0) return;
         require(t < 0x7FFFFFFFu && n < 0x7FFFFFFFu, "gemm_w8a16: dimension beyond 2^31");
         const hipStream_t st = as_stream(stream);
-        // the per-channel scale as per-group scales in the workspace, then the w8g multiply (binary16 X, Store); a
-        // binary16 output goes through float32 row chunks of at most 64 MB (a row's bits do not depend on the batch)
+        // the per-channel scale as per-group scales in the workspace, then the w8g multiply (binary16 X, Store). Above
+        // the small-M size a binary16 output comes straight from the large-M kernels; below it, through float32 row
+        // chunks of at most 64 MB and a conversion (the same rounding; a row's bits do not depend on the batch).
         const std::size_t groups = k / 128, s_bytes = (n * groups * 4 + 255) / 256 * 256;
-        const std::size_t chunk = y_type == SEPAL_HIP_F32 ? t : std::max<std::size_t>(1, (std::size_t{64} << 20) / (n * 4));
+        const bool direct = y_type == SEPAL_HIP_F32 || t > static_cast<std::size_t>(kSmallM);
+        const std::size_t chunk = direct ? t : std::max<std::size_t>(1, (std::size_t{64} << 20) / (n * 4));
         const std::size_t rows = std::min(t, chunk);
-        char* ws = static_cast<char*>(workspace(kScratchOffset + s_bytes + (y_type == SEPAL_HIP_F32 ? 0 : rows * n * 4), st));
+        char* ws = static_cast<char*>(workspace(kScratchOffset + s_bytes + (direct ? 0 : rows * n * 4), st));
         float* s = reinterpret_cast<float*>(ws + kScratchOffset);
         float* tmp = reinterpret_cast<float*>(ws + kScratchOffset + s_bytes);
         launch_broadcast_scales(sw, s, n, groups, st);
@@ -340,16 +342,16 @@ int32_t sepal_hip_gemm_w8a16(const void* x, size_t ld_x, const int8_t* wq, size_
             a.ld_w = ld_w;
             a.s = s;
             a.ld_s = groups;
-            a.y = y_type == SEPAL_HIP_F32 ? static_cast<void*>(static_cast<float*>(y) + r0 * ld_y) : static_cast<void*>(tmp);
-            a.y_type = SEPAL_HIP_F32;
-            a.ld_y = y_type == SEPAL_HIP_F32 ? ld_y : n;
+            a.y = direct ? static_cast<void*>(static_cast<char*>(y) + r0 * ld_y * (y_type == SEPAL_HIP_F32 ? 4 : 2))
+                         : static_cast<void*>(tmp);
+            a.y_type = direct ? y_type : SEPAL_HIP_F32;
+            a.ld_y = direct ? ld_y : n;
             a.t = tr;
             a.n = n;
             a.k = k;
             a.epilogue = SEPAL_HIP_STORE;
             launch_gemm_w8g(a, st);
-            if (y_type == SEPAL_HIP_F16)
-                launch_f32_to_f16(tmp, n, static_cast<std::uint16_t*>(y) + r0 * ld_y, ld_y, tr, n, st);
+            if (!direct) launch_f32_to_f16(tmp, n, static_cast<std::uint16_t*>(y) + r0 * ld_y, ld_y, tr, n, st);
         }
     });
 }

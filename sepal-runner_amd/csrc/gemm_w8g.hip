@@ -54,11 +54,18 @@ __device__ __forceinline__ f32x4 mfma16(const u32x4 a, const u32x4 b, f32x4 c) {
 // Effective scale of a group: a zero (or negative/NaN) scale marks an all-zero group and keeps the previous one.
 __device__ __forceinline__ float next_scale(float s, float prev) { return s > 0.0f ? s : prev; }
 
-// Epilogue of one output element (row, col) of the plain multiply.
-template <int EP>
-__device__ __forceinline__ void put_plain(float* y, std::size_t idx, float v) {
-    if constexpr (EP == SEPAL_HIP_ADD) y[idx] = __fadd_rn(y[idx], v);
-    else y[idx] = v;
+// Epilogue of one output element (row, col) of the plain multiply: float32 Store / Add, or a binary16 Store (the
+// float32 value rounded to nearest even, as a separate conversion would).
+template <int EP, int YT>
+__device__ __forceinline__ void put_plain(void* y, std::size_t idx, float v) {
+    if constexpr (YT != SEPAL_HIP_F32) {
+        static_assert(EP == SEPAL_HIP_STORE, "16-bit outputs of the plain multiply are Store only");
+        store_out<YT>(y, idx, v);
+    } else if constexpr (EP == SEPAL_HIP_ADD) {
+        static_cast<float*>(y)[idx] = __fadd_rn(static_cast<float*>(y)[idx], v);
+    } else {
+        static_cast<float*>(y)[idx] = v;
+    }
 }
 
 // ---- large-M path ----------------------------------------------------------------------------------------------------
@@ -282,9 +289,8 @@ __global__ void __launch_bounds__(128 * WN) __attribute__((amdgpu_waves_per_eu(2
                 const int f = n0 / 2 + 64 * ib + 32 * hh + lane % 32;
                 if (2 * f < p.n) store_out<YT>(p.y, static_cast<std::size_t>(row) * p.ld_y + f, swiglu_fast(v0, v1));
             } else {
-                float* y = static_cast<float*>(p.y);
-                if (col[0] < p.n) put_plain<EP>(y, static_cast<std::size_t>(row) * p.ld_y + col[0], v0);
-                if (col[1] < p.n) put_plain<EP>(y, static_cast<std::size_t>(row) * p.ld_y + col[1], v1);
+                if (col[0] < p.n) put_plain<EP, YT>(p.y, static_cast<std::size_t>(row) * p.ld_y + col[0], v0);
+                if (col[1] < p.n) put_plain<EP, YT>(p.y, static_cast<std::size_t>(row) * p.ld_y + col[1], v1);
             }
         }
     }
@@ -543,9 +549,8 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
                 const int f = n0 / 2 + 64 * ib + 32 * hh + lane % 32;
                 if (2 * f < p.n) store_out<YT>(p.y, static_cast<std::size_t>(row) * p.ld_y + f, swiglu_fast(v0, v1));
             } else {
-                float* y = static_cast<float*>(p.y);
-                if (col[0] < p.n) put_plain<EP>(y, static_cast<std::size_t>(row) * p.ld_y + col[0], v0);
-                if (col[1] < p.n) put_plain<EP>(y, static_cast<std::size_t>(row) * p.ld_y + col[1], v1);
+                if (col[0] < p.n) put_plain<EP, YT>(p.y, static_cast<std::size_t>(row) * p.ld_y + col[0], v0);
+                if (col[1] < p.n) put_plain<EP, YT>(p.y, static_cast<std::size_t>(row) * p.ld_y + col[1], v1);
             }
         }
     }
@@ -636,7 +641,8 @@ void launch_big(const GemmArgs& a, hipStream_t stream) {
 
 template <int XT, int EP, int YT>
 void dispatch_path(const GemmArgs& a, hipStream_t stream) {
-    const bool small = a.config == 1 || (a.config < 0 && a.t <= kSmallM);
+    // the small-M kernels write float32 (or SwiGLU outputs); a binary16 Store always takes the large-M kernels
+    const bool small = (YT == SEPAL_HIP_F32 || EP == SEPAL_HIP_SWIGLU) && (a.config == 1 || (a.config < 0 && a.t <= kSmallM));
     if (small) launch_stream_w8g(a, stream);
     else launch_big<XT, EP, YT>(a, stream);
 }
@@ -644,7 +650,10 @@ void dispatch_path(const GemmArgs& a, hipStream_t stream) {
 template <int XT>
 void dispatch_ep(const GemmArgs& a, hipStream_t stream) {
     switch (a.epilogue) {
-    case SEPAL_HIP_STORE: dispatch_path<XT, SEPAL_HIP_STORE, SEPAL_HIP_F32>(a, stream); break;
+    case SEPAL_HIP_STORE:
+        if (a.y_type == SEPAL_HIP_F16) dispatch_path<XT, SEPAL_HIP_STORE, SEPAL_HIP_F16>(a, stream);
+        else dispatch_path<XT, SEPAL_HIP_STORE, SEPAL_HIP_F32>(a, stream);
+        break;
     case SEPAL_HIP_ADD: dispatch_path<XT, SEPAL_HIP_ADD, SEPAL_HIP_F32>(a, stream); break;
     default:
         switch (a.y_type) {

@@ -728,8 +728,8 @@ def test_s8_family_row_invariance(sm):
 @pytest.mark.parametrize("t,n,k", [(100, 256, 1024), (16, 384, 2560), (5000, 4096, 256)])
 def test_gemm_w8a16_against_float64(sm, t, n, k):
     """binary16 x times per-channel int8 weights, against float64 of the dequantised weights (the reference test's
-    check) at the parity bar; the binary16 output (row chunks through float32 at 5000 x 4096) is the float32 one
-    rounded."""
+    check) at the parity bar; the binary16 output (straight from the large-M kernels above 64 rows, through float32
+    and a conversion at 16) is the float32 one rounded."""
     say("gemm w8a16", t, n, k)
     rng = np.random.default_rng(t + k)
     x = rng.standard_normal((t, k)).astype(np.float16)
