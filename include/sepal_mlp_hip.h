@@ -138,8 +138,9 @@ SEPAL_HIP_API int32_t sepal_hip_gemm_s8(const int8_t* xq, size_t ld_x, const flo
 
 /* binary16 activations times int8 weights with per-channel scales: Y[t, n] = sw[n] * sum over K of x[t,k] * wq[n,k],
  * the weights widened exactly and multiplied with float32 accumulation (the gpu-w8g kernels with the channel's scale
- * in every group: within float32 rounding of one accumulator times sw). Y float32 or binary16 [T, ld_y] (binary16 goes
- * through float32 row chunks of at most 64 MB of workspace). Shape rules as sepal_hip_gemm_s8; wq in the Plain layout.
+ * in every group: within float32 rounding of one accumulator times sw). Y float32 or binary16 [T, ld_y] (binary16 is
+ * the float32 result rounded to nearest even; at T <= 64 it goes through float32 in the workspace). Shape rules as
+ * sepal_hip_gemm_s8; wq in the Plain layout.
  * Replaces launch_gemm_w8a16 (runner/cuda/src/gemm_s8_kernels.hpp:51-57), the reference's gpu-q8w profile multiply. */
 SEPAL_HIP_API int32_t sepal_hip_gemm_w8a16(const void* x, size_t ld_x, const int8_t* wq, size_t ld_w, const float* sw, void* y,
                                            int32_t y_type, size_t ld_y, size_t t, size_t n, size_t k, void* stream);
