@@ -11,11 +11,12 @@
 // of a different summation order, not bit for bit.
 //
 // Two paths:
-//   large M: 256 x BN tiles (BN 128 or 256), 4 or 8 waves of 128 x 64 outputs (4 x 2 blocks of 32 x 32, MFMA
-//            32x32x16), K through a double-buffered LDS tile; the weights are widened once per tile when staged; 1-D
-//            grid with an XCD-aware tile order (a block's id modulo 8 is its XCD; consecutive logical tiles are kept
-//            on one XCD so they share its L2). 256 x 256 tiles (gemm_big3) step K by 64 with whole-cache-line loads;
-//            256 x 128 tiles (gemm_big2) step K by 32.
+//   large M: waves of 128 x 64 outputs (4 x 2 blocks of 32 x 32, MFMA 32x32x16; 64 x 64 in the half tiles), the
+//            weights widened once per tile when staged into LDS; 1-D grid with an XCD-aware tile order (a block's id
+//            modulo 8 is its XCD; consecutive logical tiles are kept on one XCD so they share its L2). gemm_big3:
+//            256 x 256 tiles (and 128 x 256 halves for a launch's last partial round), K in steps of 64, X straight
+//            from global memory into LDS. gemm_big2 (grids of fewer than 512 large tiles): 256 x 128 or 256 x 256
+//            tiles, K in steps of 32.
 //   small M: stream.hip (the weights streamed once, HBM-bound).
 #include "common.hpp"
 #include "gemm_kernels.hpp"
@@ -108,16 +109,15 @@ __device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int& 
     tile_from_id(xcd_id(bid, tiles_m * tiles_n), tiles_m, tiles_n, tm, tn);
 }
 
-// ---- large-M kernel: fragment-order LDS, direct global->LDS X tiles, 4-stage pipeline ----------------------------
+// ---- large-M kernel for small grids: fragment-order LDS, 32-wide k steps (gemm_big2) ---------------------------------
 //
 // LDS holds every MFMA operand fragment in the order a wave reads it: fragment (block b, substep st) is 64 lanes x 16
 // bytes, lane l at byte 16 l, so an operand read is one contiguous kilobyte (no bank conflicts, one address per lane
-// for the whole kernel). A fragment of X (m-block mb of 32 rows, 16 values of k) is filled straight from global memory
-// by global_load_lds_dwordx4 (each lane loads the 16 bytes it will later read: row mb*32 + l%32, k 16st + 8(l/32));
-// a W fragment is filled by the wave that widens the weight bytes (row nb*32 + l%32, k 16st .. 16st + 15 -> lanes l%32
-// and 32 + l%32). K runs in steps of 32 through 4 LDS stages; the loads of step kt + 3 are issued while step kt is
-// multiplied, and one barrier per step publishes step kt + 1. Each lane's two column scales come with the step's
-// loads.
+// for the whole kernel). Each lane loads into registers the 16 bytes of X it will later read (row mb*32 + l%32, k
+// 16st + 8(l/32)) and writes them to its slot; a W fragment is filled by the wave that widens the weight bytes (row
+// nb*32 + l%32, k 16st .. 16st + 15 -> lanes l%32 and 32 + l%32). K runs in steps of 32 through two LDS stages; the
+// loads of step kt + 3 are issued while step kt is multiplied (four rotating register sets), and one barrier per step
+// publishes step kt + 1. Each lane's two column scales come with the group's loads.
 namespace v2 {
 
 constexpr int BM = 256, BK = 32, STAGES = 2;
