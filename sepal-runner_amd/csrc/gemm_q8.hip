@@ -202,8 +202,9 @@ __global__ void __launch_bounds__(512) gemm_big(const Params p) {
     // activation scales into LDS; one barrier. The loads are issued at every step, past the last group too (repeats
     // into stages nothing reads again), so the wait count of the barrier stays exact.
     Set s0, s1, s2;
-    const auto step = [&](int g, auto jt) {
+    const auto step = [&](int g, auto jt, auto first_t) {
         constexpr int j = decltype(jt)::value;
+        constexpr bool first = decltype(first_t)::value;  // group 0: its link multiplies (known at compile time)
         Set& cur = j == 0 ? s0 : (j == 1 ? s1 : s2);
         Set& next = j == 0 ? s1 : (j == 1 ? s2 : s0);
         Set& free_ = j == 0 ? s2 : (j == 1 ? s0 : s1);
@@ -260,7 +261,7 @@ __global__ void __launch_bounds__(512) gemm_big(const Params p) {
                         const int rl = wm * 64 + i * 32 + 8 * (r / 4) + 4 * (lane / 32) + (r % 4);
                         const float xsv = PER_TOKEN ? 1.0f : lds_xs[buf][rl];
 #pragma unroll
-                        for (int q = 0; q < 2; ++q) acc[i][q][r] = chain<PER_TOKEN>(acc[i][q][r], sacc[i][q][r], cur.ws[q], xsv, g == 0);
+                        for (int q = 0; q < 2; ++q) acc[i][q][r] = chain<PER_TOKEN>(acc[i][q][r], sacc[i][q][r], cur.ws[q], xsv, first);
                     }
             }
             if (g + 1 < groups) stage_xs(buf ^ 1, next);
@@ -276,10 +277,12 @@ __global__ void __launch_bounds__(512) gemm_big(const Params p) {
     wait_vm_lgkm0<XDMA + WDMA + NSC>();  // group 0's loads
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-    for (int g = 0; g < groups; g += 3) {
-        step(g, std::integral_constant<int, 0>{});
-        step(g + 1, std::integral_constant<int, 1>{});
-        step(g + 2, std::integral_constant<int, 2>{});
+    // group 0 on its own (its link of the chain multiplies), then three groups per iteration (stage g mod 3)
+    step(0, std::integral_constant<int, 0>{}, std::true_type{});
+    for (int g = 1; g < groups; g += 3) {
+        step(g, std::integral_constant<int, 1>{}, std::false_type{});
+        step(g + 1, std::integral_constant<int, 2>{}, std::false_type{});
+        step(g + 2, std::integral_constant<int, 0>{}, std::false_type{});
     }
     // the repeated loads of the last steps may still be writing LDS: drain them before the block reuses or leaves it
     wait_vm_lgkm0<0>();
