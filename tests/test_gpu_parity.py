@@ -334,7 +334,7 @@ def test_w8g_gate_up_tail_split_and_batch_invariance(sm):
 
 # ---- q8 ----------------------------------------------------------------------------------------------------------------
 
-Q8_CASES = [(37, 256, 256), (130, 128, 512), (300, 512, 1280), (16, 256, 2560), (64, 384, 640)]
+Q8_CASES = [(37, 256, 256), (130, 128, 512), (300, 512, 1280), (16, 256, 2560), (64, 384, 640), (100, 256, 128)]
 
 
 @pytest.mark.parametrize("case", Q8_CASES)
