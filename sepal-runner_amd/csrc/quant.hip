@@ -235,6 +235,14 @@ __global__ void __launch_bounds__(256) rmsnorm_kernel(const float* __restrict__ 
         if (lane < 32) {
             const int end32 = min(len, full - s0);  // this segment's part of the 32-wide loop
             int c = 0;
+            // eight reads in flight, then their eight links of the chain, in order
+            for (; c + 256 <= end32; c += 256) {
+                float v8[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) v8[u] = buf[c + 32 * u + L];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) a = __builtin_fmaf(v8[u], v8[u], a);
+            }
             for (; c + 32 <= end32; c += 32) {
                 const float e = buf[c + L];
                 a = __builtin_fmaf(e, e, a);

@@ -449,8 +449,18 @@ __global__ void __launch_bounds__(1024) finish_kernel(const float* __restrict__ 
         float a = 0.0f;
         const int full = n / 32 * 32;
         if (tid < 32) {
-            for (int c = 0; c < full; c += 32) a = __builtin_fmaf(row_buf[c + L], row_buf[c + L], a);
-            for (int c = full; c + 8 <= n; c += 8)
+            // eight reads in flight, then their eight links of the chain, in order (one read at a time left the wave
+            // waiting on LDS latency at every link)
+            int c = 0;
+            for (; c + 256 <= full; c += 256) {
+                float v[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) v[u] = row_buf[c + 32 * u + L];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) a = __builtin_fmaf(v[u], v[u], a);
+            }
+            for (; c < full; c += 32) a = __builtin_fmaf(row_buf[c + L], row_buf[c + L], a);
+            for (c = full; c + 8 <= n; c += 8)
                 if (L < 8) a = __builtin_fmaf(row_buf[c + L], row_buf[c + L], a);
         }
         const int l8 = L % 8;
