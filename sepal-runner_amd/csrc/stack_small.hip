@@ -352,11 +352,13 @@ __global__ void __launch_bounds__(kThreads) pass_kernel(const PassParams p) {
     }
     if (tid < kWorkers) worker_first[tid] = min(tid * per, total - 1) / gpt;
     __syncthreads();
-    // the tile's sum in worker order; tile tl sits in slot tl - (first tile of w) of worker w
+    // the tile's sum in worker order; tile tl sits in slot tl - (first tile of w) of worker w, which is slot 0 for every
+    // worker after the first (it starts inside the tile)
     const auto sum_tile = [&](int tl, int e) {
         const int lo = cover_lo[tl], hi = cover_hi[tl];
         float v = red[(lo * kSlots + (tl - worker_first[lo])) * 256 + e];
-        for (int w = lo + 1; w <= hi; ++w) v = __fadd_rn(v, red[(w * kSlots + (tl - worker_first[w])) * 256 + e]);
+#pragma unroll 4
+        for (int w = lo + 1; w <= hi; ++w) v = __fadd_rn(v, red[w * kSlots * 256 + e]);
         return v;
     };
     if constexpr (Q8 && SWIGLU) {
