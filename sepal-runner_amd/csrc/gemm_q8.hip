@@ -70,11 +70,16 @@ struct Params {
     unsigned* counters;
 };
 
-__device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int& tm, int& tn) {
-    const int total = tiles_m * tiles_n;
+// Logical id of block `bid` among `total`: the hardware places block b on XCD b % 8, and each XCD takes a contiguous
+// range of ids, so that consecutive tiles share its L2.
+__device__ __forceinline__ int xcd_id(int bid, int total) {
     const int q = total / 8, r = total % 8;
     const int xcd = bid % 8, idx = bid / 8;
-    const int id = xcd * q + min(xcd, r) + idx;
+    return xcd * q + min(xcd, r) + idx;
+}
+
+// Tile of logical id `id`: groups of GM M tiles sweep N with the same few X row panels.
+__device__ __forceinline__ void tile_from_id(int id, int tiles_m, int tiles_n, int& tm, int& tn) {
     constexpr int GM = 4;
     const int per_group = GM * tiles_n;
     const int group = id / per_group, first_m = group * GM;
@@ -82,6 +87,10 @@ __device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int& 
     const int in_group = id % per_group;
     tm = first_m + in_group % gm;
     tn = in_group / gm;
+}
+
+__device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int& tm, int& tn) {
+    tile_from_id(xcd_id(bid, tiles_m * tiles_n), tiles_m, tiles_n, tm, tn);
 }
 
 // 128-byte LDS rows of 8 chunks; chunk c of row r stored at c ^ ((r / 2) & 7). A 16-byte read is served 16 lanes at a
@@ -405,6 +414,157 @@ __global__ void __launch_bounds__(512) gemm_big(const Params p) {
     }
 }
 
+// ---- gemm_s8 (per-channel W8A8, int32 sums over the whole K): 256 x 256 tiles ----------------------------------------
+//
+// 8 waves of 128 x 64 outputs (4 x 2 blocks of MFMA 32x32x32 i8, 128 int32 accumulators), K in steps of 64 bytes. Both
+// operands go straight from global memory into LDS (buffer_load ... lds, 16 bytes a lane, 16 rows x 64 bytes per
+// instruction), row-major with 64-byte rows, chunk c of row r at slot c ^ ((r / 4) & 3): every 16 lanes of a fragment
+// read (16 rows, one chunk) cover the 16 bank groups. Three stages of each, separate LDS arrays (the compiler then
+// knows which array a direct load writes); the loads of step kt + 2 are issued while step kt is multiplied, and each
+// step ends with an explicit wait and a bare barrier. MB 2 gives 128 x 256 halves for a launch's last partial round.
+// The sums are exact, so the results equal gemm_big's whole-K mode bit for bit.
+struct S8Params {
+    const signed char* x;
+    std::size_t ld_x;
+    const float* xs;
+    std::size_t ld_xs;
+    const signed char* w;
+    std::size_t ld_w;
+    const float* ws;
+    std::size_t ld_ws;
+    void* y;
+    std::size_t ld_y;
+    int t, n, k;
+    int tiles_m, tiles_n, id0, count;
+    std::size_t x_bytes, w_bytes;
+};
+
+template <int YT, int MB>
+__global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) gemm_s8_big(const S8Params p) {
+    constexpr int NW = 8, KS = 64, SUB = KS / 32, BM = 64 * MB, BN = 256;
+    constexpr int XSTAGE = BM * KS, WSTAGE = BN * KS;
+    constexpr int XLD = XSTAGE / 1024 / NW, WLD = WSTAGE / 1024 / NW;  // 1 KB direct loads per wave and step
+    __shared__ __align__(1024) unsigned char xs0[XSTAGE], xs1[XSTAGE], xs2[XSTAGE], ws0[WSTAGE], ws1[WSTAGE], ws2[WSTAGE];
+    const auto xstage = [&](auto it) -> unsigned char* {
+        constexpr int i = decltype(it)::value;
+        if constexpr (i == 0) return xs0;
+        else if constexpr (i == 1) return xs1;
+        else return xs2;
+    };
+    const auto wstage = [&](auto it) -> unsigned char* {
+        constexpr int i = decltype(it)::value;
+        if constexpr (i == 0) return ws0;
+        else if constexpr (i == 1) return ws1;
+        else return ws2;
+    };
+
+    const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
+    const int wm = wave % 2, wn = wave / 2;
+    int tm, tn, m0;
+    if constexpr (MB == 4) {
+        tile_from_id(p.id0 + xcd_id(blockIdx.x, p.count), p.tiles_m, p.tiles_n, tm, tn);
+        m0 = tm * 256;
+    } else {
+        const int b = blockIdx.x;
+        tile_from_id(p.id0 + b % p.count, p.tiles_m, p.tiles_n, tm, tn);
+        m0 = tm * 256 + (b / p.count) * BM;
+    }
+    const int n0 = tn * BN;
+    const int KT = p.k / KS;
+
+    // rows past T or N read as zero (past num_records); the launcher checks that every offset fits 32 bits
+    const __amdgpu_buffer_rsrc_t xres = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<signed char*>(p.x), 0, static_cast<int>(p.x_bytes), 0x00020000);
+    const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<signed char*>(p.w), 0, static_cast<int>(p.w_bytes), 0x00020000);
+    // direct load i of wave w fills LDS kilobyte w + 8 i = rows 16 w + 128 i + {0..15}; lane l writes slot l % 4 of row
+    // 16 w + 128 i + l / 4, which holds chunk (l % 4) ^ ((row / 4) & 3) = (l % 4) ^ ((l / 16) & 3)
+    const int lrow = 16 * wave + lane / 4, lchunk = (lane % 4) ^ ((lane / 16) & 3);
+    const int xoff = (m0 + lrow) * static_cast<int>(p.ld_x) + 16 * lchunk;
+    const int woff = (n0 + lrow) * static_cast<int>(p.ld_w) + 16 * lchunk;
+    const int xstride = 128 * static_cast<int>(p.ld_x), wstride = 128 * static_cast<int>(p.ld_w);
+    // fragment reads: lane l of a 32-row block, substep st reads row l % 32, chunk 2 st + l / 32
+    int rf[SUB];
+#pragma unroll
+    for (int st = 0; st < SUB; ++st) rf[st] = (lane % 32) * 64 + 16 * ((2 * st + lane / 32) ^ ((lane / 4) & 3));
+
+    const auto issue = [&](int kt, unsigned char* xd, unsigned char* wd) {
+#pragma unroll
+        for (int i = 0; i < XLD; ++i)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(xres, (lds_void*)(xd + (wave + 8 * i) * 1024), 16, xoff, kt * KS + i * xstride, 0, 0);
+#pragma unroll
+        for (int i = 0; i < WLD; ++i)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(wres, (lds_void*)(wd + (wave + 8 * i) * 1024), 16, woff, kt * KS + i * wstride, 0, 0);
+    };
+    const auto barrier = [&]() {
+        asm volatile("" ::: "memory");
+        wait_vm_lgkm0<XLD + WLD>();  // leaves this step's loads in flight, covers the next step's
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+    };
+
+    const i32x16 zero16 = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+    i32x16 tot[MB][2];
+#pragma unroll
+    for (int i = 0; i < MB; ++i) tot[i][0] = tot[i][1] = zero16;
+
+    const auto step = [&](int kt, auto jt) {
+        constexpr int j = decltype(jt)::value;
+        issue(min(kt + 2, KT - 1), xstage(std::integral_constant<int, (j + 2) % 3>{}), wstage(std::integral_constant<int, (j + 2) % 3>{}));
+        __builtin_amdgcn_sched_barrier(0);
+        if (kt < KT) {
+            const unsigned char* xs = xstage(std::integral_constant<int, j>{});
+            const unsigned char* ws = wstage(std::integral_constant<int, j>{});
+#pragma unroll
+            for (int st = 0; st < SUB; ++st) {
+                u32x4 a[MB], b[2];
+#pragma unroll
+                for (int i = 0; i < MB; ++i)
+                    a[i] = *reinterpret_cast<const u32x4*>(xs + (wm * MB + i) * 2048 + rf[st]);
+#pragma unroll
+                for (int q = 0; q < 2; ++q) b[q] = *reinterpret_cast<const u32x4*>(ws + (2 * wn + q) * 2048 + rf[st]);
+#pragma unroll
+                for (int i = 0; i < MB; ++i)
+#pragma unroll
+                    for (int q = 0; q < 2; ++q) tot[i][q] = mfma_i8_32(a[i], b[q], tot[i][q]);
+            }
+        }
+        barrier();
+    };
+
+    issue(0, xs0, ws0);
+    issue(min(1, KT - 1), xs1, ws1);
+    asm volatile("" ::: "memory");
+    wait_vm_lgkm0<XLD + WLD>();  // step 0's loads
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    for (int kt = 0; kt < KT; kt += 3) {
+        step(kt, std::integral_constant<int, 0>{});
+        step(kt + 1, std::integral_constant<int, 1>{});
+        step(kt + 2, std::integral_constant<int, 2>{});
+    }
+    wait_vm_lgkm0<0>();  // no direct load may still be writing LDS when the block ends
+
+    // y = (float(S) * sx[t]) * sw[n], float32 or binary16 (round to nearest even)
+#pragma unroll
+    for (int i = 0; i < MB; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int row = m0 + wm * 32 * MB + i * 32 + 8 * (r / 4) + 4 * (lane / 32) + (r % 4);
+            if (row >= p.t) continue;
+            const float sx = p.xs[static_cast<std::size_t>(row) * p.ld_xs];
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                const int col = n0 + 64 * wn + 32 * q + lane % 32;
+                if (col >= p.n) continue;
+                const float v = __fmul_rn(__fmul_rn(static_cast<float>(tot[i][q][r]), sx), p.ws[static_cast<std::size_t>(col) * p.ld_ws]);
+                const std::size_t idx = static_cast<std::size_t>(row) * p.ld_y + col;
+                if constexpr (YT == SEPAL_HIP_F16) static_cast<unsigned short*>(p.y)[idx] = f32_to_f16_bits(v);
+                else static_cast<float*>(p.y)[idx] = v;
+            }
+        }
+}
+
 // ---- launch ----------------------------------------------------------------------------------------------------------
 
 inline Params make_params(const GemmArgs& a) {
@@ -473,9 +633,70 @@ void launch_gemm_q8_swiglu_q8(const GemmArgs& a, hipStream_t stream) {
     else q8::launch_big<kSwigluQ8, SEPAL_HIP_F32, false, q8::MODE_CHAIN>(a, stream);
 }
 
+namespace q8 {
+
+// Compute units of the current device (cached per device).
+inline int device_cus() {
+    static int cached[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0) throw LaunchError("gemm_s8: hipGetDevice failed");
+    if (dev < 64 && cached[dev] > 0) return cached[dev];
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+        throw LaunchError("gemm_s8: device query failed");
+    if (dev < 64) cached[dev] = cus;
+    return cus;
+}
+
+// 256 x 256 tiles when they fill the chip at least once and every offset fits 32 bits; the last partial round, when
+// more than a quarter full and small enough, as 128 x 256 halves in a second launch.
+template <int YT>
+bool launch_s8_big(const GemmArgs& a, hipStream_t stream) {
+    const std::size_t tiles_m = (a.t + 255) / 256, tiles_n = (a.n + 255) / 256;
+    const int cus = device_cus();
+    if (tiles_m * tiles_n < static_cast<std::size_t>(cus)) return false;
+    if ((a.t + 256) * a.ld_x >= (std::size_t{1} << 31) || (a.n + 256) * a.ld_w >= (std::size_t{1} << 31)) return false;
+    S8Params p{};
+    p.x = static_cast<const signed char*>(a.x);
+    p.ld_x = a.ld_x;
+    p.xs = a.xs;
+    p.ld_xs = a.ld_xs;
+    p.w = reinterpret_cast<const signed char*>(a.w);
+    p.ld_w = a.ld_w;
+    p.ws = a.s;
+    p.ld_ws = a.ld_s;
+    p.y = a.y;
+    p.ld_y = a.ld_y;
+    p.t = static_cast<int>(a.t);
+    p.n = static_cast<int>(a.n);
+    p.k = static_cast<int>(a.k);
+    p.tiles_m = static_cast<int>(tiles_m);
+    p.tiles_n = static_cast<int>(tiles_n);
+    p.x_bytes = (a.t - 1) * a.ld_x + a.k;
+    p.w_bytes = (a.n - 1) * a.ld_w + a.k;
+    const int total = p.tiles_m * p.tiles_n, full = total / cus * cus, rest = total - full;
+    const bool split = rest > cus / 4 && full > 0 && 2 * rest <= cus;
+    p.id0 = 0;
+    p.count = split ? full : total;
+    gemm_s8_big<YT, 4><<<dim3(p.count), dim3(512), 0, stream>>>(p);
+    if (split) {
+        S8Params q = p;
+        q.id0 = full;
+        q.count = rest;
+        gemm_s8_big<YT, 2><<<dim3(2 * rest), dim3(512), 0, stream>>>(q);
+    }
+    check_launch("gemm_s8 large-M kernel launch");
+    return true;
+}
+
+} // namespace q8
+
 void launch_gemm_s8(const GemmArgs& a, hipStream_t stream) {
-    if (a.y_type == SEPAL_HIP_F16) q8::launch_big<SEPAL_HIP_STORE, SEPAL_HIP_F16, true, q8::MODE_WHOLE>(a, stream);
-    else q8::launch_big<SEPAL_HIP_STORE, SEPAL_HIP_F32, true, q8::MODE_WHOLE>(a, stream);
+    if (a.y_type == SEPAL_HIP_F16) {
+        if (!q8::launch_s8_big<SEPAL_HIP_F16>(a, stream)) q8::launch_big<SEPAL_HIP_STORE, SEPAL_HIP_F16, true, q8::MODE_WHOLE>(a, stream);
+    } else {
+        if (!q8::launch_s8_big<SEPAL_HIP_F32>(a, stream)) q8::launch_big<SEPAL_HIP_STORE, SEPAL_HIP_F32, true, q8::MODE_WHOLE>(a, stream);
+    }
 }
 
 void launch_q8_group_sums(const GemmArgs& a, hipStream_t stream) {

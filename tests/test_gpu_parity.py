@@ -687,9 +687,12 @@ def test_gemm_s8_full_size_sampled_rows(sm):
     xq, sx = sm.s8_quantize_rows(x)
     wq, sw = sm.s8_quantize_rows(dev((rng.standard_normal((n, k)) * 0.02).astype(np.float16)))
     y = sm.gemm_s8(xq, sx, wq, sw)
-    rows = np.sort(rng.choice(t, 48, replace=False))
+    # random rows and rows of the last tiles (the partial last round of 256 x 256 tiles runs as 128 x 256 halves)
+    rows = np.unique(np.concatenate([rng.choice(t, 48, replace=False), [12287, 12288, 15359, 15360, 15487, 15488, 15871]]))
     ref = orc.gemm_s8(host(xq[rows]), host(sx[rows]), host(wq), host(sw))
     assert same_bits(host(y[rows]), ref)
+    y16 = sm.gemm_s8(xq, sx, wq, sw, y_dtype=torch.float16)
+    assert same_bits(host(y16[rows]), host(y[rows]).astype(np.float16))
 
 
 def test_s8_family_row_invariance(sm):
