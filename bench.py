@@ -349,6 +349,18 @@ def main():
             del w_o, q_o, s_o, x_o, y_o
         extra["other_groups_w8g_m15872"] = others
         log(f"other int8 groups (w8g, M=15872): {others}")
+        # ---- C2's shape (one MLP block at M = 896, layer 0's weights): gate/up SwiGLU + down, w8g. A parity
+        # configuration; its GPU time is reported here for reference ----
+        x896 = bf16_x(torch, 896, 0)
+        h896 = torch.empty(896, I, dtype=torch.float16, device="cuda")
+        y896 = torch.empty(896, H, dtype=torch.float32, device="cuda")
+        ms_c2 = timed(torch, lambda: (sm.gemm_w8g(x896, wgu, sgu, y=h896, epilogue=sm.SWIGLU), sm.gemm_w8g(h896, wd, sd, y=y896)),
+                      20, 3, stream)
+        ops_c2 = OPS_PER_ROW_LAYER * 896
+        extra["c2_mlp_block_m896"] = {"ms": round(ms_c2, 4), "tops": round(ops_c2 / (ms_c2 * 1e-3) / 1e12, 1),
+                                      "frac_bf16_peak": round(ops_c2 / (ms_c2 * 1e-3) / 1e12 / PEAK["bf16_tflops"], 4)}
+        log(f"C2 shape (M=896 block): {extra['c2_mlp_block_m896']}")
+        del x896, h896, y896
         # ---- the per-channel int8 family (the reference's launch_gemm_s8 / launch_gemm_w8a16) at the MLP shapes ----
         s8 = {}
         for n_o, k_o in ((2 * I, H), (H, I)):
