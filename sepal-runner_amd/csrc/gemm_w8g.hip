@@ -14,9 +14,10 @@
 //   large M: waves of 128 x 64 outputs (4 x 2 blocks of 32 x 32, MFMA 32x32x16; 64 x 64 in the half tiles), the
 //            weights widened once per tile when staged into LDS; 1-D grid with an XCD-aware tile order (a block's id
 //            modulo 8 is its XCD; consecutive logical tiles are kept on one XCD so they share its L2). gemm_big3:
-//            256 x 256 tiles (and 128 x 256 halves for a launch's last partial round), K in steps of 64, X straight
-//            from global memory into LDS. gemm_big2 (grids of fewer than 512 large tiles): 256 x 128 or 256 x 256
-//            tiles, K in steps of 32.
+//            256 x 256 tiles (128 x 256 halves for a launch's last partial round, 64 x 256 quarters for grids of fewer
+//            than 512 large tiles), K in steps of 64, X straight from global memory into LDS. gemm_big2 (when an
+//            offset does not fit 32 bits, or a SwiGLU N is not a multiple of 256): 256 x 128 or 256 x 256 tiles, K in
+//            steps of 32.
 //   small M: stream.hip (the weights streamed once, HBM-bound).
 #include "common.hpp"
 #include "gemm_kernels.hpp"
@@ -338,7 +339,8 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
 
     const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
     const int wm = wave % 2, wn = wave / 2;
-    // MB 4: one logical 256 x 256 tile per block; MB 2: block b is half b / count (128 rows) of tile id0 + b % count
+    // MB 4: one logical 256 x 256 tile per block; MB 2 or 1: block b is part b / count (BM3 rows) of tile
+    // id0 + b % count; a part wholly past T has nothing to do
     int tm, tn, m0;
     if constexpr (MB == 4) {
         tile_from_id(p.id0 + xcd_id(blockIdx.x, p.count), p.tiles_m, p.tiles_n, tm, tn);
@@ -347,6 +349,7 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
         const int b = blockIdx.x;
         tile_from_id(p.id0 + b % p.count, p.tiles_m, p.tiles_n, tm, tn);
         m0 = tm * 256 + (b / p.count) * BM3;
+        if (m0 >= p.t) return;
     }
     const int n0 = tn * BN;
     const int KT = p.k / K3;
@@ -632,6 +635,13 @@ void launch_big(const GemmArgs& a, hipStream_t stream) {
     } else if (wide) {
         p.tiles_n = tn256;
         launch_big2<XT, EP, YT, 4>(p, stream);
+    } else if (offsets32 && (EP != SEPAL_HIP_SWIGLU || a.n % 256 == 0)) {
+        // fewer than two rounds of 256 x 256 tiles: 64 x 256 quarters of the same kernel (one m-block per wave), four
+        // times the blocks
+        p.tiles_n = tn256;
+        p.id0 = 0;
+        p.count = tiles_m * tn256;
+        launch_big3<XT, EP, YT, 1>(p, stream);
     } else {
         p.tiles_n = static_cast<int>((a.n + 127) / 128);
         launch_big2<XT, EP, YT, 2>(p, stream);
