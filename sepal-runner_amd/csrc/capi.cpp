@@ -10,13 +10,17 @@
 #include <algorithm>
 #include <cstring>
 #include <cstdlib>
+#include <map>
+#include <memory>
 #include <mutex>
 #include <new>
 #include <string>
+#include <utility>
 #include <vector>
 
 #include "common.hpp"
 #include "gemm_kernels.hpp"
+#include "stack_glue.hpp"
 
 namespace sepal::hip {
 
@@ -54,35 +58,46 @@ inline hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
 
 bool valid_type(int t) { return t == SEPAL_HIP_F32 || t == SEPAL_HIP_BF16 || t == SEPAL_HIP_F16; }
 
+// One workspace per (device, stream). Work that uses a workspace is enqueued only on its own stream, so growing it
+// waits for that stream alone before the old buffer is freed, and two streams (or two engines with their own streams)
+// never share counters or scratch. A Lease holds the workspace's mutex from the size check to the end of the entry
+// point's enqueueing, so a second thread on the same stream cannot free the buffer under a call that is still
+// enqueueing work on it.
 struct Workspace {
+    std::mutex m;
     void* ptr = nullptr;
     std::size_t bytes = 0;
 };
 std::mutex g_ws_mutex;
-std::vector<Workspace> g_ws;
+std::map<std::pair<int, hipStream_t>, std::unique_ptr<Workspace>> g_ws;
 
 } // namespace
 
-void* workspace(std::size_t bytes, hipStream_t stream) {
+Lease::Lease(std::size_t bytes, hipStream_t stream) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) throw LaunchError("hipGetDevice failed");
-    std::lock_guard<std::mutex> lock(g_ws_mutex);
-    if (g_ws.size() <= static_cast<std::size_t>(dev)) g_ws.resize(static_cast<std::size_t>(dev) + 1);
-    Workspace& w = g_ws[static_cast<std::size_t>(dev)];
-    if (w.bytes < bytes) {
-        // the old buffer may still be read by work queued on the stream: wait for it before freeing
-        if (w.ptr != nullptr) {
+    Workspace* w;
+    {
+        std::lock_guard<std::mutex> lock(g_ws_mutex);
+        auto& slot = g_ws[{dev, stream}];
+        if (!slot) slot = std::make_unique<Workspace>();
+        w = slot.get();
+    }
+    lock_ = std::unique_lock<std::mutex>(w->m);
+    if (w->bytes < bytes) {
+        // the old buffer may still be read by work queued on this stream: wait for it before freeing
+        if (w->ptr != nullptr) {
             if (hipStreamSynchronize(stream) != hipSuccess) throw LaunchError("hipStreamSynchronize failed");
-            (void)hipFree(w.ptr);
-            w.ptr = nullptr;
-            w.bytes = 0;
+            (void)hipFree(w->ptr);
+            w->ptr = nullptr;
+            w->bytes = 0;
         }
         const std::size_t grown = bytes < (std::size_t{64} << 20) ? (std::size_t{64} << 20) : bytes;
-        if (hipMalloc(&w.ptr, grown) != hipSuccess) throw std::bad_alloc();
-        if (hipMemset(w.ptr, 0, grown) != hipSuccess) throw LaunchError("hipMemset of the workspace failed");
-        w.bytes = grown;
+        if (hipMalloc(&w->ptr, grown) != hipSuccess) throw std::bad_alloc();
+        if (hipMemset(w->ptr, 0, grown) != hipSuccess) throw LaunchError("hipMemset of the workspace failed");
+        w->bytes = grown;
     }
-    return w.ptr;
+    base_ = static_cast<char*>(w->ptr);
 }
 
 namespace {
@@ -147,7 +162,7 @@ int32_t sepal_hip_quantize_gate_up_s8(const void* gate, const void* up, int32_t 
 
 int32_t sepal_hip_gemm_w8g_supports(int32_t x_type, size_t n, size_t k, size_t ld_x, size_t ld_w, size_t ld_y,
                                     int32_t epilogue) {
-    if (x_type != SEPAL_HIP_BF16 && x_type != SEPAL_HIP_F16) return 0;
+    if (!valid_type(x_type)) return 0;
     if (n == 0 || k == 0 || k % 128 != 0 || ld_x < k || ld_w < k || ld_x % 16 != 0 || ld_w % 16 != 0 || ld_y % 4 != 0) return 0;
     if (epilogue == SEPAL_HIP_SWIGLU) return n % 128 == 0 && ld_y >= n / 2 ? 1 : 0;
     if (epilogue != SEPAL_HIP_STORE && epilogue != SEPAL_HIP_ADD) return 0;
@@ -158,7 +173,7 @@ int32_t sepal_hip_gemm_w8g(const void* x, int32_t x_type, size_t ld_x, const int
                            size_t ld_s, void* y, int32_t y_type, size_t ld_y, size_t t, size_t n, size_t k,
                            int32_t epilogue, int32_t config, void* stream) {
     return guarded([&] {
-        require(x_type == SEPAL_HIP_BF16 || x_type == SEPAL_HIP_F16, "gemm_w8g: X must be bf16 or binary16");
+        require(valid_type(x_type), "gemm_w8g: X must be float32, bf16 or binary16");
         require(valid_type(y_type), "gemm_w8g: unknown output type");
         require(epilogue == SEPAL_HIP_SWIGLU || y_type == SEPAL_HIP_F32, "gemm_w8g: Store and Add write float32");
         require(config >= -1 && config <= 2, "gemm_w8g: config must be -1, 0, 1 or 2");
@@ -183,7 +198,13 @@ int32_t sepal_hip_gemm_w8g(const void* x, int32_t x_type, size_t ld_x, const int
         a.epilogue = epilogue;
         a.config = config == 2 ? 1 : config;
         a.force_splits = config == 2 ? 1 : 0;
-        launch_gemm_w8g(a, as_stream(stream));
+        const hipStream_t st = as_stream(stream);
+        const std::size_t extra = gemm_w8g_scratch_bytes(a);
+        Lease ws(kScratchOffset + extra, st);
+        a.scratch = ws.base();
+        a.xsplit = ws.base() + kScratchOffset;
+        a.ytmp = reinterpret_cast<float*>(ws.base() + kScratchOffset + gemm_w8g_split_bytes(a));
+        launch_gemm_w8g(a, st);
     });
 }
 
@@ -234,6 +255,8 @@ int32_t sepal_hip_gemm_q8(const int8_t* xq, size_t ld_x, const float* xs, size_t
         a.epilogue = epilogue;
         a.config = config == 2 ? 1 : config;
         a.force_splits = config == 2 ? 1 : 0;
+        Lease ws(kScratchOffset, as_stream(stream));
+        a.scratch = ws.base();
         launch_gemm_q8(a, as_stream(stream));
     });
 }
@@ -328,7 +351,8 @@ int32_t sepal_hip_gemm_w8a16(const void* x, size_t ld_x, const int8_t* wq, size_
         const bool direct = y_type == SEPAL_HIP_F32 || t > static_cast<std::size_t>(kSmallM);
         const std::size_t chunk = direct ? t : std::max<std::size_t>(1, (std::size_t{64} << 20) / (n * 4));
         const std::size_t rows = std::min(t, chunk);
-        char* ws = static_cast<char*>(workspace(kScratchOffset + s_bytes + (direct ? 0 : rows * n * 4), st));
+        Lease lease(kScratchOffset + s_bytes + (direct ? 0 : rows * n * 4), st);
+        char* ws = lease.base();
         float* s = reinterpret_cast<float*>(ws + kScratchOffset);
         float* tmp = reinterpret_cast<float*>(ws + kScratchOffset + s_bytes);
         launch_broadcast_scales(sw, s, n, groups, st);
@@ -350,6 +374,7 @@ int32_t sepal_hip_gemm_w8a16(const void* x, size_t ld_x, const int8_t* wq, size_
             a.n = n;
             a.k = k;
             a.epilogue = SEPAL_HIP_STORE;
+            a.scratch = ws;
             launch_gemm_w8g(a, st);
             if (!direct) launch_f32_to_f16(tmp, n, static_cast<std::uint16_t*>(y) + r0 * ld_y, ld_y, tr, n, st);
         }
@@ -396,7 +421,9 @@ int32_t sepal_hip_gemm_q8_swiglu_quantize(const int8_t* xq, size_t ld_x, const f
         }
         // small M: the float32 H through the workspace, then the activation quantizer (the same values and rule)
         const std::size_t cols = n / 2;
-        float* h = reinterpret_cast<float*>(static_cast<char*>(workspace(kScratchOffset + t * cols * 4, st)) + kScratchOffset);
+        Lease ws(kScratchOffset + t * cols * 4, st);
+        float* h = reinterpret_cast<float*>(ws.base() + kScratchOffset);
+        a.scratch = ws.base();
         a.y = h;
         a.y_type = SEPAL_HIP_F32;
         a.ld_y = cols;
@@ -474,8 +501,8 @@ int32_t sepal_hip_weight_fingerprint(const void* data, size_t bytes, uint64_t* o
         require(data != nullptr && out != nullptr, "weight_fingerprint: null pointer");
         require(aligned8(data), "weight_fingerprint: data must be 8-byte aligned");
         const hipStream_t st = as_stream(stream);
-        char* ws = static_cast<char*>(workspace(kScratchOffset + fingerprint_scratch_bytes(), st));
-        launch_fingerprint(data, bytes, out, ws + kScratchOffset, st);
+        Lease ws(kScratchOffset + fingerprint_scratch_bytes(), st);
+        launch_fingerprint(data, bytes, out, ws.base() + kScratchOffset, st);
     });
 }
 
@@ -497,8 +524,8 @@ int32_t sepal_hip_packed_save(const char* path, const int8_t* q, size_t ld_q, co
     return guarded([&] {
         check_packed("packed_save", path, q, ld_q, s, ld_s, rows, k, rule, layout);
         const hipStream_t st = as_stream(stream);
-        char* ws = static_cast<char*>(workspace(kScratchOffset + fingerprint_scratch_bytes(), st));
-        packed_save(path, q, ld_q, s, ld_s, rows, k, rule, layout, source_fp, ws + kScratchOffset, st);
+        Lease ws(kScratchOffset + fingerprint_scratch_bytes(), st);
+        packed_save(path, q, ld_q, s, ld_s, rows, k, rule, layout, source_fp, ws.base() + kScratchOffset, st);
     });
 }
 
@@ -507,154 +534,195 @@ int32_t sepal_hip_packed_load(const char* path, int8_t* q, size_t ld_q, float* s
     return guarded([&] {
         check_packed("packed_load", path, q, ld_q, s, ld_s, rows, k, rule, layout);
         const hipStream_t st = as_stream(stream);
-        char* ws = static_cast<char*>(workspace(kScratchOffset + fingerprint_scratch_bytes(), st));
-        packed_load(path, q, ld_q, s, ld_s, rows, k, rule, layout, source_fp, ws + kScratchOffset, st);
+        Lease ws(kScratchOffset + fingerprint_scratch_bytes(), st);
+        packed_load(path, q, ld_q, s, ld_s, rows, k, rule, layout, source_fp, ws.base() + kScratchOffset, st);
     });
 }
+
+} // extern "C"
+
+namespace sepal::hip {
+
+void check_stack_args(int32_t kind, size_t hidden, size_t inter, const void* x, const int8_t* const* w_gate_up,
+                      const float* const* s_gate_up, const int8_t* const* w_down, const float* const* s_down, const float* y,
+                      size_t act_block) {
+    require(kind == 0 || kind == 1 || kind == 2, "mlp_stack: kind must be 0 (w8g), 1 (q8) or 2 (w8g, float32 H)");
+    require(hidden % 128 == 0 && inter % 128 == 0 && hidden != 0 && inter != 0, "mlp_stack: hidden and inter must be multiples of 128");
+    require(w_gate_up != nullptr && s_gate_up != nullptr && w_down != nullptr && s_down != nullptr && x != nullptr && y != nullptr,
+            "mlp_stack: null pointer");
+    require(kind != 1 || act_block == 128 || act_block == 0, "mlp_stack: act_block must be 128 or 0 (one scale per token)");
+    require(hidden < 0x7FFFFFFFu && inter < 0x7FFFFFFFu, "mlp_stack: dimension beyond 2^31");
+}
+
+StackZones stack_zones(int kind, std::size_t t, std::size_t hidden, std::size_t inter, std::size_t act_block) {
+    StackZones z;
+    z.per_token = act_block == 0;
+    z.ab_h = z.per_token ? hidden : 128;
+    z.ab_i = z.per_token ? inter : 128;
+    const auto up256 = [](std::size_t b) { return (b + 255) / 256 * 256; };
+    z.off_h = kScratchOffset;
+    if (kind == 0 && small_stack_plan(t, hidden, inter, z.plan)) {
+        // M <= 16 (stack_small.hip): H binary16, the down pass's K-part sums float32
+        z.form = StackZones::SMALL_W8G;
+        z.off_p = z.off_h + up256(t * inter * 2);
+        z.end = z.off_p + static_cast<std::size_t>(z.plan.parts) * t * hidden * 4;
+        return z;
+    }
+    // (per token, the down pass reads the gate/up grid's partial row maxima: at most 256 blocks)
+    if (kind == 1 && small_stack_plan(t, hidden, inter, z.plan) &&
+        (!z.per_token || (inter / 8 + z.plan.tiles_per_block - 1) / z.plan.tiles_per_block <= 256)) {
+        // M <= 16 gpu-q8w: H float32 with, per token, its partial row maxima; K-part sums; the int8 layer input
+        z.form = StackZones::SMALL_Q8;
+        z.off_hmax = z.off_h + up256(t * inter * 4);
+        z.off_p = z.off_hmax + up256(t * static_cast<std::size_t>(z.plan.blocks) * 4);
+        z.off_qx = z.off_p + up256(static_cast<std::size_t>(z.plan.parts) * t * hidden * 4);
+        z.off_sx = z.off_qx + up256(t * hidden);
+        z.end = z.off_sx + up256(t * (hidden / z.ab_h) * 4);
+        return z;
+    }
+    // general: H [t, inter] (binary16 for w8g; float32 for kind 2, and for q8 unless the gate/up epilogue quantizes
+    // it); q8 also the int8 layer input and int8 H with their scales; kind 2 the hi + lo pairs of H for the down
+    // multiply
+    z.fused_h = kind == 1 && z.ab_i == 128 && t > kSmallM;
+    const std::size_t h_bytes = kind == 0 ? t * inter * 2 : (z.fused_h ? 0 : t * inter * 4);
+    z.off_qx = z.off_h + up256(h_bytes);
+    z.off_sx = z.off_qx + (kind == 1 ? up256(t * hidden) : 0);
+    z.off_qh = z.off_sx + (kind == 1 ? up256(t * (hidden / z.ab_h) * 4) : 0);
+    z.off_sh = z.off_qh + (kind == 1 ? up256(t * inter) : 0);
+    z.off_split = z.off_sh + (kind == 1 ? up256(t * (inter / z.ab_i) * 4) : 0);
+    std::size_t split = 0;
+    if (kind == 2) {
+        GemmArgs dn;
+        dn.x_type = SEPAL_HIP_F32;
+        dn.t = t;
+        dn.n = hidden;
+        dn.k = inter;
+        dn.ld_w = inter;
+        dn.epilogue = SEPAL_HIP_STORE;
+        split = gemm_w8g_scratch_bytes(dn);
+    }
+    z.end = z.off_split + split;
+    return z;
+}
+
+// One call of the stack on the scratch at `ws` (laid out by stack_zones).
+void run_stack(const StackZones& z, int kind, std::size_t layers, std::size_t t, std::size_t hidden, std::size_t inter,
+               void* x, const int8_t* const* w_gate_up, const float* const* s_gate_up, const int8_t* const* w_down,
+               const float* const* s_down, float* y, double eps, char* ws, hipStream_t st) {
+    if (z.form == StackZones::SMALL_W8G) {
+        // three launches per layer: whole-K gate/up tiles per CU, the down multiply in K-parts, the finish pass
+        for (std::size_t l = 0; l < layers; ++l)
+            launch_small_layer(z.plan, t, hidden, inter, x, w_gate_up[l], s_gate_up[l], w_down[l], s_down[l], ws + z.off_h,
+                               reinterpret_cast<float*>(ws + z.off_p), y, l + 1 < layers ? x : nullptr, eps, st);
+        return;
+    }
+    if (z.form == StackZones::SMALL_Q8) {
+        // the same three launches on int8 MFMAs; the down pass quantizes H while staging it; the finish pass quantizes
+        // the next layer's input
+        auto* qx = reinterpret_cast<std::int8_t*>(ws + z.off_qx);
+        auto* sx = reinterpret_cast<float*>(ws + z.off_sx);
+        launch_quantize_rows(x, SEPAL_HIP_BF16, hidden, qx, hidden, sx, hidden / z.ab_h, t, hidden, z.ab_h, st);
+        for (std::size_t l = 0; l < layers; ++l)
+            launch_small_layer_q8(z.plan, t, hidden, inter, qx, sx, z.per_token, w_gate_up[l], s_gate_up[l], w_down[l],
+                                  s_down[l], reinterpret_cast<float*>(ws + z.off_h), reinterpret_cast<float*>(ws + z.off_hmax),
+                                  reinterpret_cast<float*>(ws + z.off_p), y, l + 1 < layers ? qx : nullptr, sx,
+                                  l + 1 < layers ? x : nullptr, eps, st);
+        return;
+    }
+    void* h = ws + z.off_h;
+    auto* qx = reinterpret_cast<std::int8_t*>(ws + z.off_qx);
+    auto* sx = reinterpret_cast<float*>(ws + z.off_sx);
+    auto* qh = reinterpret_cast<std::int8_t*>(ws + z.off_qh);
+    auto* sh = reinterpret_cast<float*>(ws + z.off_sh);
+    for (std::size_t l = 0; l < layers; ++l) {
+        GemmArgs gu;
+        gu.t = t;
+        gu.n = 2 * inter;
+        gu.k = hidden;
+        gu.w = w_gate_up[l];
+        gu.ld_w = hidden;
+        gu.s = s_gate_up[l];
+        gu.ld_s = hidden / 128;
+        gu.y = h;
+        gu.ld_y = inter;
+        gu.epilogue = SEPAL_HIP_SWIGLU;
+        gu.scratch = ws;
+        GemmArgs dn;
+        dn.t = t;
+        dn.n = hidden;
+        dn.k = inter;
+        dn.w = w_down[l];
+        dn.ld_w = inter;
+        dn.s = s_down[l];
+        dn.ld_s = inter / 128;
+        dn.y = y;
+        dn.ld_y = hidden;
+        dn.epilogue = SEPAL_HIP_STORE;
+        dn.scratch = ws;
+        if (kind != 1) {
+            // w8g: H binary16 (kind 0) or float32 (kind 2, the down multiply on its bf16 hi + lo pairs)
+            gu.x = x;
+            gu.x_type = SEPAL_HIP_BF16;
+            gu.ld_x = hidden;
+            gu.y_type = kind == 0 ? SEPAL_HIP_F16 : SEPAL_HIP_F32;
+            launch_gemm_w8g(gu, st);
+            dn.x = h;
+            dn.x_type = kind == 0 ? SEPAL_HIP_F16 : SEPAL_HIP_F32;
+            dn.ld_x = inter;
+            dn.y_type = SEPAL_HIP_F32;
+            dn.xsplit = ws + z.off_split;
+            launch_gemm_w8g(dn, st);
+            if (l + 1 < layers) launch_rmsnorm(y, hidden, x, SEPAL_HIP_BF16, hidden, nullptr, t, hidden, eps, st);
+            continue;
+        }
+        // q8: the first layer's input is quantized here; later ones come quantized out of the fused RMSNorm
+        if (l == 0) launch_quantize_rows(x, SEPAL_HIP_BF16, hidden, qx, hidden, sx, hidden / z.ab_h, t, hidden, z.ab_h, st);
+        gu.x = qx;
+        gu.ld_x = hidden;
+        gu.xs = sx;
+        gu.ld_xs = hidden / z.ab_h;
+        gu.act_block = z.ab_h;
+        gu.y_type = SEPAL_HIP_F32;
+        if (z.fused_h) {
+            // SwiGLU and the int8 re-quantization of H in the gate/up epilogue
+            gu.y = qh;
+            gu.ld_y = inter;
+            gu.ys = sh;
+            gu.ld_ys = inter / 128;
+            launch_gemm_q8_swiglu_q8(gu, st);
+        } else {
+            launch_gemm_q8(gu, st);
+            launch_quantize_rows(h, SEPAL_HIP_F32, inter, qh, inter, sh, inter / z.ab_i, t, inter, z.ab_i, st);
+        }
+        dn.x = qh;
+        dn.ld_x = inter;
+        dn.xs = sh;
+        dn.ld_xs = inter / z.ab_i;
+        dn.act_block = z.ab_i;
+        dn.y_type = SEPAL_HIP_F32;
+        launch_gemm_q8(dn, st);
+        // the next layer's input: RMSNorm, bf16 and the int8 quantization in one pass (x keeps the bf16 input of the
+        // last layer)
+        if (l + 1 < layers)
+            launch_rmsnorm_quantize(y, hidden, l + 2 == layers ? static_cast<std::uint16_t*>(x) : nullptr, hidden, nullptr, qx,
+                                    hidden, sx, hidden / z.ab_h, t, hidden, z.ab_h, eps, st);
+    }
+}
+
+} // namespace sepal::hip
+
+extern "C" {
 
 int32_t sepal_hip_mlp_stack(int32_t kind, size_t layers, size_t t, size_t hidden, size_t inter, void* x,
                             const int8_t* const* w_gate_up, const float* const* s_gate_up, const int8_t* const* w_down,
                             const float* const* s_down, float* y, size_t act_block, double eps, void* stream) {
     return guarded([&] {
-        require(kind == 0 || kind == 1, "mlp_stack: kind must be 0 (w8g) or 1 (q8)");
-        require(hidden % 128 == 0 && inter % 128 == 0 && hidden != 0 && inter != 0, "mlp_stack: hidden and inter must be multiples of 128");
-        require(w_gate_up != nullptr && s_gate_up != nullptr && w_down != nullptr && s_down != nullptr && x != nullptr && y != nullptr,
-                "mlp_stack: null pointer");
-        require(kind == 0 || act_block == 128 || act_block == 0, "mlp_stack: act_block must be 128 or 0 (one scale per token)");
+        check_stack_args(kind, hidden, inter, x, w_gate_up, s_gate_up, w_down, s_down, y, act_block);
         if (layers == 0 || t == 0) return;
         const hipStream_t st = as_stream(stream);
-        // workspace: H [t, inter] (binary16 for w8g; float32 for q8 unless the gate/up epilogue quantizes it); q8 also
-        // the int8 layer input and int8 H with their scales
-        const std::size_t ab_h = act_block == 0 ? hidden : 128, ab_i = act_block == 0 ? inter : 128;
-        const bool fused_h = kind == 1 && ab_i == 128 && t > kSmallM;
-        const auto up256 = [](std::size_t b) { return (b + 255) / 256 * 256; };
-        const std::size_t h_bytes = kind == 0 ? t * inter * 2 : (fused_h ? 0 : t * inter * 4);
-        const std::size_t off_h = kScratchOffset;
-        SmallStackPlan plan{};
-        if (kind == 0 && small_stack_plan(t, hidden, inter, plan)) {
-            // M <= 16 (stack_small.hip): three launches per layer, or every layer in one cooperative launch; H
-            // binary16, the down pass's partial sums float32. SEPAL_HIP_SMALL_STACK selects the form: "layers"
-            // (default, the faster), "persistent" or "persistent-late" (weights issued only once a phase has started);
-            // all three give the same bits.
-            const std::size_t off_p = off_h + up256(h_bytes);
-            char* wsp = static_cast<char*>(workspace(off_p + static_cast<std::size_t>(plan.parts) * t * hidden * 4, st));
-            const char* mode = std::getenv("SEPAL_HIP_SMALL_STACK");
-            const std::string m = mode != nullptr ? mode : "layers";
-            require(m == "persistent" || m == "persistent-late" || m == "layers",
-                    "mlp_stack: SEPAL_HIP_SMALL_STACK must be persistent, persistent-late or layers");
-            if (m != "layers" &&
-                launch_small_stack(plan, layers, t, hidden, inter, x, w_gate_up, s_gate_up, w_down, s_down, wsp + off_h,
-                                   reinterpret_cast<float*>(wsp + off_p), y, reinterpret_cast<unsigned*>(wsp), eps,
-                                   m == "persistent", st))
-                return;
-            for (std::size_t l = 0; l < layers; ++l)
-                launch_small_layer(plan, t, hidden, inter, x, w_gate_up[l], s_gate_up[l], w_down[l], s_down[l], wsp + off_h,
-                                   reinterpret_cast<float*>(wsp + off_p), y, l + 1 < layers ? x : nullptr, eps, st);
-            return;
-        }
-        // (per token, the down pass reads the gate/up grid's partial row maxima: at most 256 blocks)
-        if (kind == 1 && small_stack_plan(t, hidden, inter, plan) &&
-            (act_block != 0 || (inter / 8 + plan.tiles_per_block - 1) / plan.tiles_per_block <= 256)) {
-            // M <= 16 gpu-q8w (stack_small.hip): three launches per layer on int8 MFMAs; H float32 with, per token,
-            // its partial row maxima; the down pass quantizes H while staging it; the finish pass quantizes the next
-            // layer's input
-            const bool per_token = act_block == 0;
-            const std::size_t ab = per_token ? hidden : 128;
-            const std::size_t q_h = off_h, q_hmax = q_h + up256(t * inter * 4);
-            const std::size_t q_p = q_hmax + up256(t * static_cast<std::size_t>(plan.blocks) * 4);
-            const std::size_t q_x = q_p + up256(static_cast<std::size_t>(plan.parts) * t * hidden * 4);
-            const std::size_t q_s = q_x + up256(t * hidden);
-            char* wsq = static_cast<char*>(workspace(q_s + up256(t * (hidden / ab) * 4), st));
-            auto* qx = reinterpret_cast<std::int8_t*>(wsq + q_x);
-            auto* sx = reinterpret_cast<float*>(wsq + q_s);
-            launch_quantize_rows(x, SEPAL_HIP_BF16, hidden, qx, hidden, sx, hidden / ab, t, hidden, ab, st);
-            for (std::size_t l = 0; l < layers; ++l)
-                launch_small_layer_q8(plan, t, hidden, inter, qx, sx, per_token, w_gate_up[l], s_gate_up[l], w_down[l], s_down[l],
-                                      reinterpret_cast<float*>(wsq + q_h), reinterpret_cast<float*>(wsq + q_hmax),
-                                      reinterpret_cast<float*>(wsq + q_p), y, l + 1 < layers ? qx : nullptr, sx,
-                                      l + 1 < layers ? x : nullptr, eps, st);
-            return;
-        }
-        const std::size_t off_qx = off_h + up256(h_bytes);
-        const std::size_t off_sx = off_qx + (kind == 1 ? up256(t * hidden) : 0);
-        const std::size_t off_qh = off_sx + (kind == 1 ? up256(t * (hidden / ab_h) * 4) : 0);
-        const std::size_t off_sh = off_qh + (kind == 1 ? up256(t * inter) : 0);
-        const std::size_t end = off_sh + (kind == 1 ? up256(t * (inter / ab_i) * 4) : 0);
-        char* ws = static_cast<char*>(workspace(end, st));
-        void* h = ws + off_h;
-        std::int8_t* qx = reinterpret_cast<std::int8_t*>(ws + off_qx);
-        float* sx = reinterpret_cast<float*>(ws + off_sx);
-        std::int8_t* qh = reinterpret_cast<std::int8_t*>(ws + off_qh);
-        float* sh = reinterpret_cast<float*>(ws + off_sh);
-        for (std::size_t l = 0; l < layers; ++l) {
-            GemmArgs gu;
-            gu.t = t;
-            gu.n = 2 * inter;
-            gu.k = hidden;
-            gu.w = w_gate_up[l];
-            gu.ld_w = hidden;
-            gu.s = s_gate_up[l];
-            gu.ld_s = hidden / 128;
-            gu.y = h;
-            gu.ld_y = inter;
-            gu.epilogue = SEPAL_HIP_SWIGLU;
-            GemmArgs dn;
-            dn.t = t;
-            dn.n = hidden;
-            dn.k = inter;
-            dn.w = w_down[l];
-            dn.ld_w = inter;
-            dn.s = s_down[l];
-            dn.ld_s = inter / 128;
-            dn.y = y;
-            dn.ld_y = hidden;
-            dn.epilogue = SEPAL_HIP_STORE;
-            if (kind == 0) {
-                gu.x = x;
-                gu.x_type = SEPAL_HIP_BF16;
-                gu.ld_x = hidden;
-                gu.y_type = SEPAL_HIP_F16;
-                launch_gemm_w8g(gu, st);
-                dn.x = h;
-                dn.x_type = SEPAL_HIP_F16;
-                dn.ld_x = inter;
-                dn.y_type = SEPAL_HIP_F32;
-                launch_gemm_w8g(dn, st);
-                if (l + 1 < layers) launch_rmsnorm(y, hidden, x, SEPAL_HIP_BF16, hidden, nullptr, t, hidden, eps, st);
-                continue;
-            }
-            // q8: the first layer's input is quantized here; later ones come quantized out of the fused RMSNorm
-            if (l == 0) launch_quantize_rows(x, SEPAL_HIP_BF16, hidden, qx, hidden, sx, hidden / ab_h, t, hidden, ab_h, st);
-            gu.x = qx;
-            gu.ld_x = hidden;
-            gu.xs = sx;
-            gu.ld_xs = hidden / ab_h;
-            gu.act_block = ab_h;
-            gu.y_type = SEPAL_HIP_F32;
-            if (fused_h) {
-                // SwiGLU and the int8 re-quantization of H in the gate/up epilogue
-                gu.y = qh;
-                gu.ld_y = inter;
-                gu.ys = sh;
-                gu.ld_ys = inter / 128;
-                launch_gemm_q8_swiglu_q8(gu, st);
-            } else {
-                launch_gemm_q8(gu, st);
-                launch_quantize_rows(h, SEPAL_HIP_F32, inter, qh, inter, sh, inter / ab_i, t, inter, ab_i, st);
-            }
-            dn.x = qh;
-            dn.ld_x = inter;
-            dn.xs = sh;
-            dn.ld_xs = inter / ab_i;
-            dn.act_block = ab_i;
-            dn.y_type = SEPAL_HIP_F32;
-            launch_gemm_q8(dn, st);
-            // the next layer's input: RMSNorm, bf16 and the int8 quantization in one pass (x keeps the bf16 input of
-            // the last layer)
-            if (l + 1 < layers)
-                launch_rmsnorm_quantize(y, hidden, l + 2 == layers ? static_cast<std::uint16_t*>(x) : nullptr, hidden, nullptr,
-                                        qx, hidden, sx, hidden / ab_h, t, hidden, ab_h, eps, st);
-        }
+        const StackZones z = stack_zones(kind, t, hidden, inter, act_block);
+        Lease ws(z.end, st);
+        run_stack(z, kind, layers, t, hidden, inter, x, w_gate_up, s_gate_up, w_down, s_down, y, eps, ws.base(), st);
     });
 }
 

@@ -30,6 +30,10 @@ struct GemmArgs {
     std::int32_t* sums = nullptr;  // group-sum mode
     float* ys = nullptr;           // kSwigluQ8: output scales [t, ld_ys], one per 128 columns of y
     std::size_t ld_ys = 0;
+    // scratch the caller (the C ABI) carves out of its workspace:
+    void* scratch = nullptr;  // the zero-at-rest split-K counters (kCounterBytes) followed by kPartialBytes of partials
+    void* xsplit = nullptr;   // w8g with float32 X: the bf16 hi + lo pairs
+    float* ytmp = nullptr;    // w8g with float32 X and SwiGLU off the one-pass kernel: the float32 sums [t, n]
 };
 
 // q8 epilogue (internal, not in the public enum): SwiGLU, then the output quantized to int8 per row and 128 columns
@@ -37,6 +41,11 @@ struct GemmArgs {
 constexpr int kSwigluQ8 = 16;
 
 void launch_gemm_w8g(const GemmArgs& a, hipStream_t stream);
+// Scratch bytes launch_gemm_w8g needs at xsplit (then ytmp, 256-byte aligned, when non-zero) for this problem; 0 for a
+// 16-bit X.
+std::size_t gemm_w8g_scratch_bytes(const GemmArgs& a);
+// The part of gemm_w8g_scratch_bytes that is the split buffer (ytmp follows it).
+inline std::size_t gemm_w8g_split_bytes(const GemmArgs& a) { return (a.t * a.k * 4 + 255) / 256 * 256; }
 void launch_stream_w8g(const GemmArgs& a, hipStream_t stream);
 void launch_stream_q8(const GemmArgs& a, hipStream_t stream);
 void launch_gemm_q8(const GemmArgs& a, hipStream_t stream);
@@ -98,12 +107,5 @@ void launch_small_layer_q8(const SmallStackPlan& plan, std::size_t t, std::size_
                            const std::int8_t* xq, const float* xs, bool per_token, const std::int8_t* w_gu, const float* s_gu,
                            const std::int8_t* w_d, const float* s_d, float* h, float* hmax, float* part, float* y,
                            std::int8_t* xq_next, float* xs_next, void* xn, double eps, hipStream_t stream);
-// Every layer in one cooperative launch per 64 layers (one block per CU), the same results as launch_small_layer per
-// layer. counters: the library's zero-at-rest counter words (hidden / 16 tile counters at the start, the grid barrier's
-// at word 4096). Returns false, launching nothing, when the device cannot keep the grid resident.
-bool launch_small_stack(const SmallStackPlan& plan, std::size_t layers, std::size_t t, std::size_t hidden, std::size_t inter,
-                        void* x, const std::int8_t* const* w_gu, const float* const* s_gu, const std::int8_t* const* w_d,
-                        const float* const* s_d, void* h, float* part, float* y, unsigned* counters, double eps,
-                        bool early, hipStream_t stream);
 
 } // namespace sepal::hip

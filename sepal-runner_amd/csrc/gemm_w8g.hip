@@ -53,9 +53,6 @@ __device__ __forceinline__ f32x4 mfma16(const u32x4 a, const u32x4 b, f32x4 c) {
         return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
 }
 
-// Effective scale of a group: a zero (or negative/NaN) scale marks an all-zero group and keeps the previous one.
-__device__ __forceinline__ float next_scale(float s, float prev) { return s > 0.0f ? s : prev; }
-
 // Epilogue of one output element (row, col) of the plain multiply: float32 Store / Add, or a binary16 Store (the
 // float32 value rounded to nearest even, as a separate conversion would).
 template <int EP, int YT>
@@ -224,7 +221,8 @@ __global__ void __launch_bounds__(128 * WN) __attribute__((amdgpu_waves_per_eu(2
     issue(2, r2);
     stage(0, r0);
     __syncthreads();
-    float e[2] = {snext[0] > 0.0f ? snext[0] : 1.0f, snext[1] > 0.0f ? snext[1] : 1.0f};
+    // the Horner state (the first step's factor multiplies zero accumulators)
+    float e[2] = {1.0f, 1.0f}, emax[2] = {0.0f, 0.0f};
 
     // One step: issue step kt + 3's loads into the registers of step kt - 1 (the next group's scales first when
     // kt + 3 starts a group); at a group's first step the Horner rescale; the multiply of step kt; then stage step
@@ -242,9 +240,7 @@ __global__ void __launch_bounds__(128 * WN) __attribute__((amdgpu_waves_per_eu(2
         if constexpr (first) {
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
-                const float en = snext[j] > 0.0f ? snext[j] : e[j];
-                const float ratio = __fmul_rn(e[j], __builtin_amdgcn_rcpf(en));
-                e[j] = en;
+                const float ratio = horner_step(snext[j], e[j], emax[j]);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) acc[i][j] = acc[i][j] * ratio;
             }
@@ -318,10 +314,14 @@ __device__ __forceinline__ void wait_vm_lgkm0() {
     __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4));  // vmcnt(N) lgkmcnt(0)
 }
 
-template <int XT, int EP, int YT, int MB>
+template <int XT, int EP, int YT, int MB, int SPLIT>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) gemm_big3(const BigParams p) {
-    // MB m-blocks of 32 rows per wave: tiles of BM3 = 64 MB rows (256, or 128 for the tail rows of a launch)
-    constexpr int NW = 8, BN = 256, K3 = 64, SUB = K3 / 16, SPG = 128 / K3, BM3 = 64 * MB;
+    // MB m-blocks of 32 rows per wave: tiles of BM3 = 64 MB rows (256, or 128 for the tail rows of a launch).
+    // SPLIT 2: X is a float32 operand as a bf16 hi + lo pair, stored as one bf16 row of 2K values (64-value chunk j of
+    // k is chunk 2j (hi) and 2j + 1 (lo)); steps 2j and 2j + 1 multiply the same weights, so p.k counts the 2K values
+    // and the weight offset of step kt is kt / 2 chunks.
+    static_assert(SPLIT == 1 || (SPLIT == 2 && XT == SEPAL_HIP_BF16), "the hi + lo form is bf16");
+    constexpr int NW = 8, BN = 256, K3 = 64, SUB = K3 / 16, SPG = SPLIT * 128 / K3, BM3 = 64 * MB;
     constexpr int XSTAGE = BM3 * K3 * 2, WSTAGE = (BN / 32) * SUB * 1024;
     constexpr int XLD = XSTAGE / 16 / (64 * NW);       // X direct loads per thread per step (4)
     constexpr int WLD = BN * K3 / 16 / (64 * NW);      // W 16-byte chunks per thread per step (2)
@@ -410,7 +410,7 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
     const auto issue_w = [&](int kt, Regs& r) {
 #pragma unroll
         for (int i = 0; i < WLD; ++i)
-            r.w[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wres, woff, kt * K3 + i * wstride, 0));
+            r.w[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wres, woff, (kt / SPLIT) * K3 + i * wstride, 0));
     };
     const auto issue_scales = [&](int g) {
         snext[0] = ssrc[0][g];
@@ -458,7 +458,8 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
     wait_vm_lgkm0<WLD>();  // everything but step 1's W (X of steps 0 and 1 included)
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-    float e[2] = {snext[0] > 0.0f ? snext[0] : 1.0f, snext[1] > 0.0f ? snext[1] : 1.0f};
+    // the Horner state (the first step's factor multiplies zero accumulators)
+    float e[2] = {1.0f, 1.0f}, emax[2] = {0.0f, 0.0f};
 
     // Step kt (j = kt mod 6): at a group's first step the Horner rescale with the group's scales (loaded one group
     // ahead), then the next group's scales are issued; the direct X loads of step kt + 2 into X stage (j + 2) mod 3 (last
@@ -467,7 +468,7 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
     // (clamped) and land in stages nothing reads again.
     const auto step = [&](int kt, auto jt) {
         constexpr int j = decltype(jt)::value;
-        constexpr bool first = j % 2 == 0;
+        constexpr bool first = j % SPG == 0;
         Regs& r_next = j % 2 == 0 ? r1 : r0;
         Regs& r_free = j % 2 == 0 ? r0 : r1;
         const lds_byte* xs = xstage(std::integral_constant<int, j % 3>{});
@@ -476,9 +477,7 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
         if constexpr (first) {
 #pragma unroll
             for (int q = 0; q < 2; ++q) {
-                const float en = snext[q] > 0.0f ? snext[q] : e[q];
-                ratio[q] = __fmul_rn(e[q], __builtin_amdgcn_rcpf(en));
-                e[q] = en;
+                ratio[q] = horner_step(snext[q], e[q], emax[q]);
             }
             issue_scales(min(kt / SPG + 1, groups - 1));
         }
@@ -520,22 +519,20 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
         stage_w(wstage(std::integral_constant<int, (j + 1) % 2>{}), r_next);
         barrier();
     };
-    static_assert(SPG == 2, "two steps per group");
+    // the loop body is three groups (6 SPLIT steps: a multiple of the 3 X stages and 2 W stages), then at most two
+    // whole groups remain
+    constexpr int U = 3 * SPG;
+    const auto steps = [&]<int... J>(int k0, std::integer_sequence<int, J...>) {
+        (step(k0 + J, std::integral_constant<int, J>{}), ...);
+    };
     int kt = 0;
-    for (; kt + 6 <= KT; kt += 6) {
-        step(kt, std::integral_constant<int, 0>{});
-        step(kt + 1, std::integral_constant<int, 1>{});
-        step(kt + 2, std::integral_constant<int, 2>{});
-        step(kt + 3, std::integral_constant<int, 3>{});
-        step(kt + 4, std::integral_constant<int, 4>{});
-        step(kt + 5, std::integral_constant<int, 5>{});
-    }
-    if (kt + 2 <= KT) {
-        step(kt, std::integral_constant<int, 0>{});
-        step(kt + 1, std::integral_constant<int, 1>{});
-        if (kt + 4 <= KT) {
-            step(kt + 2, std::integral_constant<int, 2>{});
-            step(kt + 3, std::integral_constant<int, 3>{});
+    for (; kt + U <= KT; kt += U) steps(kt, std::make_integer_sequence<int, U>{});
+    if (kt + SPG <= KT) {
+        steps(kt, std::make_integer_sequence<int, SPG>{});
+        if (kt + 2 * SPG <= KT) {
+            [&]<int... J>(std::integer_sequence<int, J...>) {
+                (step(kt + SPG + J, std::integral_constant<int, SPG + J>{}), ...);
+            }(std::make_integer_sequence<int, SPG>{});
         }
     }
     // no direct load may still be writing LDS when the block ends
@@ -596,24 +593,31 @@ inline int device_cus() {
     return cus;
 }
 
-template <int XT, int EP, int YT, int MB>
+template <int XT, int EP, int YT, int MB, int SPLIT>
 void launch_big3(const BigParams& p, hipStream_t stream) {
-    v2::gemm_big3<XT, EP, YT, MB><<<dim3(p.count * (256 / (64 * MB))), dim3(512), 0, stream>>>(p);
+    v2::gemm_big3<XT, EP, YT, MB, SPLIT><<<dim3(p.count * (256 / (64 * MB))), dim3(512), 0, stream>>>(p);
 }
 
-template <int XT, int EP, int YT>
+// gemm_big3 addresses X and W with 32-bit offsets (rows up to one tile past the end included) and writes SwiGLU outputs
+// from whole 256-column tiles. kx: X values per row (K, or 2K for the hi + lo form).
+bool big3_takes(const GemmArgs& a, std::size_t kx, std::size_t ld_x) {
+    const bool offsets32 = (a.t + 256) * ld_x * 2 < (std::size_t{1} << 31) && (a.n + 256) * a.ld_w < (std::size_t{1} << 31);
+    return offsets32 && kx <= ld_x && (a.epilogue != SEPAL_HIP_SWIGLU || a.n % 256 == 0);
+}
+
+template <int XT, int EP, int YT, int SPLIT>
 void launch_big(const GemmArgs& a, hipStream_t stream) {
+    const std::size_t kx = SPLIT * a.k;  // X values per row
     BigParams p{static_cast<const unsigned short*>(a.x), a.ld_x, reinterpret_cast<const signed char*>(a.w), a.ld_w, a.s, a.ld_s,
-                a.y, a.ld_y, static_cast<int>(a.t), static_cast<int>(a.n), static_cast<int>(a.k), 0, 0,
-                ((a.t - 1) * a.ld_x + a.k) * 2, (a.n - 1) * a.ld_w + a.k};
+                a.y, a.ld_y, static_cast<int>(a.t), static_cast<int>(a.n), static_cast<int>(kx), 0, 0,
+                ((a.t - 1) * a.ld_x + kx) * 2, (a.n - 1) * a.ld_w + a.k};
     // 256 x 256 tiles when there are enough of them to fill the chip twice, else 256 x 128
     const int tiles_m = static_cast<int>((a.t + 255) / 256);
     const int tn256 = static_cast<int>((a.n + 255) / 256);
+    const bool takes = big3_takes(a, kx, a.ld_x);
     const bool wide = static_cast<long>(tiles_m) * tn256 >= 2 * 256 && (EP != SEPAL_HIP_SWIGLU || a.n % 256 == 0);
     p.tiles_m = tiles_m;
-    // gemm_big3 addresses X and W with 32-bit offsets, rows up to one tile past the end included
-    const bool offsets32 = (a.t + 256) * a.ld_x * 2 < (std::size_t{1} << 31) && (a.n + 256) * a.ld_w < (std::size_t{1} << 31);
-    if (wide && offsets32) {
+    if (wide && takes) {
         // The last, partial round of 256 x 256 tiles is the idle tail of the launch. When it is more than a quarter
         // full and its tiles fit one round as 128 x 256 halves, they go to a second launch of half-height tiles (the
         // logical ids past the full rounds, each as two halves). Both launches run the same k order and Horner chain
@@ -625,60 +629,172 @@ void launch_big(const GemmArgs& a, hipStream_t stream) {
         p.tiles_n = tn256;
         p.id0 = 0;
         p.count = split ? full : total;
-        launch_big3<XT, EP, YT, 4>(p, stream);
+        launch_big3<XT, EP, YT, 4, SPLIT>(p, stream);
         if (split) {
             BigParams q = p;
             q.id0 = full;
             q.count = rest;
-            launch_big3<XT, EP, YT, 2>(q, stream);
+            launch_big3<XT, EP, YT, 2, SPLIT>(q, stream);
         }
-    } else if (wide) {
-        p.tiles_n = tn256;
-        launch_big2<XT, EP, YT, 4>(p, stream);
-    } else if (offsets32 && (EP != SEPAL_HIP_SWIGLU || a.n % 256 == 0)) {
+    } else if (takes && !wide) {
         // fewer than two rounds of 256 x 256 tiles: 64 x 256 quarters of the same kernel (one m-block per wave), four
         // times the blocks
         p.tiles_n = tn256;
         p.id0 = 0;
         p.count = tiles_m * tn256;
-        launch_big3<XT, EP, YT, 1>(p, stream);
+        launch_big3<XT, EP, YT, 1, SPLIT>(p, stream);
+    } else if constexpr (SPLIT == 1) {
+        p.tiles_n = wide ? tn256 : static_cast<int>((a.n + 127) / 128);
+        if (wide) launch_big2<XT, EP, YT, 4>(p, stream);
+        else launch_big2<XT, EP, YT, 2>(p, stream);
     } else {
-        p.tiles_n = static_cast<int>((a.n + 127) / 128);
-        launch_big2<XT, EP, YT, 2>(p, stream);
+        throw LaunchError("gemm_w8g: the hi + lo form runs on the 64-wide-step kernel only");
     }
     check_launch("gemm_w8g large-M kernel launch");
 }
 
-template <int XT, int EP, int YT>
-void dispatch_path(const GemmArgs& a, hipStream_t stream) {
-    // the small-M kernels write float32 (or SwiGLU outputs); a binary16 Store always takes the large-M kernels
-    const bool small = (YT == SEPAL_HIP_F32 || EP == SEPAL_HIP_SWIGLU) && (a.config == 1 || (a.config < 0 && a.t <= kSmallM));
-    if (small) launch_stream_w8g(a, stream);
-    else launch_big<XT, EP, YT>(a, stream);
+// Whether a problem takes the small-M (weight-streaming) kernels: they write float32 (or SwiGLU outputs); a binary16
+// Store always takes the large-M kernels.
+inline bool small_path(const GemmArgs& a) {
+    const bool eligible = a.y_type == SEPAL_HIP_F32 || a.epilogue == SEPAL_HIP_SWIGLU;
+    return eligible && (a.config == 1 || (a.config < 0 && a.t <= kSmallM));
 }
 
-template <int XT>
+template <int XT, int EP, int YT, int SPLIT>
+void dispatch_path(const GemmArgs& a, hipStream_t stream) {
+    if (SPLIT == 1 && small_path(a)) launch_stream_w8g(a, stream);
+    else launch_big<XT, EP, YT, SPLIT>(a, stream);
+}
+
+template <int XT, int SPLIT>
 void dispatch_ep(const GemmArgs& a, hipStream_t stream) {
     switch (a.epilogue) {
     case SEPAL_HIP_STORE:
-        if (a.y_type == SEPAL_HIP_F16) dispatch_path<XT, SEPAL_HIP_STORE, SEPAL_HIP_F16>(a, stream);
-        else dispatch_path<XT, SEPAL_HIP_STORE, SEPAL_HIP_F32>(a, stream);
+        if (a.y_type == SEPAL_HIP_F16) dispatch_path<XT, SEPAL_HIP_STORE, SEPAL_HIP_F16, SPLIT>(a, stream);
+        else dispatch_path<XT, SEPAL_HIP_STORE, SEPAL_HIP_F32, SPLIT>(a, stream);
         break;
-    case SEPAL_HIP_ADD: dispatch_path<XT, SEPAL_HIP_ADD, SEPAL_HIP_F32>(a, stream); break;
+    case SEPAL_HIP_ADD: dispatch_path<XT, SEPAL_HIP_ADD, SEPAL_HIP_F32, SPLIT>(a, stream); break;
     default:
         switch (a.y_type) {
-        case SEPAL_HIP_F32: dispatch_path<XT, SEPAL_HIP_SWIGLU, SEPAL_HIP_F32>(a, stream); break;
-        case SEPAL_HIP_BF16: dispatch_path<XT, SEPAL_HIP_SWIGLU, SEPAL_HIP_BF16>(a, stream); break;
-        default: dispatch_path<XT, SEPAL_HIP_SWIGLU, SEPAL_HIP_F16>(a, stream); break;
+        case SEPAL_HIP_F32: dispatch_path<XT, SEPAL_HIP_SWIGLU, SEPAL_HIP_F32, SPLIT>(a, stream); break;
+        case SEPAL_HIP_BF16: dispatch_path<XT, SEPAL_HIP_SWIGLU, SEPAL_HIP_BF16, SPLIT>(a, stream); break;
+        default: dispatch_path<XT, SEPAL_HIP_SWIGLU, SEPAL_HIP_F16, SPLIT>(a, stream); break;
         }
+    }
+}
+
+// ---- float32 X: the hi + lo split ----------------------------------------------------------------------------------
+//
+// A float32 x is the sum of hi = bf16(x) (nearest even) and lo = bf16(x - hi); x - hi is exact in float32 and lo is
+// within 2^-9 of it, so hi + lo is within 2^-17 |x| of x. Each bf16 times an int8 weight is exact in the float32
+// accumulator, so the multiply of the pair is the float32 product within that bound plus the accumulation's rounding.
+
+// x float32 [t, ld_x] -> pairs. Layout 0 (for gemm_big3's hi + lo form): one row of 2k bf16 per token, the 64-value
+// chunk j of k stored as chunk 2j (hi) and 2j + 1 (lo). Layout 1: hi [t, k] at out, lo [t, k] at out + t k.
+__global__ void __launch_bounds__(256) split_kernel(const float* __restrict__ x, std::size_t ld_x, unsigned short* __restrict__ out,
+                                                    int t, int k, int layout) {
+    const int per_row = k / 8;
+    const std::size_t total = static_cast<std::size_t>(t) * per_row;
+    for (std::size_t id = blockIdx.x * 256ull + threadIdx.x; id < total; id += static_cast<std::size_t>(gridDim.x) * 256) {
+        const int r = static_cast<int>(id / per_row), k0 = 8 * static_cast<int>(id % per_row);
+        const float* src = x + static_cast<std::size_t>(r) * ld_x + k0;
+        const f32x4 v0 = *reinterpret_cast<const f32x4*>(src), v1 = *reinterpret_cast<const f32x4*>(src + 4);
+        unsigned hi[4], lo[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float a = i < 2 ? v0[2 * i] : v1[2 * i - 4], b = i < 2 ? v0[2 * i + 1] : v1[2 * i - 3];
+            const unsigned short ha = f32_to_bf16_bits(a), hb = f32_to_bf16_bits(b);
+            const unsigned short la = f32_to_bf16_bits(__fsub_rn(a, bf16_bits_to_f32(ha)));
+            const unsigned short lb = f32_to_bf16_bits(__fsub_rn(b, bf16_bits_to_f32(hb)));
+            hi[i] = ha | (static_cast<unsigned>(hb) << 16);
+            lo[i] = la | (static_cast<unsigned>(lb) << 16);
+        }
+        unsigned short *dh, *dl;
+        if (layout == 0) {
+            dh = out + static_cast<std::size_t>(r) * (2 * k) + 128 * (k0 / 64) + k0 % 64;
+            dl = dh + 64;
+        } else {
+            dh = out + static_cast<std::size_t>(r) * k + k0;
+            dl = dh + static_cast<std::size_t>(t) * k;
+        }
+        *reinterpret_cast<u32x4*>(dh) = u32x4{hi[0], hi[1], hi[2], hi[3]};
+        *reinterpret_cast<u32x4*>(dl) = u32x4{lo[0], lo[1], lo[2], lo[3]};
+    }
+}
+
+// y[t, f] = swiglu(z[t, 128 (f / 64) + f % 64], z[t, 128 (f / 64) + 64 + f % 64]) for the f < n / 2 outputs.
+template <int YT>
+__global__ void __launch_bounds__(256) swiglu_rows_kernel(const float* __restrict__ z, int n, void* __restrict__ y,
+                                                          std::size_t ld_y, int t) {
+    const int half = n / 2;
+    const std::size_t total = static_cast<std::size_t>(t) * half;
+    for (std::size_t id = blockIdx.x * 256ull + threadIdx.x; id < total; id += static_cast<std::size_t>(gridDim.x) * 256) {
+        const int r = static_cast<int>(id / half), f = static_cast<int>(id % half);
+        const float* zr = z + static_cast<std::size_t>(r) * n + 128 * (f / 64) + f % 64;
+        store_out<YT>(y, static_cast<std::size_t>(r) * ld_y + f, swiglu_libm(zr[0], zr[64]));
+    }
+}
+
+inline int grid_for(std::size_t items) {
+    return static_cast<int>(std::min<std::size_t>((items + 255) / 256, std::size_t{8192}));
+}
+
+void launch_f32(const GemmArgs& a, hipStream_t stream) {
+    if (a.xsplit == nullptr) throw LaunchError("gemm_w8g: float32 X needs the split buffer");
+    const int t = static_cast<int>(a.t), k = static_cast<int>(a.k);
+    auto* pairs = static_cast<unsigned short*>(a.xsplit);
+    if (!small_path(a) && big3_takes(a, 2 * a.k, 2 * a.k)) {
+        // one pass of the 64-wide-step kernel over the hi + lo row (twice the MFMAs of a 16-bit X)
+        split_kernel<<<grid_for(a.t * (a.k / 8)), 256, 0, stream>>>(static_cast<const float*>(a.x), a.ld_x, pairs, t, k, 0);
+        check_launch("gemm_w8g split launch");
+        GemmArgs b = a;
+        b.x = pairs;
+        b.x_type = SEPAL_HIP_BF16;
+        b.ld_x = 2 * a.k;
+        dispatch_ep<SEPAL_HIP_BF16, 2>(b, stream);
+        return;
+    }
+    // any other path: hi and lo as two bf16 multiplies, the second added in float32
+    split_kernel<<<grid_for(a.t * (a.k / 8)), 256, 0, stream>>>(static_cast<const float*>(a.x), a.ld_x, pairs, t, k, 1);
+    check_launch("gemm_w8g split launch");
+    GemmArgs hi = a, lo = a;
+    hi.x = pairs;
+    lo.x = pairs + a.t * a.k;
+    hi.x_type = lo.x_type = SEPAL_HIP_BF16;
+    hi.ld_x = lo.ld_x = a.k;
+    lo.epilogue = SEPAL_HIP_ADD;
+    if (a.epilogue == SEPAL_HIP_SWIGLU) {
+        if (a.ytmp == nullptr) throw LaunchError("gemm_w8g: float32 X with SwiGLU needs the sum buffer");
+        hi.y = lo.y = a.ytmp;
+        hi.y_type = lo.y_type = SEPAL_HIP_F32;
+        hi.ld_y = lo.ld_y = a.n;
+        hi.epilogue = SEPAL_HIP_STORE;
+    }
+    dispatch_ep<SEPAL_HIP_BF16, 1>(hi, stream);
+    dispatch_ep<SEPAL_HIP_BF16, 1>(lo, stream);
+    if (a.epilogue == SEPAL_HIP_SWIGLU) {
+        const int g = grid_for(a.t * (a.n / 2));
+        const int n = static_cast<int>(a.n);
+        if (a.y_type == SEPAL_HIP_F32) swiglu_rows_kernel<SEPAL_HIP_F32><<<g, 256, 0, stream>>>(a.ytmp, n, a.y, a.ld_y, t);
+        else if (a.y_type == SEPAL_HIP_BF16) swiglu_rows_kernel<SEPAL_HIP_BF16><<<g, 256, 0, stream>>>(a.ytmp, n, a.y, a.ld_y, t);
+        else swiglu_rows_kernel<SEPAL_HIP_F16><<<g, 256, 0, stream>>>(a.ytmp, n, a.y, a.ld_y, t);
+        check_launch("gemm_w8g swiglu launch");
     }
 }
 
 } // namespace w8g
 
 void launch_gemm_w8g(const GemmArgs& a, hipStream_t stream) {
-    if (a.x_type == SEPAL_HIP_BF16) w8g::dispatch_ep<SEPAL_HIP_BF16>(a, stream);
-    else w8g::dispatch_ep<SEPAL_HIP_F16>(a, stream);
+    if (a.x_type == SEPAL_HIP_F32) w8g::launch_f32(a, stream);
+    else if (a.x_type == SEPAL_HIP_BF16) w8g::dispatch_ep<SEPAL_HIP_BF16, 1>(a, stream);
+    else w8g::dispatch_ep<SEPAL_HIP_F16, 1>(a, stream);
+}
+
+std::size_t gemm_w8g_scratch_bytes(const GemmArgs& a) {
+    if (a.x_type != SEPAL_HIP_F32) return 0;
+    const auto up256 = [](std::size_t b) { return (b + 255) / 256 * 256; };
+    const bool one_pass = !w8g::small_path(a) && w8g::big3_takes(a, 2 * a.k, 2 * a.k);
+    return up256(a.t * a.k * 4) + (!one_pass && a.epilogue == SEPAL_HIP_SWIGLU ? up256(a.t * a.n * 4) : 0);
 }
 
 } // namespace sepal::hip

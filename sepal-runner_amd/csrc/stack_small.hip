@@ -527,413 +527,6 @@ __global__ void __launch_bounds__(1024) finish_kernel(const float* __restrict__ 
 }
 
 
-// ---- the persistent form: one cooperative launch runs every layer ----------------------------------------------------
-//
-// One block per CU for the whole stack. Per layer: phase A (gate/up -> H), grid barrier, phase B (down -> P, and the
-// last block of each column tile adds its K-parts into y), grid barrier, phase C (16 waves make the next layer's X rows,
-// bf16(RMSNorm(y))), grid barrier. The phases do the same arithmetic in the same order as pass_kernel and
-// finish_kernel, with the same plan, so the results are the same bits. The loader waves do all the hand-offs (staging,
-// epilogues, barriers); the workers only stream weights and multiply, and with `early` set they issue the next phase's
-// weight loads as soon as their registers are free, so the weights stay in flight across the barriers.
-constexpr int kMaxLayers = 64;         // layers of one launch (the host splits longer stacks)
-constexpr int kNormHalf = 48;          // row values per lane of the phase-C RMSNorm: 3072 columns at most
-constexpr unsigned kSpinLimit = 1u << 16;  // grid-barrier polls before a wait gives up (about 50 ms)
-
-struct StackParams {
-    const signed char* w_gu[kMaxLayers];
-    const float* s_gu[kMaxLayers];
-    const signed char* w_d[kMaxLayers];
-    const float* s_d[kMaxLayers];
-    unsigned short* x;     // bf16 [t, hidden]: layer 0's input; receives every later layer's input
-    unsigned short* h;     // binary16 [t, inter]
-    float* part;           // float32 [parts][t][hidden]
-    float* y;              // float32 [t, hidden]
-    unsigned* tile_count;  // [hidden / 16] arrivals per down column tile, zero at rest
-    unsigned* grid_count;  // [3] barrier arrivals and block exits (zero at rest), launches that timed out
-    unsigned* timeout;     // set to 1 when a barrier wait gives up (cleared by the launch's last block out)
-    double eps;
-    int layers, t, hidden, inter;
-    int per_a;                // gate/up tiles per block
-    int parts, per_d, bpp_d;  // down K-parts, column tiles per block, blocks per part
-    int x_region;             // bytes of the staged-row region (16 rows at the widest pitch)
-    int early;                // workers issue the next phase's weights before its barrier
-};
-
-// Data that one block writes and blocks on other XCDs read (H, P, y, x) is written and read at device coherence (the
-// SC1 cache-policy bit on buffer accesses, agent-scope relaxed atomics on plain stores); a writer waits for its stores
-// to complete before it arrives at a barrier or counter. No release/acquire fences: on this part they write back and
-// invalidate the whole L2.
-constexpr int kCoherent = 16;
-
-// A buffer resource over `bytes` bytes at p: loads take one lane offset register, the uniform rest in the scalar
-// offset, and reads past the end return zero.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, std::size_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, static_cast<int>(bytes), 0x00020000);
-}
-
-// The (tile, group) work of one block in one phase: tiles tile0 .. tile0 + ntiles - 1, groups g_lo .. g_lo + gpt - 1,
-// total = ntiles * gpt pairs dealt to the workers in runs of `per`.
-struct Geo {
-    int tile0, ntiles, g_lo, gpt, total, per, part;
-};
-
-__device__ __forceinline__ Geo geo_gate_up(const StackParams& p, int b) {
-    Geo g;
-    g.tile0 = b * p.per_a;
-    g.ntiles = max(0, min(p.per_a, p.inter / 8 - g.tile0));
-    g.g_lo = 0;
-    g.gpt = p.hidden / 128;
-    g.part = 0;
-    g.total = g.ntiles * g.gpt;
-    g.per = (g.total + kWorkers - 1) / kWorkers;
-    return g;
-}
-
-__device__ __forceinline__ Geo geo_down(const StackParams& p, int b) {
-    Geo g;
-    const int gi = p.inter / 128;
-    g.part = b / p.bpp_d;
-    g.tile0 = (b % p.bpp_d) * p.per_d;
-    g.ntiles = g.part < p.parts ? max(0, min(p.per_d, p.hidden / 16 - g.tile0)) : 0;
-    const int part = min(g.part, p.parts - 1);
-    g.g_lo = part * gi / p.parts;
-    g.gpt = (part + 1) * gi / p.parts - g.g_lo;
-    g.total = g.ntiles * g.gpt;
-    g.per = (g.total + kWorkers - 1) / kWorkers;
-    return g;
-}
-
-// A worker's weight loads of one phase (as pass_kernel: two instructions of 8 rows x 128 bytes per pair; past the
-// worker's share the loads stay on its last pair). The row offset within a pair is one lane term; the rest is uniform.
-template <bool SWIGLU>
-__device__ __forceinline__ void issue_pairs(const Geo& g, const signed char* w, int ld_w, int rows, int wk, int lane,
-                                            u32x4 (&wb)[kPairs][2]) {
-    if (g.total == 0) return;
-    constexpr int kRowStep = SWIGLU ? 64 : 8;
-    (void)rows;
-    const int q0 = min(wk * g.per, g.total - 1), q1 = min(wk * g.per + g.per, g.total);
-    const int qlast = max(q1 - 1, q0);
-    const int voff = (lane / 8) * ld_w + 16 * (lane % 8);
-#pragma unroll
-    for (int i = 0; i < kPairs; ++i) {
-        const int q = min(q0 + i, qlast);
-        const int tile = g.tile0 + q / g.gpt, grp = g.g_lo + q % g.gpt;
-        // global loads (a buffer load here would make the compiler wait for every load before the first LDS read)
-        const signed char* base = w + static_cast<std::size_t>(tile_row<SWIGLU>(tile, 0)) * ld_w + 128 * grp;
-        wb[i][0] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(base + voff));
-        wb[i][1] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(base + voff + kRowStep * ld_w));
-    }
-}
-
-// A worker's multiply of one phase (the same steps as pass_kernel's workers).
-template <int XT>
-__device__ __forceinline__ void multiply_pairs(const Geo& g, const unsigned char* xs, int xpitch, float* red, const float* scl,
-                                               unsigned char* tb, int wk, int lane, const u32x4 (&wb)[kPairs][2]) {
-    const int q0 = min(wk * g.per, g.total), q1 = min(q0 + g.per, g.total);
-    const int n_pairs = q1 - q0;
-    if (n_pairs <= 0) return;
-    const int wr_lo = (lane / 8) * 128 + ((lane % 8 + lane / 16) % 8) * 16;
-    const int wr_hi = (8 + lane / 8) * 128 + ((lane % 8 + 4 + lane / 16) % 8) * 16;
-    f32x4 cur = {0.0f, 0.0f, 0.0f, 0.0f};
-    int cur_slot = 0;
-    const auto flush = [&](int slot_) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) red[(wk * kSlots + slot_) * 256 + (4 * (lane / 16) + r) * 16 + lane % 16] = cur[r];
-    };
-#pragma unroll
-    for (int i = 0; i < kPairs; ++i) {
-        if (i >= n_pairs) continue;
-        const int q = q0 + i;
-        if (i > 0 && q % g.gpt == 0) {
-            flush(cur_slot);
-            ++cur_slot;
-            cur = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-        }
-        const float sc = scl[((q / g.gpt) * 16 + lane % 16) * g.gpt + q % g.gpt];
-        const int kofs = 128 * (q % g.gpt);
-        f32x4 prt = {0.0f, 0.0f, 0.0f, 0.0f};
-        *reinterpret_cast<u32x4*>(tb + wr_lo) = wb[i][0];
-        *reinterpret_cast<u32x4*>(tb + wr_hi) = wb[i][1];
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const int rr = lane % 16, cc = 4 * h + lane / 16;
-            const u32x4 wv = *reinterpret_cast<const u32x4*>(tb + rr * 128 + ((cc + rr / 2) % 8) * 16);
-            unsigned o[8];
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                if constexpr (XT == SEPAL_HIP_BF16) s8x4_to_bf16x4(wv[c], o[2 * c], o[2 * c + 1]);
-                else s8x4_to_f16x4(wv[c], o[2 * c], o[2 * c + 1]);
-            }
-            const unsigned char* xr = xs + (lane % 16) * xpitch + 2 * (kofs + 64 * h + 16 * (lane / 16));
-            const u32x4 a0 = *reinterpret_cast<const u32x4*>(xr);
-            const u32x4 a1 = *reinterpret_cast<const u32x4*>(xr + 16);
-            prt = mfma16(XT, a0, u32x4{o[0], o[1], o[2], o[3]}, prt);
-            prt = mfma16(XT, a1, u32x4{o[4], o[5], o[6], o[7]}, prt);
-        }
-#pragma unroll
-        for (int r = 0; r < 4; ++r) cur[r] = __builtin_fmaf(prt[r], sc, cur[r]);
-    }
-    flush(cur_slot);
-}
-
-// A loader thread's share of one phase's scales (lt = 0 .. 64 kLoaders - 1), held in registers until the phase's
-// staging writes them to LDS.
-template <bool SWIGLU>
-__device__ __forceinline__ void load_scales(const Geo& g, const float* s, int ld_s, int lt, float (&sv)[kScaleLoads]) {
-    if (g.total == 0) return;
-#pragma unroll
-    for (int e = 0; e < kScaleLoads; ++e) {
-        const int idx = min(lt + e * 64 * kLoaders, g.total * 16 - 1);
-        const int tl = idx / (16 * g.gpt), rem = idx % (16 * g.gpt);
-        sv[e] = s[static_cast<std::size_t>(tile_row<SWIGLU>(g.tile0 + tl, rem / g.gpt)) * ld_s + g.g_lo + rem % g.gpt];
-    }
-}
-
-// The four loader waves meet (LDS arrival counter; `gen` counts the meetings of this thread).
-__device__ __forceinline__ void loaders_meet(unsigned* ctr, unsigned& gen, int lane) {
-    gen += kLoaders;
-    __builtin_amdgcn_s_waitcnt(0);  // this wave's global stores and LDS writes are done
-    if (lane == 0) __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
-    while (__hip_atomic_load(ctr, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < gen) __builtin_amdgcn_s_sleep(1);
-}
-
-// Grid barrier number `n` (0-based) of this launch, run by the loaders: every loader wave's stores complete
-// (loaders_meet waits for them), then thread 0 arrives and polls with agent-scope relaxed atomics; the other loader
-// waves wait in the second loaders_meet. A poll that runs past kSpinLimit (or sees another block's timeout) gives up and sets the timeout flag,
-// so every wave still reaches the end of the kernel.
-__device__ __forceinline__ void grid_barrier(const StackParams& p, unsigned n, unsigned* ctr, unsigned& gen, int tid, int lane) {
-    loaders_meet(ctr, gen, lane);
-    if (tid == 0) {
-        const unsigned target = (n + 1) * gridDim.x;
-        __hip_atomic_fetch_add(&p.grid_count[0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        for (unsigned spin = 0; __hip_atomic_load(&p.grid_count[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target; ++spin) {
-            if (spin > kSpinLimit || __hip_atomic_load(p.timeout, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u) {
-                __hip_atomic_store(p.timeout, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                break;
-            }
-            __builtin_amdgcn_s_sleep(2);
-        }
-    }
-    loaders_meet(ctr, gen, lane);
-}
-
-// Rows 4 w .. 4 w + 3 (w = loader wave) of a [t, ld] 16-bit matrix, columns col0 .. col0 + kw - 1, into the staged
-// rows (rows past T repeat row T - 1), as pass_kernel's loaders.
-__device__ __forceinline__ void stage_rows(const unsigned short* src, int ld, int col0, int kw, int t, unsigned char* xs,
-                                           int xpitch, int wave, int lane) {
-    const int cpr = kw / 8;
-#pragma unroll
-    for (int rr = 0; rr < 4; rr += 2) {
-        u32x4 xv[2][kXChunks];
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const __amdgpu_buffer_rsrc_t rr_ = rsrc(src + static_cast<std::size_t>(min(4 * wave + rr + h, t - 1)) * ld + col0, 2 * kw);
-#pragma unroll
-            for (int e = 0; e < kXChunks; ++e)
-                xv[h][e] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rr_, 16 * lane, 1024 * e, kCoherent));
-        }
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-#pragma unroll
-            for (int e = 0; e < kXChunks; ++e)
-                if (lane + 64 * e < cpr) *reinterpret_cast<u32x4*>(xs + (4 * wave + rr + h) * xpitch + 16 * (lane + 64 * e)) = xv[h][e];
-    }
-}
-
-__global__ void __launch_bounds__(kThreads) stack_kernel(const StackParams p) {
-    extern __shared__ __align__(16) unsigned char lds[];
-    __shared__ unsigned ready, done, meet, go;
-    __shared__ int is_last[kWaves];
-    const int tid = threadIdx.x, lane = tid % 64, b = blockIdx.x;
-    const int wave = __builtin_amdgcn_readfirstlane(tid / 64);  // uniform: the buffer resources built from it stay scalar
-    float* red = reinterpret_cast<float*>(lds + p.x_region);
-    float* scl = red + kWorkers * kSlots * 256;
-    unsigned char* tbuf = reinterpret_cast<unsigned char*>(scl + kWorkers * kPairs * 16);
-    if (tid == 0) {
-        ready = 0u;
-        done = 0u;
-        meet = 0u;
-        go = 0u;
-    }
-    __syncthreads();
-    const int xpitch_a = 2 * p.hidden + 16;
-
-    if (wave >= kLoaders) {
-        // ---- workers ----
-        const int wk = wave - kLoaders;
-        unsigned char* tb = tbuf + wk * 2048;
-        u32x4 wb[kPairs][2];
-        unsigned ph = 0;
-        const auto wait_ready = [&]() {
-            while (__hip_atomic_load(&ready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < kLoaders * (ph + 1))
-                __builtin_amdgcn_s_sleep(1);
-        };
-        const auto wait_go = [&]() {  // the loaders have started the phase (its barrier is behind them)
-            while (__hip_atomic_load(&go, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < kLoaders * (ph + 1))
-                __builtin_amdgcn_s_sleep(1);
-        };
-        const auto signal_done = [&]() {
-            __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS writes are done
-            if (lane == 0) __hip_atomic_fetch_add(&done, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
-            ++ph;
-        };
-        issue_pairs<true>(geo_gate_up(p, b), p.w_gu[0], p.hidden, 2 * p.inter, wk, lane, wb);
-        for (int l = 0; l < p.layers; ++l) {
-            // the geometry is recomputed per layer from an opaque block index: held across the loop, its per-pair
-            // addresses would not fit in registers
-            int bl = b;
-            asm volatile("" : "+s"(bl));
-            const Geo ga = geo_gate_up(p, bl), gd = geo_down(p, bl);
-            const int xpitch_d = 2 * 128 * gd.gpt + 16;
-            if (!p.early && l > 0) {
-                wait_go();
-                issue_pairs<true>(ga, p.w_gu[l], p.hidden, 2 * p.inter, wk, lane, wb);
-            }
-            wait_ready();
-            multiply_pairs<SEPAL_HIP_BF16>(ga, lds, xpitch_a, red, scl, tb, wk, lane, wb);
-            signal_done();
-            if (p.early) issue_pairs<false>(gd, p.w_d[l], p.inter, p.hidden, wk, lane, wb);
-            if (!p.early) {
-                wait_go();
-                issue_pairs<false>(gd, p.w_d[l], p.inter, p.hidden, wk, lane, wb);
-            }
-            wait_ready();
-            multiply_pairs<SEPAL_HIP_F16>(gd, lds, xpitch_d, red, scl, tb, wk, lane, wb);
-            signal_done();
-            if (p.early && l + 1 < p.layers) issue_pairs<true>(ga, p.w_gu[l + 1], p.hidden, 2 * p.inter, wk, lane, wb);
-        }
-        return;
-    }
-
-    // ---- loaders: lt = 0 .. 255 ----
-    const int lt = tid;
-    unsigned gen = 0, nbar = 0, ph = 0;
-    float sv[kScaleLoads];
-    const auto start = [&]() {
-        if (lane == 0) __hip_atomic_fetch_add(&go, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    };
-    const auto publish = [&](const Geo& g) {  // the phase's scales to LDS, then the ready flag
-#pragma unroll
-        for (int e = 0; e < kScaleLoads; ++e)
-            if (lt + e * 64 * kLoaders < g.total * 16) scl[lt + e * 64 * kLoaders] = sv[e];
-        __builtin_amdgcn_s_waitcnt(0xC07F);
-        if (lane == 0) __hip_atomic_fetch_add(&ready, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
-    };
-    const auto wait_done = [&]() {
-        ++ph;
-        while (__hip_atomic_load(&done, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < kWorkers * ph) __builtin_amdgcn_s_sleep(1);
-    };
-    // the tile's sum in worker order (as pass_kernel)
-    const auto sum_tile = [&](const Geo& g, int tl, int e) {
-        const int lo = tl * g.gpt / g.per, hi = ((tl + 1) * g.gpt - 1) / g.per;
-        float v = red[(lo * kSlots + (tl - min(lo * g.per, g.total - 1) / g.gpt)) * 256 + e];
-        for (int w = lo + 1; w <= hi; ++w) v = __fadd_rn(v, red[(w * kSlots + (tl - min(w * g.per, g.total - 1) / g.gpt)) * 256 + e]);
-        return v;
-    };
-    load_scales<true>(geo_gate_up(p, b), p.s_gu[0], p.hidden / 128, lt, sv);
-    for (int l = 0; l < p.layers; ++l) {
-        int bl = b;  // opaque per layer, as the workers'
-        asm volatile("" : "+s"(bl));
-        const Geo ga = geo_gate_up(p, bl), gd = geo_down(p, bl);
-        const int xpitch_d = 2 * 128 * gd.gpt + 16;
-        // ---- A: gate/up over X (staged from x) -> H ----
-        start();
-        stage_rows(p.x, p.hidden, 0, p.hidden, p.t, lds, xpitch_a, wave, lane);
-        publish(ga);
-        load_scales<false>(gd, p.s_d[l], p.inter / 128, lt, sv);
-        wait_done();
-        for (int id = lt; id < ga.ntiles * 128; id += 64 * kLoaders) {
-            const int tl = id / 128, r = (id / 8) % 16, i = id % 8;
-            const int tile = ga.tile0 + tl;
-            const int f = 64 * (tile / 8) + 8 * (tile % 8) + i;
-            if (r >= p.t) continue;
-            const float gv = sum_tile(ga, tl, r * 16 + i), uv = sum_tile(ga, tl, r * 16 + 8 + i);
-            __hip_atomic_store(p.h + static_cast<std::size_t>(r) * p.inter + f, f32_to_f16_bits(swiglu_fast(gv, uv)),
-                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-        grid_barrier(p, nbar++, &meet, gen, tid, lane);
-        // ---- B: down over H -> P[part]; the last block of a column tile adds the parts into y ----
-        start();
-        stage_rows(p.h, p.inter, 128 * gd.g_lo, 128 * gd.gpt, p.t, lds, xpitch_d, wave, lane);
-        publish(gd);
-        if (l + 1 < p.layers) load_scales<true>(ga, p.s_gu[l + 1], p.hidden / 128, lt, sv);
-        wait_done();
-        for (int id = lt; id < gd.ntiles * 256; id += 64 * kLoaders) {
-            const int tl = id / 256, r = (id / 16) % 16, c = id % 16;
-            if (r >= p.t) continue;
-            const int col = 16 * (gd.tile0 + tl) + c;
-            __hip_atomic_store(&p.part[(static_cast<std::size_t>(gd.part) * p.t + r) * p.hidden + col], sum_tile(gd, tl, r * 16 + c),
-                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-        loaders_meet(&meet, gen, lane);
-        if (lt < gd.ntiles)
-            is_last[lt] = __hip_atomic_fetch_add(&p.tile_count[gd.tile0 + lt], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                          static_cast<unsigned>(p.parts - 1);
-        loaders_meet(&meet, gen, lane);
-        const __amdgpu_buffer_rsrc_t pres = rsrc(p.part, static_cast<std::size_t>(p.parts) * p.t * p.hidden * 4);
-        for (int id = lt; id < gd.ntiles * 256; id += 64 * kLoaders) {
-            const int tl = id / 256, r = (id / 16) % 16, c = id % 16;
-            if (!is_last[tl] || r >= p.t) continue;
-            const int col = 16 * (gd.tile0 + tl) + c;
-            const int step = p.t * p.hidden * 4;
-            float pv[kFinishParts];
-#pragma unroll
-            for (int q = 0; q < kFinishParts; ++q)
-                pv[q] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(pres, 4 * (r * p.hidden + col), min(q, p.parts - 1) * step, kCoherent));
-            float v = pv[0];
-#pragma unroll
-            for (int q = 1; q < kFinishParts; ++q)
-                if (q < p.parts) v = __fadd_rn(v, pv[q]);
-            __hip_atomic_store(&p.y[static_cast<std::size_t>(r) * p.hidden + col], v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-        if (lt < gd.ntiles && is_last[lt]) __hip_atomic_store(&p.tile_count[gd.tile0 + lt], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (l + 1 == p.layers) break;
-        grid_barrier(p, nbar++, &meet, gen, tid, lane);
-        // ---- C: x[r] = bf16(RMSNorm(y[r])), one row per wave of blocks 0 .. ceil(t / 4) - 1 (cpu-q8 order: lane
-        // L = lane % 32 is accumulator lane L of runner/src/cpu/elementwise.cpp:22-59 and adds c = L, L + 32, ... in
-        // order; the upper half-wave holds the second half of the row and continues the lower half's sums) ----
-        const int r = 4 * b + wave;
-        if (r < p.t) {
-            const int L = lane % 32, half = lane / 32, jh = p.hidden / 64;
-            const __amdgpu_buffer_rsrc_t yres = rsrc(p.y + static_cast<std::size_t>(r) * p.hidden, 4 * p.hidden);
-            const int vo = 4 * (L + 32 * jh * half);
-            // all loads unconditional (past the row they read zero; values past jh are never used)
-            float v[kNormHalf];
-#pragma unroll
-            for (int j = 0; j < kNormHalf; ++j) v[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(yres, vo, 128 * j, kCoherent));
-            float acc = 0.0f;
-#pragma unroll
-            for (int j = 0; j < kNormHalf; ++j) acc = j < jh ? __builtin_fmaf(v[j], v[j], acc) : acc;
-            float acc2 = __shfl(acc, L);
-#pragma unroll
-            for (int j = 0; j < kNormHalf; ++j) acc2 = j < jh ? __builtin_fmaf(v[j], v[j], acc2) : acc2;
-            const int l8 = L % 8;
-            const float a0 = __shfl(acc2, 32 + l8), a1 = __shfl(acc2, 40 + l8), a2 = __shfl(acc2, 48 + l8),
-                        a3 = __shfl(acc2, 56 + l8);
-            const float sl = __fadd_rn(__fadd_rn(a0, a1), __fadd_rn(a2, a3));
-            const float sl4 = __shfl(sl, (l8 + 4) % 8);
-            const float hs = __fadd_rn(sl, sl4);
-            const float h0 = __shfl(hs, 0), h1 = __shfl(hs, 1), h2 = __shfl(hs, 2), h3 = __shfl(hs, 3);
-            const float sum = __fadd_rn(__fadd_rn(h0, h2), __fadd_rn(h1, h3));
-            const float inv = static_cast<float>(1.0 / __builtin_sqrt(static_cast<double>(sum) / static_cast<double>(p.hidden) + p.eps));
-            const __amdgpu_buffer_rsrc_t xres = rsrc(p.x + static_cast<std::size_t>(r) * p.hidden, 2 * p.hidden);
-#pragma unroll
-            for (int j = 0; j < kNormHalf; ++j)
-                if (j < jh) __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16_bits(__fmul_rn(v[j], inv)), xres, vo / 2, 64 * j, kCoherent);
-        }
-        grid_barrier(p, nbar++, &meet, gen, tid, lane);
-    }
-    // the last block out clears the barrier counters for the next launch
-    if (tid == 0 && __hip_atomic_fetch_add(&p.grid_count[1], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1) {
-        __hip_atomic_store(&p.grid_count[0], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(&p.grid_count[1], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        // a timeout is counted (grid_count[2]) and cleared, so the next launch waits normally
-        if (__hip_atomic_load(p.timeout, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u) {
-            __hip_atomic_fetch_add(&p.grid_count[2], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(p.timeout, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-    }
-}
 
 } // namespace stack
 } // namespace sepal::hip
@@ -1133,64 +726,6 @@ void launch_small_layer_q8(const SmallStackPlan& plan, std::size_t t, std::size_
         part, plan.parts, static_cast<int>(t), static_cast<int>(hidden), y, static_cast<std::uint16_t*>(xn), eps, xq_next,
         xs_next, per_token ? static_cast<int>(hidden) : 128);
     check_launch("small-M q8 stack finish launch");
-}
-
-bool launch_small_stack(const SmallStackPlan& plan, std::size_t layers, std::size_t t, std::size_t hidden, std::size_t inter,
-                        void* x, const std::int8_t* const* w_gu, const float* const* s_gu, const std::int8_t* const* w_d,
-                        const float* const* s_d, void* h, float* part, float* y, unsigned* counters, double eps,
-                        bool early, hipStream_t stream) {
-    using namespace stack;
-    const std::size_t gpt_d = (inter / 128 + plan.parts - 1) / plan.parts;
-    const std::size_t xr = 16 * std::max(2 * hidden + 16, 2 * 128 * gpt_d + 16);
-    const std::size_t lds = pass_lds(0) - 16 * 16 + xr;
-    // one block per CU, all resident at once: the kernel's grid barriers need every block running
-    static std::size_t raised = 0;
-    raise_lds(stack_kernel, lds, raised);
-    int dev = 0, coop = 0, per_cu = 0;
-    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev) != hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(stack_kernel), kThreads, lds) != hipSuccess)
-        throw LaunchError("small-M stack: cooperative-launch query failed");
-    if (coop == 0 || per_cu < 1) return false;
-    StackParams p{};
-    p.x = static_cast<unsigned short*>(x);
-    p.h = static_cast<unsigned short*>(h);
-    p.part = part;
-    p.y = y;
-    p.tile_count = counters;
-    p.grid_count = counters + 4096;
-    p.timeout = counters + 4096 + 3;
-    p.eps = eps;
-    p.t = static_cast<int>(t);
-    p.hidden = static_cast<int>(hidden);
-    p.inter = static_cast<int>(inter);
-    p.per_a = plan.tiles_per_block;
-    p.parts = plan.parts;
-    p.per_d = plan.units_per_block;
-    p.bpp_d = static_cast<int>((hidden / 16 + plan.units_per_block - 1) / plan.units_per_block);
-    p.x_region = static_cast<int>(xr);
-    p.early = early ? 1 : 0;
-    for (std::size_t l0 = 0; l0 < layers; l0 += kMaxLayers) {
-        const std::size_t n = std::min<std::size_t>(kMaxLayers, layers - l0);
-        if (l0 > 0) {
-            // the previous launch ended after its last down pass: its y and parts are final; make this launch's input
-            finish_kernel<<<dim3(static_cast<unsigned>(t)), dim3(1024), hidden * sizeof(float), stream>>>(
-                part, plan.parts, static_cast<int>(t), static_cast<int>(hidden), y, static_cast<std::uint16_t*>(x), eps,
-                nullptr, nullptr, 0);
-            check_launch("small-M stack finish launch");
-        }
-        p.layers = static_cast<int>(n);
-        for (std::size_t i = 0; i < n; ++i) {
-            p.w_gu[i] = reinterpret_cast<const signed char*>(w_gu[l0 + i]);
-            p.s_gu[i] = s_gu[l0 + i];
-            p.w_d[i] = reinterpret_cast<const signed char*>(w_d[l0 + i]);
-            p.s_d[i] = s_d[l0 + i];
-        }
-        void* args[] = {&p};
-        if (hipLaunchCooperativeKernel(reinterpret_cast<const void*>(stack_kernel), dim3(static_cast<unsigned>(plan.blocks)),
-                                       dim3(kThreads), args, static_cast<unsigned>(lds), stream) != hipSuccess)
-            throw LaunchError("small-M stack: cooperative launch failed");
-    }
-    return true;
 }
 
 } // namespace sepal::hip

@@ -172,7 +172,7 @@ __global__ void __launch_bounds__(256) gemm_stream(const Params p) {
     f32x4 acc[MT];
 #pragma unroll
     for (int i = 0; i < MT; ++i) acc[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    float e = sc[0] > 0.0f ? sc[0] : 1.0f;  // the Horner ratio of the first group is then exactly 1
+    float e = 1.0f, emax = 0.0f;  // the Horner state (the first group's factor multiplies zero accumulators)
     // (all weight loads have landed by now: the X staging above waited for its own loads, which were issued after)
 #pragma unroll
     for (int u = 0; u < kGMax; ++u) {
@@ -181,13 +181,11 @@ __global__ void __launch_bounds__(256) gemm_stream(const Params p) {
         if constexpr (!K::q8) {
             // Horner step: rescale the running sum from the previous group's scale to this one; a zero scale marks an
             // all-zero group and keeps e
-            const float en = sc[u] > 0.0f ? sc[u] : e;
-            const float ratio = __fmul_rn(e, __builtin_amdgcn_rcpf(en));
+            const float ratio = horner_step(sc[u], e, emax);
 #pragma unroll
             for (int i = 0; i < MT; ++i)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) acc[i][r] = __fmul_rn(acc[i][r], ratio);
-            e = en;
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
                 unsigned o[8];
@@ -381,7 +379,8 @@ void launch_mt(const GemmArgs& a, hipStream_t stream) {
         const std::size_t part = static_cast<std::size_t>(p.splits) * rows * p.spans * kSpan * sizeof(float);
         require(static_cast<std::size_t>(p.spans) * sizeof(unsigned) <= kCounterBytes && part <= kPartialBytes,
                 "small-M multiply: workspace zone too small for this shape");
-        char* ws = static_cast<char*>(workspace(kScratchOffset, stream));
+        if (a.scratch == nullptr) throw LaunchError("small-M multiply: split-K scratch missing");
+        char* ws = static_cast<char*>(a.scratch);
         p.counters = reinterpret_cast<unsigned*>(ws);
         p.partial = reinterpret_cast<float*>(ws + kCounterBytes);
     }

@@ -325,8 +325,9 @@ def float_to_bf16(x, stream=None):
 
 
 def mlp_stack(kind: int, x, layers, y=None, act_block: int = 128, eps: float = 1e-6, stream=None):
-    """Runs the per-layer MLP stack in one call. kind 0 = w8g, 1 = q8. x bf16 [T, H] (overwritten with the last layer's
-    input); layers: list of (w_gate_up, s_gate_up, w_down, s_down) device tensors. Returns y float32 [T, H]."""
+    """Runs the per-layer MLP stack in one call. kind 0 = w8g (binary16 H), 1 = q8, 2 = w8g with float32 H. x bf16
+    [T, H] (overwritten with the last layer's input); layers: list of (w_gate_up, s_gate_up, w_down, s_down) device
+    tensors. Returns y float32 [T, H]."""
     torch = _torch()
     t, hidden = x.shape
     inter = layers[0][2].shape[1]

@@ -30,9 +30,9 @@ def test_gemm_w8g_refusals():
     assert "multiple of 128" in _err()
     # SwiGLU with N not a multiple of 128
     assert L.sepal_hip_gemm_w8g(FAKE, sm.BF16, 256, FAKE, 256, FAKE, 2, FAKE, sm.F32, 96, 4, 192, 256, sm.SWIGLU, -1, None) == sm.EINVAL
-    # unknown config, float32 X, null pointer, misaligned Y, stride below K
+    # unknown config, unknown X type, null pointer, misaligned Y, stride below K
     assert L.sepal_hip_gemm_w8g(FAKE, sm.BF16, 256, FAKE, 256, FAKE, 2, FAKE, sm.F32, 128, 4, 128, 256, sm.STORE, 7, None) == sm.EINVAL
-    assert L.sepal_hip_gemm_w8g(FAKE, sm.F32, 256, FAKE, 256, FAKE, 2, FAKE, sm.F32, 128, 4, 128, 256, sm.STORE, -1, None) == sm.EINVAL
+    assert L.sepal_hip_gemm_w8g(FAKE, 9, 256, FAKE, 256, FAKE, 2, FAKE, sm.F32, 128, 4, 128, 256, sm.STORE, -1, None) == sm.EINVAL
     assert L.sepal_hip_gemm_w8g(None, sm.BF16, 256, FAKE, 256, FAKE, 2, FAKE, sm.F32, 128, 4, 128, 256, sm.STORE, -1, None) == sm.EINVAL
     assert L.sepal_hip_gemm_w8g(FAKE, sm.BF16, 256, FAKE, 256, FAKE, 2, FAKE + 4, sm.F32, 128, 4, 128, 256, sm.STORE, -1, None) == sm.EINVAL
     assert L.sepal_hip_gemm_w8g(FAKE, sm.BF16, 128, FAKE, 256, FAKE, 2, FAKE, sm.F32, 128, 4, 128, 256, sm.STORE, -1, None) == sm.EINVAL
@@ -49,6 +49,9 @@ def test_supports_mirrors_reference_rules():
     assert not sm.gemm_w8g_supports(sm.BF16, 192, 256, 256, 256, 96, sm.SWIGLU)
     assert sm.gemm_w8g_supports(sm.BF16, 256, 256, 256, 256, 128, sm.SWIGLU)
     assert sm.gemm_w8g_supports(sm.F16, 2560, 9728, 9728, 9728, 2560, sm.ADD)
+    # float32 X, the reference's operand type (launch_gemm_simt(const float* x, ...))
+    assert sm.gemm_w8g_supports(sm.F32, 19456, 2560, 2560, 2560, 9728, sm.SWIGLU)
+    assert not sm.gemm_w8g_supports(9, 256, 256, 256, 256, 256, sm.STORE)
 
 
 def test_q8_and_quantizer_refusals():

@@ -297,7 +297,7 @@ def test_w8g_wide_tiles_every_element(sm, epilogue):
 def test_w8g_wide_tail_split_and_batch_invariance(sm):
     # 62 x 10 tiles of 256 x 256 on 256 CUs leave a 108-tile last round: those tiles run as 128 x 256 halves in a second
     # launch. Every element is checked, and rows from both launches match, bit for bit, the same rows computed in a
-    # small batch (the 256 x 128 kernel), as runner/cuda/tests/test_gemm_simt_kernels.cpp:193-211 asks.
+    # small batch (64 x 256 quarters of the same kernel), as runner/cuda/tests/test_gemm_simt_kernels.cpp:193-211 asks.
     t, n, k = 15800, 2560, 384
     rng = np.random.default_rng(777)
     x, q, s = _w8g_problem(rng, t, n, k, torch.bfloat16)
@@ -331,6 +331,146 @@ def test_w8g_gate_up_tail_split_and_batch_invariance(sm):
     for r0, nr in [(0, 100), (15360, 130), (15600, 200)]:
         part = host(sm.gemm_w8g(xt[r0:r0 + nr], qt, st, epilogue=sm.SWIGLU, y_dtype=torch.float16, config=0).float())
         assert same_bits(part, y[r0:r0 + nr]), r0
+
+def test_w8g_swiglu_narrow_tiles_match_wide(sm):
+    """A SwiGLU N of 128 mod 256 runs the 256 x 128 tiles (gemm_big2): against the oracle, and its first 128 features
+    bit for bit against the same features from a 256-column problem, which runs the 64-wide-step kernel."""
+    t, n, k = 100, 384, 512
+    rng = np.random.default_rng(384)
+    x = bf16_inputs(rng, (t, k))
+    gate = (rng.standard_normal((n // 2, k)) / np.sqrt(k)).astype(np.float32)
+    up = (rng.standard_normal((n // 2, k)) / np.sqrt(k)).astype(np.float32)
+    q, s = sm.quantize_gate_up_s8(dev(gate), dev(up), rule=0)
+    say("w8g swiglu narrow tiles", t, n, k)
+    y = host(sm.gemm_w8g(dev(x, torch.bfloat16), q, s, epilogue=sm.SWIGLU, config=0))
+    ref = orc.gemm_w8g(x, host(q), host(s), epilogue=orc.SWIGLU)
+    assert max_rel_over_rms(y, ref) < 2e-3 and rel_rms(y, ref) < 1e-5
+    y256 = host(sm.gemm_w8g(dev(x, torch.bfloat16), q[:256].contiguous(), s[:256].contiguous(), epilogue=sm.SWIGLU,
+                            config=0))
+    assert same_bits(y[:, :128], y256)
+
+
+# ---- float32 X (the reference's operand type, launch_gemm_simt(const float* x, ...)) ---------------------------------
+
+# (t, n, k, epilogue, config): the one-pass hi + lo kernel (64 x 256 quarters), the small-M path (two bf16 multiplies,
+# the second added), and the large-M two-pass path (a SwiGLU N of 128 mod 256)
+F32X_CASES = [(300, 512, 1280, "store", 0), (300, 512, 384, "add", 0), (200, 1024, 512, "swiglu", 0),
+              (16, 512, 2560, "store", -1), (5, 256, 384, "swiglu", -1), (40, 512, 640, "add", 1),
+              (100, 384, 512, "swiglu", 0)]
+
+
+@pytest.mark.parametrize("case", F32X_CASES)
+def test_w8g_float32_x(sm, case):
+    """float32 X that is not bf16-valued against the oracle's float32 chain: the hi + lo pair keeps the error at float32
+    rounding level (a bf16-rounded X alone would be ~1e-3 rms)."""
+    t, n, k, ep, cfg = case
+    rng = np.random.default_rng(t + n + k + cfg)
+    x = rng.standard_normal((t, k)).astype(np.float32)
+    w = (rng.standard_normal((n, k)) / np.sqrt(k)).astype(np.float32)
+    w[0, :128] = 0.0
+    q, s = orc.quantize_group_r1(w)
+    epi = {"store": sm.STORE, "add": sm.ADD, "swiglu": sm.SWIGLU}[ep]
+    base = rng.standard_normal((t, n)).astype(np.float32)
+    ref = orc.gemm_w8g(x, q, s, epilogue=epi, y=base if ep == "add" else None)
+    say("w8g float32 X", case)
+    y = dev(base) if ep == "add" else None
+    y = host(sm.gemm_w8g(dev(x), dev(q), dev(s), y=y, epilogue=epi, config=cfg))
+    assert max_rel_over_rms(y, ref) < 2e-3 and rel_rms(y, ref) < 1e-5, (max_rel_over_rms(y, ref), rel_rms(y, ref))
+    if ep == "swiglu":
+        for ydt in (torch.float16, torch.bfloat16):
+            yh = sm.gemm_w8g(dev(x), dev(q), dev(s), epilogue=epi, y_dtype=ydt, config=cfg)
+            yh = host(yh.float()) if ydt == torch.float16 else host(yh)
+            if ydt == torch.float16:
+                assert max_rel_over_rms(yh, ref) < 2e-3
+            else:
+                assert_within_one_bf16_step(yh, ref)
+
+
+@pytest.mark.parametrize("shape", [(15800, 2560, 256, "store"), (4000, 8192, 384, "swiglu")])
+def test_w8g_float32_x_wide_every_element(sm, shape):
+    """float32 X on the 256 x 256 tiles (and, at 15800 x 2560, the 128 x 256 halves of the last round): every element
+    against float64 of the same float32 X times the dequantized weights."""
+    t, n, k, ep = shape
+    rng = np.random.default_rng(t + n)
+    x = rng.standard_normal((t, k)).astype(np.float32)
+    w = (rng.standard_normal((n, k)) / np.sqrt(k)).astype(np.float32)
+    q, s = orc.quantize_group_r1(w)
+    xt, qt, st = dev(x), dev(q), dev(s)
+    ref = _deq_ref(xt, qt, st, k)
+    say("w8g float32 X wide", shape)
+    if ep == "swiglu":
+        f = torch.arange(n // 2, device=ref.device)
+        g, u = ref[:, 128 * (f // 64) + f % 64], ref[:, 128 * (f // 64) + 64 + f % 64]
+        ref = g * torch.sigmoid(g) * u
+        y = host(sm.gemm_w8g(xt, qt, st, epilogue=sm.SWIGLU))
+    else:
+        y = host(sm.gemm_w8g(xt, qt, st))
+    ref = host(ref)
+    assert max_rel_over_rms(y, ref) < 2e-3 and rel_rms(y, ref) < 1e-5, (max_rel_over_rms(y, ref), rel_rms(y, ref))
+
+
+# ---- extreme group scales in the Horner chain -------------------------------------------------------------------------
+
+@pytest.mark.parametrize("t,cfg", [(300, 0), (16, 1), (5000, 0)])
+def test_w8g_extreme_group_scales(sm, t, cfg):
+    """float32 weights whose groups span a huge range of scales, packed by the R1 rule: a subnormal group scale
+    (absmax 1e-37) between normal groups, 1e-30 groups, a row of tiny groups with one normal group, and alternating
+    1e-20 / normal groups. The output stays finite and within the parity bar of the reference's dequantize-first
+    chain, on every path (large-M, small-M)."""
+    n, k = 256, 1280
+    rng = np.random.default_rng(37 + t)
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+
+    def scale_group(r, g, amax):
+        seg = w[r, 128 * g:128 * (g + 1)]
+        w[r, 128 * g:128 * (g + 1)] = seg / np.max(np.abs(seg)) * amax
+
+    scale_group(3, 4, 1e-37)
+    scale_group(5, 2, 1e-30)
+    for g in range(9):
+        scale_group(7, g, 1e-36)
+    for g in range(0, 10, 2):
+        scale_group(9, g, 1e-20)
+    scale_group(11, 0, 1e-37)
+    q, s = sm.quantize_group_s8(dev(w))
+    qo, so = orc.quantize_group_r1(w)
+    assert same_bits(host(q), qo) and same_bits(host(s), so)
+    assert 0.0 < so[3, 4] < np.finfo(np.float32).tiny  # a subnormal scale
+    x = bf16_inputs(rng, (t, k))
+    ref = orc.gemm_w8g(x, qo, so) if t <= 300 else None
+    say("w8g extreme scales t", t, "config", cfg)
+    y = host(sm.gemm_w8g(dev(x, torch.bfloat16), q, s, config=cfg))
+    assert np.all(np.isfinite(y))
+    if ref is None:
+        ref = host(_deq_ref(dev(x, torch.bfloat16), q, s, k))
+    assert max_rel_over_rms(y, ref) < 2e-3 and rel_rms(y, ref) < 1e-5
+    for r in (3, 5, 7, 9, 11):
+        rr = np.sqrt(np.mean(ref[:, r].astype(np.float64) ** 2))
+        assert np.max(np.abs(y[:, r] - ref[:, r])) < 2e-3 * rr, r
+
+
+# ---- workspaces: one per (device, stream) -----------------------------------------------------------------------------
+
+def test_workspace_per_stream(sm):
+    """Split-K multiplies on two streams at once keep their own arrival counters and partial sums: interleaved
+    enqueues on both streams, without waiting, give the bits of the same calls run alone."""
+    rng = np.random.default_rng(2)
+    t, n, k = 16, 512, 2560
+    probs = [_w8g_problem(rng, t, n, k, torch.bfloat16) for _ in range(2)]
+    ins = [(dev(x, torch.bfloat16), dev(q), dev(s)) for x, q, s in probs]
+    alone = [host(sm.gemm_w8g(*a, config=1)) for a in ins]
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    outs = [[], []]
+    say("workspace per stream")
+    for _ in range(20):
+        for i in range(2):
+            with torch.cuda.stream(streams[i]):
+                outs[i].append(sm.gemm_w8g(*ins[i], config=1, stream=streams[i]))
+    torch.cuda.synchronize()
+    for i in range(2):
+        for o in outs[i]:
+            assert same_bits(host(o), alone[i])
+
 
 # ---- q8 ----------------------------------------------------------------------------------------------------------------
 
@@ -445,6 +585,13 @@ def test_q8_group_sums_exact_with_outliers(sm):
 
 # ---- the stack -----------------------------------------------------------------------------------------------------------
 
+# Drift of a three-layer stack (each layer's input re-rounded to bf16) against the oracle, which keeps H in float32 as
+# the reference does: the binary16 H of kind 0 costs ~8e-4 of the 2e-3 single-layer bar, and the bf16 re-rounding
+# between layers carries that to ~3e-3 rel rms after three layers; kind 2 (float32 H as bf16 hi + lo) stays at the
+# float32-rounding level of one layer and within 2e-3 after three.
+STACK3_DRIFT = {0: 4e-3, 2: 2e-3}
+
+
 def _stack_weights(sm, rng, layers, hidden, inter, rule):
     out = []
     for _ in range(layers):
@@ -462,8 +609,9 @@ def _oracle_stack(kind, x, layers, act_block):
     y = None
     for li, (wgu, sgu, wd, sd) in enumerate(layers):
         wgu, sgu, wd, sd = host(wgu), host(sgu), host(wd), host(sd)
-        if kind == 0:
-            h = f16_round(orc.gemm_w8g(x, wgu, sgu, epilogue=orc.SWIGLU))
+        if kind in (0, 2):
+            # H stays float32, as in the reference's engine (runner/cuda/src/cuda_engine.cpp:1928)
+            h = orc.gemm_w8g(x, wgu, sgu, epilogue=orc.SWIGLU)
             y = orc.gemm_w8g(h, wd, sd)
         else:
             ab_h = 128 if act_block == 128 else x.shape[1]
@@ -482,8 +630,8 @@ def _gpu_composition(sm, kind, x, layers, act):
     xt = dev(x, torch.bfloat16)
     y = None
     for li, (wgu, sgu, wd, sd) in enumerate(layers):
-        if kind == 0:
-            h = sm.gemm_w8g(xt, wgu, sgu, epilogue=sm.SWIGLU, y_dtype=torch.float16)
+        if kind in (0, 2):
+            h = sm.gemm_w8g(xt, wgu, sgu, epilogue=sm.SWIGLU, y_dtype=torch.float16 if kind == 0 else torch.float32)
             y = sm.gemm_w8g(h, wd, sd)
         else:
             ab_h = 128 if act == 128 else x.shape[1]
@@ -497,13 +645,13 @@ def _gpu_composition(sm, kind, x, layers, act):
     return host(y)
 
 
-@pytest.mark.parametrize("kind,act", [(0, 128), (1, 128), (1, 0)])
+@pytest.mark.parametrize("kind,act", [(0, 128), (2, 128), (1, 128), (1, 0)])
 @pytest.mark.parametrize("t", [16, 100])
 def test_mlp_stack(sm, kind, act, t):
     say("mlp stack kind", kind, "act", act, "t", t)
     rng = np.random.default_rng(1000 + t + kind)
     hidden, inter, nl = 256, 512, 3
-    layers = _stack_weights(sm, rng, nl, hidden, inter, rule=0 if kind == 0 else 1)
+    layers = _stack_weights(sm, rng, nl, hidden, inter, rule=1 if kind == 1 else 0)
     x = bf16_inputs(rng, (t, hidden))
     xt = dev(x, torch.bfloat16)
     y = host(sm.mlp_stack(kind, xt, layers, act_block=act))
@@ -519,10 +667,13 @@ def test_mlp_stack(sm, kind, act, t):
     if kind == 1 and t > 64:
         assert same_bits(y1, ref1) and same_bits(y, ref)  # the large-M q8 path is the reference's arithmetic
     else:
+        say("errors: one layer max rel", f"{max_rel_over_rms(y1, ref1):.3e}", "three layers rel rms", f"{rel_rms(y, ref):.3e}")
         assert max_rel_over_rms(y1, ref1) < 2e-3, max_rel_over_rms(y1, ref1)
         # through 3 layers the bf16 rounding of each layer's input turns ulp-level differences into whole bf16
         # steps on a few activations; the stack stays within a few bf16 steps of the oracle
-        assert rel_rms(y, ref) < 2e-3, rel_rms(y, ref)
+        assert rel_rms(y, ref) < STACK3_DRIFT.get(kind, 2e-3), rel_rms(y, ref)
+        if kind == 2:
+            assert max_rel_over_rms(y1, ref1) < 1e-4  # float32 H: the float32 rounding level
 
 
 @pytest.mark.parametrize("t", [1, 5, 16])
@@ -538,38 +689,16 @@ def test_mlp_stack_small_path(sm, t):
     xt = dev(x, torch.bfloat16)
     y = host(sm.mlp_stack(0, xt, layers))
     ref = _oracle_stack(0, x, layers, 128)
-    assert rel_rms(y, ref) < 2e-3, rel_rms(y, ref)
+    say("errors: three layers rel rms", f"{rel_rms(y, ref):.3e}")
+    assert rel_rms(y, ref) < STACK3_DRIFT[0], rel_rms(y, ref)
     comp = _gpu_composition(sm, 0, x, layers, 128)
     assert rel_rms(y, comp) < 2e-3, rel_rms(y, comp)
     # x now holds the last layer's input, bf16(RMSNorm(y of layer nl - 2))
     y2 = _oracle_stack(0, x, layers[:2], 128)
-    assert rel_rms(host(xt).astype(np.float32), orc.bf16_round(orc.rmsnorm_rows(y2))) < 2e-3
+    assert rel_rms(host(xt).astype(np.float32), orc.bf16_round(orc.rmsnorm_rows(y2))) < STACK3_DRIFT[0]
     y1 = host(sm.mlp_stack(0, dev(x, torch.bfloat16), layers[:1]))
     ref1 = _oracle_stack(0, x, layers[:1], 128)
     assert max_rel_over_rms(y1, ref1) < 2e-3, max_rel_over_rms(y1, ref1)
-
-
-@pytest.mark.parametrize("t,nl,hidden,inter", [(1, 3, 512, 1024), (5, 3, 512, 1024), (16, 3, 512, 1024),
-                                                (16, 66, 512, 1024), (16, 2, 2560, 9728)])
-def test_mlp_stack_small_persistent_same_bits(sm, monkeypatch, t, nl, hidden, inter):
-    """The one-launch (cooperative, grid barriers) form of the M <= 16 stack, with the weights issued before or after
-    each phase's barrier, gives the same bits as three launches per layer: same plan, same summation orders. 66 layers
-    take two launches (64 layers each at most) with the part sum and RMSNorm between them."""
-    say("mlp stack persistent t", t, "layers", nl, "hidden", hidden, "inter", inter)
-    rng = np.random.default_rng(300 + t + nl)
-    layers = _stack_weights(sm, rng, nl, hidden, inter, rule=0)
-    x = bf16_inputs(rng, (t, hidden))
-    out = {}
-    for mode in ("layers", "persistent", "persistent-late"):
-        monkeypatch.setenv("SEPAL_HIP_SMALL_STACK", mode)
-        xt = dev(x, torch.bfloat16)
-        y = host(sm.mlp_stack(0, xt, layers))
-        out[mode] = (y, host(xt))
-    for mode in ("persistent", "persistent-late"):
-        assert same_bits(out[mode][0], out["layers"][0]), mode
-        assert same_bits(out[mode][1], out["layers"][1]), mode
-    if nl <= 3:
-        assert rel_rms(out["layers"][0], _oracle_stack(0, x, layers, 128)) < 2e-3
 
 
 @pytest.mark.parametrize("t,act", [(1, 0), (5, 128), (16, 0), (16, 128)])
@@ -618,7 +747,7 @@ def test_mlp_stack_small_path_full_size(sm):
     ref1 = _oracle_stack(0, x, layers[:1], 128)
     assert max_rel_over_rms(y1, ref1) < 2e-3, max_rel_over_rms(y1, ref1)
     y = host(sm.mlp_stack(0, dev(x, torch.bfloat16), layers))
-    assert rel_rms(y, _oracle_stack(0, x, layers, 128)) < 2e-3
+    assert rel_rms(y, _oracle_stack(0, x, layers, 128)) < STACK3_DRIFT[0]
 
 
 # ---- the GPU int8 path with per-channel scales (launch_quantize_rows_s8 / launch_gemm_s8 / launch_gemm_w8a16) ------------
@@ -787,8 +916,11 @@ def test_full_size_block_sampled_rows(sm, big_layer, m):
     hh = host(h.float())[rows]
     href = orc.gemm_w8g(x[rows], host(wgu), host(sgu), epilogue=orc.SWIGLU)
     assert max_rel_over_rms(hh, href) < 2e-3
-    yref = orc.gemm_w8g(hh, host(wd), host(sd))  # the down multiply on the GPU's own binary16 H
-    assert max_rel_over_rms(y[rows], yref) < 2e-3 and rel_rms(y[rows], yref) < 1e-5
+    # Y against the reference's arithmetic (float32 H), and the down multiply alone on the GPU's own binary16 H
+    yref = orc.gemm_w8g(href, host(wd), host(sd))
+    assert max_rel_over_rms(y[rows], yref) < 2e-3, max_rel_over_rms(y[rows], yref)
+    yref16 = orc.gemm_w8g(hh, host(wd), host(sd))
+    assert max_rel_over_rms(y[rows], yref16) < 2e-3 and rel_rms(y[rows], yref16) < 1e-5
     # q8 (one scale per 128 activations: the cpu-q8 arithmetic)
     say("full-size q8 block m", m)
     qgu, qsgu = sm.quantize_gate_up_s8(gate, up, rule=1)
