@@ -228,6 +228,20 @@ SEPAL_HIP_API int32_t sepal_hip_mlp_stack(int32_t kind, size_t layers, size_t t,
                             const int8_t* const* w_gate_up, const float* const* s_gate_up, const int8_t* const* w_down,
                             const float* const* s_down, float* y, size_t act_block, double eps, void* stream);
 
+/* sepal_hip_mlp_stack with no allocation of any kind: the same arguments, work and bits, with every scratch buffer in
+ * a static device array of 64 MiB that the library holds on each device it runs on until the process ends (the split-K
+ * counter zone, then the stack's intermediates as sepal_hip_mlp_stack lays them out in its workspace). No counterpart
+ * in the reference: it is for callers that cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc). A shape whose scratch exceeds 64 MiB is refused with SEPAL_HIP_EINVAL (at
+ * the model's shape, hidden 2560 and intermediate 9728: up to 1721 rows for kind 0, about 2600 for kind 1 per 128,
+ * about 430 for kind 2; the M <= 16 forms always fit). Every call on one device shares that device's array: calls that overlap on one device (other streams or
+ * threads) race; serialise them. The first call on a device looks the array up and enqueues the clearing of its
+ * counter zone on `stream`. */
+SEPAL_HIP_API int32_t sepal_hip_mlp_stack_noalloc(int32_t kind, size_t layers, size_t t, size_t hidden, size_t inter, void* x,
+                                                  const int8_t* const* w_gate_up, const float* const* s_gate_up,
+                                                  const int8_t* const* w_down, const float* const* s_down, float* y,
+                                                  size_t act_block, double eps, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -62,6 +62,7 @@ def library() -> C.CDLL:
         L.sepal_hip_gemm_q8_swiglu_quantize.argtypes = [vp, sz, vp, sz, sz, vp, sz, vp, sz, vp, sz, vp, sz, sz, sz, sz,
                                                         i32, vp]
         L.sepal_hip_mlp_stack.argtypes = [i32, sz, sz, sz, sz, vp, vp, vp, vp, vp, vp, sz, d, vp]
+        L.sepal_hip_mlp_stack_noalloc.argtypes = [i32, sz, sz, sz, sz, vp, vp, vp, vp, vp, vp, sz, d, vp]
         L.sepal_hip_s8_quantize_rows.argtypes = [vp, i32, sz, vp, vp, sz, vp, sz, sz, vp]
         L.sepal_hip_gemm_s8.argtypes = [vp, sz, vp, vp, sz, vp, vp, i32, sz, sz, sz, sz, vp]
         L.sepal_hip_gemm_w8a16.argtypes = [vp, sz, vp, sz, vp, vp, i32, sz, sz, sz, sz, vp]
@@ -70,6 +71,7 @@ def library() -> C.CDLL:
         for name in ("sepal_hip_quantize_group_s8", "sepal_hip_quantize_gate_up_s8", "sepal_hip_gemm_w8g",
                      "sepal_hip_quantize_rows_s8", "sepal_hip_gemm_q8", "sepal_hip_q8_group_sums",
                      "sepal_hip_rmsnorm_rows", "sepal_hip_float_to_bf16", "sepal_hip_mlp_stack",
+                     "sepal_hip_mlp_stack_noalloc",
                      "sepal_hip_rmsnorm_quantize_rows", "sepal_hip_gemm_q8_swiglu_quantize",
                      "sepal_hip_weight_fingerprint", "sepal_hip_packed_save", "sepal_hip_packed_load",
                      "sepal_hip_s8_quantize_rows", "sepal_hip_gemm_s8", "sepal_hip_gemm_w8a16",
@@ -324,10 +326,11 @@ def float_to_bf16(x, stream=None):
     return out
 
 
-def mlp_stack(kind: int, x, layers, y=None, act_block: int = 128, eps: float = 1e-6, stream=None):
+def mlp_stack(kind: int, x, layers, y=None, act_block: int = 128, eps: float = 1e-6, stream=None, noalloc=False):
     """Runs the per-layer MLP stack in one call. kind 0 = w8g (binary16 H), 1 = q8, 2 = w8g with float32 H. x bf16
     [T, H] (overwritten with the last layer's input); layers: list of (w_gate_up, s_gate_up, w_down, s_down) device
-    tensors. Returns y float32 [T, H]."""
+    tensors. Returns y float32 [T, H]. noalloc: the entry point that allocates nothing (the library's static scratch; a
+    shape whose scratch does not fit is refused)."""
     torch = _torch()
     t, hidden = x.shape
     inter = layers[0][2].shape[1]
@@ -336,6 +339,6 @@ def mlp_stack(kind: int, x, layers, y=None, act_block: int = 128, eps: float = 1
         return (C.c_void_p * len(layers))(*[l[i].data_ptr() for l in layers])
 
     wgu, sgu, wd, sd = arr(0), arr(1), arr(2), arr(3)
-    _check(library().sepal_hip_mlp_stack(kind, len(layers), t, hidden, inter, _ptr(x), wgu, sgu, wd, sd, _ptr(y),
-                                         act_block, eps, _stream(stream)))
+    fn = library().sepal_hip_mlp_stack_noalloc if noalloc else library().sepal_hip_mlp_stack
+    _check(fn(kind, len(layers), t, hidden, inter, _ptr(x), wgu, sgu, wd, sd, _ptr(y), act_block, eps, _stream(stream)))
     return y

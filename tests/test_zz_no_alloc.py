@@ -1,0 +1,96 @@
+"""The entry point that allocates nothing (sepal_hip_mlp_stack_noalloc, MI355X only): its scratch is the library's
+static device array, so it gives the bits of sepal_hip_mlp_stack, which uses a per-stream workspace, on two calls in a
+row (the second smaller, over the array's leftover contents), for every path of the stack; it refuses a shape whose
+scratch does not fit, and a call on a new stream takes no device memory."""
+import sys
+
+import numpy as np
+import pytest
+
+from helpers import bf16_inputs, same_bits
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+def say(*a):
+    print("[case]", *a, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def sm():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    import sepal_mlp
+    sepal_mlp.library()
+    return sepal_mlp
+
+
+def _layers(sm, rng, n, hidden, inter, rule):
+    out = []
+    for _ in range(n):
+        gate = torch.from_numpy((rng.standard_normal((inter, hidden)) * 0.02).astype(np.float16)).cuda()
+        up = torch.from_numpy((rng.standard_normal((inter, hidden)) * 0.02).astype(np.float16)).cuda()
+        down = torch.from_numpy((rng.standard_normal((hidden, inter)) * 0.02).astype(np.float16)).cuda()
+        wgu, sgu = sm.quantize_gate_up_s8(gate, up, rule=rule)
+        wd, sd = sm.quantize_group_s8(down, rule=rule)
+        out.append((wgu, sgu, wd, sd))
+    return out
+
+
+def _host(t):
+    torch.cuda.synchronize()
+    if t.dtype == torch.bfloat16:
+        return t.view(torch.int16).cpu().numpy()
+    return t.cpu().numpy()
+
+
+# (kind, act_block, hidden, inter, first T, second T): the M <= 16 three-launch forms (w8g, q8 per token), the small-M
+# multiplies with their split-K counters (T <= 64), the large-M kernels, q8 per 128 with the fused producers, and
+# float32 H
+CASES = [(0, 128, 512, 1024, 16, 5), (1, 0, 512, 1024, 16, 1), (0, 128, 256, 512, 64, 40), (0, 128, 2560, 9728, 300, 100),
+         (1, 128, 256, 512, 200, 70), (1, 0, 256, 512, 50, 20), (2, 128, 256, 512, 130, 16)]
+
+
+@pytest.mark.parametrize("case", CASES)
+def test_noalloc_matches_mlp_stack(sm, case):
+    kind, act, hidden, inter, t1, t2 = case
+    rng = np.random.default_rng(hidden + t1 + kind)
+    layers = _layers(sm, rng, 3, hidden, inter, rule=1 if kind == 1 else 0)
+    for t in (t1, t2):
+        say("noalloc", case, "t", t)
+        x = bf16_inputs(rng, (t, hidden))
+        xa = torch.from_numpy(x).cuda().to(torch.bfloat16)
+        xb = xa.clone()
+        ya = sm.mlp_stack(kind, xa, layers, act_block=act)
+        yb = sm.mlp_stack(kind, xb, layers, act_block=act, noalloc=True)
+        assert same_bits(_host(yb), _host(ya))
+        assert same_bits(_host(xb), _host(xa))  # the last layer's input
+
+
+def test_noalloc_refuses_oversize_and_allocates_nothing(sm):
+    """A shape beyond the static scratch is refused with a message; calls of other shapes on a stream already used
+    leave the device's free memory unchanged (the per-stream workspace of sepal_hip_mlp_stack would take 64 MiB)."""
+    rng = np.random.default_rng(5)
+    layers = _layers(sm, rng, 1, 2560, 9728, rule=0)
+    say("noalloc refusal and device memory")
+    x = torch.zeros(15872, 2560, dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(sm.SepalHipInvalid, match="static scratch"):
+        sm.mlp_stack(0, x, layers, noalloc=True)
+    s = torch.cuda.Stream()
+    small = torch.from_numpy(bf16_inputs(rng, (16, 2560))).cuda().to(torch.bfloat16)
+    mid = torch.from_numpy(bf16_inputs(rng, (200, 2560))).cuda().to(torch.bfloat16)
+    ys = torch.empty(16, 2560, device="cuda")
+    ym = torch.empty(200, 2560, device="cuda")
+    torch.cuda.synchronize()
+    sm.mlp_stack(0, small, layers, y=ys, noalloc=True, stream=s)
+    s.synchronize()
+    free0 = torch.cuda.mem_get_info()[0]
+    for _ in range(3):
+        sm.mlp_stack(0, mid, layers, y=ym, noalloc=True, stream=s)
+        sm.mlp_stack(0, small, layers, y=ys, noalloc=True, stream=s)
+    s.synchronize()
+    assert torch.cuda.mem_get_info()[0] == free0
+    assert torch.isfinite(ym).all() and torch.isfinite(ys).all()
