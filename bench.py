@@ -113,6 +113,39 @@ def cpu_info():
     return model, "avx512_vnni" in flags
 
 
+def host_cores():
+    """The host's CPU resources as this process sees them: logical CPUs, physical cores, the CPUs this process may run
+    on, and the cgroup CPU quota (cpu.max) when one is set."""
+    info = {"logical_cpus": os.cpu_count()}
+    try:
+        info["affinity_cpus"] = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        pass
+    try:
+        cores = set()
+        phys = core = None
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("physical id"):
+                    phys = line.split(":")[1].strip()
+                elif line.startswith("core id"):
+                    core = line.split(":")[1].strip()
+                elif not line.strip() and core is not None:
+                    cores.add((phys, core))
+                    phys = core = None
+        if cores:
+            info["physical_cores"] = len(cores)
+    except OSError:
+        pass
+    try:
+        with open("/sys/fs/cgroup/cpu.max") as f:
+            quota, period = f.read().split()[:2]
+            info["cgroup_cpu_max"] = "unlimited" if quota == "max" else round(int(quota) / int(period), 2)
+    except (OSError, ValueError):
+        pass
+    return info
+
+
 def cpu_baseline(rows):
     """The reference's cpu-q8 MLP block (pack_acts + gemm_packed SwiGLU + pack_acts + gemm_packed) on `rows` rows of
     the C3 layer shape, one thread per physical core (the reference's default pool), median of 7 timed calls."""
@@ -137,7 +170,7 @@ def cpu_baseline(rows):
                 "sample": f"one C3 MLP block (gate/up SwiGLU + down, H {H}, I {I}) on {rows} of the 15872 rows, "
                           f"median of 7 calls after a warm-up; reference cpu-q8 {variant}; activation packing "
                           f"{pack / total * 100:.1f}% of the call",
-                "cpu": model, "avx512_vnni": vnni}
+                "cpu": model, "avx512_vnni": vnni, "host": host_cores()}
     # no reference build: the scalar C oracle on a few rows (one thread)
     small = 4
     wq, ws = orc.quantize_block_r2(orc.interleave_gate_up(gate, up))
@@ -150,7 +183,7 @@ def cpu_baseline(rows):
     total = time.time() - t0
     return {"value": round(OPS_PER_ROW_LAYER * small / total / 1e12, 6), "unit": "TOPS", "cores": 1, "kind": "port",
             "sample": f"one C3 MLP block on {small} rows by the scalar C oracle (oracle/_ref absent)", "cpu": model,
-            "avx512_vnni": vnni}
+            "avx512_vnni": vnni, "host": host_cores()}
 
 
 def load_traffic():
@@ -190,6 +223,28 @@ def profile_kernels():
         sm.gemm_w8g(x, wgu, sgu, y=h, epilogue=sm.SWIGLU)
     for _ in range(3):
         sm.gemm_w8g(h, wd, sd, y=y)
+    torch.cuda.synchronize()
+    del h
+    # C4's kernels: the q8 gate/up (SwiGLU) and down multiplies with one activation scale per token
+    qgu, qsgu = sm.quantize_gate_up_s8(gate, up, rule=sm.RULE_RECIPROCAL)
+    qd, qsd = sm.quantize_group_s8(down, rule=sm.RULE_RECIPROCAL)
+    xq, xs = sm.quantize_rows_s8(x, block=H)
+    hf = torch.empty(M_BIG, I, dtype=torch.float32, device="cuda")
+    for _ in range(3):
+        sm.gemm_q8(xq, xs, qgu, qsgu, y=hf, epilogue=sm.SWIGLU, act_block=H)
+    hq, hs = sm.quantize_rows_s8(hf, block=I)
+    for _ in range(3):
+        sm.gemm_q8(hq, hs, qd, qsd, y=y, act_block=I)
+    torch.cuda.synchronize()
+    del hf, hq, hs, xq, xs, qgu, qsgu, qd, qsd, gate, up, down, x
+    torch.cuda.empty_cache()
+    # C5's kernels: two passes of the M = 16 w8g stack over 36 distinct layers (more bytes than the memory-side
+    # cache holds, so the weights stream from HBM)
+    layers = make_layers(torch, sm, sm.RULE_DIVIDE)
+    xs16 = bf16_x(torch, M_SMALL, 5)
+    y16 = torch.empty(M_SMALL, H, dtype=torch.float32, device="cuda")
+    for _ in range(2):
+        sm.mlp_stack(0, xs16, layers, y=y16)
     torch.cuda.synchronize()
     log("profile-kernels: done")
 
@@ -250,6 +305,17 @@ def main():
     extra = {"c3_down_kernel": {"ms": round(ms_dn, 4), "tflops": round(dn_tflops, 1),
                                 "frac_bf16_peak": round(dn_tflops / PEAK["bf16_tflops"], 4)}}
     if not args.no_extra:
+        # ---- C3 with H kept in float32 (mlp_stack kind 2: the down multiply on bf16 hi + lo pairs) ----
+        def step_c3_f32h():
+            x.copy_(x0)
+            sm.mlp_stack(2, x, layers, y=y)
+
+        ms_c3f = timed(torch, step_c3_f32h, max(3, args.steps // 2), 1, stream)
+        tops_c3f = ops_step / (ms_c3f * 1e-3) / 1e12
+        extra["c3_w8g_float32_h"] = {"ms_per_step": round(ms_c3f, 3), "tops": round(tops_c3f, 1),
+                                     "frac_bf16_peak": round(tops_c3f / PEAK["bf16_tflops"], 4),
+                                     "note": "H float32 as the reference keeps it; down multiply on bf16 hi + lo"}
+        log(f"C3 w8g stack with float32 H: {ms_c3f:.2f} ms/step, {tops_c3f:.1f} TOPS")
         # ---- C5: M = 16 through the stack (w8g), weight streaming ----
         xs0 = bf16_x(torch, M_SMALL, 5)
         xs_ = xs0.clone()

@@ -110,6 +110,108 @@ __device__ __forceinline__ void wait_vm_lgkm0() {
 typedef __attribute__((address_space(3))) void lds_void;
 typedef const __attribute__((address_space(1))) void global_void;
 
+// The chain modes' epilogue of a 128 x 256 tile: acc[i][q][r] holds the chain of output (row m0 + wm 64 + 32 i +
+// 8 (r / 4) + 4 (lane / 32) + r % 4, column col[q]); per token it is multiplied by the row's activation scale here.
+// hb: LDS scratch of 32 KB (kSwigluQ8 only; free when called).
+template <int EP, int YT, bool PER_TOKEN>
+__device__ __forceinline__ void chain_epilogue(const Params& p, float (&acc)[2][2][16], int m0, int n0, int wm, int ib, int hh,
+                                               int lane, int tid, const int (&col)[2], float* hb) {
+    constexpr int BM = 128;
+    if constexpr (EP == kSwigluQ8) {
+        // The tile's 128 output columns are one quantization block. H goes through LDS (the first W stage, free after
+        // the loop) in two halves of 64 columns: 128 rows of 256 bytes, 16-byte chunk c of row r at c ^ (r % 16). Thread
+        // (row, q) takes 16 columns of one row from each half: the max over them, the four quarters combined through
+        // LDS, the scale, and 32 int8 values stored as two 16-byte chunks. max is exact in any order, so this equals
+        // quantize_rows on the float32 H (rule RECIPROCAL).
+        __shared__ float lds_amax[4][BM];
+        const int c = 32 * hh + lane % 32;  // this lane's column within its half (half ib)
+        const int row_l = tid % BM, quarter = tid / BM;
+        float hv[32];
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+            if (ib == half) {
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int rl = wm * 64 + i * 32 + 8 * (r / 4) + 4 * (lane / 32) + (r % 4);
+                        float v0 = acc[i][0][r], v1 = acc[i][1][r];
+                        if constexpr (PER_TOKEN) {
+                            const float xs = p.xs[static_cast<std::size_t>(min(m0 + rl, p.t - 1)) * p.ld_xs];
+                            v0 = __fmul_rn(v0, xs);
+                            v1 = __fmul_rn(v1, xs);
+                        }
+                        hb[rl * 64 + (((c / 4) ^ (rl % 16)) * 4) + c % 4] = swiglu_cephes(v0, v1);
+                    }
+            }
+            __syncthreads();
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float4 v = *reinterpret_cast<const float4*>(hb + row_l * 64 + (((4 * quarter + j) ^ (row_l % 16)) * 4));
+                hv[16 * half + 4 * j] = v.x;
+                hv[16 * half + 4 * j + 1] = v.y;
+                hv[16 * half + 4 * j + 2] = v.z;
+                hv[16 * half + 4 * j + 3] = v.w;
+            }
+            __syncthreads();
+        }
+        float m = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 32; ++j) {
+            const float a = fabsf(hv[j]);
+            m = a > m ? a : m;
+        }
+        lds_amax[quarter][row_l] = m;
+        __syncthreads();
+        m = lds_amax[0][row_l];
+#pragma unroll
+        for (int w = 1; w < 4; ++w) m = lds_amax[w][row_l] > m ? lds_amax[w][row_l] : m;
+        const float scale = m > 0.0f ? __fdiv_rn(m, 127.0f) : 1.0f;
+        const float inverse = __fdiv_rn(1.0f, scale);
+        const int row = m0 + row_l;
+        if (row < p.t) {
+            unsigned packed[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                packed[j] = 0u;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    float qv = __builtin_rintf(__fmul_rn(hv[4 * j + e], inverse));
+                    qv = qv < -127.0f ? -127.0f : (qv > 127.0f ? 127.0f : qv);
+                    packed[j] |= (static_cast<unsigned>(static_cast<int>(qv)) & 0xFFu) << (8 * e);
+                }
+            }
+            signed char* dst = static_cast<signed char*>(p.y) + static_cast<std::size_t>(row) * p.ld_y + n0 / 2 + 16 * quarter;
+            *reinterpret_cast<u32x4*>(dst) = u32x4{packed[0], packed[1], packed[2], packed[3]};
+            *reinterpret_cast<u32x4*>(dst + 64) = u32x4{packed[4], packed[5], packed[6], packed[7]};
+            if (quarter == 0) p.ys[static_cast<std::size_t>(row) * p.ld_ys + n0 / 256] = scale;
+        }
+        return;
+    } else {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int row = m0 + wm * 64 + i * 32 + 8 * (r / 4) + 4 * (lane / 32) + (r % 4);
+            if (row >= p.t) continue;
+            float v0 = acc[i][0][r], v1 = acc[i][1][r];
+            if constexpr (PER_TOKEN) {
+                const float xs = p.xs[static_cast<std::size_t>(row) * p.ld_xs];
+                v0 = __fmul_rn(v0, xs);
+                v1 = __fmul_rn(v1, xs);
+            }
+            if constexpr (EP == SEPAL_HIP_SWIGLU) {
+                const int f = n0 / 2 + 64 * ib + 32 * hh + lane % 32;
+                if (2 * f < p.n) store_out<YT>(p.y, static_cast<std::size_t>(row) * p.ld_y + f, swiglu_cephes(v0, v1));
+            } else {
+                if (col[0] < p.n) put<EP, YT>(p.y, p.ld_y, row, col[0], v0);
+                if (col[1] < p.n) put<EP, YT>(p.y, p.ld_y, row, col[1], v1);
+            }
+        }
+    }
+    }
+}
+
 template <int EP, int YT, bool PER_TOKEN, int MODE>
 __global__ void __launch_bounds__(512) gemm_big(const Params p) {
     constexpr int BM = 128, BN = 256;
@@ -318,100 +420,210 @@ __global__ void __launch_bounds__(512) gemm_big(const Params p) {
         return;
     }
 
-    if constexpr (EP == kSwigluQ8) {
-        // The tile's 128 output columns are one quantization block. H goes through LDS (the first W stage, free after
-        // the loop) in two halves of 64 columns: 128 rows of 256 bytes, 16-byte chunk c of row r at c ^ (r % 16). Thread
-        // (row, q) takes 16 columns of one row from each half: the max over them, the four quarters combined through
-        // LDS, the scale, and 32 int8 values stored as two 16-byte chunks. max is exact in any order, so this equals
-        // quantize_rows on the float32 H (rule RECIPROCAL).
-        float* hb = reinterpret_cast<float*>(lw0);
-        __shared__ float lds_amax[4][BM];
-        const int c = 32 * hh + lane % 32;  // this lane's column within its half (half ib)
-        const int row_l = tid % BM, quarter = tid / BM;
-        float hv[32];
+    chain_epilogue<EP, YT, PER_TOKEN>(p, acc, m0, n0, wm, ib, hh, lane, tid, col, reinterpret_cast<float*>(lw0));
+}
+
+// ---- the chain modes, one 32 x 32 block at a time (gemm_chain) -----------------------------------------------------
+//
+// The tile, waves, LDS stages and swizzle of gemm_big's chain mode, in another order. At the top of group g, after the
+// barrier that publishes its stage, each wave reads all 16 operand fragments of the group into registers (stage g is
+// then free, and group g + 2's loads are issued into the stage of group g - 1). It then runs its four 32 x 32 blocks
+// one after the other: the block's four MFMAs (one per 32-wide substep) give its exact int32 group sums, and while
+// they run, the previous block's sums go through their link of the float chain. The chain thus trails the MFMAs by one
+// block, and only two blocks of int32 sums are ever live (the group's sums of all four blocks, as in gemm_big, would
+// not leave room for the fragments). The links run in the same order with the same operands as gemm_big's, so the
+// results are the same bits. The direct loads go through buffer descriptors (a 32-bit lane offset: the row, clamped to
+// the last row, and the swizzled chunk; the group's offset in the scalar offset; the LDS destination in scalar
+// registers), so issuing a group's loads costs no vector instruction. The launcher uses this kernel when every
+// offset fits 32 bits.
+struct ChainParams {
+    Params p;
+    unsigned x_bytes, w_bytes, ws_bytes, xs_bytes;  // extents of X, W and their scales (buffer ranges)
+};
+
+template <int EP, int YT, bool PER_TOKEN>
+__global__ void __launch_bounds__(512) gemm_chain(const ChainParams cp) {
+    const Params& p = cp.p;
+    constexpr int BM = 128, BN = 256;
+    constexpr int XDMA = BM / 64, WDMA = BN / 64;
+    constexpr int NSC = PER_TOKEN ? 2 : 3;  // scale loads per thread and group
+    __shared__ __align__(1024) u32x4 lx0[BM * 8], lx1[BM * 8], lx2[BM * 8];
+    __shared__ __align__(1024) u32x4 lw0[BN * 8], lw1[BN * 8], lw2[BN * 8];
+    __shared__ float lds_xs[3][BM];  // per-128 activation scales of group g in buffer g mod 3
+    const auto xstage = [&](auto it) -> u32x4* {
+        constexpr int i = decltype(it)::value;
+        if constexpr (i == 0) return lx0;
+        else if constexpr (i == 1) return lx1;
+        else return lx2;
+    };
+    const auto wstage = [&](auto it) -> u32x4* {
+        constexpr int i = decltype(it)::value;
+        if constexpr (i == 0) return lw0;
+        else if constexpr (i == 1) return lw1;
+        else return lw2;
+    };
+
+    const int tid = threadIdx.x, lane = tid % 64;
+    const int wave = __builtin_amdgcn_readfirstlane(tid / 64);  // wave-uniform: LDS destinations stay scalar
+    const int wm = wave % 2, wn = wave / 2;
+    int tm, tn;
+    tile_of(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int groups = p.k / 128;
+
+    const __amdgpu_buffer_rsrc_t xres = __builtin_amdgcn_make_buffer_rsrc(const_cast<signed char*>(p.x), 0, static_cast<int>(cp.x_bytes), 0x00020000);
+    const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(const_cast<signed char*>(p.w), 0, static_cast<int>(cp.w_bytes), 0x00020000);
+    const __amdgpu_buffer_rsrc_t wsres = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(p.ws), 0, static_cast<int>(cp.ws_bytes), 0x00020000);
+    const __amdgpu_buffer_rsrc_t xsres = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(p.xs), 0, static_cast<int>(cp.xs_bytes), 0x00020000);
+    // direct load e of wave w fills LDS kilobyte w + 8 e = rows 8 w + 64 e + {0..7}; lane l writes slot l % 8 of row
+    // 8 w + 64 e + l / 8, which holds chunk (l % 8) ^ sw8(row) = (l % 8) ^ ((4 w + l / 16) & 7); rows past T or N
+    // repeat the last row (never stored)
+    const int chunk = (lane % 8) ^ ((4 * wave + lane / 16) & 7);
+    int xoff[XDMA], woff[WDMA];
 #pragma unroll
-        for (int half = 0; half < 2; ++half) {
-            if (ib == half) {
+    for (int e = 0; e < XDMA; ++e)
+        xoff[e] = min(m0 + 8 * wave + 64 * e + lane / 8, p.t - 1) * static_cast<int>(p.ld_x) + 16 * chunk;
 #pragma unroll
-                for (int i = 0; i < 2; ++i)
+    for (int e = 0; e < WDMA; ++e)
+        woff[e] = min(n0 + 8 * wave + 64 * e + lane / 8, p.n - 1) * static_cast<int>(p.ld_w) + 16 * chunk;
+    const int xs_off = PER_TOKEN ? 0 : min(m0 + (tid % BM), p.t - 1) * static_cast<int>(p.ld_xs) * 4;
+
+    const int ib = wn / 2, hh = wn % 2;
+    const int colrel[2] = {128 * ib + 32 * hh + lane % 32, 128 * ib + 64 + 32 * hh + lane % 32};
+    int col[2];
 #pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        const int rl = wm * 64 + i * 32 + 8 * (r / 4) + 4 * (lane / 32) + (r % 4);
-                        float v0 = acc[i][0][r], v1 = acc[i][1][r];
-                        if constexpr (PER_TOKEN) {
-                            const float xs = p.xs[static_cast<std::size_t>(min(m0 + rl, p.t - 1)) * p.ld_xs];
-                            v0 = __fmul_rn(v0, xs);
-                            v1 = __fmul_rn(v1, xs);
-                        }
-                        hb[rl * 64 + (((c / 4) ^ (rl % 16)) * 4) + c % 4] = swiglu_cephes(v0, v1);
-                    }
-            }
-            __syncthreads();
+    for (int j = 0; j < 2; ++j) col[j] = n0 + colrel[j];
+    const int ws_off0 = min(col[0], p.n - 1) * static_cast<int>(p.ld_ws) * 4;
+    const int ws_off1 = min(col[1], p.n - 1) * static_cast<int>(p.ld_ws) * 4;
+    // fragment reads (u32x4 units): lane l of m-block i, substep st reads row wm 64 + 32 i + l % 32, chunk 2 st + l / 32
+    // at slot chunk ^ sw8(row); of n-block q, row colrel[q]. Rows 32 apart (m-blocks) and 64 apart (n-blocks) share
+    // sw8, so one offset per substep serves both, the second block at a constant distance.
+    int ra[4], rb[4];
+    {
+        const int rowa = wm * 64 + lane % 32, rowb = colrel[0];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const float4 v = *reinterpret_cast<const float4*>(hb + row_l * 64 + (((4 * quarter + j) ^ (row_l % 16)) * 4));
-                hv[16 * half + 4 * j] = v.x;
-                hv[16 * half + 4 * j + 1] = v.y;
-                hv[16 * half + 4 * j + 2] = v.z;
-                hv[16 * half + 4 * j + 3] = v.w;
-            }
-            __syncthreads();
+        for (int st = 0; st < 4; ++st) {
+            const int c = 2 * st + lane / 32;
+            ra[st] = rowa * 8 + (c ^ sw8(rowa));
+            rb[st] = rowb * 8 + (c ^ sw8(rowb));
         }
-        float m = 0.0f;
+    }
+
+    struct Set {
+        float xs, ws[2];
+    };
+    Set s0, s1, s2;  // group g's scales in set g mod 3
+    const auto issue = [&](int g, u32x4* xd, u32x4* wd, Set& s) {
+        const int k0 = g * 128;
 #pragma unroll
-        for (int j = 0; j < 32; ++j) {
-            const float a = fabsf(hv[j]);
-            m = a > m ? a : m;
-        }
-        lds_amax[quarter][row_l] = m;
-        __syncthreads();
-        m = lds_amax[0][row_l];
+        for (int e = 0; e < XDMA; ++e)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(xres, (__attribute__((address_space(3))) void*)(xd + (wave + 8 * e) * 64), 16,
+                                                     xoff[e], k0, 0, 0);
 #pragma unroll
-        for (int w = 1; w < 4; ++w) m = lds_amax[w][row_l] > m ? lds_amax[w][row_l] : m;
-        const float scale = m > 0.0f ? __fdiv_rn(m, 127.0f) : 1.0f;
-        const float inverse = __fdiv_rn(1.0f, scale);
-        const int row = m0 + row_l;
-        if (row < p.t) {
-            unsigned packed[8];
+        for (int e = 0; e < WDMA; ++e)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(wres, (__attribute__((address_space(3))) void*)(wd + (wave + 8 * e) * 64), 16,
+                                                     woff[e], k0, 0, 0);
+        if constexpr (!PER_TOKEN)
+            s.xs = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(xsres, xs_off, (g >> p.act_shift) * 4, 0));
+        s.ws[0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(wsres, ws_off0, g * 4, 0));
+        s.ws[1] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(wsres, ws_off1, g * 4, 0));
+    };
+
+    float acc[2][2][16];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                packed[j] = 0u;
+    for (int i = 0; i < 2; ++i)
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    float qv = __builtin_rintf(__fmul_rn(hv[4 * j + e], inverse));
-                    qv = qv < -127.0f ? -127.0f : (qv > 127.0f ? 127.0f : qv);
-                    packed[j] |= (static_cast<unsigned>(static_cast<int>(qv)) & 0xFFu) << (8 * e);
-                }
-            }
-            signed char* dst = static_cast<signed char*>(p.y) + static_cast<std::size_t>(row) * p.ld_y + n0 / 2 + 16 * quarter;
-            *reinterpret_cast<u32x4*>(dst) = u32x4{packed[0], packed[1], packed[2], packed[3]};
-            *reinterpret_cast<u32x4*>(dst + 64) = u32x4{packed[4], packed[5], packed[6], packed[7]};
-            if (quarter == 0) p.ys[static_cast<std::size_t>(row) * p.ld_ys + n0 / 256] = scale;
-        }
-        return;
-    } else {
+        for (int j = 0; j < 2; ++j)
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+    const i32x16 zero16 = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+    i32x16 T0, T1;  // int32 sums of the blocks in flight (block b of a group in T(b mod 2))
+
+    // link of the chain for block (i, q): acc += sums * scale (the first group's link multiplies)
+    const auto link = [&](const i32x16& S, int i, int q, float ws, int xbuf, bool first) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            const int row = m0 + wm * 64 + i * 32 + 8 * (r / 4) + 4 * (lane / 32) + (r % 4);
-            if (row >= p.t) continue;
-            float v0 = acc[i][0][r], v1 = acc[i][1][r];
-            if constexpr (PER_TOKEN) {
-                const float xs = p.xs[static_cast<std::size_t>(row) * p.ld_xs];
-                v0 = __fmul_rn(v0, xs);
-                v1 = __fmul_rn(v1, xs);
-            }
-            if constexpr (EP == SEPAL_HIP_SWIGLU) {
-                const int f = n0 / 2 + 64 * ib + 32 * hh + lane % 32;
-                if (2 * f < p.n) store_out<YT>(p.y, static_cast<std::size_t>(row) * p.ld_y + f, swiglu_cephes(v0, v1));
+            float sc = ws;
+            if constexpr (!PER_TOKEN) sc = __fmul_rn(ws, lds_xs[xbuf][wm * 64 + i * 32 + 8 * (r / 4) + 4 * (lane / 32) + (r % 4)]);
+            const float f = static_cast<float>(S[r]);
+            acc[i][q][r] = first ? __fmul_rn(f, sc) : __builtin_fmaf(f, sc, acc[i][q][r]);
+        }
+    };
+
+    // Group g, stage j = g mod 3 (its scales in set j): wait for the group's loads, put its per-128 activation scales in
+    // LDS, barrier; read its 16 fragments; copy group g - 1's weight scales out of set (g + 2) mod 3 and issue group
+    // g + 2's loads there (clamped; past the end they repeat into stages nothing reads again, so the wait counts stay
+    // exact); then blocks 0..3, each block's MFMAs with the previous block's link (block 3 of group g - 1 at block 0).
+    float pw0 = 0.0f, pw1 = 0.0f;  // group g - 1's weight scales
+    const auto group_step = [&](int g, auto jt, auto prev_t) {
+        constexpr int j = decltype(jt)::value;
+        // 0: group 0 (no previous group; its own links multiply); 1: group 1 (group 0's block 3 links by a
+        // multiply); 2: later groups
+        constexpr int pmode = decltype(prev_t)::value;
+        constexpr bool first = pmode == 0;
+        Set& cur = j == 0 ? s0 : (j == 1 ? s1 : s2);
+        Set& prev = j == 0 ? s2 : (j == 1 ? s0 : s1);  // group g - 1's set, reused for group g + 2
+        asm volatile("" ::: "memory");
+        wait_vm_lgkm0<XDMA + WDMA + NSC>();  // everything but group g + 1's loads
+        if constexpr (!PER_TOKEN)
+            if (tid < BM) lds_xs[g % 3][tid] = cur.xs;
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        const u32x4* tx = xstage(std::integral_constant<int, j>{});
+        const u32x4* tw = wstage(std::integral_constant<int, j>{});
+        u32x4 a[2][4], b[2][4];
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+            a[0][st] = tx[ra[st]];
+            b[0][st] = tw[rb[st]];
+        }
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+            a[1][st] = tx[ra[st] + 256];
+            b[1][st] = tw[rb[st] + 512];
+        }
+        const float cws0 = pw0, cws1 = pw1;
+        issue(min(g + 2, groups - 1), xstage(std::integral_constant<int, (j + 2) % 3>{}),
+              wstage(std::integral_constant<int, (j + 2) % 3>{}), prev);
+        const float gws0 = cur.ws[0], gws1 = cur.ws[1];
+#pragma unroll
+        for (int blk = 0; blk < 4; ++blk) {
+            const int i = blk / 2, q = blk % 2;
+            i32x16& S = blk % 2 == 0 ? T0 : T1;
+#pragma unroll
+            for (int st = 0; st < 4; ++st) S = mfma_i8_32(a[i][st], b[q][st], st == 0 ? zero16 : S);
+            if (blk == 0) {
+                if constexpr (pmode > 0) link(T1, 1, 1, cws1, (g + 2) % 3, pmode == 1);
             } else {
-                if (col[0] < p.n) put<EP, YT>(p.y, p.ld_y, row, col[0], v0);
-                if (col[1] < p.n) put<EP, YT>(p.y, p.ld_y, row, col[1], v1);
+                const int pi = (blk - 1) / 2, pq = (blk - 1) % 2;
+                link(blk % 2 == 0 ? T1 : T0, pi, pq, pq == 0 ? gws0 : gws1, g % 3, first);
             }
         }
+        pw0 = gws0;
+        pw1 = gws1;
+    };
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    issue(0, lx0, lw0, s0);
+    issue(min(1, groups - 1), lx1, lw1, s1);
+    // group 0, group 1, then three groups per iteration (stage and scale set g mod 3)
+    group_step(0, I0{}, I0{});
+    if (groups > 1) group_step(1, I1{}, I1{});
+    int g = 2;
+    for (; g + 3 <= groups; g += 3) {
+        group_step(g, I2{}, I2{});
+        group_step(g + 1, I0{}, I2{});
+        group_step(g + 2, I1{}, I2{});
     }
-    }
+    if (g < groups) group_step(g, I2{}, I2{});
+    if (g + 1 < groups) group_step(g + 1, I0{}, I2{});
+    // the last group's block 3
+    link(T1, 1, 1, pw1, (groups - 1) % 3, groups == 1);
+    // the repeated loads of the last steps may still be writing LDS: drain them before the block reuses or leaves it
+    wait_vm_lgkm0<0>();
+    __syncthreads();
+    chain_epilogue<EP, YT, PER_TOKEN>(p, acc, m0, n0, wm, ib, hh, lane, tid, col, reinterpret_cast<float*>(lw0));
 }
 
 // ---- gemm_s8 (per-channel W8A8, int32 sums over the whole K): 256 x 256 tiles ----------------------------------------
@@ -596,6 +808,19 @@ void launch_big(const GemmArgs& a, hipStream_t stream) {
     Params p = make_params(a);
     p.tiles_m = static_cast<int>((a.t + 127) / 128);
     p.tiles_n = static_cast<int>((a.n + 255) / 256);
+    const std::size_t x_bytes = (a.t - 1) * a.ld_x + a.k, w_bytes = (a.n - 1) * a.ld_w + a.k;
+    const std::size_t ws_bytes = MODE == MODE_CHAIN ? ((a.n - 1) * a.ld_s + a.k / 128) * 4 : 0;
+    const std::size_t xs_bytes = MODE == MODE_CHAIN ? ((a.t - 1) * a.ld_xs + a.k / a.act_block) * 4 : 0;
+    const std::size_t lim = std::size_t{1} << 31;
+    if constexpr (MODE == MODE_CHAIN && PT) {
+        if (x_bytes < lim && w_bytes < lim && ws_bytes < lim && xs_bytes < lim) {
+            const ChainParams cp{p, static_cast<unsigned>(x_bytes), static_cast<unsigned>(w_bytes),
+                                 static_cast<unsigned>(ws_bytes), static_cast<unsigned>(xs_bytes)};
+            gemm_chain<EP, YT, PT><<<dim3(p.tiles_m * p.tiles_n), dim3(512), 0, stream>>>(cp);
+            check_launch("gemm_q8 large-M kernel launch");
+            return;
+        }
+    }
     gemm_big<EP, YT, PT, MODE><<<dim3(p.tiles_m * p.tiles_n), dim3(512), 0, stream>>>(p);
     check_launch("gemm_q8 large-M kernel launch");
 }
