@@ -412,32 +412,32 @@ __global__ void __launch_bounds__(kThreads) pass_kernel(const PassParams p) {
     }
 }
 
-// y[r][c] = sum over parts (in order) of P[part][r][c]; then, if xn is set, xn[r] = bf16(RMSNorm(y[r])) with the
+// y[r][c] = sum over the P parts (in order) of P[part][r][c]; then, if xn is set, xn[r] = bf16(RMSNorm(y[r])) with the
 // cpu-q8 summation order (runner/src/cpu/elementwise.cpp:22-59) and eps. One block of 1024 threads per row; each
-// thread's partial loads (up to kFinishParts) are all in flight at once.
+// thread's P partial loads are all in flight at once (P is a template argument, so no load repeats a part).
 constexpr int kFinishParts = 16;
 
 // With q set (the gpu-q8w stack), the bf16 values are also quantized as quantize_rows does (rule RECIPROCAL), with
 // one scale per row (qblock = n) or per 128 columns (qblock = 128), into q [t, n] and qs [t, n / qblock].
-__global__ void __launch_bounds__(1024) finish_kernel(const float* __restrict__ part, int parts, int t, int n, float* __restrict__ y,
+template <int P>
+__global__ void __launch_bounds__(1024) finish_kernel(const float* __restrict__ part, int t, int n, float* __restrict__ y,
                                                       std::uint16_t* __restrict__ xn, double eps, std::int8_t* __restrict__ q,
                                                       float* __restrict__ qs, int qblock) {
     extern __shared__ __align__(16) float row_buf[];  // [n]
     const int r = blockIdx.x, tid = threadIdx.x;
     for (int c4 = tid; c4 < n / 4; c4 += 1024) {
-        float4 v[kFinishParts];
+        float4 v[P];
 #pragma unroll
-        for (int q = 0; q < kFinishParts; ++q)
-            v[q] = *reinterpret_cast<const float4*>(part + (static_cast<std::size_t>(min(q, parts - 1)) * t + r) * n + 4 * c4);
+        for (int q = 0; q < P; ++q)
+            v[q] = *reinterpret_cast<const float4*>(part + (static_cast<std::size_t>(q) * t + r) * n + 4 * c4);
         float4 a = v[0];
 #pragma unroll
-        for (int q = 1; q < kFinishParts; ++q)
-            if (q < parts) {
-                a.x = __fadd_rn(a.x, v[q].x);
-                a.y = __fadd_rn(a.y, v[q].y);
-                a.z = __fadd_rn(a.z, v[q].z);
-                a.w = __fadd_rn(a.w, v[q].w);
-            }
+        for (int q = 1; q < P; ++q) {
+            a.x = __fadd_rn(a.x, v[q].x);
+            a.y = __fadd_rn(a.y, v[q].y);
+            a.z = __fadd_rn(a.z, v[q].z);
+            a.w = __fadd_rn(a.w, v[q].w);
+        }
         *reinterpret_cast<float4*>(row_buf + 4 * c4) = a;
         *reinterpret_cast<float4*>(y + static_cast<std::size_t>(r) * n + 4 * c4) = a;
     }
@@ -562,6 +562,21 @@ void raise_lds(Kernel kernel, std::size_t lds, std::size_t& raised) {
 
 } // namespace
 
+// The finish pass with the plan's part count as a compile-time constant.
+template <int P = 1>
+void launch_finish(int parts, std::size_t t, std::size_t hidden, const float* part, float* y, void* xn, double eps,
+                   std::int8_t* q, float* qs, int qblock, hipStream_t stream) {
+    if constexpr (P < stack::kFinishParts) {
+        if (parts != P) {
+            launch_finish<P + 1>(parts, t, hidden, part, y, xn, eps, q, qs, qblock, stream);
+            return;
+        }
+    }
+    if (parts != P) throw LaunchError("small-M stack: K-part count beyond the finish pass");
+    stack::finish_kernel<P><<<dim3(static_cast<unsigned>(t)), dim3(1024), hidden * sizeof(float), stream>>>(
+        part, static_cast<int>(t), static_cast<int>(hidden), y, static_cast<std::uint16_t*>(xn), eps, q, qs, qblock);
+}
+
 bool small_stack_plan(std::size_t t, std::size_t hidden, std::size_t inter, SmallStackPlan& plan) {
     constexpr std::size_t kLds = 160u << 10;
     constexpr int kMaxPairs = stack::kWorkers * stack::kPairs;  // pairs of one block
@@ -654,9 +669,7 @@ void launch_small_layer(const SmallStackPlan& plan, std::size_t t, std::size_t h
     kd<<<dim3(d.parts * d.blocks_per_part), dim3(kThreads), lds_d, stream>>>(d);
     check_launch("small-M stack down launch");
     // y = sum of the parts; next layer's input
-    finish_kernel<<<dim3(static_cast<unsigned>(t)), dim3(1024), hidden * sizeof(float), stream>>>(
-        part, plan.parts, static_cast<int>(t), static_cast<int>(hidden), y, static_cast<std::uint16_t*>(xn), eps, nullptr,
-        nullptr, 0);
+    launch_finish(plan.parts, t, hidden, part, y, xn, eps, nullptr, nullptr, 0, stream);
     check_launch("small-M stack finish launch");
 }
 
@@ -722,9 +735,8 @@ void launch_small_layer_q8(const SmallStackPlan& plan, std::size_t t, std::size_
     kd<<<dim3(d.parts * d.blocks_per_part), dim3(kThreads), lds_d, stream>>>(d);
     check_launch("small-M q8 stack down launch");
     // y = sum of the parts; the next layer's bf16 input (xn) and its int8 form
-    finish_kernel<<<dim3(static_cast<unsigned>(t)), dim3(1024), hidden * sizeof(float), stream>>>(
-        part, plan.parts, static_cast<int>(t), static_cast<int>(hidden), y, static_cast<std::uint16_t*>(xn), eps, xq_next,
-        xs_next, per_token ? static_cast<int>(hidden) : 128);
+    launch_finish(plan.parts, t, hidden, part, y, xn, eps, xq_next, xs_next, per_token ? static_cast<int>(hidden) : 128,
+                  stream);
     check_launch("small-M q8 stack finish launch");
 }
 
