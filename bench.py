@@ -437,16 +437,24 @@ def main():
             ms_q = timed(torch, lambda: sm.s8_quantize_rows(x_o), 10, 2, stream)
             ms_s8 = timed(torch, lambda: sm.gemm_s8(xq_o, sx_o, wq_o, sw_o), 10, 2, stream)
             ms_a16 = timed(torch, lambda: sm.gemm_w8a16(x_o, wq_o, sw_o), 10, 2, stream)
+            # the cpu-q8 AVX2 int8 multiply (kernel_i8_y): one scale per row over the whole K, the MLP's epilogue
+            wqy, wsy = sm.quantize_rows_s8(w_o, block=k_o)
+            xqy, xsy = sm.quantize_rows_s8(x_o, block=k_o)
+            wsy, xsy = wsy.reshape(-1).contiguous(), xsy.reshape(-1).contiguous()
+            ep_y = sm.SWIGLU if n_o == 2 * I else sm.STORE
+            ms_y = timed(torch, lambda: sm.gemm_q8y(xqy, xsy, wqy, wsy, epilogue=ep_y), 10, 2, stream)
             ops = 2.0 * M_BIG * n_o * k_o
             s8[f"{n_o}x{k_o}"] = {"gemm_s8_ms": round(ms_s8, 4), "gemm_s8_tops": round(ops / (ms_s8 * 1e-3) / 1e12, 1),
                                   "gemm_s8_frac_int8_peak": round(ops / (ms_s8 * 1e-3) / 1e12 / PEAK["int8_tops"], 4),
                                   "gemm_w8a16_ms": round(ms_a16, 4),
                                   "gemm_w8a16_tflops": round(ops / (ms_a16 * 1e-3) / 1e12, 1),
                                   "quantize_rows_us": round(ms_q * 1e3, 1),
-                                  "quantize_rows_gbs": round(M_BIG * k_o * 3 / (ms_q * 1e-3) / 1e9, 1)}
-            del w_o, wq_o, sw_o, x_o, xq_o, sx_o
+                                  "quantize_rows_gbs": round(M_BIG * k_o * 3 / (ms_q * 1e-3) / 1e9, 1),
+                                  "gemm_q8y_ms": round(ms_y, 4), "gemm_q8y_tops": round(ops / (ms_y * 1e-3) / 1e12, 1),
+                                  "gemm_q8y_epilogue": "swiglu" if ep_y == sm.SWIGLU else "store"}
+            del w_o, wq_o, sw_o, x_o, xq_o, sx_o, wqy, wsy, xqy, xsy
         extra["per_channel_int8_m15872"] = s8
-        log(f"per-channel int8 family (M=15872): {s8}")
+        log(f"per-channel int8 family and the AVX2 int8 multiply (M=15872): {s8}")
 
     cpu = None
     if not args.no_cpu:

@@ -140,6 +140,20 @@ SEPAL_HIP_API int32_t sepal_hip_gemm_s8(const int8_t* xq, size_t ld_x, const flo
                                         const float* sw, void* y, int32_t y_type, size_t ld_y, size_t t, size_t n, size_t k,
                                         void* stream);
 
+/* The cpu-q8 AVX2 int8 multiply (one scale per activation row and one per weight feature): y = (float(S) * ws[n]) * xs[t],
+ * S the exact int32 sum over the whole K (int8 MFMA), then the epilogue STORE / ADD / SWIGLU (silu with the cpu-q8 exp
+ * polynomial; gate and up rows in the 64-row interleave), bit for bit the reference's results. xq int8 [T, ld_x] with
+ * xs float32 [T]; wq int8 [N, ld_w] with ws float32 [N]; both packed by sepal_hip_quantize_rows_s8 with block = K (its
+ * rule is the reference's pack_acts and, for the weights, its Avx2 panel packer). Y float32 [T, ld_y], or y_type for
+ * SWIGLU with N/2 columns. K a multiple of 128 (the reference takes any K); N any for STORE/ADD, a multiple of 128 for
+ * SWIGLU; ld_x, ld_w multiples of 16; 16-byte aligned X and W.
+ * Replaces kernel_i8_y + finish_tile (runner/src/cpu/gemm_kernels_avx2.cpp:40-76, gemm.cpp:417-447) as gemm_packed runs
+ * them (gemm.cpp:451-570) for weights packed for Isa::Avx2 or on a CPU without AVX-512 VNNI (pick_variant, gemm.cpp:56-69;
+ * pack_acts' I8_Y branch gemm.cpp:286-306). */
+SEPAL_HIP_API int32_t sepal_hip_gemm_q8y(const int8_t* xq, size_t ld_x, const float* xs, const int8_t* wq, size_t ld_w,
+                                         const float* ws, void* y, int32_t y_type, size_t ld_y, size_t t, size_t n, size_t k,
+                                         int32_t epilogue, void* stream);
+
 /* binary16 activations times int8 weights with per-channel scales: Y[t, n] = sw[n] * sum over K of x[t,k] * wq[n,k],
  * the weights widened exactly and multiplied with float32 accumulation (the gpu-w8g kernels with the channel's scale
  * in every group: within float32 rounding of one accumulator times sw). Y float32 or binary16 [T, ld_y] (binary16 is

@@ -45,6 +45,7 @@ def lib():
         L.orc_quantize_block_r2.argtypes = [vp, sz, sz, sz, sz, vp, sz, vp, sz]
         L.orc_group_sums.argtypes = [vp, sz, vp, sz, sz, sz, sz, vp]
         L.orc_gemm_q8.argtypes = [vp, sz, vp, sz, sz, vp, sz, vp, sz, vp, sz, sz, sz, sz, i32]
+        L.orc_gemm_q8y.argtypes = [vp, sz, vp, vp, sz, vp, vp, sz, sz, sz, sz, i32]
         L.orc_gemm_w8g.argtypes = [vp, sz, vp, sz, vp, sz, vp, sz, sz, sz, sz, i32]
         L.orc_rmsnorm_rows.argtypes = [vp, sz, vp, sz, sz, sz, vp, d]
         L.orc_exp_cephes.argtypes = [f32]
@@ -80,6 +81,9 @@ def ref():
         L.ref_gemm_i8.argtypes = [vp, sz, vp, sz, sz, vp, i32, u]
         L.ref_gemm_i8_swiglu.argtypes = [vp, sz, vp, vp, sz, sz, vp, u]
         L.ref_rmsnorm.argtypes = [vp, sz, sz, vp, d, vp]
+        L.ref_gemm_i8y.argtypes = [vp, sz, vp, sz, sz, vp, i32, u]
+        L.ref_gemm_i8y_swiglu.argtypes = [vp, sz, vp, vp, sz, sz, vp, u]
+        L.ref_pack_weight_i8y.argtypes = [vp, sz, sz, vp, vp]
         L.ref_time_mlp_block.argtypes = [vp, sz, vp, vp, vp, sz, sz, u, i32, C.POINTER(d), C.POINTER(d), C.POINTER(u)]
         _ref = L
     return _ref
@@ -182,6 +186,17 @@ def gemm_w8g(x, q, s, epilogue=STORE, y=None):
     return y
 
 
+def gemm_q8y(xq, xs, wq, ws, epilogue=STORE, y=None):
+    """kernel_i8_y: xs [t] per row, ws [n] per feature, one int32 sum over k."""
+    xq, wq, xs, ws = _i8(xq), _i8(wq), _f32(xs).reshape(-1), _f32(ws).reshape(-1)
+    t, k = xq.shape
+    n = wq.shape[0]
+    ncols = n // 2 if epilogue == SWIGLU else n
+    y = np.zeros((t, ncols), np.float32) if y is None else _f32(y).copy()
+    lib().orc_gemm_q8y(_p(xq), k, _p(xs), _p(wq), k, _p(ws), _p(y), ncols, t, n, k, epilogue)
+    return y
+
+
 def rmsnorm_rows(x, eps=1e-6, w1=None):
     x = _f32(x)
     rows, cols = x.shape
@@ -250,6 +265,35 @@ def ref_gemm_i8_swiglu(x, gate, up, threads=4):
     y = np.zeros((rows, n), np.float32)
     _chk(ref().ref_gemm_i8_swiglu(_p(x), rows, _p(gate), _p(up), n, k, _p(y), threads))
     return y
+
+
+def ref_gemm_i8y(x, w, y=None, threads=4):
+    """The reference's AVX2 int8 path (I8_Y) on x [rows, k] and w [n, k]."""
+    x, w = _f32(x), _f32(w)
+    rows, k = x.shape
+    n = w.shape[0]
+    acc = y is not None
+    y = np.zeros((rows, n), np.float32) if y is None else _f32(y).copy()
+    _chk(ref().ref_gemm_i8y(_p(x), rows, _p(w), n, k, _p(y), int(acc), threads))
+    return y
+
+
+def ref_gemm_i8y_swiglu(x, gate, up, threads=4):
+    x, gate, up = _f32(x), _f32(gate), _f32(up)
+    rows, k = x.shape
+    n = gate.shape[0]
+    y = np.zeros((rows, n), np.float32)
+    _chk(ref().ref_gemm_i8y_swiglu(_p(x), rows, _p(gate), _p(up), n, k, _p(y), threads))
+    return y
+
+
+def ref_pack_weight_i8y(w):
+    w = _f32(w)
+    n, k = w.shape
+    q = np.zeros((n, k), np.int8)
+    s = np.zeros(n, np.float32)
+    _chk(ref().ref_pack_weight_i8y(_p(w), n, k, _p(q), _p(s)))
+    return q, s
 
 
 def ref_rmsnorm(x, eps=1e-6, w1=None):

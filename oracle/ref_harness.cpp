@@ -108,6 +108,51 @@ int ref_gemm_i8_swiglu(const float* x, std::size_t rows, const float* gate, cons
     });
 }
 
+// The reference's AVX2 int8 path, Variant::I8_Y (kernel_i8_y, runner/src/cpu/gemm_kernels_avx2.cpp:40-79): one
+// activation scale per row and one weight scale per feature (a single block spanning k), int16 pairs of int8 values,
+// forced by packing for Isa::Avx2 (runner/src/cpu/gemm.cpp:58-62). y [rows][n] = (accumulate ? y : 0) + product.
+int ref_gemm_i8y(const float* x, std::size_t rows, const float* w, std::size_t n, std::size_t k, float* y, int accumulate,
+                 unsigned threads) {
+    return guarded([&] {
+        ThreadPool pool(threads);
+        const PackedWeight pw = pack_weight(w, k, n, k, WeightKind::I8, Isa::Avx2, pool);
+        if (pw.variant() != Variant::I8_Y) throw std::runtime_error("the reference did not pick I8_Y for Isa::Avx2");
+        PackedActs pa;
+        pack_acts(pa, x, k, rows, k, pw.variant(), pool);
+        gemm_packed(pw, pa, y, n, accumulate != 0, pool);
+    });
+}
+
+// The I8_Y SwiGLU product (pack_weight_swiglu for Isa::Avx2): y [rows][n] = silu(x gate^T) * (x up^T).
+int ref_gemm_i8y_swiglu(const float* x, std::size_t rows, const float* gate, const float* up, std::size_t n, std::size_t k,
+                        float* y, unsigned threads) {
+    return guarded([&] {
+        ThreadPool pool(threads);
+        const PackedWeight pw = pack_weight_swiglu(gate, up, k, n, k, WeightKind::I8, Isa::Avx2, pool);
+        if (pw.variant() != Variant::I8_Y) throw std::runtime_error("the reference did not pick I8_Y for Isa::Avx2");
+        PackedActs pa;
+        pack_acts(pa, x, k, rows, k, pw.variant(), pool);
+        gemm_packed(pw, pa, y, n, false, pool);
+    });
+}
+
+// pack_weight(I8, Isa::Avx2): q [n][k] int8 (from the int16 pairs) and one scale per feature, unpacked from the panels
+// (nr 16, group 2: value kk of column jj at ((kk / 2) * 16 + jj) * 2 + kk % 2, runner/src/cpu/gemm.cpp:137-165).
+int ref_pack_weight_i8y(const float* w, std::size_t n, std::size_t k, std::int8_t* q, float* scale) {
+    return guarded([&] {
+        ThreadPool pool(1);
+        const PackedWeight pw = pack_weight(w, k, n, k, WeightKind::I8, Isa::Avx2, pool);
+        if (pw.variant() != Variant::I8_Y) throw std::runtime_error("the reference did not pick I8_Y for Isa::Avx2");
+        const std::size_t nr = 16, g = 2;
+        for (std::size_t c = 0; c < n; ++c) {
+            const std::size_t p = c / nr, jj = c % nr;
+            const auto* panel = reinterpret_cast<const std::int16_t*>(pw.panel(p));
+            for (std::size_t kk = 0; kk < k; ++kk) q[c * k + kk] = static_cast<std::int8_t>(panel[((kk / g) * nr + jj) * g + kk % g]);
+            scale[c] = pw.scale(p)[jj];
+        }
+    });
+}
+
 int ref_rmsnorm(const float* x, std::size_t rows, std::size_t cols, const float* w1, double eps, float* y) {
     return guarded([&] {
         ThreadPool pool(1);

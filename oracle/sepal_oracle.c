@@ -168,6 +168,37 @@ void orc_gemm_q8(const int8_t* xq, size_t ld_xq, const float* xs, size_t ld_xs, 
     free(acc);
 }
 
+/* The cpu-q8 AVX2 kernel (runner/src/cpu/gemm_kernels_avx2.cpp:40-79, kernel_i8_y and its I4_STORE): one int32 sum
+ * over the whole k (the int16 pairs of vpmaddwd are exact), tile = (float(S) * ws[c]) * xs[r], then finish_tile
+ * (runner/src/cpu/gemm.cpp:417-447) as in orc_gemm_q8. */
+void orc_gemm_q8y(const int8_t* xq, size_t ld_xq, const float* xs, const int8_t* wq, size_t ld_wq, const float* ws,
+                  float* y, size_t ld_y, size_t t, size_t n, size_t k, int epilogue) {
+    float* acc = (float*)malloc(n * sizeof(float));
+    for (size_t r = 0; r < t; ++r) {
+        const int8_t* a = xq + r * ld_xq;
+        for (size_t c = 0; c < n; ++c) {
+            const int8_t* b = wq + c * ld_wq;
+            int32_t sum = 0;
+            for (size_t i = 0; i < k; ++i) sum += (int32_t)a[i] * (int32_t)b[i];
+            const float v = (float)sum * ws[c];
+            acc[c] = v * xs[r];
+        }
+        float* out = y + r * ld_y;
+        if (epilogue == ORC_SWIGLU) {
+            for (size_t c = 0; c < n / 2; ++c) {
+                const size_t blk = c / 64, rr = c % 64;
+                const float g = acc[128 * blk + rr], u = acc[128 * blk + 64 + rr];
+                out[c] = orc_silu_cephes(g) * u;
+            }
+        } else if (epilogue == ORC_ADD) {
+            for (size_t c = 0; c < n; ++c) out[c] = out[c] + acc[c];
+        } else {
+            for (size_t c = 0; c < n; ++c) out[c] = acc[c];
+        }
+    }
+    free(acc);
+}
+
 /* runner/cuda/src/gemm_simt_kernels.cu:27-29 with the C library's expf / log1pf. */
 float orc_swiglu_libm(float g, float u) {
     const float ng = -g;

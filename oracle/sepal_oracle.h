@@ -12,6 +12,8 @@
  *                           (pack_weight / pack_acts, I8_Z), plus the same special cases.
  *   orc_group_sums          brute-force int64 sums on tiny shapes; the integer identity corr = 128 * sum(q).
  *   orc_gemm_q8             bit-exact against the compiled reference gemm_packed (I8_Z) fixtures: Store, Add, SwiGLU.
+ *   orc_gemm_q8y            bit-exact against the compiled reference gemm_packed (I8_Y, the AVX2 kernel forced by
+ *                           packing for Isa::Avx2) fixtures: Store, Add, SwiGLU.
  *   orc_gemm_w8g            float64 brute force bound and the group identity sum_g s_g * sum_k x q; the fmaf chain
  *                           order is the reference's stated schedule (CUDA source, not buildable here).
  *   orc_exp_cephes / silu   bit-exact via orc_gemm_q8's SwiGLU fixtures; against libm exp within 2 ulp.
@@ -71,6 +73,10 @@ void orc_group_sums(const int8_t* xq, size_t ld_xq, const int8_t* wq, size_t ld_
  * Y[t, 64c + r] = silu_cephes(acc[128c + r]) * acc[128c + 64 + r] with n = 2I.
  * (runner/src/cpu/gemm_kernels_avx512.cpp:74 Z_FLUSH_I, :102-113; runner/src/cpu/gemm.cpp:417-447 finish_tile;
  *  emulation in runner/tests/test_cpu_gemm.cpp:194-203.) */
+/* kernel_i8_y (runner/src/cpu/gemm_kernels_avx2.cpp:40-79): one activation scale per row, one weight scale per
+ * feature; y = (float(S) * ws[n]) * xs[t], S the exact int32 sum over k; finish_tile epilogues as orc_gemm_q8. */
+void orc_gemm_q8y(const int8_t* xq, size_t ld_xq, const float* xs, const int8_t* wq, size_t ld_wq, const float* ws,
+                  float* y, size_t ld_y, size_t t, size_t n, size_t k, int epilogue);
 void orc_gemm_q8(const int8_t* xq, size_t ld_xq, const float* xs, size_t ld_xs, size_t act_block, const int8_t* wq,
                  size_t ld_wq, const float* ws, size_t ld_ws, float* y, size_t ld_y, size_t t, size_t n, size_t k,
                  int epilogue);

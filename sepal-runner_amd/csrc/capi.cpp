@@ -337,6 +337,43 @@ int32_t sepal_hip_gemm_s8(const int8_t* xq, size_t ld_x, const float* sx, const 
     });
 }
 
+int32_t sepal_hip_gemm_q8y(const int8_t* xq, size_t ld_x, const float* xs, const int8_t* wq, size_t ld_w, const float* ws,
+                           void* y, int32_t y_type, size_t ld_y, size_t t, size_t n, size_t k, int32_t epilogue, void* stream) {
+    return guarded([&] {
+        require(xq != nullptr && xs != nullptr && wq != nullptr && ws != nullptr && y != nullptr, "gemm_q8y: null pointer");
+        require(epilogue == SEPAL_HIP_STORE || epilogue == SEPAL_HIP_ADD || epilogue == SEPAL_HIP_SWIGLU, "gemm_q8y: unknown epilogue");
+        require(valid_type(y_type), "gemm_q8y: unknown output type");
+        require(epilogue == SEPAL_HIP_SWIGLU || y_type == SEPAL_HIP_F32, "gemm_q8y: Store and Add write float32");
+        require(n != 0 && k != 0 && k % 128 == 0, "gemm_q8y: K must be a non-zero multiple of 128 and N non-zero");
+        require(ld_x >= k && ld_w >= k && ld_x % 16 == 0 && ld_w % 16 == 0,
+                "gemm_q8y: row strides of X and W must be multiples of 16 and at least K");
+        if (epilogue == SEPAL_HIP_SWIGLU) require(n % 128 == 0 && ld_y >= n / 2, "gemm_q8y: SwiGLU needs N a multiple of 128 and ld_y >= N/2");
+        else require(ld_y >= n, "gemm_q8y: ld_y must be at least N");
+        require(aligned16(xq) && aligned16(wq) && reinterpret_cast<std::uintptr_t>(y) % 4 == 0,
+                "gemm_q8y: X and W must be 16-byte aligned, Y 4-byte aligned");
+        if (t == 0) return;
+        require(t < 0x7FFFFFFFu && n < 0x7FFFFFFFu && k < 0x7FFFFFFFu, "gemm_q8y: dimension beyond 2^31");
+        GemmArgs a;
+        a.x = xq;
+        a.ld_x = ld_x;
+        a.xs = xs;
+        a.ld_xs = 1;
+        a.act_block = k;
+        a.w = wq;
+        a.ld_w = ld_w;
+        a.s = ws;
+        a.ld_s = 1;
+        a.y = y;
+        a.y_type = y_type;
+        a.ld_y = ld_y;
+        a.t = t;
+        a.n = n;
+        a.k = k;
+        a.epilogue = epilogue;
+        launch_gemm_q8y(a, as_stream(stream));
+    });
+}
+
 int32_t sepal_hip_gemm_w8a16(const void* x, size_t ld_x, const int8_t* wq, size_t ld_w, const float* sw, void* y,
                              int32_t y_type, size_t ld_y, size_t t, size_t n, size_t k, void* stream) {
     return guarded([&] {

@@ -52,6 +52,7 @@ void launch_gemm_q8(const GemmArgs& a, hipStream_t stream);
 // The int8-activation multiply with per-channel weight scales: y = (float(sum over K of xq * wq) * xs[t]) * s[n] (a.s
 // holds one scale per row, a.ld_s = 1); y float32 or binary16 (a.y_type).
 void launch_gemm_s8(const GemmArgs& a, hipStream_t stream);
+void launch_gemm_q8y(const GemmArgs& a, hipStream_t stream);
 // The GPU int8 path's per-row quantizer (rule 127 / amax, zero rows scale 0), with an optional per-column factor.
 void launch_s8_quantize_rows(const void* x, int x_type, std::size_t ld_x, const float* smooth, std::int8_t* q, std::size_t ld_q,
                              float* scales, std::size_t rows, std::size_t cols, hipStream_t stream);

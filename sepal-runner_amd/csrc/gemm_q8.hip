@@ -21,8 +21,10 @@ namespace sepal::hip {
 namespace q8 {
 
 // MODE_CHAIN: the per-group float chain; MODE_SUMS: the int32 group sums out; MODE_WHOLE: one int32 sum over the whole
-// K (per-channel weight scales), then (float(S) * sx) * sw (runner/cuda/src/gemm_s8_kernels.cu:255-266)
-enum { MODE_CHAIN = 0, MODE_SUMS = 1, MODE_WHOLE = 2 };
+// K (per-channel weight scales), then (float(S) * sx) * sw (runner/cuda/src/gemm_s8_kernels.cu:255-266); MODE_WHOLE_Y:
+// the same sum, then (float(S) * ws) * xs and the chain epilogues (kernel_i8_y, runner/src/cpu/gemm_kernels_avx2.cpp:40-76,
+// with finish_tile, gemm.cpp:417-447).
+enum { MODE_CHAIN = 0, MODE_SUMS = 1, MODE_WHOLE = 2, MODE_WHOLE_Y = 3 };
 
 __device__ __forceinline__ i32x16 mfma_i8_32(const u32x4 a, const u32x4 b, i32x16 c) {
     return __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(i32x4, a), __builtin_bit_cast(i32x4, b), c, 0, 0, 0);
@@ -217,6 +219,7 @@ __global__ void __launch_bounds__(512) gemm_big(const Params p) {
     constexpr int BM = 128, BN = 256;
     constexpr int XDMA = BM / 64, WDMA = BN / 64;  // direct loads per thread and group (8 rows of 128 bytes each)
     constexpr int NSC = MODE == MODE_CHAIN ? (PER_TOKEN ? 2 : 3) : 0;  // scale loads per thread and group
+    constexpr bool WHOLE = MODE == MODE_WHOLE || MODE == MODE_WHOLE_Y;
     // Three stages of each operand, each its own LDS array: the compiler then knows which array a direct load writes,
     // and a fragment read waits only for loads into the array it reads.
     __shared__ __align__(1024) u32x4 lx0[BM * 8], lx1[BM * 8], lx2[BM * 8];
@@ -345,11 +348,11 @@ __global__ void __launch_bounds__(512) gemm_big(const Params p) {
                 for (int i = 0; i < 2; ++i)
 #pragma unroll
                     for (int q = 0; q < 2; ++q) {
-                        if constexpr (MODE == MODE_WHOLE) tot[i][q] = mfma_i8_32(a[i], b[q], tot[i][q]);
+                        if constexpr (WHOLE) tot[i][q] = mfma_i8_32(a[i], b[q], tot[i][q]);
                         else sacc[i][q] = mfma_i8_32(a[i], b[q], st == 0 ? zero16 : sacc[i][q]);
                     }
             }
-            if constexpr (MODE == MODE_WHOLE) {
+            if constexpr (WHOLE) {
             } else if constexpr (MODE == MODE_SUMS) {
                 // the row base is opaque here, so that the 64 store addresses are not hoisted out of the loop (spills)
                 int mb = m0;
@@ -419,6 +422,15 @@ __global__ void __launch_bounds__(512) gemm_big(const Params p) {
             }
         return;
     }
+    if constexpr (MODE == MODE_WHOLE_Y) {
+        // float(S) * ws[n]; the per-token epilogue multiplies by xs[t]
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[i][j][r] = __fmul_rn(static_cast<float>(tot[i][j][r]), wsrow[j][0]);
+    }
 
     chain_epilogue<EP, YT, PER_TOKEN>(p, acc, m0, n0, wm, ib, hh, lane, tid, col, reinterpret_cast<float*>(lw0));
 }
@@ -450,17 +462,18 @@ __global__ void __launch_bounds__(512) gemm_chain(const ChainParams cp) {
     __shared__ __align__(1024) u32x4 lx0[BM * 8], lx1[BM * 8], lx2[BM * 8];
     __shared__ __align__(1024) u32x4 lw0[BN * 8], lw1[BN * 8], lw2[BN * 8];
     __shared__ float lds_xs[3][BM];  // per-128 activation scales of group g in buffer g mod 3
-    const auto xstage = [&](auto it) -> u32x4* {
+    typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
+    const auto xstage = [&](auto it) -> lds_u32x4* {
         constexpr int i = decltype(it)::value;
-        if constexpr (i == 0) return lx0;
-        else if constexpr (i == 1) return lx1;
-        else return lx2;
+        if constexpr (i == 0) return (lds_u32x4*)lx0;
+        else if constexpr (i == 1) return (lds_u32x4*)lx1;
+        else return (lds_u32x4*)lx2;
     };
-    const auto wstage = [&](auto it) -> u32x4* {
+    const auto wstage = [&](auto it) -> lds_u32x4* {
         constexpr int i = decltype(it)::value;
-        if constexpr (i == 0) return lw0;
-        else if constexpr (i == 1) return lw1;
-        else return lw2;
+        if constexpr (i == 0) return (lds_u32x4*)lw0;
+        else if constexpr (i == 1) return (lds_u32x4*)lw1;
+        else return (lds_u32x4*)lw2;
     };
 
     const int tid = threadIdx.x, lane = tid % 64;
@@ -513,7 +526,7 @@ __global__ void __launch_bounds__(512) gemm_chain(const ChainParams cp) {
         float xs, ws[2];
     };
     Set s0, s1, s2;  // group g's scales in set g mod 3
-    const auto issue = [&](int g, u32x4* xd, u32x4* wd, Set& s) {
+    const auto issue = [&](int g, lds_u32x4* xd, lds_u32x4* wd, Set& s) {
         const int k0 = g * 128;
 #pragma unroll
         for (int e = 0; e < XDMA; ++e)
@@ -569,8 +582,13 @@ __global__ void __launch_bounds__(512) gemm_chain(const ChainParams cp) {
             if (tid < BM) lds_xs[g % 3][tid] = cur.xs;
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
-        const u32x4* tx = xstage(std::integral_constant<int, j>{});
-        const u32x4* tw = wstage(std::integral_constant<int, j>{});
+        // group g + 2's loads into the stage and set of group g - 1 (read before the barrier; its weight scales
+        // copied out first)
+        const float cws0 = pw0, cws1 = pw1;
+        issue(min(g + 2, groups - 1), xstage(std::integral_constant<int, (j + 2) % 3>{}),
+              wstage(std::integral_constant<int, (j + 2) % 3>{}), prev);
+        const lds_u32x4* tx = xstage(std::integral_constant<int, j>{});
+        const lds_u32x4* tw = wstage(std::integral_constant<int, j>{});
         u32x4 a[2][4], b[2][4];
 #pragma unroll
         for (int st = 0; st < 4; ++st) {
@@ -582,9 +600,6 @@ __global__ void __launch_bounds__(512) gemm_chain(const ChainParams cp) {
             a[1][st] = tx[ra[st] + 256];
             b[1][st] = tw[rb[st] + 512];
         }
-        const float cws0 = pw0, cws1 = pw1;
-        issue(min(g + 2, groups - 1), xstage(std::integral_constant<int, (j + 2) % 3>{}),
-              wstage(std::integral_constant<int, (j + 2) % 3>{}), prev);
         const float gws0 = cur.ws[0], gws1 = cur.ws[1];
 #pragma unroll
         for (int blk = 0; blk < 4; ++blk) {
@@ -605,8 +620,8 @@ __global__ void __launch_bounds__(512) gemm_chain(const ChainParams cp) {
     using I0 = std::integral_constant<int, 0>;
     using I1 = std::integral_constant<int, 1>;
     using I2 = std::integral_constant<int, 2>;
-    issue(0, lx0, lw0, s0);
-    issue(min(1, groups - 1), lx1, lw1, s1);
+    issue(0, xstage(I0{}), wstage(I0{}), s0);
+    issue(min(1, groups - 1), xstage(I1{}), wstage(I1{}), s1);
     // group 0, group 1, then three groups per iteration (stage and scale set g mod 3)
     group_step(0, I0{}, I0{});
     if (groups > 1) group_step(1, I1{}, I1{});
@@ -921,6 +936,19 @@ void launch_gemm_s8(const GemmArgs& a, hipStream_t stream) {
         if (!q8::launch_s8_big<SEPAL_HIP_F16>(a, stream)) q8::launch_big<SEPAL_HIP_STORE, SEPAL_HIP_F16, true, q8::MODE_WHOLE>(a, stream);
     } else {
         if (!q8::launch_s8_big<SEPAL_HIP_F32>(a, stream)) q8::launch_big<SEPAL_HIP_STORE, SEPAL_HIP_F32, true, q8::MODE_WHOLE>(a, stream);
+    }
+}
+
+void launch_gemm_q8y(const GemmArgs& a, hipStream_t stream) {
+    switch (a.epilogue) {
+    case SEPAL_HIP_STORE: q8::launch_big<SEPAL_HIP_STORE, SEPAL_HIP_F32, true, q8::MODE_WHOLE_Y>(a, stream); break;
+    case SEPAL_HIP_ADD: q8::launch_big<SEPAL_HIP_ADD, SEPAL_HIP_F32, true, q8::MODE_WHOLE_Y>(a, stream); break;
+    default:
+        switch (a.y_type) {
+        case SEPAL_HIP_F32: q8::launch_big<SEPAL_HIP_SWIGLU, SEPAL_HIP_F32, true, q8::MODE_WHOLE_Y>(a, stream); break;
+        case SEPAL_HIP_BF16: q8::launch_big<SEPAL_HIP_SWIGLU, SEPAL_HIP_BF16, true, q8::MODE_WHOLE_Y>(a, stream); break;
+        default: q8::launch_big<SEPAL_HIP_SWIGLU, SEPAL_HIP_F16, true, q8::MODE_WHOLE_Y>(a, stream); break;
+        }
     }
 }
 

@@ -66,6 +66,7 @@ def library() -> C.CDLL:
         L.sepal_hip_s8_quantize_rows.argtypes = [vp, i32, sz, vp, vp, sz, vp, sz, sz, vp]
         L.sepal_hip_gemm_s8.argtypes = [vp, sz, vp, vp, sz, vp, vp, i32, sz, sz, sz, sz, vp]
         L.sepal_hip_gemm_w8a16.argtypes = [vp, sz, vp, sz, vp, vp, i32, sz, sz, sz, sz, vp]
+        L.sepal_hip_gemm_q8y.argtypes = [vp, sz, vp, vp, sz, vp, vp, i32, sz, sz, sz, sz, i32, vp]
         L.sepal_hip_column_absmax.argtypes = [vp, sz, vp, sz, sz, vp]
         L.sepal_hip_channel_stats.argtypes = [vp, sz, sz, sz, vp, vp, vp]
         for name in ("sepal_hip_quantize_group_s8", "sepal_hip_quantize_gate_up_s8", "sepal_hip_gemm_w8g",
@@ -74,7 +75,7 @@ def library() -> C.CDLL:
                      "sepal_hip_mlp_stack_noalloc",
                      "sepal_hip_rmsnorm_quantize_rows", "sepal_hip_gemm_q8_swiglu_quantize",
                      "sepal_hip_weight_fingerprint", "sepal_hip_packed_save", "sepal_hip_packed_load",
-                     "sepal_hip_s8_quantize_rows", "sepal_hip_gemm_s8", "sepal_hip_gemm_w8a16",
+                     "sepal_hip_s8_quantize_rows", "sepal_hip_gemm_s8", "sepal_hip_gemm_w8a16", "sepal_hip_gemm_q8y",
                      "sepal_hip_column_absmax", "sepal_hip_channel_stats"):
             getattr(L, name).restype = i32
         L.sepal_hip_gemm_w8g_supports.restype = i32
@@ -245,6 +246,20 @@ def gemm_q8(xq, xs, w, ws, y=None, epilogue: int = STORE, act_block: int = 128, 
     _check(library().sepal_hip_gemm_q8(_ptr(xq), _ld(xq), _ptr(xs), _ld(xs), act_block, _ptr(w), _ld(w), _ptr(ws),
                                        _ld(ws), _ptr(y), _type_of(y), _ld(y), t, n, k, epilogue, config,
                                        _stream(stream)))
+    return y
+
+
+def gemm_q8y(xq, xs, wq, ws, y=None, epilogue: int = STORE, y_dtype=None, stream=None):
+    """The cpu-q8 AVX2 int8 multiply: y = (float(S) * ws[n]) * xs[t] then the epilogue; xs [T], ws [N] (one scale per
+    activation row and per weight feature, both from quantize_rows_s8 with block = K)."""
+    torch = _torch()
+    t, k = xq.shape
+    n = wq.shape[0]
+    cols = n // 2 if epilogue == SWIGLU else n
+    if y is None:
+        y = torch.empty(t, cols, dtype=y_dtype or torch.float32, device=xq.device)
+    _check(library().sepal_hip_gemm_q8y(_ptr(xq), _ld(xq), _ptr(xs), _ptr(wq), _ld(wq), _ptr(ws), _ptr(y), _type_of(y),
+                                        _ld(y), t, n, k, epilogue, _stream(stream)))
     return y
 
 

@@ -19,4 +19,4 @@ def golden():
     import numpy as np
     d = os.path.join(ROOT, "tests", "golden")
     return {name: np.load(os.path.join(d, name + ".npz"), allow_pickle=False)
-            for name in ("ref_suite", "ref_mlp", "ref_rmsnorm")}
+            for name in ("ref_suite", "ref_mlp", "ref_rmsnorm", "ref_i8y")}

@@ -9,6 +9,11 @@ read them. What is dumped:
   ref_mlp.npz     MLP-shaped cases with K a multiple of 128 (what the GPU kernels take): gemm_packed Store, Add and the
                   SwiGLU pair (pack_weight_swiglu), weights ~N(0, 0.02), activations ~N(0, 1) with 1% of channels x20.
   ref_rmsnorm.npz rmsnorm_rows with an identity weight and eps 1e-6.
+  ref_i8y.npz     the reference's AVX2 int8 path (Variant::I8_Y, kernel_i8_y: one activation scale per row, one
+                  weight scale per feature), forced by packing for Isa::Avx2: its weight packing (q, one scale per
+                  feature) and gemm_packed Store, Add and SwiGLU, at the suite's odd shapes and at K multiples of 128;
+                  the weights are binary16 values (stored as binary16).
+`python tests/golden/make_golden.py i8y` writes ref_i8y.npz only.
 """
 from __future__ import annotations
 
@@ -36,7 +41,38 @@ def lcg_uniform(seed: int, count: int) -> np.ndarray:
     return out
 
 
+def write_i8y() -> None:
+    rng = np.random.default_rng(20261202)
+    out = {}
+    # weights are binary16 values (stored as such, handed to the reference widened to float32)
+    cases = [(13, 37, 70), (29, 100, 129), (37, 128, 256), (130, 128, 512), (16, 128, 1280), (3, 128, 2560)]
+    half = lambda a: (a * 0.02).astype(np.float16)  # noqa: E731
+    for i, (t, n, k) in enumerate(cases):
+        x = rng.standard_normal((t, k)).astype(np.float32)
+        hot = rng.choice(k, size=max(1, k // 100), replace=False)
+        x[:, hot] *= np.float32(20.0)
+        x = orc.bf16_round(x)
+        w = half(rng.standard_normal((n, k)))
+        wf = w.astype(np.float32)
+        base = rng.standard_normal((t, n)).astype(np.float32)
+        q, s = orc.ref_pack_weight_i8y(wf)
+        entry = {"x": x, "w": w, "wq": q, "ws": s, "base": base, "y": orc.ref_gemm_i8y(x, wf),
+                 "y_acc": orc.ref_gemm_i8y(x, wf, y=base)}
+        if n % 128 == 0:
+            gate = half(rng.standard_normal((n // 2, k)))
+            up = half(rng.standard_normal((n // 2, k)))
+            entry.update({"gate": gate, "up": up,
+                          "y_swiglu": orc.ref_gemm_i8y_swiglu(x, gate.astype(np.float32), up.astype(np.float32))})
+        out.update({f"c{i}_{name}": v for name, v in entry.items()})
+    out["count"] = np.array(len(cases))
+    np.savez_compressed(os.path.join(HERE, "ref_i8y.npz"), **out)
+
+
 def main() -> None:
+    if len(sys.argv) > 1 and sys.argv[1] == "i8y":
+        write_i8y()
+        print("wrote ref_i8y.npz")
+        return
     if not orc.ref().ref_i8_variant_is_z():
         raise SystemExit("this CPU does not run the reference's I8_Z kernel (AVX-512 VNNI)")
     # ---- the reference suite's shapes and inputs ----
@@ -80,6 +116,7 @@ def main() -> None:
     x3 = (rng.standard_normal((5, 136))).astype(np.float32)  # a tail of 8-chunks after the 32-chunks
     np.savez_compressed(os.path.join(HERE, "ref_rmsnorm.npz"), x0=x, y0=orc.ref_rmsnorm(x), x1=x2,
                         y1=orc.ref_rmsnorm(x2), x2=x3, y2=orc.ref_rmsnorm(x3))
+    write_i8y()
     print("wrote", sorted(f for f in os.listdir(HERE) if f.endswith(".npz")))
 
 

@@ -229,3 +229,21 @@ def test_oracle_against_live_reference_random_shapes():
         xq, xs = orc.quantize_block_r2(x)
         wq, ws = orc.quantize_block_r2(w)
         assert same_bits(orc.gemm_q8(xq, xs, wq, ws), orc.ref_gemm_i8(x, w))
+
+
+def test_q8y_matches_reference_avx2_path(golden):
+    """kernel_i8_y (runner/src/cpu/gemm_kernels_avx2.cpp): one scale per activation row and per weight feature, both
+    from the R2 rule over the whole K; y = ((float)S * ws[n]) * xs[t] then the Store/Add/SwiGLU epilogue."""
+    g = golden["ref_i8y"]
+    for i in range(int(g["count"])):
+        x, w = g[f"c{i}_x"], g[f"c{i}_w"].astype(np.float32)
+        k = x.shape[1]
+        wq, ws = orc.quantize_block_r2(w, block=k)
+        assert same_bits(wq, g[f"c{i}_wq"]) and same_bits(ws.reshape(-1), g[f"c{i}_ws"].reshape(-1))
+        xq, xs = orc.quantize_block_r2(x, block=k)
+        assert same_bits(orc.gemm_q8y(xq, xs, wq, ws), g[f"c{i}_y"])
+        assert same_bits(orc.gemm_q8y(xq, xs, wq, ws, epilogue=orc.ADD, y=g[f"c{i}_base"]), g[f"c{i}_y_acc"])
+        if f"c{i}_gate" in g:
+            W = orc.interleave_gate_up(g[f"c{i}_gate"].astype(np.float32), g[f"c{i}_up"].astype(np.float32))
+            Wq, Ws = orc.quantize_block_r2(W, block=k)
+            assert same_bits(orc.gemm_q8y(xq, xs, Wq, Ws, epilogue=orc.SWIGLU), g[f"c{i}_y_swiglu"])
