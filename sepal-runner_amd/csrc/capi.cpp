@@ -298,11 +298,13 @@ int32_t sepal_hip_channel_stats(const void* x, size_t ld_x, size_t rows, size_t 
 
 namespace {
 void check_s8_family(const char* who, const void* x, size_t ld_x, const void* w, size_t ld_w, const float* sw, const void* y,
-                     int32_t y_type, size_t ld_y, size_t n, size_t k) {
+                     int32_t y_type, size_t ld_y, size_t n, size_t k, size_t k_step) {
     const std::string w_ = who;
     require(x != nullptr && w != nullptr && sw != nullptr && y != nullptr, w_ + ": null pointer");
     require(y_type == SEPAL_HIP_F32 || y_type == SEPAL_HIP_F16, w_ + ": the output is float32 or binary16");
-    require(n != 0 && k != 0 && k % 128 == 0, w_ + ": K must be a non-zero multiple of 128 (this library's group step) and N non-zero");
+    require(n != 0 && k != 0 && k % k_step == 0,
+            w_ + (k_step == 128 ? ": K must be a non-zero multiple of 128 (this library's group step) and N non-zero"
+                                : ": K must be a non-zero multiple of 16 and N non-zero"));
     require(ld_x >= k && ld_w >= k && ld_x % 16 == 0 && ld_w % 16 == 0, w_ + ": row strides of X and W must be multiples of 16 and at least K");
     require(ld_y >= n, w_ + ": ld_y must be at least N");
     require(aligned16(x) && aligned16(w) && aligned8(y), w_ + ": X and W must be 16-byte aligned, Y 8-byte aligned");
@@ -312,7 +314,7 @@ void check_s8_family(const char* who, const void* x, size_t ld_x, const void* w,
 int32_t sepal_hip_gemm_s8(const int8_t* xq, size_t ld_x, const float* sx, const int8_t* wq, size_t ld_w, const float* sw,
                           void* y, int32_t y_type, size_t ld_y, size_t t, size_t n, size_t k, void* stream) {
     return guarded([&] {
-        check_s8_family("gemm_s8", xq, ld_x, wq, ld_w, sw, y, y_type, ld_y, n, k);
+        check_s8_family("gemm_s8", xq, ld_x, wq, ld_w, sw, y, y_type, ld_y, n, k, 16);
         require(sx != nullptr, "gemm_s8: null pointer");
         if (t == 0) return;
         require(t < 0x7FFFFFFFu && n < 0x7FFFFFFFu, "gemm_s8: dimension beyond 2^31");
@@ -344,7 +346,7 @@ int32_t sepal_hip_gemm_q8y(const int8_t* xq, size_t ld_x, const float* xs, const
         require(epilogue == SEPAL_HIP_STORE || epilogue == SEPAL_HIP_ADD || epilogue == SEPAL_HIP_SWIGLU, "gemm_q8y: unknown epilogue");
         require(valid_type(y_type), "gemm_q8y: unknown output type");
         require(epilogue == SEPAL_HIP_SWIGLU || y_type == SEPAL_HIP_F32, "gemm_q8y: Store and Add write float32");
-        require(n != 0 && k != 0 && k % 128 == 0, "gemm_q8y: K must be a non-zero multiple of 128 and N non-zero");
+        require(n != 0 && k != 0 && k % 16 == 0, "gemm_q8y: K must be a non-zero multiple of 16 and N non-zero");
         require(ld_x >= k && ld_w >= k && ld_x % 16 == 0 && ld_w % 16 == 0,
                 "gemm_q8y: row strides of X and W must be multiples of 16 and at least K");
         if (epilogue == SEPAL_HIP_SWIGLU) require(n % 128 == 0 && ld_y >= n / 2, "gemm_q8y: SwiGLU needs N a multiple of 128 and ld_y >= N/2");
@@ -377,7 +379,7 @@ int32_t sepal_hip_gemm_q8y(const int8_t* xq, size_t ld_x, const float* xs, const
 int32_t sepal_hip_gemm_w8a16(const void* x, size_t ld_x, const int8_t* wq, size_t ld_w, const float* sw, void* y,
                              int32_t y_type, size_t ld_y, size_t t, size_t n, size_t k, void* stream) {
     return guarded([&] {
-        check_s8_family("gemm_w8a16", x, ld_x, wq, ld_w, sw, y, y_type, ld_y, n, k);
+        check_s8_family("gemm_w8a16", x, ld_x, wq, ld_w, sw, y, y_type, ld_y, n, k, 128);
         if (t == 0) return;
         require(t < 0x7FFFFFFFu && n < 0x7FFFFFFFu, "gemm_w8a16: dimension beyond 2^31");
         const hipStream_t st = as_stream(stream);

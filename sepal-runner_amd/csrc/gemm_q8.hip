@@ -383,6 +383,8 @@ __global__ void __launch_bounds__(512) gemm_big(const Params p) {
         barrier();
     };
 
+    // the whole-K modes take K a multiple of 16: whole groups here, the rest (tail) after the loop
+    if (groups > 0) {
     issue(0, lx0, lw0, s0);
     issue(min(1, groups - 1), lx1, lw1, s1);
     __builtin_amdgcn_sched_barrier(0);
@@ -401,6 +403,37 @@ __global__ void __launch_bounds__(512) gemm_big(const Params p) {
     // the repeated loads of the last steps may still be writing LDS: drain them before the block reuses or leaves it
     wait_vm_lgkm0<0>();
     __syncthreads();
+    }
+    if constexpr (WHOLE) {
+        // the last K % 128 values (a multiple of 16): each lane loads its fragment chunks straight from global memory
+        // (rows clamped as above, chunks at or past K read as zero) and the MFMAs add them to the int32 sums
+        const int k0 = groups * 128, tail = p.k - k0;
+        if (tail > 0) {
+#pragma unroll
+            for (int st = 0; st < 4; ++st) {
+                if (32 * st >= tail) break;
+                const int c = 2 * st + lane / 32;
+                const bool in = 16 * c < tail;
+                u32x4 a[2], b[2];
+#pragma unroll
+                for (int i = 0; i < 2; ++i) {
+                    const int row = min(m0 + wm * 64 + i * 32 + lane % 32, p.t - 1);
+                    a[i] = in ? *reinterpret_cast<const u32x4*>(p.x + static_cast<std::size_t>(row) * p.ld_x + k0 + 16 * c)
+                              : u32x4{0u, 0u, 0u, 0u};
+                }
+#pragma unroll
+                for (int q = 0; q < 2; ++q) {
+                    const int row = min(n0 + colrel[q], p.n - 1);
+                    b[q] = in ? *reinterpret_cast<const u32x4*>(p.w + static_cast<std::size_t>(row) * p.ld_w + k0 + 16 * c)
+                              : u32x4{0u, 0u, 0u, 0u};
+                }
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+#pragma unroll
+                    for (int q = 0; q < 2; ++q) tot[i][q] = mfma_i8_32(a[i], b[q], tot[i][q]);
+            }
+        }
+    }
     if constexpr (MODE == MODE_SUMS) return;
     if constexpr (MODE == MODE_WHOLE) {
         // y = (float(S) * sx[t]) * sw[n], float32 or binary16 (round to nearest even)
@@ -888,13 +921,13 @@ inline int device_cus() {
     return cus;
 }
 
-// 256 x 256 tiles when they fill the chip at least once and every offset fits 32 bits; the last partial round, when
+// 256 x 256 tiles when they fill the chip at least once, K is a multiple of 128 and every offset fits 32 bits; the last partial round, when
 // more than a quarter full and small enough, as 128 x 256 halves in a second launch.
 template <int YT>
 bool launch_s8_big(const GemmArgs& a, hipStream_t stream) {
     const std::size_t tiles_m = (a.t + 255) / 256, tiles_n = (a.n + 255) / 256;
     const int cus = device_cus();
-    if (tiles_m * tiles_n < static_cast<std::size_t>(cus)) return false;
+    if (tiles_m * tiles_n < static_cast<std::size_t>(cus) || a.k % 128 != 0) return false;
     if ((a.t + 256) * a.ld_x >= (std::size_t{1} << 31) || (a.n + 256) * a.ld_w >= (std::size_t{1} << 31)) return false;
     S8Params p{};
     p.x = static_cast<const signed char*>(a.x);

@@ -11,7 +11,7 @@ read them. What is dumped:
   ref_rmsnorm.npz rmsnorm_rows with an identity weight and eps 1e-6.
   ref_i8y.npz     the reference's AVX2 int8 path (Variant::I8_Y, kernel_i8_y: one activation scale per row, one
                   weight scale per feature), forced by packing for Isa::Avx2: its weight packing (q, one scale per
-                  feature) and gemm_packed Store, Add and SwiGLU, at the suite's odd shapes and at K multiples of 128;
+                  feature) and gemm_packed Store, Add and SwiGLU, at the suite's odd shapes and at K multiples of 16 and 128;
                   the weights are binary16 values (stored as binary16).
 `python tests/golden/make_golden.py i8y` writes ref_i8y.npz only.
 """
@@ -45,7 +45,8 @@ def write_i8y() -> None:
     rng = np.random.default_rng(20261202)
     out = {}
     # weights are binary16 values (stored as such, handed to the reference widened to float32)
-    cases = [(13, 37, 70), (29, 100, 129), (37, 128, 256), (130, 128, 512), (16, 128, 1280), (3, 128, 2560)]
+    cases = [(13, 37, 70), (29, 100, 129), (37, 128, 256), (130, 128, 512), (16, 128, 1280), (3, 128, 2560),
+             (21, 100, 208), (9, 128, 48)]
     half = lambda a: (a * 0.02).astype(np.float16)  # noqa: E731
     for i, (t, n, k) in enumerate(cases):
         x = rng.standard_normal((t, k)).astype(np.float32)

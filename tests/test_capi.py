@@ -104,9 +104,14 @@ def test_s8_family_refusals():
     assert L.sepal_hip_s8_quantize_rows(FAKE, 2, 256, FAKE + 4, FAKE, 256, FAKE, 4, 256, None) == sm.EINVAL
     assert L.sepal_hip_s8_quantize_rows(FAKE, 9, 256, None, FAKE, 256, FAKE, 4, 256, None) == sm.EINVAL
     assert L.sepal_hip_s8_quantize_rows(FAKE, 2, 256, None, FAKE, 256, FAKE, 0, 256, None) == sm.OK
-    # gemm_s8 / gemm_w8a16: K a multiple of 128, output float32 or binary16, ld_y >= N, null scales; T = 0 is a no-op
-    assert L.sepal_hip_gemm_s8(FAKE, 272, FAKE, FAKE, 272, FAKE, FAKE, 0, 64, 4, 64, 272, None) == sm.EINVAL
+    # gemm_s8 / gemm_w8a16: K a multiple of 16 / of 128, output float32 or binary16, ld_y >= N, null scales; T = 0 is a
+    # no-op
+    assert L.sepal_hip_gemm_s8(FAKE, 272, FAKE, FAKE, 272, FAKE, FAKE, 0, 64, 4, 64, 264, None) == sm.EINVAL
+    assert "multiple of 16" in _err()
+    assert L.sepal_hip_gemm_w8a16(FAKE, 272, FAKE, 272, FAKE, FAKE, 0, 64, 4, 64, 272, None) == sm.EINVAL
     assert "multiple of 128" in _err()
+    assert L.sepal_hip_gemm_q8y(FAKE, 272, FAKE, FAKE, 272, FAKE, FAKE, 0, 64, 4, 64, 264, 0, None) == sm.EINVAL
+    assert "multiple of 16" in _err()
     assert L.sepal_hip_gemm_s8(FAKE, 256, FAKE, FAKE, 256, FAKE, FAKE, 1, 64, 4, 64, 256, None) == sm.EINVAL
     assert L.sepal_hip_gemm_s8(FAKE, 256, FAKE, FAKE, 256, FAKE, FAKE, 0, 32, 4, 64, 256, None) == sm.EINVAL
     assert L.sepal_hip_gemm_s8(FAKE, 256, None, FAKE, 256, FAKE, FAKE, 0, 64, 4, 64, 256, None) == sm.EINVAL

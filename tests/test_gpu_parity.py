@@ -794,10 +794,12 @@ def test_calibration_statistics(sm):
     assert same_bits(host(amax), want_a) and same_bits(host(sums), want_s)
 
 
-@pytest.mark.parametrize("t,n,k", [(100, 200, 1024), (37, 66, 3584), (5, 40, 6144), (300, 130, 2048), (1, 8, 128)])
+@pytest.mark.parametrize("t,n,k", [(100, 200, 1024), (37, 66, 3584), (5, 40, 6144), (300, 130, 2048), (1, 8, 128),
+                                   (50, 33, 16), (13, 37, 80), (29, 100, 1040), (300, 130, 2576), (4096, 4096, 2576)])
 def test_gemm_s8_bit_exact(sm, t, n, k):
-    """y = (float(S) * sx) * sw bit for bit against the oracle (the reference test's shapes with K a multiple of 128),
-    and the binary16 result is the float32 one rounded."""
+    """y = (float(S) * sx) * sw bit for bit against the oracle: the reference test's shapes with K a multiple of 128,
+    K multiples of 16 below and above 128 (the tail after the whole 128-groups), one of them on a grid that fills the
+    chip; the binary16 result is the float32 one rounded."""
     say("gemm s8", t, n, k)
     rng = np.random.default_rng(t + n + k)
     xq, sx = sm.s8_quantize_rows(dev((rng.standard_normal((t, k)) * 3.0).astype(np.float16)))
