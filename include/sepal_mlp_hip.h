@@ -77,9 +77,11 @@ SEPAL_HIP_API int32_t sepal_hip_quantize_gate_up_s8(const void* gate, const void
  * multiplied: twice the MFMA work of a 16-bit X, results within float32 rounding of the reference's chain; the split
  * takes 4 T K bytes of the workspace. Y float32 [T, ld_y] for STORE/ADD; for SWIGLU Y is [T, ld_y] of y_type
  * (F32, BF16 or F16) with N/2 columns. K a multiple of 128; N a multiple of 128 for SWIGLU, of 16 otherwise; ld_x,
- * ld_w multiples of 16; ld_y a multiple of 4; 16-byte aligned pointers. `config` -1 picks a path by T (small-M at T <= 64);
- * 0 forces the large-M tiled path, 1 the small-M weight-streaming path, 2 the small-M path without a split of K (the
- * whole K of a column block in one block; K at most 1280).
+ * ld_w multiples of 16; ld_y a multiple of 4; 16-byte aligned pointers. `config` -1 picks a path by T (small-M at T <= 64;
+ * above, grids too small to fill the chip may split K over blocks, so a row's bits depend on T); 0 forces the large-M
+ * tiled path without a split of K (a row's bits do not depend on the batch, as the reference's), 1 the small-M
+ * weight-streaming path, 2 the small-M path without a split of K (the whole K of a column block in one block; K at
+ * most 1280).
  * Replaces launch_gemm_simt with SimtWeight::Int8Group (runner/cuda/src/gemm_simt_kernels.hpp:55-57, .cu:312-332). */
 SEPAL_HIP_API int32_t sepal_hip_gemm_w8g(const void* x, int32_t x_type, size_t ld_x, const int8_t* w, size_t ld_w, const float* s,
                            size_t ld_s, void* y, int32_t y_type, size_t ld_y, size_t t, size_t n, size_t k,

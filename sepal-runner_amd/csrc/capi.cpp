@@ -413,6 +413,7 @@ int32_t sepal_hip_gemm_w8a16(const void* x, size_t ld_x, const int8_t* wq, size_
             a.n = n;
             a.k = k;
             a.epilogue = SEPAL_HIP_STORE;
+            a.config = tr > static_cast<std::size_t>(kSmallM) ? 0 : -1;  // no K split: a row's bits do not depend on the batch
             a.scratch = ws;
             launch_gemm_w8g(a, st);
             if (!direct) launch_f32_to_f16(tmp, n, static_cast<std::uint16_t*>(y) + r0 * ld_y, ld_y, tr, n, st);

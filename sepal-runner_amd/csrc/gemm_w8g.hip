@@ -82,6 +82,12 @@ struct BigParams {
     int tiles_m, tiles_n;
     std::size_t x_bytes, w_bytes;  // extents of X and W (buffer range checks of gemm_big3)
     int id0 = 0, count = 0;        // gemm_big3: the logical 256 x 256 tiles [id0, id0 + count) of this launch
+    // gemm_big3 split-K: each block tile (BM3 x 256) is computed by `splits` blocks over consecutive ranges of whole
+    // groups; each writes its float32 partial to `part` and counts in on counters[tile]; the last to arrive adds the
+    // partials in split order and runs the epilogue
+    int splits = 1;
+    float* part = nullptr;
+    unsigned* counters = nullptr;
 };
 
 // Tile of logical id `id`: groups of GM M tiles sweep N with the same few X row panels.
@@ -314,9 +320,10 @@ __device__ __forceinline__ void wait_vm_lgkm0() {
     __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4));  // vmcnt(N) lgkmcnt(0)
 }
 
-template <int XT, int EP, int YT, int MB, int SPLIT>
+template <int XT, int EP, int YT, int MB, int SPLIT, bool SK>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) gemm_big3(const BigParams p) {
     // MB m-blocks of 32 rows per wave: tiles of BM3 = 64 MB rows (256, or 128 for the tail rows of a launch).
+    // SK: split-K (the block's K range is its split of the groups; BigParams::splits).
     // SPLIT 2: X is a float32 operand as a bf16 hi + lo pair, stored as one bf16 row of 2K values (64-value chunk j of
     // k is chunk 2j (hi) and 2j + 1 (lo)); steps 2j and 2j + 1 multiply the same weights, so p.k counts the 2K values
     // and the weight offset of step kt is kt / 2 chunks.
@@ -342,7 +349,16 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
     // MB 4: one logical 256 x 256 tile per block; MB 2 or 1: block b is part b / count (BM3 rows) of tile
     // id0 + b % count; a part wholly past T has nothing to do
     int tm, tn, m0;
-    if constexpr (MB == 4) {
+    // split-K: the splits of one block tile take consecutive logical ids, which stay on one XCD (shared L2)
+    int sub = 0, split = 0;
+    if constexpr (SK) {
+        const int logical = xcd_id(blockIdx.x, static_cast<int>(gridDim.x));
+        sub = logical / p.splits;
+        split = logical % p.splits;
+        tile_from_id(p.id0 + sub % p.count, p.tiles_m, p.tiles_n, tm, tn);
+        m0 = tm * 256 + (sub / p.count) * BM3;
+        if (m0 >= p.t) return;  // every split of this block tile returns here: none counts in
+    } else if constexpr (MB == 4) {
         tile_from_id(p.id0 + xcd_id(blockIdx.x, p.count), p.tiles_m, p.tiles_n, tm, tn);
         m0 = tm * 256;
     } else {
@@ -352,7 +368,12 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
         if (m0 >= p.t) return;
     }
     const int n0 = tn * BN;
-    const int KT = p.k / K3;
+    // this block's whole groups [g0, g1) of the k range, as steps [kbase, kbase + KT)
+    const int all_groups = p.k / K3 / SPG;
+    const int nsplit = SK ? p.splits : 1;
+    const int g0 = split * all_groups / nsplit, g1 = (split + 1) * all_groups / nsplit;
+    const int kbase = g0 * SPG;
+    const int KT = (g1 - g0) * SPG;
 
     // Loads go through buffer descriptors: 32-bit lane offsets, the step and the instruction in the scalar offset, and
     // rows past T or N read as zero (past num_records); the launcher checks that every offset fits.
@@ -405,16 +426,16 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
 #pragma unroll
         for (int i = 0; i < XLD; ++i)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(xres, (__attribute__((address_space(3))) void*)(xd + (wave + 8 * i) * 1024), 16,
-                                                     xoff, kt * K3 * 2 + i * xstride, 0, 0);
+                                                     xoff, (kbase + kt) * K3 * 2 + i * xstride, 0, 0);
     };
     const auto issue_w = [&](int kt, Regs& r) {
 #pragma unroll
         for (int i = 0; i < WLD; ++i)
-            r.w[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wres, woff, (kt / SPLIT) * K3 + i * wstride, 0));
+            r.w[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wres, woff, ((kbase + kt) / SPLIT) * K3 + i * wstride, 0));
     };
     const auto issue_scales = [&](int g) {
-        snext[0] = ssrc[0][g];
-        snext[1] = ssrc[1][g];
+        snext[0] = ssrc[0][g0 + g];
+        snext[1] = ssrc[1][g0 + g];
     };
     const auto stage_w = [&](lds_byte* wd, const Regs& r) {
 #pragma unroll
@@ -538,6 +559,60 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
     // no direct load may still be writing LDS when the block ends
     wait_vmcnt<0>();
 
+    if constexpr (SK) {
+        // This split's sums s_g P_g over its groups, value v of thread tid at part[((sub S + split) 32 MB + v) 512 + tid].
+        // The hand-off between the splits of a block tile uses no device-wide fence (on gfx950 one writes back and
+        // invalidates the L2 of the XCD): the partials are written and read with device-scope relaxed atomics, which go
+        // to the device coherence point; each thread waits for its stores to complete before the barrier, and only
+        // then does one thread count the block in. The last block to arrive adds the S partials in split order (its
+        // own read back like the others), so the result does not depend on the arrival order.
+        constexpr int NV = MB * 32;
+        float* mine = p.part + (static_cast<std::size_t>(sub) * p.splits + split) * NV * 512 + tid;
+#pragma unroll
+        for (int i = 0; i < MB; ++i)
+#pragma unroll
+            for (int q = 0; q < 2; ++q)
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    __hip_atomic_store(mine + ((i * 2 + q) * 16 + r) * 512, __fmul_rn(acc[i][q][r], e[q]), __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_s_waitcnt(0);  // also every direct load of this wave: after the barrier no load writes LDS
+        __syncthreads();
+        unsigned* last = reinterpret_cast<unsigned*>(xs0);  // the stages are free now (the LDS is full)
+        if (tid == 0)
+            *last = __hip_atomic_fetch_add(&p.counters[sub], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                            static_cast<unsigned>(p.splits - 1) ? 1u : 0u;
+        __syncthreads();
+        if (*last == 0u) return;
+        // C partials' loads in flight at a time (128 values per thread), then added in split order
+        constexpr int C = 4 / MB;
+        const float* base = p.part + static_cast<std::size_t>(sub) * p.splits * NV * 512 + tid;
+        for (int sp0 = 0; sp0 < p.splits; sp0 += C) {
+            float v[C][NV];
+#pragma unroll
+            for (int c = 0; c < C; ++c) {
+                const float* src = base + static_cast<std::size_t>(min(sp0 + c, p.splits - 1)) * NV * 512;
+#pragma unroll
+                for (int u = 0; u < NV; ++u) v[c][u] = __hip_atomic_load(src + u * 512, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+#pragma unroll
+            for (int c = 0; c < C; ++c)
+                if (sp0 + c < p.splits) {
+#pragma unroll
+                    for (int i = 0; i < MB; ++i)
+#pragma unroll
+                        for (int q = 0; q < 2; ++q)
+#pragma unroll
+                            for (int r = 0; r < 16; ++r) {
+                                const float x = v[c][(i * 2 + q) * 16 + r];
+                                acc[i][q][r] = sp0 + c == 0 ? x : __fadd_rn(acc[i][q][r], x);
+                            }
+                }
+        }
+        if (tid == 0) __hip_atomic_store(&p.counters[sub], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        e[0] = e[1] = 1.0f;  // the sums are final values (x 1 is exact)
+    }
+
 #pragma unroll
     for (int i = 0; i < MB; ++i) {
 #pragma unroll
@@ -595,7 +670,53 @@ inline int device_cus() {
 
 template <int XT, int EP, int YT, int MB, int SPLIT>
 void launch_big3(const BigParams& p, hipStream_t stream) {
-    v2::gemm_big3<XT, EP, YT, MB, SPLIT><<<dim3(p.count * (256 / (64 * MB))), dim3(512), 0, stream>>>(p);
+    if (p.splits > 1) v2::gemm_big3<XT, EP, YT, MB, SPLIT, true><<<dim3(p.count * (256 / (64 * MB)) * p.splits), dim3(512), 0, stream>>>(p);
+    else v2::gemm_big3<XT, EP, YT, MB, SPLIT, false><<<dim3(p.count * (256 / (64 * MB))), dim3(512), 0, stream>>>(p);
+}
+
+// Grids of fewer than two rounds of 256 x 256 tiles. The block tile is 64, 128 or 256 rows high (MB 1, 2, 4), and when
+// allowed the K range is split over S blocks in whole groups (split-K), by the plan of least modelled time. Every tile
+// height runs the same k order and Horner chain per output, so MB does not change a row's bits; a split does (the
+// splits' partial sums are added in float32), so callers that need a row's bits independent of the batch keep S = 1
+// (config 0).
+struct SmallGridPlan {
+    int mb = 1, splits = 1;
+};
+
+inline SmallGridPlan plan_small_grid(const GemmArgs& a, int tiles_m, int tiles_n, int groups, bool allow_split) {
+    // Fitted to times measured on MI355X (the MLP shapes, M from 65 to 4096, every plan): the time per 128-value group
+    // of a lone block of 64, 128 or 256 rows (MB 1, 2, 4); the rate at which the blocks' operand reads are served;
+    // and the split hand-off, a fixed cost plus the last block's reads of the S partials of its tile (one block's
+    // coherent reads are slow). More than 6 splits measured slower than 6 in every case.
+    constexpr double us_per_group[5] = {0.0, 1.46, 1.84, 0.0, 3.05};
+    constexpr double operand_bytes_per_us = 6.0e6, handoff_us = 8.0, tail_bytes_per_us = 8.0e4;
+    const int cus = device_cus();
+    SmallGridPlan best;
+    double best_cost = 1e30;
+    for (int mb : {4, 2, 1}) {
+        const int rows = 64 * mb;
+        const long subs = static_cast<long>((a.t + rows - 1) / rows) * tiles_n;  // block tiles with rows to do
+        const long launched = static_cast<long>(tiles_m) * (4 / mb) * tiles_n;
+        for (int sp = 1; sp <= 6 && sp <= groups; ++sp) {
+            if (sp > 1) {
+                if (!allow_split || a.scratch == nullptr) break;
+                const std::size_t part = static_cast<std::size_t>(launched) * sp * rows * 256 * sizeof(float);
+                if (launched * static_cast<long>(sizeof(unsigned)) > static_cast<long>(kCounterBytes) || part > kPartialBytes) break;
+            }
+            const long blocks = subs * sp, rounds = (blocks + cus - 1) / cus;
+            const int per_block = (groups + sp - 1) / sp;
+            const double compute = static_cast<double>(rounds) * per_block * us_per_group[mb];
+            const double operand = static_cast<double>(blocks) * per_block * 128.0 * (2.0 * rows + 256.0) / operand_bytes_per_us;
+            double cost = compute > operand ? compute : operand;
+            if (sp > 1) cost += handoff_us + static_cast<double>(sp) * rows * 256 * sizeof(float) / tail_bytes_per_us;
+            if (cost < best_cost) {
+                best_cost = cost;
+                best.mb = mb;
+                best.splits = sp;
+            }
+        }
+    }
+    return best;
 }
 
 // gemm_big3 addresses X and W with 32-bit offsets (rows up to one tile past the end included) and writes SwiGLU outputs
@@ -637,12 +758,19 @@ void launch_big(const GemmArgs& a, hipStream_t stream) {
             launch_big3<XT, EP, YT, 2, SPLIT>(q, stream);
         }
     } else if (takes && !wide) {
-        // fewer than two rounds of 256 x 256 tiles: 64 x 256 quarters of the same kernel (one m-block per wave), four
-        // times the blocks
+        // fewer than two rounds of 256 x 256 tiles: the plan's tile height and K split
         p.tiles_n = tn256;
         p.id0 = 0;
         p.count = tiles_m * tn256;
-        launch_big3<XT, EP, YT, 1, SPLIT>(p, stream);
+        const SmallGridPlan plan = plan_small_grid(a, tiles_m, tn256, static_cast<int>(a.k / 128), a.config < 0);
+        if (plan.splits > 1) {
+            p.splits = plan.splits;
+            p.counters = static_cast<unsigned*>(a.scratch);
+            p.part = reinterpret_cast<float*>(static_cast<char*>(a.scratch) + kCounterBytes);
+        }
+        if (plan.mb == 4) launch_big3<XT, EP, YT, 4, SPLIT>(p, stream);
+        else if (plan.mb == 2) launch_big3<XT, EP, YT, 2, SPLIT>(p, stream);
+        else launch_big3<XT, EP, YT, 1, SPLIT>(p, stream);
     } else if constexpr (SPLIT == 1) {
         p.tiles_n = wide ? tn256 : static_cast<int>((a.n + 127) / 128);
         if (wide) launch_big2<XT, EP, YT, 4>(p, stream);

@@ -211,7 +211,7 @@ def test_w8g_store_add(sm, case, xdt):
     x, q, s = _w8g_problem(rng, t, n, k, xdt)
     ref = orc.gemm_w8g(x, q, s)
     base = rng.standard_normal((t, n)).astype(np.float32)
-    configs = [0, 1, 2] if t <= 64 else [0]
+    configs = [0, 1, 2] if t <= 64 else [0, -1]  # -1: above 64 rows, small grids may split K
     for cfg in configs:
         if cfg == 2 and k > 1280:
             continue
@@ -236,7 +236,7 @@ def test_w8g_swiglu(sm, case, ydt):
     qo, so = host(q), host(s)
     ref = orc.gemm_w8g(x, qo, so, epilogue=orc.SWIGLU)
     tdt = {"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16}[ydt]
-    for cfg in ([0, 1] if t <= 64 else [0]):
+    for cfg in ([0, 1] if t <= 64 else [0, -1]):
         say("w8g swiglu", case, ydt, "config", cfg)
         y = sm.gemm_w8g(dev(x, torch.bfloat16), q, s, epilogue=sm.SWIGLU, y_dtype=tdt, config=cfg)
         yh = host(y.float()) if tdt != torch.bfloat16 else host(y)
@@ -246,6 +246,32 @@ def test_w8g_swiglu(sm, case, ydt):
             assert max_rel_over_rms(yh, ref) < 2e-3
         else:  # bfloat16 rounding alone is up to 2^-8: within one bf16 step of the rounded reference
             assert_within_one_bf16_step(yh, ref)
+
+
+@pytest.mark.parametrize("t", [65, 300, 896, 2048])
+def test_w8g_split_k_mlp_shapes(sm, t):
+    """Small grids at the MLP shapes (gate/up SwiGLU 19456 x 2560, down 2560 x 9728) with the default plan, which
+    splits K over blocks where it pays: every element against float64 of the dequantized weights, within the bar, and
+    the same bits on a second call (the last block adds the splits' partials in split order, whatever the order in
+    which they arrive)."""
+    say("w8g split-K", t)
+    g = torch.Generator(device="cuda").manual_seed(t)
+    for n, k, ep in ((2560, 9728, sm.STORE), (19456, 2560, sm.SWIGLU)):
+        w = (torch.randn(n, k, generator=g, device="cuda") * 0.02).half()
+        q, s = sm.quantize_group_s8(w)
+        x = torch.randn(t, k, generator=g, device="cuda").bfloat16()
+        y = sm.gemm_w8g(x, q, s, epilogue=ep)
+        y2 = sm.gemm_w8g(x, q, s, epilogue=ep)
+        assert torch.equal(y, y2), (t, n, k)
+        ref = _deq_ref(x, q, s, k)
+        if ep == sm.SWIGLU:
+            z = ref.view(t, n // 128, 2, 64)
+            gate, up = z[:, :, 0, :].reshape(t, n // 2), z[:, :, 1, :].reshape(t, n // 2)
+            ref = gate / (1.0 + torch.exp(-gate)) * up
+        err = max_rel_over_rms(host(y.float()), ref.cpu().numpy())
+        assert err < 2e-3, (t, n, k, err)
+        y0 = sm.gemm_w8g(x, q, s, epilogue=ep, config=0)
+        assert max_rel_over_rms(host(y.float()), host(y0.float()).astype(np.float64)) < 2e-3
 
 
 def test_w8g_large_path_rows_are_batch_invariant(sm):
