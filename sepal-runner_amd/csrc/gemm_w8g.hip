@@ -19,6 +19,8 @@
 //            offset does not fit 32 bits, or a SwiGLU N is not a multiple of 256): 256 x 128 or 256 x 256 tiles, K in
 //            steps of 32.
 //   small M: stream.hip (the weights streamed once, HBM-bound).
+#include <algorithm>
+
 #include "common.hpp"
 #include "gemm_kernels.hpp"
 
@@ -88,6 +90,9 @@ struct BigParams {
     int splits = 1;
     float* part = nullptr;
     unsigned* counters = nullptr;
+    // split-K launches run the live block tiles sub0 .. sub0 + nsub - 1 of the dense order: block tile s at rows
+    // (s mod sub_m) BM3 and columns (s / sub_m) 256, sub_m = ceil(T / BM3)
+    int dense = 0, sub_m = 0, sub0 = 0, nsub = 0;
 };
 
 // Tile of logical id `id`: groups of GM M tiles sweep N with the same few X row panels.
@@ -346,18 +351,19 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
 
     const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
     const int wm = wave % 2, wn = wave / 2;
-    // MB 4: one logical 256 x 256 tile per block; MB 2 or 1: block b is part b / count (BM3 rows) of tile
-    // id0 + b % count; a part wholly past T has nothing to do
+    // Split-K (the dense order): logical id -> block tile sub0 + id / S (sub-rows fastest, so consecutive ids share
+    // the weight tile) and split id mod S; the splits of one block tile take consecutive logical ids, which stay on
+    // one XCD (shared L2). Otherwise MB 4: one logical 256 x 256 tile per block; MB 2 or 1: block b is part b / count
+    // (BM3 rows) of tile id0 + b % count; a part wholly past T has nothing to do.
     int tm, tn, m0;
-    // split-K: the splits of one block tile take consecutive logical ids, which stay on one XCD (shared L2)
     int sub = 0, split = 0;
     if constexpr (SK) {
         const int logical = xcd_id(blockIdx.x, static_cast<int>(gridDim.x));
         sub = logical / p.splits;
         split = logical % p.splits;
-        tile_from_id(p.id0 + sub % p.count, p.tiles_m, p.tiles_n, tm, tn);
-        m0 = tm * 256 + (sub / p.count) * BM3;
-        if (m0 >= p.t) return;  // every split of this block tile returns here: none counts in
+        const int sg = p.sub0 + sub;
+        m0 = (sg % p.sub_m) * BM3;
+        tn = sg / p.sub_m;
     } else if constexpr (MB == 4) {
         tile_from_id(p.id0 + xcd_id(blockIdx.x, p.count), p.tiles_m, p.tiles_n, tm, tn);
         m0 = tm * 256;
@@ -670,8 +676,9 @@ inline int device_cus() {
 
 template <int XT, int EP, int YT, int MB, int SPLIT>
 void launch_big3(const BigParams& p, hipStream_t stream) {
-    if (p.splits > 1) v2::gemm_big3<XT, EP, YT, MB, SPLIT, true><<<dim3(p.count * (256 / (64 * MB)) * p.splits), dim3(512), 0, stream>>>(p);
-    else v2::gemm_big3<XT, EP, YT, MB, SPLIT, false><<<dim3(p.count * (256 / (64 * MB))), dim3(512), 0, stream>>>(p);
+    const int blocks = p.dense ? p.nsub * p.splits : p.count * (256 / (64 * MB));
+    if (p.splits > 1) v2::gemm_big3<XT, EP, YT, MB, SPLIT, true><<<dim3(blocks), dim3(512), 0, stream>>>(p);
+    else v2::gemm_big3<XT, EP, YT, MB, SPLIT, false><<<dim3(blocks), dim3(512), 0, stream>>>(p);
 }
 
 // Grids of fewer than two rounds of 256 x 256 tiles. The block tile is 64, 128 or 256 rows high (MB 1, 2, 4), and when
@@ -683,11 +690,13 @@ struct SmallGridPlan {
     int mb = 1, splits = 1;
 };
 
-inline SmallGridPlan plan_small_grid(const GemmArgs& a, int tiles_m, int tiles_n, int groups, bool allow_split) {
+inline SmallGridPlan plan_small_grid(const GemmArgs& a, int tiles_n, int groups, bool allow_split) {
     // Fitted to times measured on MI355X (the MLP shapes, M from 65 to 4096, every plan): the time per 128-value group
     // of a lone block of 64, 128 or 256 rows (MB 1, 2, 4); the rate at which the blocks' operand reads are served;
     // and the split hand-off, a fixed cost plus the last block's reads of the S partials of its tile (one block's
-    // coherent reads are slow). More than 6 splits measured slower than 6 in every case.
+    // coherent reads are slow). More than 6 splits measured slower than 6 in every case. (Splitting only the last
+    // partial round's block tiles never won under this model at the MLP shapes: those grids are bound by the operand
+    // reads, not by the idle CUs of the last round.)
     constexpr double us_per_group[5] = {0.0, 1.46, 1.84, 0.0, 3.05};
     constexpr double operand_bytes_per_us = 6.0e6, handoff_us = 8.0, tail_bytes_per_us = 8.0e4;
     const int cus = device_cus();
@@ -696,12 +705,11 @@ inline SmallGridPlan plan_small_grid(const GemmArgs& a, int tiles_m, int tiles_n
     for (int mb : {4, 2, 1}) {
         const int rows = 64 * mb;
         const long subs = static_cast<long>((a.t + rows - 1) / rows) * tiles_n;  // block tiles with rows to do
-        const long launched = static_cast<long>(tiles_m) * (4 / mb) * tiles_n;
         for (int sp = 1; sp <= 6 && sp <= groups; ++sp) {
             if (sp > 1) {
                 if (!allow_split || a.scratch == nullptr) break;
-                const std::size_t part = static_cast<std::size_t>(launched) * sp * rows * 256 * sizeof(float);
-                if (launched * static_cast<long>(sizeof(unsigned)) > static_cast<long>(kCounterBytes) || part > kPartialBytes) break;
+                const std::size_t part = static_cast<std::size_t>(subs) * sp * rows * 256 * sizeof(float);
+                if (subs * static_cast<long>(sizeof(unsigned)) > static_cast<long>(kCounterBytes) || part > kPartialBytes) break;
             }
             const long blocks = subs * sp, rounds = (blocks + cus - 1) / cus;
             const int per_block = (groups + sp - 1) / sp;
@@ -762,8 +770,13 @@ void launch_big(const GemmArgs& a, hipStream_t stream) {
         p.tiles_n = tn256;
         p.id0 = 0;
         p.count = tiles_m * tn256;
-        const SmallGridPlan plan = plan_small_grid(a, tiles_m, tn256, static_cast<int>(a.k / 128), a.config < 0);
+        const SmallGridPlan plan = plan_small_grid(a, tn256, static_cast<int>(a.k / 128), a.config < 0);
         if (plan.splits > 1) {
+            // split-K runs the live block tiles in the dense order
+            const int rows = 64 * plan.mb;
+            p.dense = 1;
+            p.sub_m = static_cast<int>((a.t + rows - 1) / rows);
+            p.nsub = p.sub_m * tn256;
             p.splits = plan.splits;
             p.counters = static_cast<unsigned*>(a.scratch);
             p.part = reinterpret_cast<float*>(static_cast<char*>(a.scratch) + kCounterBytes);
