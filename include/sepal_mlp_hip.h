@@ -156,6 +156,14 @@ SEPAL_HIP_API int32_t sepal_hip_gemm_q8y(const int8_t* xq, size_t ld_x, const fl
                                          const float* ws, void* y, int32_t y_type, size_t ld_y, size_t t, size_t n, size_t k,
                                          int32_t epilogue, void* stream);
 
+/* 1 when sepal_hip_gemm_s8 / sepal_hip_gemm_w8a16 take these dimensions and strides (pointer alignment and the output
+ * type are the caller's), else 0: N non-zero, K a non-zero multiple of 16 (gemm_s8) or 128 (gemm_w8a16), ld_x and ld_w
+ * multiples of 16 and at least K, ld_y at least N. Replace gemm_s8_supports / gemm_w8a16_supports
+ * (runner/cuda/src/gemm_s8_kernels.hpp:59-65), which the engine asks before it routes a matrix to the int8 multiplies
+ * (cuda_engine.cpp:806). */
+SEPAL_HIP_API int32_t sepal_hip_gemm_s8_supports(size_t n, size_t k, size_t ld_x, size_t ld_w, size_t ld_y);
+SEPAL_HIP_API int32_t sepal_hip_gemm_w8a16_supports(size_t n, size_t k, size_t ld_x, size_t ld_w, size_t ld_y);
+
 /* binary16 activations times int8 weights with per-channel scales: Y[t, n] = sw[n] * sum over K of x[t,k] * wq[n,k],
  * the weights widened exactly and multiplied with float32 accumulation (the gpu-w8g kernels with the channel's scale
  * in every group: within float32 rounding of one accumulator times sw). Y float32 or binary16 [T, ld_y] (binary16 is

@@ -297,6 +297,12 @@ int32_t sepal_hip_channel_stats(const void* x, size_t ld_x, size_t rows, size_t 
 }
 
 namespace {
+// The shape rules of sepal_hip_gemm_s8 (k_step 16) and sepal_hip_gemm_w8a16 (k_step 128).
+bool s8_family_shape_ok(size_t n, size_t k, size_t ld_x, size_t ld_w, size_t ld_y, size_t k_step) {
+    return n != 0 && k != 0 && k % k_step == 0 && ld_x >= k && ld_w >= k && ld_x % 16 == 0 && ld_w % 16 == 0 && ld_y >= n &&
+           n < 0x7FFFFFFFu;
+}
+
 void check_s8_family(const char* who, const void* x, size_t ld_x, const void* w, size_t ld_w, const float* sw, const void* y,
                      int32_t y_type, size_t ld_y, size_t n, size_t k, size_t k_step) {
     const std::string w_ = who;
@@ -310,6 +316,14 @@ void check_s8_family(const char* who, const void* x, size_t ld_x, const void* w,
     require(aligned16(x) && aligned16(w) && aligned8(y), w_ + ": X and W must be 16-byte aligned, Y 8-byte aligned");
 }
 } // namespace
+
+int32_t sepal_hip_gemm_s8_supports(size_t n, size_t k, size_t ld_x, size_t ld_w, size_t ld_y) {
+    return s8_family_shape_ok(n, k, ld_x, ld_w, ld_y, 16) ? 1 : 0;
+}
+
+int32_t sepal_hip_gemm_w8a16_supports(size_t n, size_t k, size_t ld_x, size_t ld_w, size_t ld_y) {
+    return s8_family_shape_ok(n, k, ld_x, ld_w, ld_y, 128) ? 1 : 0;
+}
 
 int32_t sepal_hip_gemm_s8(const int8_t* xq, size_t ld_x, const float* sx, const int8_t* wq, size_t ld_w, const float* sw,
                           void* y, int32_t y_type, size_t ld_y, size_t t, size_t n, size_t k, void* stream) {

@@ -49,6 +49,8 @@ def library() -> C.CDLL:
         L.sepal_hip_quantize_gate_up_s8.argtypes = [vp, vp, i32, sz, vp, sz, vp, sz, sz, sz, i32, vp]
         L.sepal_hip_gemm_w8g.argtypes = [vp, i32, sz, vp, sz, vp, sz, vp, i32, sz, sz, sz, sz, i32, i32, vp]
         L.sepal_hip_gemm_w8g_supports.argtypes = [i32, sz, sz, sz, sz, sz, i32]
+        L.sepal_hip_gemm_s8_supports.argtypes = [sz, sz, sz, sz, sz]
+        L.sepal_hip_gemm_w8a16_supports.argtypes = [sz, sz, sz, sz, sz]
         L.sepal_hip_quantize_rows_s8.argtypes = [vp, i32, sz, vp, sz, vp, sz, sz, sz, sz, vp]
         L.sepal_hip_gemm_q8.argtypes = [vp, sz, vp, sz, sz, vp, sz, vp, sz, vp, i32, sz, sz, sz, sz, i32, i32, vp]
         L.sepal_hip_q8_group_sums.argtypes = [vp, sz, vp, sz, vp, sz, sz, sz, vp]
@@ -79,6 +81,8 @@ def library() -> C.CDLL:
                      "sepal_hip_column_absmax", "sepal_hip_channel_stats"):
             getattr(L, name).restype = i32
         L.sepal_hip_gemm_w8g_supports.restype = i32
+        L.sepal_hip_gemm_s8_supports.restype = i32
+        L.sepal_hip_gemm_w8a16_supports.restype = i32
         _lib = L
     return _lib
 
@@ -158,6 +162,14 @@ def quantize_gate_up_s8(gate, up, rule: int = RULE_DIVIDE, stream=None):
 
 def gemm_w8g_supports(x_type: int, n: int, k: int, ld_x: int, ld_w: int, ld_y: int, epilogue: int) -> bool:
     return bool(library().sepal_hip_gemm_w8g_supports(x_type, n, k, ld_x, ld_w, ld_y, epilogue))
+
+
+def gemm_s8_supports(n: int, k: int, ld_x: int, ld_w: int, ld_y: int) -> bool:
+    return bool(library().sepal_hip_gemm_s8_supports(n, k, ld_x, ld_w, ld_y))
+
+
+def gemm_w8a16_supports(n: int, k: int, ld_x: int, ld_w: int, ld_y: int) -> bool:
+    return bool(library().sepal_hip_gemm_w8a16_supports(n, k, ld_x, ld_w, ld_y))
 
 
 def gemm_w8g(x, w, s, y=None, epilogue: int = STORE, y_dtype=None, config: int = -1, stream=None):

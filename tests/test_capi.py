@@ -52,6 +52,16 @@ def test_supports_mirrors_reference_rules():
     # float32 X, the reference's operand type (launch_gemm_simt(const float* x, ...))
     assert sm.gemm_w8g_supports(sm.F32, 19456, 2560, 2560, 2560, 9728, sm.SWIGLU)
     assert not sm.gemm_w8g_supports(9, 256, 256, 256, 256, 256, sm.STORE)
+    # gemm_s8_supports / gemm_w8a16_supports (runner/cuda/src/gemm_s8_kernels.hpp:59-65): K a multiple of 16 / 128
+    assert sm.gemm_s8_supports(2560, 9728, 9728, 9728, 2560)
+    assert sm.gemm_s8_supports(33, 80, 80, 80, 33)
+    assert not sm.gemm_s8_supports(64, 72, 80, 80, 64)     # K not a multiple of 16
+    assert not sm.gemm_s8_supports(64, 80, 72, 80, 64)     # ld_x not a multiple of 16
+    assert not sm.gemm_s8_supports(64, 96, 80, 96, 64)     # ld_x below K
+    assert not sm.gemm_s8_supports(64, 80, 80, 80, 63)     # ld_y below N
+    assert not sm.gemm_s8_supports(0, 80, 80, 80, 0)
+    assert sm.gemm_w8a16_supports(19456, 2560, 2560, 2560, 19456)
+    assert not sm.gemm_w8a16_supports(64, 80, 80, 80, 64)  # K not a multiple of 128 here
 
 
 def test_q8_and_quantizer_refusals():
