@@ -795,10 +795,14 @@ void launch_big(const GemmArgs& a, hipStream_t stream) {
 }
 
 // Whether a problem takes the small-M (weight-streaming) kernels: they write float32 (or SwiGLU outputs); a binary16
-// Store always takes the large-M kernels.
+// Store always takes the large-M kernels. By default they take T <= 32 with N < 8192: measured on the model's weight
+// shapes, the large-M kernels' small-grid plan (64-row blocks, K split) is faster above 32 rows (the streaming kernels
+// double their time from 33 rows, at 64-row tiles) and at any T for N >= 8192 (gate/up 19456 x 2560: 20 against
+// 24 us at T = 1), and the streaming kernels are faster for the narrow, long-K down shape (2560 x 9728: 22.5 against
+// 29 us at T <= 16).
 inline bool small_path(const GemmArgs& a) {
     const bool eligible = a.y_type == SEPAL_HIP_F32 || a.epilogue == SEPAL_HIP_SWIGLU;
-    return eligible && (a.config == 1 || (a.config < 0 && a.t <= kSmallM));
+    return eligible && (a.config == 1 || (a.config < 0 && a.t <= 32 && a.n < 8192));
 }
 
 template <int XT, int EP, int YT, int SPLIT>

@@ -14,6 +14,7 @@
 //     last block of the span to arrive (an atomic counter, reset by that block) adds the splits in order and runs the
 //     epilogue, so the result does not depend on which block finishes last. With one split the chain is whole and
 //     the q8 result equals cpu-q8 bit for bit.
+#include <algorithm>
 #include <cstdlib>
 #include <mutex>
 #include <vector>
@@ -371,6 +372,12 @@ void launch_mt(const GemmArgs& a, hipStream_t stream) {
     const int lds_cap = ((64 << 10) / (16 * MT) - 16) / (128 * K::xbytes);  // as pick_gps
     const int resident = resident_blocks(reinterpret_cast<const void*>(kernel), lds_of(max(1, min(kGMax, min(groups, lds_cap)))));
     p.gps = pick_gps(p.spans, groups, MT, K::xbytes, a.force_splits, resident);
+    {
+        // no more splits than the workspace's partial zone holds (wide N at 64 rows: 5 MB per split at N = 19456)
+        const std::size_t per_split = rows * static_cast<std::size_t>(p.spans) * kSpan * sizeof(float);
+        const int max_splits = static_cast<int>(std::max<std::size_t>(1, kPartialBytes / per_split));
+        p.gps = max(p.gps, (groups + max_splits - 1) / max_splits);
+    }
     p.splits = (groups + p.gps - 1) / p.gps;
     require(a.force_splits != 1 || p.gps <= kGMax, "small-M multiply without a K split (config 2) takes K <= 1280");
     const std::size_t lds = lds_of(p.gps);

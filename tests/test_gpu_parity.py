@@ -211,7 +211,7 @@ def test_w8g_store_add(sm, case, xdt):
     x, q, s = _w8g_problem(rng, t, n, k, xdt)
     ref = orc.gemm_w8g(x, q, s)
     base = rng.standard_normal((t, n)).astype(np.float32)
-    configs = [0, 1, 2] if t <= 64 else [0, -1]  # -1: above 64 rows, small grids may split K
+    configs = [0, 1, 2, -1] if t <= 64 else [0, -1]  # -1: the default routing (small grids may split K)
     for cfg in configs:
         if cfg == 2 and k > 1280:
             continue
@@ -236,7 +236,7 @@ def test_w8g_swiglu(sm, case, ydt):
     qo, so = host(q), host(s)
     ref = orc.gemm_w8g(x, qo, so, epilogue=orc.SWIGLU)
     tdt = {"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16}[ydt]
-    for cfg in ([0, 1] if t <= 64 else [0, -1]):
+    for cfg in ([0, 1, -1] if t <= 64 else [0, -1]):
         say("w8g swiglu", case, ydt, "config", cfg)
         y = sm.gemm_w8g(dev(x, torch.bfloat16), q, s, epilogue=sm.SWIGLU, y_dtype=tdt, config=cfg)
         yh = host(y.float()) if tdt != torch.bfloat16 else host(y)
@@ -272,6 +272,28 @@ def test_w8g_split_k_mlp_shapes(sm, t):
         assert err < 2e-3, (t, n, k, err)
         y0 = sm.gemm_w8g(x, q, s, epilogue=ep, config=0)
         assert max_rel_over_rms(host(y.float()), host(y0.float()).astype(np.float64)) < 2e-3
+
+
+@pytest.mark.parametrize("t", [33, 64])
+def test_small_m_wide_n_split_fits_the_workspace(sm, t):
+    """The small-M path at the gate/up shape (N 19456, K 2560) with 33 and 64 rows: its K split is bounded by the
+    workspace's partial zone (each split's partials take T x N floats), so the default plan runs; the results agree with
+    the large-M path (w8g within the bar; q8 per token within the bar of the split chains)."""
+    say("small-M wide N", t)
+    g = torch.Generator(device="cuda").manual_seed(64 + t)
+    n, k = 19456, 2560
+    w = (torch.randn(n, k, generator=g, device="cuda") * 0.02).half()
+    x = torch.randn(t, k, generator=g, device="cuda")
+    q, s = sm.quantize_group_s8(w)
+    xb = x.bfloat16()
+    y = sm.gemm_w8g(xb, q, s, epilogue=sm.SWIGLU)
+    y0 = sm.gemm_w8g(xb, q, s, epilogue=sm.SWIGLU, config=0)
+    assert max_rel_over_rms(host(y), host(y0).astype(np.float64)) < 2e-3
+    qq, qs = sm.quantize_group_s8(w, rule=sm.RULE_RECIPROCAL)
+    xq, xs = sm.quantize_rows_s8(x, block=k)
+    z = sm.gemm_q8(xq, xs, qq, qs, epilogue=sm.SWIGLU, act_block=k)
+    z0 = sm.gemm_q8(xq, xs, qq, qs, epilogue=sm.SWIGLU, act_block=k, config=0)
+    assert max_rel_over_rms(host(z), host(z0).astype(np.float64)) < 2e-3
 
 
 def test_w8g_large_path_rows_are_batch_invariant(sm):
