@@ -107,9 +107,11 @@ SEPAL_HIP_API int32_t sepal_hip_quantize_rows_s8(const void* x, int32_t x_type, 
  * act_block = 128 (cpu-q8 I8_Z): y = f_0 * (ws_0 * xs_0), then y = fma(f_b, ws_b * xs_b, y), f_b = float(S_b), so the
  * large-M path reproduces cpu-q8 bit for bit. act_block = K (one scale per token): y = (f_0 * ws_0, then
  * fma(f_b, ws_b, y)) * xs. Epilogues STORE / ADD / SWIGLU (silu with the cpu-q8 exp polynomial); Y float32
- * [T, ld_y], or y_type for SWIGLU. K a multiple of 128; strides multiples of 16; 16-byte aligned pointers. `config` as
- * sepal_hip_gemm_w8g; the small-M path splits K across blocks when N is narrow, which keeps the sums exact but adds
- * the splits' partial chains (within tolerance, not bit for bit); config 2 keeps the chain whole (bit for bit).
+ * [T, ld_y], or y_type for SWIGLU. K a multiple of 128; strides multiples of 16; 16-byte aligned pointers. `config`
+ * -1 takes the small-M path up to 64 rows (above 32 rows only for N < 8192), 0 the large-M path, 1 the small-M path,
+ * 2 the small-M path with the chain whole; the small-M path splits K across blocks when N is narrow, which keeps the
+ * sums exact but adds the splits' partial chains (within tolerance, not bit for bit); config 2 keeps the chain whole
+ * (bit for bit).
  * Replaces kernel_i8_z + finish_tile (runner/src/cpu/gemm_kernels_avx512.cpp:67-115, gemm.cpp:417-447, 545-569)
  * with per-group scales (the per-channel launch_gemm_s8 is sepal_hip_gemm_s8). */
 SEPAL_HIP_API int32_t sepal_hip_gemm_q8(const int8_t* xq, size_t ld_x, const float* xs, size_t ld_xs, size_t act_block,

@@ -464,7 +464,7 @@ int32_t sepal_hip_gemm_q8_swiglu_quantize(const int8_t* xq, size_t ld_x, const f
         a.t = t;
         a.n = n;
         a.k = k;
-        const bool large = config == 0 || (config < 0 && t > kSmallM);
+        const bool large = config == 0 || (config < 0 && !q8_streams(t, n));
         if (large) {
             a.y = hq;
             a.ld_y = ld_hq;
@@ -637,7 +637,7 @@ StackZones stack_zones(int kind, std::size_t t, std::size_t hidden, std::size_t 
     // general: H [t, inter] (binary16 for w8g; float32 for kind 2, and for q8 unless the gate/up epilogue quantizes
     // it); q8 also the int8 layer input and int8 H with their scales; kind 2 the hi + lo pairs of H for the down
     // multiply
-    z.fused_h = kind == 1 && z.ab_i == 128 && t > kSmallM;
+    z.fused_h = kind == 1 && z.ab_i == 128 && !q8_streams(t, 2 * inter);
     const std::size_t h_bytes = kind == 0 ? t * inter * 2 : (z.fused_h ? 0 : t * inter * 4);
     z.off_qx = z.off_h + up256(h_bytes);
     z.off_sx = z.off_qx + (kind == 1 ? up256(t * hidden) : 0);

@@ -8,6 +8,11 @@ namespace sepal::hip {
 // Rows at or below which the multiplies take the weight-streaming small-M path.
 inline constexpr std::size_t kSmallM = 64;
 
+// Default routing of the q8 multiply (config -1): the small-M (streaming) kernels up to kSmallM rows, except above 32
+// rows with N >= 8192, where the large-M kernels are faster (gate/up 19456 x 2560 at T = 40-64: 28-30 against 41-43 us
+// per token, 35-37 against 43-44 per 128; 12288 x 2560: 29-33 against 35) and also bit-exact to cpu-q8.
+inline bool q8_streams(std::size_t t, std::size_t n) { return t <= kSmallM && (t <= 32 || n < 8192); }
+
 struct GemmArgs {
     const void* x = nullptr;
     int x_type = SEPAL_HIP_BF16;

@@ -875,7 +875,7 @@ void launch_big(const GemmArgs& a, hipStream_t stream) {
 
 template <int EP, int YT, bool PT>
 void dispatch_path(const GemmArgs& a, hipStream_t stream) {
-    const bool small = a.config == 1 || (a.config < 0 && a.t <= kSmallM);
+    const bool small = a.config == 1 || (a.config < 0 && q8_streams(a.t, a.n));
     if (small) launch_stream_q8(a, stream);
     else launch_big<EP, YT, PT, MODE_CHAIN>(a, stream);
 }
