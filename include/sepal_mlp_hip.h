@@ -77,9 +77,10 @@ SEPAL_HIP_API int32_t sepal_hip_quantize_gate_up_s8(const void* gate, const void
  * multiplied: twice the MFMA work of a 16-bit X, results within float32 rounding of the reference's chain; the split
  * takes 4 T K bytes of the workspace. Y float32 [T, ld_y] for STORE/ADD; for SWIGLU Y is [T, ld_y] of y_type
  * (F32, BF16 or F16) with N/2 columns. K a multiple of 128; N a multiple of 128 for SWIGLU, of 16 otherwise; ld_x,
- * ld_w multiples of 16; ld_y a multiple of 4; 16-byte aligned pointers. `config` -1 picks a path by T and N (small-M at
- * T <= 32 with N < 8192; on the large-M path grids too small to fill the chip may split K over blocks; a row's bits
- * then depend on T); 0 forces the large-M
+ * ld_w multiples of 16; ld_y a multiple of 4; 16-byte aligned pointers. `config` -1 picks a path by T and N (at
+ * T <= 16 with a 16-bit X the M <= 16 stack's pass kernels where the shape fits them; small-M streaming at T <= 32 with
+ * N < 8192; on the large-M path grids too small to fill the chip may split K over blocks; a row's bits then depend on
+ * T); 0 forces the large-M
  * tiled path without a split of K (a row's bits do not depend on the batch, as the reference's), 1 the small-M
  * weight-streaming path, 2 the small-M path without a split of K (the whole K of a column block in one block; K at
  * most 1280).

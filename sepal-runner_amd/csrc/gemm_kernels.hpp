@@ -101,6 +101,15 @@ struct SmallStackPlan {
     int units_per_block;  // (K-part, column tile) units per block of the down pass
 };
 bool small_stack_plan(std::size_t t, std::size_t hidden, std::size_t inter, SmallStackPlan& plan);
+// One w8g multiply at T <= 16 on the stack's pass kernels: SwiGLU straight to Y, Store / Add through K-parts in the
+// workspace's partial zone and a parts sum. small_gemm_plan returns false for shapes the pass kernels do not take.
+struct SmallGemmPlan {
+    int parts;      // K-parts (1 for SwiGLU)
+    int per_block;  // weight tiles (SwiGLU) or (K-part, column tile) units per block
+    std::size_t lds;
+};
+bool small_gemm_plan(const GemmArgs& a, SmallGemmPlan& plan);
+void launch_small_gemm_w8g(const GemmArgs& a, const SmallGemmPlan& plan, hipStream_t stream);
 // x bf16 [t, hidden] -> h binary16 [t, inter] -> part float32 [parts][t][hidden] -> y float32 [t, hidden] and, when
 // xn is set, xn bf16 [t, hidden] = RMSNorm(y) (cpu-q8 order, identity weight).
 void launch_small_layer(const SmallStackPlan& plan, std::size_t t, std::size_t hidden, std::size_t inter, const void* x,

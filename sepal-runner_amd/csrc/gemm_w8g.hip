@@ -807,6 +807,14 @@ inline bool small_path(const GemmArgs& a) {
 
 template <int XT, int EP, int YT, int SPLIT>
 void dispatch_path(const GemmArgs& a, hipStream_t stream) {
+    if constexpr (SPLIT == 1) {
+        // T <= 16 by default: the M <= 16 stack's pass kernels where they take the shape
+        SmallGemmPlan plan;
+        if (a.config < 0 && a.t <= 16 && small_gemm_plan(a, plan)) {
+            launch_small_gemm_w8g(a, plan, stream);
+            return;
+        }
+    }
     if (SPLIT == 1 && small_path(a)) launch_stream_w8g(a, stream);
     else launch_big<XT, EP, YT, SPLIT>(a, stream);
 }

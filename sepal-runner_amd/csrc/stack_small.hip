@@ -527,6 +527,40 @@ __global__ void __launch_bounds__(1024) finish_kernel(const float* __restrict__ 
 }
 
 
+// y[r, c] = (or +=) the sum of part[q][r][c] over the P parts, in part order (the single-call form of the pass kernels'
+// K-parts: Store or Add, any row stride of y).
+template <int P, bool ADD>
+__global__ void __launch_bounds__(256) parts_sum_kernel(const float* __restrict__ part, int t, int n, float* __restrict__ y,
+                                                        std::size_t ld_y) {
+    const int per_row = n / 4;
+    const int total = t * per_row;
+    for (int id = blockIdx.x * 256 + threadIdx.x; id < total; id += gridDim.x * 256) {
+        const int r = id / per_row, c = 4 * (id % per_row);
+        float4 v[P];
+#pragma unroll
+        for (int q = 0; q < P; ++q) v[q] = *reinterpret_cast<const float4*>(part + (static_cast<std::size_t>(q) * t + r) * n + c);
+        float4 a = v[0];
+#pragma unroll
+        for (int q = 1; q < P; ++q) {
+            a.x = __fadd_rn(a.x, v[q].x);
+            a.y = __fadd_rn(a.y, v[q].y);
+            a.z = __fadd_rn(a.z, v[q].z);
+            a.w = __fadd_rn(a.w, v[q].w);
+        }
+        float* dst = y + static_cast<std::size_t>(r) * ld_y + c;
+        if constexpr (ADD) {
+            dst[0] = __fadd_rn(dst[0], a.x);
+            dst[1] = __fadd_rn(dst[1], a.y);
+            dst[2] = __fadd_rn(dst[2], a.z);
+            dst[3] = __fadd_rn(dst[3], a.w);
+        } else {
+            dst[0] = a.x;
+            dst[1] = a.y;
+            dst[2] = a.z;
+            dst[3] = a.w;
+        }
+    }
+}
 
 } // namespace stack
 } // namespace sepal::hip
@@ -738,6 +772,128 @@ void launch_small_layer_q8(const SmallStackPlan& plan, std::size_t t, std::size_
     launch_finish(plan.parts, t, hidden, part, y, xn, eps, xq_next, xs_next, per_token ? static_cast<int>(hidden) : 128,
                   stream);
     check_launch("small-M q8 stack finish launch");
+}
+
+
+// ---- one multiply at M <= 16 on the pass kernels (sepal_hip_gemm_w8g's default for T <= 16) -------------------------
+
+namespace {
+
+template <int P = 1>
+void launch_parts_sum(int parts, bool add, std::size_t t, std::size_t n, const float* part, float* y, std::size_t ld_y,
+                      hipStream_t stream) {
+    if constexpr (P < stack::kFinishParts) {
+        if (parts != P) {
+            launch_parts_sum<P + 1>(parts, add, t, n, part, y, ld_y, stream);
+            return;
+        }
+    }
+    if (parts != P) throw LaunchError("small-M multiply: K-part count beyond the parts sum");
+    const int grid = static_cast<int>(std::min<std::size_t>((t * n / 4 + 255) / 256, 1024));
+    if (add) stack::parts_sum_kernel<P, true><<<grid, 256, 0, stream>>>(part, static_cast<int>(t), static_cast<int>(n), y, ld_y);
+    else stack::parts_sum_kernel<P, false><<<grid, 256, 0, stream>>>(part, static_cast<int>(t), static_cast<int>(n), y, ld_y);
+}
+
+template <int XT, bool SWIGLU, int YT>
+void launch_pass(const stack::PassParams& p, std::size_t lds, hipStream_t stream) {
+    const auto kernel = stack::pass_kernel<XT, SWIGLU, YT>;
+    static std::size_t raised = 0;
+    raise_lds(kernel, lds, raised);
+    kernel<<<dim3(p.parts * p.blocks_per_part), dim3(stack::kThreads), lds, stream>>>(p);
+    check_launch("small-M multiply pass launch");
+}
+
+} // namespace
+
+bool small_gemm_plan(const GemmArgs& a, SmallGemmPlan& plan) {
+    constexpr std::size_t kLds = 160u << 10;
+    constexpr int kMaxPairs = stack::kWorkers * stack::kPairs;
+    constexpr std::size_t kMaxK = stack::kXChunks * stack::kThreads * 16 / (16 * 2);
+    if (a.t == 0 || a.t > 16 || (a.x_type != SEPAL_HIP_BF16 && a.x_type != SEPAL_HIP_F16) || a.k % 128 != 0) return false;
+    const int g = device_cus();
+    const int groups = static_cast<int>(a.k / 128);
+    if (a.epilogue == SEPAL_HIP_SWIGLU) {
+        // whole tiles (8 features: 8 gate and 8 up rows) over the full K, tiles dealt to one block per CU
+        if (a.n % 128 != 0 || groups < 4 || a.k > kMaxK || pass_lds(2 * a.k) > kLds) return false;
+        const int tiles = static_cast<int>(a.n / 16);
+        const int per = (tiles + g - 1) / g;
+        if (per > stack::kWaves || per * groups > kMaxPairs) return false;
+        plan.parts = 1;
+        plan.per_block = per;
+        plan.lds = pass_lds(2 * a.k);
+        return true;
+    }
+    if (a.y_type != SEPAL_HIP_F32 || a.n % 16 != 0) return false;
+    // (K-part, 16-column tile) units: the fewest pairs per block (plus the parts sum's reads) within one block per CU
+    const int ntile = static_cast<int>(a.n / 16);
+    int best_kp = 0, best_pb = 0, best_cost = 0;
+    for (int kp = 1; kp <= stack::kFinishParts && groups / kp >= 4; ++kp) {
+        const int gpt = (groups + kp - 1) / kp;
+        if (static_cast<std::size_t>(gpt) * 128 > kMaxK || pass_lds(static_cast<std::size_t>(gpt) * 256) > kLds) continue;
+        if (static_cast<std::size_t>(kp) * a.t * a.n * sizeof(float) > kPartialBytes) break;
+        for (int pb = 1; pb <= ntile; ++pb) {
+            const int blocks = kp * ((ntile + pb - 1) / pb);
+            if (blocks > g) continue;
+            if (pb * gpt > kMaxPairs || pb > stack::kWaves) break;
+            const int cost = pb * gpt + 2 * kp;
+            if (best_kp == 0 || cost < best_cost) {
+                best_kp = kp;
+                best_pb = pb;
+                best_cost = cost;
+            }
+            break;
+        }
+    }
+    if (best_kp == 0) return false;
+    plan.parts = best_kp;
+    plan.per_block = best_pb;
+    plan.lds = pass_lds(static_cast<std::size_t>((groups + best_kp - 1) / best_kp) * 256);
+    return true;
+}
+
+void launch_small_gemm_w8g(const GemmArgs& a, const SmallGemmPlan& plan, hipStream_t stream) {
+    using namespace stack;
+    PassParams p{};
+    p.x = static_cast<const unsigned short*>(a.x);
+    p.ld_x = a.ld_x;
+    p.w = reinterpret_cast<const signed char*>(a.w);
+    p.ld_w = a.ld_w;
+    p.s = a.s;
+    p.ld_s = a.ld_s;
+    p.t = static_cast<int>(a.t);
+    p.n = static_cast<int>(a.n);
+    p.k = static_cast<int>(a.k);
+    p.parts = plan.parts;
+    p.per_block = plan.per_block;
+    if (a.epilogue == SEPAL_HIP_SWIGLU) {
+        p.y = a.y;
+        p.ld_y = a.ld_y;
+        p.tiles = static_cast<int>(a.n / 16);
+        p.blocks_per_part = (p.tiles + p.per_block - 1) / p.per_block;
+        const bool bf = a.x_type == SEPAL_HIP_BF16;
+        switch (a.y_type) {
+        case SEPAL_HIP_F32:
+            bf ? launch_pass<SEPAL_HIP_BF16, true, SEPAL_HIP_F32>(p, plan.lds, stream) : launch_pass<SEPAL_HIP_F16, true, SEPAL_HIP_F32>(p, plan.lds, stream);
+            break;
+        case SEPAL_HIP_BF16:
+            bf ? launch_pass<SEPAL_HIP_BF16, true, SEPAL_HIP_BF16>(p, plan.lds, stream) : launch_pass<SEPAL_HIP_F16, true, SEPAL_HIP_BF16>(p, plan.lds, stream);
+            break;
+        default:
+            bf ? launch_pass<SEPAL_HIP_BF16, true, SEPAL_HIP_F16>(p, plan.lds, stream) : launch_pass<SEPAL_HIP_F16, true, SEPAL_HIP_F16>(p, plan.lds, stream);
+            break;
+        }
+        return;
+    }
+    if (a.scratch == nullptr) throw LaunchError("small-M multiply: the K-parts need the workspace");
+    float* part = reinterpret_cast<float*>(static_cast<char*>(a.scratch) + kCounterBytes);
+    p.y = part;
+    p.ld_y = a.n;
+    p.tiles = static_cast<int>(a.n / 16);
+    p.blocks_per_part = (p.tiles + p.per_block - 1) / p.per_block;
+    if (a.x_type == SEPAL_HIP_BF16) launch_pass<SEPAL_HIP_BF16, false, SEPAL_HIP_F32>(p, plan.lds, stream);
+    else launch_pass<SEPAL_HIP_F16, false, SEPAL_HIP_F32>(p, plan.lds, stream);
+    launch_parts_sum(plan.parts, a.epilogue == SEPAL_HIP_ADD, a.t, a.n, part, static_cast<float*>(a.y), a.ld_y, stream);
+    check_launch("small-M multiply parts sum launch");
 }
 
 } // namespace sepal::hip

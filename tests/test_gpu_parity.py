@@ -274,6 +274,40 @@ def test_w8g_split_k_mlp_shapes(sm, t):
         assert max_rel_over_rms(host(y.float()), host(y0.float()).astype(np.float64)) < 2e-3
 
 
+@pytest.mark.parametrize("t", [1, 7, 16])
+@pytest.mark.parametrize("xdt", ["bf16", "f16"])
+def test_w8g_single_call_pass_kernels(sm, t, xdt):
+    """T <= 16 at the default config runs one multiply on the M <= 16 stack's pass kernels: SwiGLU straight to Y (three
+    output types), Store and Add through K-parts and an in-order parts sum, Y with a row stride wider than N. Every
+    element against float64 of the dequantized weights within the bar; the same bits on a second call."""
+    say("w8g single-call pass kernels", t, xdt)
+    dt = torch.bfloat16 if xdt == "bf16" else torch.float16
+    g = torch.Generator(device="cuda").manual_seed(300 + t)
+    for n, k, ep in ((19456, 2560, sm.SWIGLU), (2560, 9728, sm.STORE), (384, 640, sm.ADD), (1024, 4096, sm.STORE)):
+        w = (torch.randn(n, k, generator=g, device="cuda") * 0.02).half()
+        q, s = sm.quantize_group_s8(w)
+        x = torch.randn(t, k, generator=g, device="cuda").to(dt)
+        ref = _deq_ref(x, q, s, k)
+        if ep == sm.SWIGLU:
+            z = ref.view(t, n // 128, 2, 64)
+            gate, up = z[:, :, 0, :].reshape(t, n // 2), z[:, :, 1, :].reshape(t, n // 2)
+            ref = gate / (1.0 + torch.exp(-gate)) * up
+            for ydt in (torch.float32, torch.bfloat16, torch.float16):
+                y = sm.gemm_w8g(x, q, s, epilogue=ep, y_dtype=ydt)
+                bar = 2e-3 if ydt != torch.bfloat16 else 8e-3  # bf16 output rounding alone is up to 2^-8
+                assert max_rel_over_rms(host(y.float()), ref.cpu().numpy()) < bar, (n, k, ydt)
+            continue
+        base = torch.randn(t, n + 16, generator=g, device="cuda")
+        yv = base.clone()[:, :n]
+        if ep == sm.ADD:
+            ref = ref + base[:, :n].double()
+        sm.gemm_w8g(x, q, s, y=yv, epilogue=ep)
+        assert max_rel_over_rms(host(yv), ref.cpu().numpy()) < 2e-3, (n, k, ep)
+        y2 = base.clone()[:, :n]
+        sm.gemm_w8g(x, q, s, y=y2, epilogue=ep)
+        assert torch.equal(yv, y2)
+
+
 @pytest.mark.parametrize("t", [33, 64])
 def test_small_m_wide_n_split_fits_the_workspace(sm, t):
     """The small-M path at the gate/up shape (N 19456, K 2560) with 33 and 64 rows: its K split is bounded by the
