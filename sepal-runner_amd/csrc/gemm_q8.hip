@@ -875,6 +875,14 @@ void launch_big(const GemmArgs& a, hipStream_t stream) {
 
 template <int EP, int YT, bool PT>
 void dispatch_path(const GemmArgs& a, hipStream_t stream) {
+    if constexpr (EP == SEPAL_HIP_SWIGLU && YT == SEPAL_HIP_F32) {
+        // T <= 16 by default: the q8 stack's gate/up pass where it takes the shape
+        SmallGemmPlan plan;
+        if (a.config < 0 && a.t <= 16 && small_gemm_plan_q8(a, plan)) {
+            launch_small_gemm_q8(a, plan, stream);
+            return;
+        }
+    }
     const bool small = a.config == 1 || (a.config < 0 && q8_streams(a.t, a.n));
     if (small) launch_stream_q8(a, stream);
     else launch_big<EP, YT, PT, MODE_CHAIN>(a, stream);

@@ -851,6 +851,44 @@ bool small_gemm_plan(const GemmArgs& a, SmallGemmPlan& plan) {
     return true;
 }
 
+bool small_gemm_plan_q8(const GemmArgs& a, SmallGemmPlan& plan) {
+    // the q8 gate/up pass (int8 X staged as it is, exact int32 group sums, the cpu-q8 float chain per worker's run of
+    // groups): SwiGLU to a float32 H only
+    if (a.epilogue != SEPAL_HIP_SWIGLU || a.y_type != SEPAL_HIP_F32) return false;
+    GemmArgs b = a;
+    b.x_type = SEPAL_HIP_BF16;  // the tile plan does not depend on the activation type
+    if (!small_gemm_plan(b, plan)) return false;
+    const bool per_token = a.act_block == a.k && a.k != 128;
+    // the staged int8 rows (16-byte chunks) and the per-128 scales (16 rows x 24 groups) fit the pass's LDS plan
+    return per_token || a.k / 128 <= 24;
+}
+
+void launch_small_gemm_q8(const GemmArgs& a, const SmallGemmPlan& plan, hipStream_t stream) {
+    using namespace stack;
+    if (a.scratch == nullptr) throw LaunchError("small-M multiply: the row maxima need the workspace");
+    PassParams p{};
+    p.x = static_cast<const unsigned short*>(a.x);
+    p.ld_x = a.ld_x;
+    p.w = reinterpret_cast<const signed char*>(a.w);
+    p.ld_w = a.ld_w;
+    p.s = a.s;
+    p.ld_s = a.ld_s;
+    p.y = a.y;
+    p.ld_y = a.ld_y;
+    p.t = static_cast<int>(a.t);
+    p.n = static_cast<int>(a.n);
+    p.k = static_cast<int>(a.k);
+    p.parts = 1;
+    p.per_block = plan.per_block;
+    p.tiles = static_cast<int>(a.n / 16);
+    p.blocks_per_part = (p.tiles + p.per_block - 1) / p.per_block;
+    p.xs = a.xs;
+    p.ld_xs = a.ld_xs;
+    p.per_token = a.act_block == a.k && a.k != 128 ? 1 : 0;
+    p.pmax = reinterpret_cast<float*>(static_cast<char*>(a.scratch) + kCounterBytes);  // unused by the caller
+    launch_pass<kActI8, true, SEPAL_HIP_F32>(p, plan.lds, stream);
+}
+
 void launch_small_gemm_w8g(const GemmArgs& a, const SmallGemmPlan& plan, hipStream_t stream) {
     using namespace stack;
     PassParams p{};

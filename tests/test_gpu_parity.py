@@ -308,6 +308,26 @@ def test_w8g_single_call_pass_kernels(sm, t, xdt):
         assert torch.equal(yv, y2)
 
 
+@pytest.mark.parametrize("t", [1, 7, 16])
+def test_q8_single_call_pass_kernel(sm, t):
+    """T <= 16 at the default config runs the q8 SwiGLU multiply (float32 H) on the q8 stack's gate/up pass: every
+    element within the bar of the large-M path's result (cpu-q8 bit for bit), both activation-scale modes, outlier
+    channels."""
+    say("q8 single-call pass kernel", t)
+    g = torch.Generator(device="cuda").manual_seed(500 + t)
+    n, k = 19456, 2560
+    w = (torch.randn(n, k, generator=g, device="cuda") * 0.02).half()
+    q, s = sm.quantize_group_s8(w, rule=sm.RULE_RECIPROCAL)
+    x = torch.randn(t, k, generator=g, device="cuda")
+    x[:, ::97] *= 20.0
+    for blk in (k, 128):
+        xq, xs = sm.quantize_rows_s8(x, block=blk)
+        y = sm.gemm_q8(xq, xs, q, s, epilogue=sm.SWIGLU, act_block=blk)
+        y0 = sm.gemm_q8(xq, xs, q, s, epilogue=sm.SWIGLU, act_block=blk, config=0)
+        assert max_rel_over_rms(host(y), host(y0).astype(np.float64)) < 2e-3, blk
+        assert torch.equal(y, sm.gemm_q8(xq, xs, q, s, epilogue=sm.SWIGLU, act_block=blk))
+
+
 @pytest.mark.parametrize("t", [33, 64])
 def test_small_m_wide_n_split_fits_the_workspace(sm, t):
     """The small-M path at the gate/up shape (N 19456, K 2560) with 33 and 64 rows: its K split is bounded by the
