@@ -109,8 +109,8 @@ SEPAL_HIP_API int32_t sepal_hip_quantize_rows_s8(const void* x, int32_t x_type, 
  * large-M path reproduces cpu-q8 bit for bit. act_block = K (one scale per token): y = (f_0 * ws_0, then
  * fma(f_b, ws_b, y)) * xs. Epilogues STORE / ADD / SWIGLU (silu with the cpu-q8 exp polynomial); Y float32
  * [T, ld_y], or y_type for SWIGLU. K a multiple of 128; strides multiples of 16; 16-byte aligned pointers. `config`
- * -1 takes the small-M path up to 64 rows (above 32 rows only for N < 8192; a SWIGLU multiply with a float32 Y at
- * T <= 16 runs the M <= 16 stack's q8 gate/up pass where the shape fits it), 0 the large-M path, 1 the small-M path,
+ * -1 takes the small-M path up to 64 rows (above 32 rows only for N < 8192; at T <= 16 with a float32 Y the M <= 16
+ * stack's q8 passes where the shape fits them), 0 the large-M path, 1 the small-M path,
  * 2 the small-M path with the chain whole; the small-M path splits K across blocks when N is narrow, which keeps the
  * sums exact but adds the splits' partial chains (within tolerance, not bit for bit); config 2 keeps the chain whole
  * (bit for bit).

@@ -113,6 +113,9 @@ void launch_small_gemm_w8g(const GemmArgs& a, const SmallGemmPlan& plan, hipStre
 // The q8 form for the SwiGLU multiply (float32 H): the gate/up pass of the q8 stack.
 bool small_gemm_plan_q8(const GemmArgs& a, SmallGemmPlan& plan);
 void launch_small_gemm_q8(const GemmArgs& a, const SmallGemmPlan& plan, hipStream_t stream);
+// ... and for the Store / Add multiply (float32 Y through K-parts and the parts sum).
+bool small_gemm_plan_q8_parts(const GemmArgs& a, SmallGemmPlan& plan);
+void launch_small_gemm_q8_parts(const GemmArgs& a, const SmallGemmPlan& plan, hipStream_t stream);
 // x bf16 [t, hidden] -> h binary16 [t, inter] -> part float32 [parts][t][hidden] -> y float32 [t, hidden] and, when
 // xn is set, xn bf16 [t, hidden] = RMSNorm(y) (cpu-q8 order, identity weight).
 void launch_small_layer(const SmallStackPlan& plan, std::size_t t, std::size_t hidden, std::size_t inter, const void* x,

@@ -882,6 +882,13 @@ void dispatch_path(const GemmArgs& a, hipStream_t stream) {
             launch_small_gemm_q8(a, plan, stream);
             return;
         }
+    } else if constexpr (EP != SEPAL_HIP_SWIGLU) {
+        // ... and its int8-X pass with K-parts for Store / Add
+        SmallGemmPlan plan;
+        if (a.config < 0 && a.t <= 16 && small_gemm_plan_q8_parts(a, plan)) {
+            launch_small_gemm_q8_parts(a, plan, stream);
+            return;
+        }
     }
     const bool small = a.config == 1 || (a.config < 0 && q8_streams(a.t, a.n));
     if (small) launch_stream_q8(a, stream);

@@ -42,6 +42,8 @@ __device__ __forceinline__ f32x4 mfma16(int xt, const u32x4 a, const u32x4 b, f3
 
 // Activation type of the gpu-q8w stack: int8 X (and int8 H, quantized by the down pass's loaders) on int8 MFMAs.
 constexpr int kActI8 = 8;
+// The same with the multiply's X already int8 in every pass (one q8 Store / Add multiply: K-parts of int8 X).
+constexpr int kActI8X = 9;
 
 // The activation quantizer's rounding (rule RECIPROCAL: rint(v / scale) as v * (1 / scale), clamped to +-127), as
 // quantize_rows applies it (runner/src/cpu/gemm.cpp pack_acts).
@@ -168,7 +170,7 @@ __global__ void __launch_bounds__(kThreads) pass_kernel(const PassParams p) {
     const int g_lo = part * groups / p.parts, g_hi = (part + 1) * groups / p.parts;
     const int gpt = g_hi - g_lo;              // groups per tile in this part
     const int kw = 128 * gpt;                 // staged X columns [128 g_lo, 128 g_hi)
-    constexpr bool Q8 = XT == kActI8;
+    constexpr bool Q8 = XT == kActI8 || XT == kActI8X;
     const int xpitch = (Q8 ? kw : 2 * kw) + 16;  // bytes per staged row (padded: an operand read's 16 rows hit distinct banks)
     float* red = reinterpret_cast<float*>(lds + 16 * xpitch);  // [kWorkers][kSlots][16 x 16]
     float* scl = red + kWorkers * kSlots * 256;                 // [block tile][16 rows][gpt] scales
@@ -184,7 +186,7 @@ __global__ void __launch_bounds__(kThreads) pass_kernel(const PassParams p) {
     // before any weight load is issued: behind a weight burst these loads would wait in the memory queues (M = 16
     // stack: w8g 1.240 -> 1.197 ms per pass; q8 1.46 -> 1.30 ms) ----
     const int xr = min(wave, p.t - 1);
-    if constexpr (Q8 && !SWIGLU) {
+    if constexpr (XT == kActI8 && !SWIGLU) {
         // q8 down: H float32 quantized as the activation quantizer does (rule RECIPROCAL, scale = max / 127), per 128
         // columns or with the row maximum of the gate/up pass's partial maxima (per token)
         if (gpt <= 14) stage_h_q8<7, 1>(p, lds, xsc, xpitch, g_lo, gpt, wave, 1, lane);
@@ -887,6 +889,44 @@ void launch_small_gemm_q8(const GemmArgs& a, const SmallGemmPlan& plan, hipStrea
     p.per_token = a.act_block == a.k && a.k != 128 ? 1 : 0;
     p.pmax = reinterpret_cast<float*>(static_cast<char*>(a.scratch) + kCounterBytes);  // unused by the caller
     launch_pass<kActI8, true, SEPAL_HIP_F32>(p, plan.lds, stream);
+}
+
+bool small_gemm_plan_q8_parts(const GemmArgs& a, SmallGemmPlan& plan) {
+    // one q8 Store / Add multiply: int8 X staged per K-part, the cpu-q8 chain per worker's run of groups, K-parts
+    if (a.epilogue == SEPAL_HIP_SWIGLU || a.y_type != SEPAL_HIP_F32) return false;
+    GemmArgs b = a;
+    b.x_type = SEPAL_HIP_BF16;
+    if (!small_gemm_plan(b, plan)) return false;
+    const bool per_token = a.act_block == a.k && a.k != 128;
+    return per_token || static_cast<std::size_t>((a.k / 128 + plan.parts - 1) / plan.parts) <= 24;
+}
+
+void launch_small_gemm_q8_parts(const GemmArgs& a, const SmallGemmPlan& plan, hipStream_t stream) {
+    using namespace stack;
+    if (a.scratch == nullptr) throw LaunchError("small-M multiply: the K-parts need the workspace");
+    float* part = reinterpret_cast<float*>(static_cast<char*>(a.scratch) + kCounterBytes);
+    PassParams p{};
+    p.x = static_cast<const unsigned short*>(a.x);
+    p.ld_x = a.ld_x;
+    p.w = reinterpret_cast<const signed char*>(a.w);
+    p.ld_w = a.ld_w;
+    p.s = a.s;
+    p.ld_s = a.ld_s;
+    p.y = part;
+    p.ld_y = a.n;
+    p.t = static_cast<int>(a.t);
+    p.n = static_cast<int>(a.n);
+    p.k = static_cast<int>(a.k);
+    p.parts = plan.parts;
+    p.per_block = plan.per_block;
+    p.tiles = static_cast<int>(a.n / 16);
+    p.blocks_per_part = (p.tiles + p.per_block - 1) / p.per_block;
+    p.xs = a.xs;
+    p.ld_xs = a.ld_xs;
+    p.per_token = a.act_block == a.k && a.k != 128 ? 1 : 0;
+    launch_pass<kActI8X, false, SEPAL_HIP_F32>(p, plan.lds, stream);
+    launch_parts_sum(plan.parts, a.epilogue == SEPAL_HIP_ADD, a.t, a.n, part, static_cast<float*>(a.y), a.ld_y, stream);
+    check_launch("small-M multiply parts sum launch");
 }
 
 void launch_small_gemm_w8g(const GemmArgs& a, const SmallGemmPlan& plan, hipStream_t stream) {

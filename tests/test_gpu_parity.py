@@ -310,9 +310,9 @@ def test_w8g_single_call_pass_kernels(sm, t, xdt):
 
 @pytest.mark.parametrize("t", [1, 7, 16])
 def test_q8_single_call_pass_kernel(sm, t):
-    """T <= 16 at the default config runs the q8 SwiGLU multiply (float32 H) on the q8 stack's gate/up pass: every
-    element within the bar of the large-M path's result (cpu-q8 bit for bit), both activation-scale modes, outlier
-    channels."""
+    """T <= 16 at the default config runs the q8 SwiGLU multiply (float32 H) on the q8 stack's gate/up pass, and Store /
+    Add on its int8-X pass with K-parts: every element within the bar of the large-M path's result (cpu-q8 bit for
+    bit), both activation-scale modes, outlier channels."""
     say("q8 single-call pass kernel", t)
     g = torch.Generator(device="cuda").manual_seed(500 + t)
     n, k = 19456, 2560
@@ -326,6 +326,20 @@ def test_q8_single_call_pass_kernel(sm, t):
         y0 = sm.gemm_q8(xq, xs, q, s, epilogue=sm.SWIGLU, act_block=blk, config=0)
         assert max_rel_over_rms(host(y), host(y0).astype(np.float64)) < 2e-3, blk
         assert torch.equal(y, sm.gemm_q8(xq, xs, q, s, epilogue=sm.SWIGLU, act_block=blk))
+    # Store / Add: the int8-X pass with K-parts (the down shape), then the in-order parts sum
+    n, k = 2560, 9728
+    w = (torch.randn(n, k, generator=g, device="cuda") * 0.02).half()
+    q, s = sm.quantize_group_s8(w, rule=sm.RULE_RECIPROCAL)
+    x = torch.randn(t, k, generator=g, device="cuda")
+    base = torch.randn(t, n, generator=g, device="cuda")
+    for blk in (k, 128):
+        xq, xs = sm.quantize_rows_s8(x, block=blk)
+        y0 = sm.gemm_q8(xq, xs, q, s, act_block=blk, config=0)
+        y = sm.gemm_q8(xq, xs, q, s, act_block=blk)
+        assert max_rel_over_rms(host(y), host(y0).astype(np.float64)) < 2e-3, blk
+        ya = base.clone()
+        sm.gemm_q8(xq, xs, q, s, y=ya, epilogue=sm.ADD, act_block=blk)
+        assert max_rel_over_rms(host(ya), (host(y0) + host(base)).astype(np.float64)) < 2e-3, blk
 
 
 @pytest.mark.parametrize("t", [33, 64])
