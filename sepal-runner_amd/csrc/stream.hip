@@ -15,7 +15,6 @@
 //     epilogue, so the result does not depend on which block finishes last. With one split the chain is whole and
 //     the q8 result equals cpu-q8 bit for bit.
 #include <algorithm>
-#include <cstdlib>
 #include <mutex>
 #include <vector>
 
@@ -322,17 +321,11 @@ inline int resident_blocks(const void* kernel, std::size_t lds) {
 
 // Groups per split: the fewest splits (fewest partial sums) that still fill the blocks the device holds at once,
 // without passing that number (a second round of blocks would wait for the first to drain), at most kGMax groups
-// (every weight load of a split is issued at once) and an X slice within 64 KB of LDS. SEPAL_HIP_STREAM_GPS
-// overrides it (tuning).
+// (every weight load of a split is issued at once) and an X slice within 64 KB of LDS.
 inline int pick_gps(int spans, int groups, int mt, int xbytes, int force_splits, int resident) {
     const int lds_cap = ((64 << 10) / (16 * mt) - 16) / (128 * xbytes);
-    static const int env = [] {
-        const char* v = std::getenv("SEPAL_HIP_STREAM_GPS");
-        return v != nullptr ? std::atoi(v) : 0;
-    }();
     if (force_splits == 1) return groups;  // the caller's LDS check refuses what does not fit
     const int cap = max(1, min(groups, min(lds_cap, kGMax)));
-    if (env > 0) return max(1, min(env, cap));
     const int max_splits = max(1, resident / max(1, spans));   // splits that fit in one round
     int gps = (groups + max_splits - 1) / max_splits;          // fewest groups per split within that
     return max(1, min(gps < 1 ? 1 : gps, cap));
