@@ -72,6 +72,31 @@ def timed(torch, fn, steps, warmup, stream):
     return start.elapsed_time(stop) / steps
 
 
+def graph_timed(torch, fn, reps=20, replays=10):
+    """Microseconds of GPU time per call of fn(stream): `reps` calls captured in one HIP graph on a side stream (after
+    warm-up calls there, which size the stream's workspace), replayed `replays` times between HIP events. Excludes
+    the host's per-call overhead (the Python binding), which at these sizes exceeds the kernels' time."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(3):
+            fn(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        for _ in range(reps):
+            fn(s)
+    g.replay()
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(replays):
+        g.replay()
+    stop.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / (replays * reps) * 1e3
+
+
 def make_layers(torch, sm, rule, seed0=1000):
     layers = []
     for l in range(LAYERS):
@@ -427,6 +452,35 @@ def main():
                                       "frac_bf16_peak": round(ops_c2 / (ms_c2 * 1e-3) / 1e12 / PEAK["bf16_tflops"], 4)}
         log(f"C2 shape (M=896 block): {extra['c2_mlp_block_m896']}")
         del x896, h896, y896
+        # ---- one MLP block as single calls at decode sizes (T = 1 and 16): gate/up SwiGLU + down, w8g and q8 (per
+        # token), GPU time per call from HIP graph replays; weights and scales streamed per block: 77.1 MB ----
+        dec = {}
+        qwgu, qsgu = sm.quantize_gate_up_s8((torch.randn(I, H, generator=g2, device="cuda") * 0.02).half(),
+                                            (torch.randn(I, H, generator=g2, device="cuda") * 0.02).half(),
+                                            rule=sm.RULE_RECIPROCAL)
+        qwd, qsd = sm.quantize_group_s8((torch.randn(H, I, generator=g2, device="cuda") * 0.02).half(),
+                                        rule=sm.RULE_RECIPROCAL)
+        for t_dec in (1, 16):
+            xd = bf16_x(torch, t_dec, 9)
+            hd = torch.empty(t_dec, I, dtype=torch.bfloat16, device="cuda")
+            yd = torch.empty(t_dec, H, dtype=torch.float32, device="cuda")
+            us_gu = graph_timed(torch, lambda st: sm.gemm_w8g(xd, wgu, sgu, y=hd, epilogue=sm.SWIGLU, stream=st))
+            us_dn = graph_timed(torch, lambda st: sm.gemm_w8g(hd, wd, sd, y=yd, stream=st))
+            xq_d, xs_d = sm.quantize_rows_s8(xd, block=H)
+            hq_d = torch.zeros(t_dec, I, dtype=torch.int8, device="cuda")
+            hs_d = torch.ones(t_dec, 1, dtype=torch.float32, device="cuda")
+            hf_d = torch.empty(t_dec, I, dtype=torch.float32, device="cuda")
+            us_qgu = graph_timed(torch, lambda st: sm.gemm_q8(xq_d, xs_d, qwgu, qsgu, y=hf_d, epilogue=sm.SWIGLU,
+                                                              act_block=H, stream=st))
+            us_qdn = graph_timed(torch, lambda st: sm.gemm_q8(hq_d, hs_d, qwd, qsd, y=yd, act_block=I, stream=st))
+            block_bytes = C5_BYTES / LAYERS
+            dec[f"t{t_dec}"] = {"w8g_gate_up_us": round(us_gu, 2), "w8g_down_us": round(us_dn, 2),
+                                "w8g_block_gbs": round(block_bytes / ((us_gu + us_dn) * 1e-6) / 1e9, 1),
+                                "q8_gate_up_us": round(us_qgu, 2), "q8_down_us": round(us_qdn, 2),
+                                "q8_block_gbs": round(block_bytes / ((us_qgu + us_qdn) * 1e-6) / 1e9, 1)}
+        extra["decode_single_calls"] = dec
+        log(f"decode single calls (GPU time per call): {dec}")
+        del qwgu, qsgu, qwd, qsd
         # ---- the per-channel int8 family (the reference's launch_gemm_s8 / launch_gemm_w8a16) at the MLP shapes ----
         s8 = {}
         for n_o, k_o in ((2 * I, H), (H, I)):
