@@ -10,15 +10,16 @@
 // scale keeps the previous one: its group's bytes are all zero). Results match the fmaf chain within float32 rounding
 // of a different summation order, not bit for bit.
 //
-// Two paths:
+// Paths:
 //   large M: waves of 128 x 64 outputs (4 x 2 blocks of 32 x 32, MFMA 32x32x16; 64 x 64 in the half tiles), the
 //            weights widened once per tile when staged into LDS; 1-D grid with an XCD-aware tile order (a block's id
 //            modulo 8 is its XCD; consecutive logical tiles are kept on one XCD so they share its L2). gemm_big3:
-//            256 x 256 tiles (128 x 256 halves for a launch's last partial round, 64 x 256 quarters for grids of fewer
-//            than 512 large tiles), K in steps of 64, X straight from global memory into LDS. gemm_big2 (when an
-//            offset does not fit 32 bits, or a SwiGLU N is not a multiple of 256): 256 x 128 or 256 x 256 tiles, K in
-//            steps of 32.
-//   small M: stream.hip (the weights streamed once, HBM-bound).
+//            256 x 256 tiles (128 x 256 halves for a launch's last partial round; for grids of fewer than 512 large
+//            tiles, blocks of 64, 128 or 256 rows and, by default, K split over blocks, by plan_small_grid), K in steps
+//            of 64, X straight from global memory into LDS. gemm_big2 (when an offset does not fit 32 bits, or a
+//            SwiGLU N is not a multiple of 256): 256 x 128 or 256 x 256 tiles, K in steps of 32.
+//   small M: at T <= 16 the M <= 16 stack's pass kernels (stack_small.hip) where the shape fits them; else, at
+//            T <= 32 with N < 8192, stream.hip (the weights streamed once, HBM-bound); else the large-M plan.
 #include <algorithm>
 
 #include "common.hpp"
