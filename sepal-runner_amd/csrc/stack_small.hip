@@ -1,5 +1,7 @@
 // The M <= 16 layer of the MLP stack (gpu-w8g, and its gpu-q8w form): three launches per layer, no cross-block
-// hand-off inside a kernel.
+// hand-off inside a kernel. The same pass kernels also run single multiplies at T <= 16 (sepal_hip_gemm_w8g and
+// sepal_hip_gemm_q8 at the default config, end of this file): SwiGLU straight to Y, Store / Add through K-parts and an
+// in-order parts sum.
 //
 // At 16 tokens each layer is a single pass over 77 MB of int8 weights and scales, so the kernels are shaped to keep
 // every CU streaming its share of weights for the whole kernel:
