@@ -190,6 +190,43 @@ __device__ __forceinline__ void chain_epilogue(const Params& p, float (&acc)[2][
         }
         return;
     } else {
+    // A whole tile needs no bounds checks: the row and the wave's column base are wave-uniform (scalar registers) and
+    // the lane adds a 32-bit offset, so a store (and, per token, the row scale's load) costs no vector address
+    // arithmetic.
+    if (m0 + BM <= p.t && n0 + 256 <= p.n) {
+        constexpr unsigned ES = YT == SEPAL_HIP_F32 ? 4 : 2;
+        const int wmu = __builtin_amdgcn_readfirstlane(wm), ibu = __builtin_amdgcn_readfirstlane(ib),
+                  hhu = __builtin_amdgcn_readfirstlane(hh);
+        const unsigned lrow = 4u * static_cast<unsigned>(lane / 32);
+        const unsigned voff = (lrow * static_cast<unsigned>(p.ld_y) + lane % 32) * ES;
+        const unsigned xoff = lrow * static_cast<unsigned>(p.ld_xs) * 4u;
+        char* const yb = static_cast<char*>(p.y);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const std::size_t row = static_cast<std::size_t>(m0 + wmu * 64 + i * 32 + 8 * (r / 4) + (r % 4));
+                float v0 = acc[i][0][r], v1 = acc[i][1][r];
+                if constexpr (PER_TOKEN) {
+                    const float xs = *reinterpret_cast<const float*>(
+                        reinterpret_cast<const char*>(p.xs + row * p.ld_xs) + xoff);
+                    v0 = __fmul_rn(v0, xs);
+                    v1 = __fmul_rn(v1, xs);
+                }
+                if constexpr (EP == SEPAL_HIP_SWIGLU) {
+                    char* const rp = yb + (row * p.ld_y + n0 / 2 + 64 * ibu + 32 * hhu) * ES;
+                    store_out<YT>(rp + voff, 0, swiglu_cephes(v0, v1));
+                } else {
+                    // put writes float32
+                    const unsigned foff = (lrow * static_cast<unsigned>(p.ld_y) + lane % 32) * 4u;
+                    char* const rp0 = yb + (row * p.ld_y + n0 + 128 * ibu + 32 * hhu) * 4;
+                    put<EP, YT>(rp0 + foff, 0, 0, 0, v0);
+                    put<EP, YT>(rp0 + 256 + foff, 0, 0, 0, v1);
+                }
+            }
+        }
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
 #pragma unroll
@@ -806,6 +843,33 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
     wait_vm_lgkm0<0>();  // no direct load may still be writing LDS when the block ends
 
     // y = (float(S) * sx[t]) * sw[n], float32 or binary16 (round to nearest even)
+    if (m0 + BM <= p.t && n0 + BN <= p.n) {
+        // a whole tile: no bounds checks; wave-uniform row and column bases, 32-bit lane offsets
+        constexpr unsigned ES = YT == SEPAL_HIP_F16 ? 2 : 4;
+        const int wmu = __builtin_amdgcn_readfirstlane(wm), wnu = __builtin_amdgcn_readfirstlane(wn);
+        const unsigned lrow = 4u * static_cast<unsigned>(lane / 32);
+        const unsigned voff = (lrow * static_cast<unsigned>(p.ld_y) + lane % 32) * ES;
+        const unsigned xoff = lrow * static_cast<unsigned>(p.ld_xs) * 4u;
+        float sw[2];
+#pragma unroll
+        for (int q = 0; q < 2; ++q) sw[q] = p.ws[static_cast<std::size_t>(n0 + 64 * wn + 32 * q + lane % 32) * p.ld_ws];
+        char* const yb = static_cast<char*>(p.y);
+#pragma unroll
+        for (int i = 0; i < MB; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const std::size_t row = static_cast<std::size_t>(m0 + wmu * 32 * MB + i * 32 + 8 * (r / 4) + (r % 4));
+                const float sx = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(p.xs + row * p.ld_xs) + xoff);
+#pragma unroll
+                for (int q = 0; q < 2; ++q) {
+                    const float v = __fmul_rn(__fmul_rn(static_cast<float>(tot[i][q][r]), sx), sw[q]);
+                    char* const dst = yb + (row * p.ld_y + n0 + 64 * wnu + 32 * q) * ES + voff;
+                    if constexpr (YT == SEPAL_HIP_F16) *reinterpret_cast<unsigned short*>(dst) = f32_to_f16_bits(v);
+                    else *reinterpret_cast<float*>(dst) = v;
+                }
+            }
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < MB; ++i)
 #pragma unroll

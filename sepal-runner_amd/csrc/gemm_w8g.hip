@@ -620,6 +620,33 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
         e[0] = e[1] = 1.0f;  // the sums are final values (x 1 is exact)
     }
 
+    // A whole tile needs no bounds checks: the row and the wave's column base are wave-uniform (scalar registers) and
+    // the lane adds a 32-bit offset, so a store costs no vector address arithmetic.
+    if (m0 + BM3 <= p.t && n0 + BN <= p.n) {
+        constexpr unsigned ES = YT == SEPAL_HIP_F32 ? 4 : 2;
+        const int wu = __builtin_amdgcn_readfirstlane(wave);
+        const int wmu = wu % 2, ibu = (wu / 2) / 2, hhu = (wu / 2) % 2;
+        const unsigned voff = (4u * static_cast<unsigned>(lane / 32) * static_cast<unsigned>(p.ld_y) + lane % 32) * ES;
+        char* const yb = static_cast<char*>(p.y);
+#pragma unroll
+        for (int i = 0; i < MB; ++i) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const std::size_t row = static_cast<std::size_t>(m0 + wmu * 32 * MB + i * 32 + 8 * (r / 4) + (r % 4));
+                const float v0 = __fmul_rn(acc[i][0][r], e[0]), v1 = __fmul_rn(acc[i][1][r], e[1]);
+                if constexpr (EP == SEPAL_HIP_SWIGLU) {
+                    char* const rp = yb + (row * p.ld_y + n0 / 2 + 64 * ibu + 32 * hhu) * ES;
+                    store_out<YT>(rp + voff, 0, swiglu_fast(v0, v1));
+                } else {
+                    char* const rp0 = yb + (row * p.ld_y + n0 + 32 * (4 * ibu + hhu)) * ES;
+                    char* const rp1 = yb + (row * p.ld_y + n0 + 32 * (4 * ibu + 2 + hhu)) * ES;
+                    put_plain<EP, YT>(rp0 + voff, 0, v0);
+                    put_plain<EP, YT>(rp1 + voff, 0, v1);
+                }
+            }
+        }
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < MB; ++i) {
 #pragma unroll
