@@ -199,11 +199,14 @@ int32_t sepal_hip_gemm_w8g(const void* x, int32_t x_type, size_t ld_x, const int
         a.config = config == 2 ? 1 : config;
         a.force_splits = config == 2 ? 1 : 0;
         const hipStream_t st = as_stream(stream);
-        const std::size_t extra = gemm_w8g_scratch_bytes(a);
-        Lease ws(kScratchOffset + extra, st);
+        const std::size_t extra = (gemm_w8g_scratch_bytes(a) + 255) / 256 * 256;
+        const std::size_t img = gemm_w8g_image_bytes(a);
+        Lease ws(kScratchOffset + extra + img, st);
         a.scratch = ws.base();
         a.xsplit = ws.base() + kScratchOffset;
         a.ytmp = reinterpret_cast<float*>(ws.base() + kScratchOffset + gemm_w8g_split_bytes(a));
+        a.wimage = img != 0 ? ws.base() + kScratchOffset + extra : nullptr;
+        a.wimage_bytes = img;
         launch_gemm_w8g(a, st);
     });
 }
@@ -404,7 +407,13 @@ int32_t sepal_hip_gemm_w8a16(const void* x, size_t ld_x, const int8_t* wq, size_
         const bool direct = y_type == SEPAL_HIP_F32 || t > static_cast<std::size_t>(kSmallM);
         const std::size_t chunk = direct ? t : std::max<std::size_t>(1, (std::size_t{64} << 20) / (n * 4));
         const std::size_t rows = std::min(t, chunk);
-        Lease lease(kScratchOffset + s_bytes + (direct ? 0 : rows * n * 4), st);
+        GemmArgs probe;
+        probe.t = rows;
+        probe.n = n;
+        probe.k = k;
+        const std::size_t img = direct ? gemm_w8g_image_bytes(probe) : 0;
+        const std::size_t tmp_bytes = direct ? 0 : (rows * n * 4 + 255) / 256 * 256;
+        Lease lease(kScratchOffset + s_bytes + tmp_bytes + img, st);
         char* ws = lease.base();
         float* s = reinterpret_cast<float*>(ws + kScratchOffset);
         float* tmp = reinterpret_cast<float*>(ws + kScratchOffset + s_bytes);
@@ -429,6 +438,8 @@ int32_t sepal_hip_gemm_w8a16(const void* x, size_t ld_x, const int8_t* wq, size_
             a.epilogue = SEPAL_HIP_STORE;
             a.config = tr > static_cast<std::size_t>(kSmallM) ? 0 : -1;  // no K split: a row's bits do not depend on the batch
             a.scratch = ws;
+            a.wimage = img != 0 ? ws + kScratchOffset + s_bytes + tmp_bytes : nullptr;
+            a.wimage_bytes = img;
             launch_gemm_w8g(a, st);
             if (!direct) launch_f32_to_f16(tmp, n, static_cast<std::uint16_t*>(y) + r0 * ld_y, ld_y, tr, n, st);
         }
@@ -645,6 +656,13 @@ StackZones stack_zones(int kind, std::size_t t, std::size_t hidden, std::size_t 
     z.off_sh = z.off_qh + (kind == 1 ? up256(t * inter) : 0);
     z.off_split = z.off_sh + (kind == 1 ? up256(t * (inter / z.ab_i) * 4) : 0);
     std::size_t split = 0;
+    GemmArgs gu, dn;
+    gu.t = dn.t = t;
+    gu.n = 2 * inter;
+    gu.k = dn.n = hidden;
+    dn.k = inter;
+    gu.epilogue = SEPAL_HIP_SWIGLU;
+    z.img = kind == 1 ? 0 : std::max(gemm_w8g_image_bytes(gu), gemm_w8g_image_bytes(dn));
     if (kind == 2) {
         GemmArgs dn;
         dn.x_type = SEPAL_HIP_F32;
@@ -655,7 +673,8 @@ StackZones stack_zones(int kind, std::size_t t, std::size_t hidden, std::size_t 
         dn.epilogue = SEPAL_HIP_STORE;
         split = gemm_w8g_scratch_bytes(dn);
     }
-    z.end = z.off_split + split;
+    z.off_img = z.off_split + up256(split);
+    z.end = z.off_img + z.img;
     return z;
 }
 
@@ -713,6 +732,10 @@ void run_stack(const StackZones& z, int kind, std::size_t layers, std::size_t t,
         dn.ld_y = hidden;
         dn.epilogue = SEPAL_HIP_STORE;
         dn.scratch = ws;
+        if (z.img != 0) {
+            gu.wimage = dn.wimage = ws + z.off_img;
+            gu.wimage_bytes = dn.wimage_bytes = z.img;
+        }
         if (kind != 1) {
             // w8g: H binary16 (kind 0) or float32 (kind 2, the down multiply on its bf16 hi + lo pairs)
             gu.x = x;
@@ -813,7 +836,12 @@ int32_t sepal_hip_mlp_stack_noalloc(int32_t kind, size_t layers, size_t t, size_
         check_stack_args(kind, hidden, inter, x, w_gate_up, s_gate_up, w_down, s_down, y, act_block);
         if (layers == 0 || t == 0) return;
         const hipStream_t st = as_stream(stream);
-        const StackZones z = stack_zones(kind, t, hidden, inter, act_block);
+        StackZones z = stack_zones(kind, t, hidden, inter, act_block);
+        if (z.end > kStaticScratchBytes && z.img != 0) {
+            // without the weight image (the kernels widen the weights themselves; the same bits)
+            z.img = 0;
+            z.end = z.off_img;
+        }
         require(z.end <= kStaticScratchBytes,
                 "mlp_stack_noalloc: this shape needs " + std::to_string(z.end) + " bytes of scratch, beyond the " +
                     std::to_string(kStaticScratchBytes) + " of the static scratch (call with fewer rows)");

@@ -39,6 +39,8 @@ struct GemmArgs {
     void* scratch = nullptr;  // the zero-at-rest split-K counters (kCounterBytes) followed by kPartialBytes of partials
     void* xsplit = nullptr;   // w8g with float32 X: the bf16 hi + lo pairs
     float* ytmp = nullptr;    // w8g with float32 X and SwiGLU off the one-pass kernel: the float32 sums [t, n]
+    void* wimage = nullptr;   // w8g at large M: room for the widened weight image (gemm_w8g_image_bytes)
+    std::size_t wimage_bytes = 0;
 };
 
 // q8 epilogue (internal, not in the public enum): SwiGLU, then the output quantized to int8 per row and 128 columns
@@ -49,6 +51,9 @@ void launch_gemm_w8g(const GemmArgs& a, hipStream_t stream);
 // Scratch bytes launch_gemm_w8g needs at xsplit (then ytmp, 256-byte aligned, when non-zero) for this problem; 0 for a
 // 16-bit X.
 std::size_t gemm_w8g_scratch_bytes(const GemmArgs& a);
+// Bytes of the widened weight image the large-M w8g kernels use for this problem (0: they widen in the kernel). The
+// image is written by every call, so it only needs to be scratch.
+std::size_t gemm_w8g_image_bytes(const GemmArgs& a);
 // The part of gemm_w8g_scratch_bytes that is the split buffer (ytmp follows it).
 inline std::size_t gemm_w8g_split_bytes(const GemmArgs& a) { return (a.t * a.k * 4 + 255) / 256 * 256; }
 void launch_stream_w8g(const GemmArgs& a, hipStream_t stream);

@@ -11,9 +11,12 @@
 // of a different summation order, not bit for bit.
 //
 // Paths:
-//   large M: waves of 128 x 64 outputs (4 x 2 blocks of 32 x 32, MFMA 32x32x16; 64 x 64 in the half tiles), the
-//            weights widened once per tile when staged into LDS; 1-D grid with an XCD-aware tile order (a block's id
-//            modulo 8 is its XCD; consecutive logical tiles are kept on one XCD so they share its L2). gemm_big3:
+//   large M: waves of 128 x 64 outputs (4 x 2 blocks of 32 x 32, MFMA 32x32x16; 64 x 64 in the half tiles); 1-D grid
+//            with an XCD-aware tile order (a block's id modulo 8 is its XCD; consecutive logical tiles are kept on one
+//            XCD so they share its L2). Grids of at least two rounds of 256 x 256 tiles: the weights are widened once
+//            per call into an image of the W stages (widen_image_kernel, one streaming pass), which gemm_pp (two wave
+//            groups in alternation) and the half tiles of gemm_big3 load straight into LDS. Otherwise the weights are
+//            widened per tile by the waves when staged into LDS. gemm_big3:
 //            256 x 256 tiles (128 x 256 halves for a launch's last partial round; for grids of fewer than 512 large
 //            tiles, blocks of 64, 128 or 256 rows and, by default, K split over blocks, by plan_small_grid), K in steps
 //            of 64, X straight from global memory into LDS. gemm_big2 (when an offset does not fit 32 bits, or a
@@ -94,6 +97,11 @@ struct BigParams {
     // split-K launches run the live block tiles sub0 .. sub0 + nsub - 1 of the dense order: block tile s at rows
     // (s mod sub_m) BM3 and columns (s / sub_m) 256, sub_m = ceil(T / BM3)
     int dense = 0, sub_m = 0, sub0 = 0, nsub = 0;
+    // gemm_big3 with the weights from an image (WI): the widened W stage of 256-column tile tn and weight step ks (64
+    // values of k) is the 32 KB at wimg + (tn * wsteps + ks) * 32768, in the LDS order the fragment reads use
+    const unsigned char* wimg = nullptr;
+    std::size_t wimg_bytes = 0;
+    int wsteps = 0;
 };
 
 // Tile of logical id `id`: groups of GM M tiles sweep N with the same few X row panels.
@@ -326,18 +334,74 @@ __device__ __forceinline__ void wait_vm_lgkm0() {
     __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4));  // vmcnt(N) lgkmcnt(0)
 }
 
-template <int XT, int EP, int YT, int MB, int SPLIT, bool SK>
+// The epilogue of a 256-column tile of the large-M kernels: wave `wave` holds MB x 2 blocks of 32 x 32 outputs (rows
+// m0 + 32 MB wm + 32 i.., columns n0 + 32 nbj[q]..), its Horner state e, and applies the last scale and the epilogue.
+template <int EP, int YT, int MB>
+__device__ __forceinline__ void tile_epilogue(const BigParams& p, const f32x16 (&acc)[MB][2], const float (&e)[2], int m0, int n0,
+                                              int wave, int lane) {
+    constexpr int BM3 = 64 * MB, BN = 256;
+    const int wm = wave % 2, wn = wave / 2, ib = wn / 2, hh = wn % 2;
+    const int col[2] = {n0 + 32 * (4 * ib + hh) + lane % 32, n0 + 32 * (4 * ib + 2 + hh) + lane % 32};
+    // A whole tile needs no bounds checks: the row and the wave's column base are wave-uniform (scalar registers) and
+    // the lane adds a 32-bit offset, so a store costs no vector address arithmetic.
+    if (m0 + BM3 <= p.t && n0 + BN <= p.n) {
+        constexpr unsigned ES = YT == SEPAL_HIP_F32 ? 4 : 2;
+        const int wu = __builtin_amdgcn_readfirstlane(wave);
+        const int wmu = wu % 2, ibu = (wu / 2) / 2, hhu = (wu / 2) % 2;
+        const unsigned voff = (4u * static_cast<unsigned>(lane / 32) * static_cast<unsigned>(p.ld_y) + lane % 32) * ES;
+        char* const yb = static_cast<char*>(p.y);
+#pragma unroll
+        for (int i = 0; i < MB; ++i) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const std::size_t row = static_cast<std::size_t>(m0 + wmu * 32 * MB + i * 32 + 8 * (r / 4) + (r % 4));
+                const float v0 = __fmul_rn(acc[i][0][r], e[0]), v1 = __fmul_rn(acc[i][1][r], e[1]);
+                if constexpr (EP == SEPAL_HIP_SWIGLU) {
+                    char* const rp = yb + (row * p.ld_y + n0 / 2 + 64 * ibu + 32 * hhu) * ES;
+                    store_out<YT>(rp + voff, 0, swiglu_fast(v0, v1));
+                } else {
+                    char* const rp0 = yb + (row * p.ld_y + n0 + 32 * (4 * ibu + hhu)) * ES;
+                    char* const rp1 = yb + (row * p.ld_y + n0 + 32 * (4 * ibu + 2 + hhu)) * ES;
+                    put_plain<EP, YT>(rp0 + voff, 0, v0);
+                    put_plain<EP, YT>(rp1 + voff, 0, v1);
+                }
+            }
+        }
+        return;
+    }
+#pragma unroll
+    for (int i = 0; i < MB; ++i) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int row = m0 + wm * 32 * MB + i * 32 + 8 * (r / 4) + 4 * (lane / 32) + (r % 4);
+            if (row >= p.t) continue;
+            const float v0 = __fmul_rn(acc[i][0][r], e[0]), v1 = __fmul_rn(acc[i][1][r], e[1]);
+            if constexpr (EP == SEPAL_HIP_SWIGLU) {
+                const int f = n0 / 2 + 64 * ib + 32 * hh + lane % 32;
+                if (2 * f < p.n) store_out<YT>(p.y, static_cast<std::size_t>(row) * p.ld_y + f, swiglu_fast(v0, v1));
+            } else {
+                if (col[0] < p.n) put_plain<EP, YT>(p.y, static_cast<std::size_t>(row) * p.ld_y + col[0], v0);
+                if (col[1] < p.n) put_plain<EP, YT>(p.y, static_cast<std::size_t>(row) * p.ld_y + col[1], v1);
+            }
+        }
+    }
+}
+
+template <int XT, int EP, int YT, int MB, int SPLIT, bool SK, bool WI>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) gemm_big3(const BigParams p) {
     // MB m-blocks of 32 rows per wave: tiles of BM3 = 64 MB rows (256, or 128 for the tail rows of a launch).
     // SK: split-K (the block's K range is its split of the groups; BigParams::splits).
     // SPLIT 2: X is a float32 operand as a bf16 hi + lo pair, stored as one bf16 row of 2K values (64-value chunk j of
     // k is chunk 2j (hi) and 2j + 1 (lo)); steps 2j and 2j + 1 multiply the same weights, so p.k counts the 2K values
     // and the weight offset of step kt is kt / 2 chunks.
+    // WI: the W stage of a step is loaded straight into LDS from the weight image (widen_image_kernel), one step ahead,
+    // instead of being loaded to registers two steps ahead and widened into the stage by the waves.
     static_assert(SPLIT == 1 || (SPLIT == 2 && XT == SEPAL_HIP_BF16), "the hi + lo form is bf16");
     constexpr int NW = 8, BN = 256, K3 = 64, SUB = K3 / 16, SPG = SPLIT * 128 / K3, BM3 = 64 * MB;
     constexpr int XSTAGE = BM3 * K3 * 2, WSTAGE = (BN / 32) * SUB * 1024;
     constexpr int XLD = XSTAGE / 16 / (64 * NW);       // X direct loads per thread per step (4)
     constexpr int WLD = BN * K3 / 16 / (64 * NW);      // W 16-byte chunks per thread per step (2)
+    constexpr int WLDI = WSTAGE / 16 / (64 * NW);      // WI: W direct loads per thread per step (4)
     __shared__ __align__(1024) unsigned char xs0[XSTAGE], xs1[XSTAGE], xs2[XSTAGE], ws0[WSTAGE], ws1[WSTAGE];
     const auto xstage = [&](auto it) -> lds_byte* {
         constexpr int i = decltype(it)::value;
@@ -388,6 +452,8 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
         const_cast<unsigned short*>(p.x), 0, static_cast<int>(p.x_bytes), 0x00020000);
     const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<signed char*>(p.w), 0, static_cast<int>(p.w_bytes), 0x00020000);
+    const __amdgpu_buffer_rsrc_t wires = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<unsigned char*>(p.wimg), 0, static_cast<int>(p.wimg_bytes), 0x00020000);
     // X: direct load i of wave w fills LDS kilobyte w + 8 i = rows 8 w + 64 i + {0..7}; lane l writes slot l % 8 of row
     // 8 w + 64 i + l / 8, which holds chunk (l % 8) ^ ((row / 2) & 7) = (l % 8) ^ ((4 w + l / 16) & 7)
     int xoff;
@@ -410,9 +476,9 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
         wdst0 = frag + 16 * (L ^ (2 * q));             // + 256 i
         wdst1 = frag + 16 * ((L + 32) ^ (2 * q + 1));  // + 256 i
     }
-    int rd[SUB];  // this lane's slot in a W fragment of substep st
+    int rd[SUB];  // this lane's slot in a W fragment of substep st (the image keeps the fragments in lane order)
 #pragma unroll
-    for (int st = 0; st < SUB; ++st) rd[st] = 16 * (lane ^ ((2 * st + lane / 32) & 7));
+    for (int st = 0; st < SUB; ++st) rd[st] = WI ? 16 * lane : 16 * (lane ^ ((2 * st + lane / 32) & 7));
 
     const int ib = wn / 2, hh = wn % 2;
     const int nbj[2] = {4 * ib + hh, 4 * ib + 2 + hh};
@@ -440,6 +506,14 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
         for (int i = 0; i < WLD; ++i)
             r.w[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wres, woff, ((kbase + kt) / SPLIT) * K3 + i * wstride, 0));
     };
+    // WI: direct load i of wave w fills kilobyte w + 8 i of the W stage from the same kilobyte of the image
+    const int wimg_tile = tn * p.wsteps;
+    const auto issue_wi = [&](int kt, lds_byte* wd) {
+#pragma unroll
+        for (int i = 0; i < WLDI; ++i)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(wires, (__attribute__((address_space(3))) void*)(wd + (wave + 8 * i) * 1024), 16,
+                                                     tid * 16, (wimg_tile + (kbase + kt) / SPLIT) * WSTAGE + i * 8192, 0, 0);
+    };
     const auto issue_scales = [&](int g) {
         snext[0] = ssrc[0][g0 + g];
         snext[1] = ssrc[1][g0 + g];
@@ -457,7 +531,8 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
     // earlier one, among them the next step's X
     const auto barrier = [&]() {
         asm volatile("" ::: "memory");
-        wait_vm_lgkm0<2 + XLD + WLD>();
+        if constexpr (WI) wait_vm_lgkm0<XLD>();  // only the X loads of step kt + 2 stay in flight
+        else wait_vm_lgkm0<2 + XLD + WLD>();
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
     };
@@ -478,12 +553,18 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
     issue_x(0, xstage(I0{}));
     issue_x(min(1, KT - 1), xstage(I1{}));
     __builtin_amdgcn_sched_barrier(0);
-    issue_w(0, r0);
-    issue_w(min(1, KT - 1), r1);
-    __builtin_amdgcn_sched_barrier(0);
-    stage_w(wstage(I0{}), r0);
-    asm volatile("" ::: "memory");
-    wait_vm_lgkm0<WLD>();  // everything but step 1's W (X of steps 0 and 1 included)
+    if constexpr (WI) {
+        issue_wi(0, wstage(I0{}));
+        asm volatile("" ::: "memory");
+        wait_vm_lgkm0<0>();
+    } else {
+        issue_w(0, r0);
+        issue_w(min(1, KT - 1), r1);
+        __builtin_amdgcn_sched_barrier(0);
+        stage_w(wstage(I0{}), r0);
+        asm volatile("" ::: "memory");
+        wait_vm_lgkm0<WLD>();  // everything but step 1's W (X of steps 0 and 1 included)
+    }
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     // the Horner state (the first step's factor multiplies zero accumulators)
@@ -509,42 +590,90 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
             }
             issue_scales(min(kt / SPG + 1, groups - 1));
         }
+        if constexpr (WI) {
+            // step kt + 1's W stage (last read by step kt - 1), then step kt + 2's X
+            issue_wi(min(kt + 1, KT - 1), wstage(std::integral_constant<int, (j + 1) % 2>{}));
+            __builtin_amdgcn_sched_barrier(0);
+        }
         issue_x(min(kt + 2, KT - 1), xstage(std::integral_constant<int, (j + 2) % 3>{}));
         __builtin_amdgcn_sched_barrier(0);
-        issue_w(min(kt + 2, KT - 1), r_free);
+        if constexpr (!WI) issue_w(min(kt + 2, KT - 1), r_free);
         // keep the loads at the top of the step, in this order: the wait for a step's operands then leaves the later
         // steps' loads in flight
         __builtin_amdgcn_sched_barrier(0);
+        if constexpr (WI) {
+            // the fragments double-buffered: substep st + 1's reads are issued before substep st's MFMAs, so their
+            // latency hides behind the MFMAs (the register budget allows it without the weight staging registers)
+            u32x4 a[2][MB], b[2][2];
+            const auto read_frags = [&](int st, int sl) {
 #pragma unroll
-        for (int st = 0; st < SUB; ++st) {
-            u32x4 a[MB], b[2];
+                for (int i = 0; i < MB; ++i)
+                    a[sl][i] = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(xs + (wm * MB + i) * 4096 + rx[st]);
 #pragma unroll
-            for (int i = 0; i < MB; ++i)
-                a[i] = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(xs + (wm * MB + i) * 4096 + rx[st]);
+                for (int q = 0; q < 2; ++q)
+                    b[sl][q] = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(ws + (nbj[q] * SUB + st) * 1024 + rd[st]);
+            };
+            read_frags(0, 0);
 #pragma unroll
-            for (int q = 0; q < 2; ++q)
-                b[q] = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(ws + (nbj[q] * SUB + st) * 1024 + rd[st]);
+            for (int st = 0; st < SUB; ++st) {
+                if (st + 1 < SUB) read_frags(st + 1, (st + 1) % 2);
 #pragma unroll
-            for (int i = 0; i < MB; ++i)
+                for (int i = 0; i < MB; ++i)
 #pragma unroll
-                for (int q = 0; q < 2; ++q) {
-                    // a group's Horner rescale of each accumulator block right before its first MFMA of the group:
-                    // the multiplies of one block overlap the MFMA of the previous one
-                    if constexpr (first)
-                        if (st == 0) acc[i][q] = acc[i][q] * ratio[q];
-                    acc[i][q] = mfma32<XT>(a[i], b[q], acc[i][q]);
-                }
-        }
-        if constexpr (first) {
-            // the first substep's fragment reads, then each block's 16 rescale multiplies and its MFMA, in turn
+                    for (int q = 0; q < 2; ++q) {
+                        if constexpr (first)
+                            if (st == 0) acc[i][q] = acc[i][q] * ratio[q];
+                        acc[i][q] = mfma32<XT>(a[st % 2][i], b[st % 2][q], acc[i][q]);
+                    }
+            }
+            // in this order: substep 0's reads; per substep the next substep's reads, then its MFMAs (at a group's
+            // first step, substep 0's MFMAs each after its block's 16 rescale multiplies)
             __builtin_amdgcn_sched_group_barrier(0x100, MB + 2, 0);
 #pragma unroll
-            for (int q = 0; q < 2 * MB; ++q) {
-                __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            for (int st = 0; st < SUB; ++st) {
+                if (st + 1 < SUB) __builtin_amdgcn_sched_group_barrier(0x100, MB + 2, 0);
+                if (first && st == 0) {
+#pragma unroll
+                    for (int q = 0; q < 2 * MB; ++q) {
+                        __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);
+                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    }
+                } else {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 2 * MB, 0);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int st = 0; st < SUB; ++st) {
+                u32x4 a[MB], b[2];
+#pragma unroll
+                for (int i = 0; i < MB; ++i)
+                    a[i] = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(xs + (wm * MB + i) * 4096 + rx[st]);
+#pragma unroll
+                for (int q = 0; q < 2; ++q)
+                    b[q] = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(ws + (nbj[q] * SUB + st) * 1024 + rd[st]);
+#pragma unroll
+                for (int i = 0; i < MB; ++i)
+#pragma unroll
+                    for (int q = 0; q < 2; ++q) {
+                        // a group's Horner rescale of each accumulator block right before its first MFMA of the group:
+                        // the multiplies of one block overlap the MFMA of the previous one
+                        if constexpr (first)
+                            if (st == 0) acc[i][q] = acc[i][q] * ratio[q];
+                        acc[i][q] = mfma32<XT>(a[i], b[q], acc[i][q]);
+                    }
+            }
+            if constexpr (first) {
+                // the first substep's fragment reads, then each block's 16 rescale multiplies and its MFMA, in turn
+                __builtin_amdgcn_sched_group_barrier(0x100, MB + 2, 0);
+#pragma unroll
+                for (int q = 0; q < 2 * MB; ++q) {
+                    __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                }
             }
         }
-        stage_w(wstage(std::integral_constant<int, (j + 1) % 2>{}), r_next);
+        if constexpr (!WI) stage_w(wstage(std::integral_constant<int, (j + 1) % 2>{}), r_next);
         barrier();
     };
     // the loop body is three groups (6 SPLIT steps: a multiple of the 3 X stages and 2 W stages), then at most two
@@ -620,49 +749,224 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
         e[0] = e[1] = 1.0f;  // the sums are final values (x 1 is exact)
     }
 
-    // A whole tile needs no bounds checks: the row and the wave's column base are wave-uniform (scalar registers) and
-    // the lane adds a 32-bit offset, so a store costs no vector address arithmetic.
-    if (m0 + BM3 <= p.t && n0 + BN <= p.n) {
-        constexpr unsigned ES = YT == SEPAL_HIP_F32 ? 4 : 2;
-        const int wu = __builtin_amdgcn_readfirstlane(wave);
-        const int wmu = wu % 2, ibu = (wu / 2) / 2, hhu = (wu / 2) % 2;
-        const unsigned voff = (4u * static_cast<unsigned>(lane / 32) * static_cast<unsigned>(p.ld_y) + lane % 32) * ES;
-        char* const yb = static_cast<char*>(p.y);
+    tile_epilogue<EP, YT, MB>(p, acc, e, m0, n0, wave, lane);
+}
+
+// ---- large-M kernel, two wave groups in alternation (gemm_pp) --------------------------------------------------------
+//
+// The tile, waves, outputs, k order and Horner chain of gemm_big3<MB = 4, WI> (so the same bits), scheduled so that the
+// MFMA units, the LDS and the VALU work at the same time instead of in turn. Waves 0-3 (group A, one per SIMD) and
+// 4-7 (group B) each alternate two slots per 64-wide step, separated by block barriers: L(k) issues the stage loads
+// of a later step and reads 16 of step k's 24 operand fragments (every W fragment, X of substeps 0 and 1); M(k) issues
+// the step's 32 MFMAs (at a group's first step each block's Horner rescale right before its first MFMA) and reads X of
+// substeps 2 and 3 behind the MFMAs of substeps 0 and 1 (all 24 fragments at once would not fit the registers).
+// Group B runs one slot behind group A (one extra barrier at its start, one at A's end), so in every slot one wave of
+// each SIMD multiplies while the other mostly reads. Slot 2k: A L(k), B M(k - 1); slot 2k + 1: A M(k), B L(k). An X
+// stage is read until the end of group B's M(k), slot 2k + 2, and reloaded from slot 2k + 3.
+// Stages: X of step k in X stage k mod 3, W of step k in W stage k mod 2 (from the weight image). Group A issues all
+// W loads (step k + 1 at the start of L(k), due by the barrier that ends slot 2k + 1), group B all X loads (step k + 2
+// at the start of its L(k), slot 2k + 1, due by the barrier that ends slot 2k + 3). A stage is reloaded only after
+// the barrier that follows both groups' reads of it, and every L slot waits for its reads before its barrier.
+template <int XT, int EP, int YT, int SPLIT>
+__global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) gemm_pp(const BigParams p) {
+    static_assert(SPLIT == 1 || (SPLIT == 2 && XT == SEPAL_HIP_BF16), "the hi + lo form is bf16");
+    constexpr int MB = 4, BN = 256, K3 = 64, SUB = K3 / 16, SPG = SPLIT * 128 / K3;
+    constexpr int XSTAGE = 256 * K3 * 2, WSTAGE = (BN / 32) * SUB * 1024;
+    constexpr int LDG = XSTAGE / 1024 / 4;  // direct loads per wave of its group per step (8)
+    __shared__ __align__(1024) unsigned char xs0[XSTAGE], xs1[XSTAGE], xs2[XSTAGE], ws0[WSTAGE], ws1[WSTAGE];
+    const auto xstage = [&](auto it) -> lds_byte* {
+        constexpr int i = decltype(it)::value;
+        if constexpr (i == 0) return (lds_byte*)xs0;
+        else if constexpr (i == 1) return (lds_byte*)xs1;
+        else return (lds_byte*)xs2;
+    };
+    const auto wstage = [&](auto it) -> lds_byte* {
+        if constexpr (decltype(it)::value == 0) return (lds_byte*)ws0;
+        else return (lds_byte*)ws1;
+    };
+
+    const int tid = threadIdx.x, lane = tid % 64;
+    const int wave = __builtin_amdgcn_readfirstlane(tid / 64);
+    const int wg = wave % 4;            // the wave's index in its group
+    const bool group_b = wave >= 4;
+    const int wm = wave % 2, wn = wave / 2;
+    int tm, tn;
+    tile_from_id(p.id0 + xcd_id(blockIdx.x, p.count), p.tiles_m, p.tiles_n, tm, tn);
+    const int m0 = tm * 256, n0 = tn * BN;
+    const int KT = p.k / K3, groups = KT / SPG;
+
+    const __amdgpu_buffer_rsrc_t xres = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<unsigned short*>(p.x), 0, static_cast<int>(p.x_bytes), 0x00020000);
+    const __amdgpu_buffer_rsrc_t wires = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<unsigned char*>(p.wimg), 0, static_cast<int>(p.wimg_bytes), 0x00020000);
+    // X (group B): direct load i of group wave g fills LDS kilobyte g + 4 i = rows 8 g + 32 i + {0..7}; lane l writes
+    // slot l % 8 of row 8 g + 32 i + l / 8, which holds chunk (l % 8) ^ ((row / 2) & 7) = (l % 8) ^ ((4 g + l / 16) & 7)
+    int xoff;
+    {
+        const int r = 8 * wg + lane / 8, c = (lane % 8) ^ ((4 * wg + lane / 16) & 7);
+        xoff = (m0 + r) * static_cast<int>(p.ld_x) * 2 + 16 * c;
+    }
+    const int xstride = 32 * static_cast<int>(p.ld_x) * 2;
+    int rx[SUB];
 #pragma unroll
-        for (int i = 0; i < MB; ++i) {
+    for (int st = 0; st < SUB; ++st) rx[st] = (lane % 32) * 128 + 16 * ((2 * st + lane / 32) ^ ((lane / 2) & 7));
+    const int ib = wn / 2, hh = wn % 2;
+    const int nbj[2] = {4 * ib + hh, 4 * ib + 2 + hh};
+    // the scales through a buffer descriptor: a 32-bit byte offset per lane and column, the group in the scalar offset
+    const __amdgpu_buffer_rsrc_t sres = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(p.s), 0, static_cast<int>(static_cast<std::size_t>(p.n) * p.ld_s * 4), 0x00020000);
+    // (columns past N read as 0: a zero scale keeps the Horner state; the second column is 64 columns on)
+    const int soff = (n0 + 32 * nbj[0] + lane % 32) * static_cast<int>(p.ld_s) * 4;
+    const int soff1 = 64 * static_cast<int>(p.ld_s) * 4;
+
+    // The wave's load role, chosen once (no branch in the loop): group B loads X, group A the weight image. Load i of
+    // group wave g fills LDS kilobyte g + 4 i of the stage.
+    const int wimg_tile = tn * p.wsteps;
+    const __amdgpu_buffer_rsrc_t lres = group_b ? xres : wires;
+    const int lvoff = group_b ? xoff : wg * 1024 + lane * 16;
+    const int lstride = group_b ? xstride : 4096;
+    const auto issue = [&](int soff, lds_byte* dst) __attribute__((always_inline)) {
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const std::size_t row = static_cast<std::size_t>(m0 + wmu * 32 * MB + i * 32 + 8 * (r / 4) + (r % 4));
-                const float v0 = __fmul_rn(acc[i][0][r], e[0]), v1 = __fmul_rn(acc[i][1][r], e[1]);
-                if constexpr (EP == SEPAL_HIP_SWIGLU) {
-                    char* const rp = yb + (row * p.ld_y + n0 / 2 + 64 * ibu + 32 * hhu) * ES;
-                    store_out<YT>(rp + voff, 0, swiglu_fast(v0, v1));
-                } else {
-                    char* const rp0 = yb + (row * p.ld_y + n0 + 32 * (4 * ibu + hhu)) * ES;
-                    char* const rp1 = yb + (row * p.ld_y + n0 + 32 * (4 * ibu + 2 + hhu)) * ES;
-                    put_plain<EP, YT>(rp0 + voff, 0, v0);
-                    put_plain<EP, YT>(rp1 + voff, 0, v1);
+        for (int i = 0; i < LDG; ++i)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(lres, (__attribute__((address_space(3))) void*)(dst + (wg + 4 * i) * 1024), 16,
+                                                     lvoff, soff + i * lstride, 0, 0);
+    };
+    const auto x_soff = [&](int kt) __attribute__((always_inline)) { return kt * K3 * 2; };
+    const auto w_soff = [&](int kt) __attribute__((always_inline)) { return (wimg_tile + kt / SPLIT) * WSTAGE; };
+    float snext[2];
+    const auto issue_scales = [&](int g) __attribute__((always_inline)) {
+        snext[0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(sres, soff, 4 * g, 0));
+        snext[1] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(sres, soff, 4 * g + soff1, 0));
+    };
+    const auto barrier = [&]() __attribute__((always_inline)) {
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_sched_barrier(0);
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+    };
+
+    f32x16 acc[MB][2];
+#pragma unroll
+    for (int i = 0; i < MB; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+    float e[2] = {1.0f, 1.0f}, emax[2] = {0.0f, 0.0f};
+    u32x4 a[2][MB], b[SUB][2];
+
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    issue_scales(0);
+    if (group_b) {
+        issue(x_soff(0), xstage(I0{}));
+        issue(x_soff(min(1, KT - 1)), xstage(I1{}));
+    } else {
+        issue(w_soff(0), wstage(I0{}));
+    }
+    wait_vm_lgkm0<0>();
+    barrier();
+    if (group_b) barrier();  // B runs one slot behind A
+
+    // Step kt (j = kt mod 6): slot L then slot M, each ended by a barrier.
+    const auto step = [&](int kt, auto jt) __attribute__((always_inline)) {
+        constexpr int j = decltype(jt)::value;
+        constexpr bool first = j % SPG == 0;
+        const lds_byte* xs = xstage(std::integral_constant<int, j % 3>{});
+        const lds_byte* ws = wstage(std::integral_constant<int, j % 2>{});
+        // ---- L(kt): loads of later steps, this step's fragments (the Horner factors at a group's first step)
+        float ratio[2] = {1.0f, 1.0f};
+        if constexpr (first) {
+#pragma unroll
+            for (int q = 0; q < 2; ++q) ratio[q] = horner_step(snext[q], e[q], emax[q]);
+        }
+        issue(group_b ? x_soff(min(kt + 2, KT - 1)) : w_soff(min(kt + 1, KT - 1)),
+              group_b ? xstage(std::integral_constant<int, (j + 2) % 3>{}) : wstage(std::integral_constant<int, (j + 1) % 2>{}));
+        // the next group's scales after the stage loads (needed two steps later)
+        if constexpr (first) issue_scales(min(kt / SPG + 1, groups - 1));
+        __builtin_amdgcn_sched_barrier(0);
+        const auto read_x = [&](int st) __attribute__((always_inline)) {
+#pragma unroll
+            for (int i = 0; i < MB; ++i)
+                a[st % 2][i] = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(xs + (wm * MB + i) * 4096 + rx[st]);
+        };
+        // every W fragment of the step and the X fragments of substeps 0 and 1 (those of 2 and 3 are read in the M
+        // slot, into the registers substeps 0 and 1 free: the X stage is reloaded only two slots after the M slot)
+#pragma unroll
+        for (int st = 0; st < SUB; ++st)
+#pragma unroll
+            for (int q = 0; q < 2; ++q)
+                b[st][q] = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(ws + (nbj[q] * SUB + st) * 1024 + 16 * lane);
+        read_x(0);
+        read_x(1);
+        // the reads are complete before the barrier (a stage is reloaded right after the barrier that follows them).
+        // Group B's X loads of step kt + 1 are due (group A reads them in the next slot); the loads issued after them
+        // stay in flight: this slot's stage loads, and the scales issued after the stage loads at this step and the
+        // step before. (Group A's older loads are complete already.)
+        __builtin_amdgcn_sched_barrier(0);
+        asm volatile("" ::: "memory");
+        {
+            constexpr bool prev_first = (j + 6 - 1) % SPG == 0;
+            wait_vm_lgkm0<LDG + (first ? 2 : 0) + (prev_first ? 2 : 0)>();
+        }
+        barrier();
+        // ---- M(kt): the step's MFMAs
+#pragma unroll
+        for (int st = 0; st < SUB; ++st) {
+#pragma unroll
+            for (int i = 0; i < MB; ++i)
+#pragma unroll
+                for (int q = 0; q < 2; ++q) {
+                    // a group's Horner rescale of each block right before its first MFMA of the group
+                    if constexpr (first)
+                        if (st == 0) acc[i][q] = acc[i][q] * ratio[q];
+                    acc[i][q] = mfma32<XT>(a[st % 2][i], b[st][q], acc[i][q]);
                 }
-            }
+            if (st + 2 < SUB) read_x(st + 2);
         }
-        return;
-    }
+        // in this order: substep 0's MFMAs (at a group's first step each after its block's 16 rescale multiplies: the
+        // multiplies of one block overlap the MFMA of the previous one), substep 2's X reads, substep 1's MFMAs,
+        // substep 3's X reads, the rest (each read has the next substep's MFMAs to hide behind)
+        if constexpr (first) {
 #pragma unroll
-    for (int i = 0; i < MB; ++i) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int row = m0 + wm * 32 * MB + i * 32 + 8 * (r / 4) + 4 * (lane / 32) + (r % 4);
-            if (row >= p.t) continue;
-            const float v0 = __fmul_rn(acc[i][0][r], e[0]), v1 = __fmul_rn(acc[i][1][r], e[1]);
-            if constexpr (EP == SEPAL_HIP_SWIGLU) {
-                const int f = n0 / 2 + 64 * ib + 32 * hh + lane % 32;
-                if (2 * f < p.n) store_out<YT>(p.y, static_cast<std::size_t>(row) * p.ld_y + f, swiglu_fast(v0, v1));
-            } else {
-                if (col[0] < p.n) put_plain<EP, YT>(p.y, static_cast<std::size_t>(row) * p.ld_y + col[0], v0);
-                if (col[1] < p.n) put_plain<EP, YT>(p.y, static_cast<std::size_t>(row) * p.ld_y + col[1], v1);
+            for (int q = 0; q < 2 * MB; ++q) {
+                __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
             }
+        } else {
+            __builtin_amdgcn_sched_group_barrier(0x008, 2 * MB, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x100, MB, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 2 * MB, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, MB, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 4 * MB, 0);
+        // group A's W loads of step kt + 1 are due (group A reads that stage in the next slot); group B's X loads of
+        // step kt + 2 complete here too, a slot before they are due
+        __builtin_amdgcn_sched_barrier(0);
+        asm volatile("" ::: "memory");
+        wait_vm_lgkm0<0>();
+        barrier();
+    };
+    constexpr int U = 3 * SPG;
+    const auto steps = [&]<int... J>(int k0, std::integer_sequence<int, J...>) __attribute__((always_inline)) {
+        (step(k0 + J, std::integral_constant<int, J>{}), ...);
+    };
+    int kt = 0;
+    for (; kt + U <= KT; kt += U) steps(kt, std::make_integer_sequence<int, U>{});
+    if (kt + SPG <= KT) {
+        steps(kt, std::make_integer_sequence<int, SPG>{});
+        if (kt + 2 * SPG <= KT) {
+            [&]<int... J>(std::integer_sequence<int, J...>) __attribute__((always_inline)) {
+                (step(kt + SPG + J, std::integral_constant<int, SPG + J>{}), ...);
+            }(std::make_integer_sequence<int, SPG>{});
         }
     }
+    if (!group_b) barrier();  // matches group B's extra barrier
+    wait_vmcnt<0>();          // no direct load may still be writing LDS when the block ends
+    tile_epilogue<EP, YT, MB>(p, acc, e, m0, n0, wave, lane);
 }
 
 template <int WN>
@@ -705,8 +1009,54 @@ inline int device_cus() {
 template <int XT, int EP, int YT, int MB, int SPLIT>
 void launch_big3(const BigParams& p, hipStream_t stream) {
     const int blocks = p.dense ? p.nsub * p.splits : p.count * (256 / (64 * MB));
-    if (p.splits > 1) v2::gemm_big3<XT, EP, YT, MB, SPLIT, true><<<dim3(blocks), dim3(512), 0, stream>>>(p);
-    else v2::gemm_big3<XT, EP, YT, MB, SPLIT, false><<<dim3(blocks), dim3(512), 0, stream>>>(p);
+    if (p.splits > 1) v2::gemm_big3<XT, EP, YT, MB, SPLIT, true, false><<<dim3(blocks), dim3(512), 0, stream>>>(p);
+    else if constexpr (MB >= 2) {
+        if (p.wimg != nullptr) v2::gemm_big3<XT, EP, YT, MB, SPLIT, false, true><<<dim3(blocks), dim3(512), 0, stream>>>(p);
+        else v2::gemm_big3<XT, EP, YT, MB, SPLIT, false, false><<<dim3(blocks), dim3(512), 0, stream>>>(p);
+    } else v2::gemm_big3<XT, EP, YT, MB, SPLIT, false, false><<<dim3(blocks), dim3(512), 0, stream>>>(p);
+}
+
+// The weight image of gemm_big3's WI form: for every 256-column tile tn and weight step ks (64 values of k), the 32 KB
+// W stage in the order the fragment reads use it. Kilobyte 4 nb + st holds n-block nb (32 columns) at substep st (16
+// values of k); in it, lane l's 16 bytes are column 32 nb + l % 32 at k 16 st + 8 (l / 32) .. + 7, widened exactly to
+// the MFMA type (the same values the waves would widen into the stage). Columns past N are zero. One thread widens 128
+// bytes of one weight row (two steps) into 16 chunks; the threads of a wave write 512 contiguous bytes at a time.
+template <int XT>
+__global__ void __launch_bounds__(256) widen_image_kernel(const signed char* __restrict__ w, std::size_t ld_w, int n,
+                                                          int wsteps, int tiles_n, unsigned char* __restrict__ img) {
+    const int pairs = wsteps / 2;
+    const std::size_t total = static_cast<std::size_t>(tiles_n) * pairs * 256;
+    for (std::size_t id = blockIdx.x * 256ull + threadIdx.x; id < total; id += static_cast<std::size_t>(gridDim.x) * 256) {
+        const int c = static_cast<int>(id % 32), nb = static_cast<int>((id / 32) % 8);
+        const int kp = static_cast<int>((id / 256) % pairs), tn = static_cast<int>(id / 256 / pairs);
+        const int row = tn * 256 + nb * 32 + c;
+        u32x4 v[8];
+        if (row < n) {
+            const u32x4* src = reinterpret_cast<const u32x4*>(w + static_cast<std::size_t>(row) * ld_w + 128 * kp);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] = src[i];
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] = u32x4{0u, 0u, 0u, 0u};
+        }
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            unsigned char* stage = img + (static_cast<std::size_t>(tn) * wsteps + 2 * kp + h) * 32768;
+#pragma unroll
+            for (int st = 0; st < 4; ++st) {
+                unsigned o[8];
+                widen16<XT>(v[4 * h + st], o);
+                *reinterpret_cast<u32x4*>(stage + (nb * 4 + st) * 1024 + c * 16) = u32x4{o[0], o[1], o[2], o[3]};
+                *reinterpret_cast<u32x4*>(stage + (nb * 4 + st) * 1024 + (c + 32) * 16) = u32x4{o[4], o[5], o[6], o[7]};
+            }
+        }
+    }
+}
+
+// Bytes of the weight image for an N x K multiply (0 when it would not fit 32-bit offsets).
+inline std::size_t image_bytes(std::size_t n, std::size_t k) {
+    const std::size_t b = (n + 255) / 256 * (k / 64) * 32768;
+    return b < (std::size_t{1} << 31) ? b : 0;
 }
 
 // Grids of fewer than two rounds of 256 x 256 tiles. The block tile is 64, 128 or 256 rows high (MB 1, 2, 4), and when
@@ -786,7 +1136,19 @@ void launch_big(const GemmArgs& a, hipStream_t stream) {
         p.tiles_n = tn256;
         p.id0 = 0;
         p.count = split ? full : total;
-        launch_big3<XT, EP, YT, 4, SPLIT>(p, stream);
+        // the weights widened once into the image (one streaming pass), then loaded straight into LDS by every tile
+        const std::size_t img = image_bytes(a.n, a.k);
+        if (a.wimage != nullptr && img != 0 && a.wimage_bytes >= img) {
+            p.wimg = static_cast<const unsigned char*>(a.wimage);
+            p.wimg_bytes = img;
+            p.wsteps = static_cast<int>(a.k / 64);
+            const std::size_t items = static_cast<std::size_t>(tn256) * (p.wsteps / 2) * 256;
+            widen_image_kernel<XT><<<static_cast<int>(std::min<std::size_t>((items + 255) / 256, 8192)), 256, 0, stream>>>(
+                reinterpret_cast<const signed char*>(a.w), a.ld_w, static_cast<int>(a.n), p.wsteps, tn256, static_cast<unsigned char*>(a.wimage));
+            check_launch("gemm_w8g weight image launch");
+        }
+        if (p.wimg != nullptr) v2::gemm_pp<XT, EP, YT, SPLIT><<<dim3(p.count), dim3(512), 0, stream>>>(p);
+        else launch_big3<XT, EP, YT, 4, SPLIT>(p, stream);
         if (split) {
             BigParams q = p;
             q.id0 = full;
@@ -969,6 +1331,13 @@ void launch_gemm_w8g(const GemmArgs& a, hipStream_t stream) {
     if (a.x_type == SEPAL_HIP_F32) w8g::launch_f32(a, stream);
     else if (a.x_type == SEPAL_HIP_BF16) w8g::dispatch_ep<SEPAL_HIP_BF16, 1>(a, stream);
     else w8g::dispatch_ep<SEPAL_HIP_F16, 1>(a, stream);
+}
+
+std::size_t gemm_w8g_image_bytes(const GemmArgs& a) {
+    if (a.t <= kSmallM) return 0;
+    const std::size_t tiles = (a.t + 255) / 256 * ((a.n + 255) / 256);
+    if (tiles < 2 * 256 || (a.epilogue == SEPAL_HIP_SWIGLU && a.n % 256 != 0)) return 0;
+    return w8g::image_bytes(a.n, a.k);
 }
 
 std::size_t gemm_w8g_scratch_bytes(const GemmArgs& a) {
