@@ -320,8 +320,9 @@ def main():
     dn_tflops = dn_flop / (ms_dn * 1e-3) / 1e12
     log(f"gate/up kernel {ms_gu:.3f} ms ({gu_tflops:.0f} TFLOP/s), down kernel {ms_dn:.3f} ms ({dn_tflops:.0f} TFLOP/s)")
     traffic = load_traffic()
-    roofline = {"bound": "mfma", "kernel": "w8g::v2::gemm_big3<bf16, SwiGLU, f16> (C3 gate/up, M 15872, N 19456, K 2560; "
-                "one call = 4608 tiles of 256x256 + the last round as 208 halves of 128x256)",
+    roofline = {"bound": "mfma", "kernel": "w8g::v2::gemm_pp<bf16, SwiGLU, f16> (C3 gate/up, M 15872, N 19456, K 2560; "
+                "one call = the weight image pass (widen_image_kernel) + 4608 tiles of 256x256 + the last round as "
+                "208 halves of 128x256)",
                 "achieved": round(gu_tflops, 1), "peak": PEAK["bf16_tflops"], "unit": "TFLOP/s",
                 "frac": round(gu_tflops / PEAK["bf16_tflops"], 4), "ms_per_launch": round(ms_gu, 4),
                 "algorithmic_flop_per_launch": gu_flop,

@@ -97,8 +97,8 @@ struct BigParams {
     // split-K launches run the live block tiles sub0 .. sub0 + nsub - 1 of the dense order: block tile s at rows
     // (s mod sub_m) BM3 and columns (s / sub_m) 256, sub_m = ceil(T / BM3)
     int dense = 0, sub_m = 0, sub0 = 0, nsub = 0;
-    // gemm_big3 with the weights from an image (WI): the widened W stage of 256-column tile tn and weight step ks (64
-    // values of k) is the 32 KB at wimg + (tn * wsteps + ks) * 32768, in the LDS order the fragment reads use
+    // gemm_pp: the widened W stage of 256-column tile tn and weight step ks (64 values of k) is the 32 KB at wimg +
+    // (tn * wsteps + ks) * 32768, in the LDS order the fragment reads use
     const unsigned char* wimg = nullptr;
     std::size_t wimg_bytes = 0;
     int wsteps = 0;
@@ -387,21 +387,18 @@ __device__ __forceinline__ void tile_epilogue(const BigParams& p, const f32x16 (
     }
 }
 
-template <int XT, int EP, int YT, int MB, int SPLIT, bool SK, bool WI>
+template <int XT, int EP, int YT, int MB, int SPLIT, bool SK>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) gemm_big3(const BigParams p) {
     // MB m-blocks of 32 rows per wave: tiles of BM3 = 64 MB rows (256, or 128 for the tail rows of a launch).
     // SK: split-K (the block's K range is its split of the groups; BigParams::splits).
     // SPLIT 2: X is a float32 operand as a bf16 hi + lo pair, stored as one bf16 row of 2K values (64-value chunk j of
     // k is chunk 2j (hi) and 2j + 1 (lo)); steps 2j and 2j + 1 multiply the same weights, so p.k counts the 2K values
     // and the weight offset of step kt is kt / 2 chunks.
-    // WI: the W stage of a step is loaded straight into LDS from the weight image (widen_image_kernel), one step ahead,
-    // instead of being loaded to registers two steps ahead and widened into the stage by the waves.
     static_assert(SPLIT == 1 || (SPLIT == 2 && XT == SEPAL_HIP_BF16), "the hi + lo form is bf16");
     constexpr int NW = 8, BN = 256, K3 = 64, SUB = K3 / 16, SPG = SPLIT * 128 / K3, BM3 = 64 * MB;
     constexpr int XSTAGE = BM3 * K3 * 2, WSTAGE = (BN / 32) * SUB * 1024;
     constexpr int XLD = XSTAGE / 16 / (64 * NW);       // X direct loads per thread per step (4)
     constexpr int WLD = BN * K3 / 16 / (64 * NW);      // W 16-byte chunks per thread per step (2)
-    constexpr int WLDI = WSTAGE / 16 / (64 * NW);      // WI: W direct loads per thread per step (4)
     __shared__ __align__(1024) unsigned char xs0[XSTAGE], xs1[XSTAGE], xs2[XSTAGE], ws0[WSTAGE], ws1[WSTAGE];
     const auto xstage = [&](auto it) -> lds_byte* {
         constexpr int i = decltype(it)::value;
@@ -452,8 +449,6 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
         const_cast<unsigned short*>(p.x), 0, static_cast<int>(p.x_bytes), 0x00020000);
     const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<signed char*>(p.w), 0, static_cast<int>(p.w_bytes), 0x00020000);
-    const __amdgpu_buffer_rsrc_t wires = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<unsigned char*>(p.wimg), 0, static_cast<int>(p.wimg_bytes), 0x00020000);
     // X: direct load i of wave w fills LDS kilobyte w + 8 i = rows 8 w + 64 i + {0..7}; lane l writes slot l % 8 of row
     // 8 w + 64 i + l / 8, which holds chunk (l % 8) ^ ((row / 2) & 7) = (l % 8) ^ ((4 w + l / 16) & 7)
     int xoff;
@@ -476,9 +471,9 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
         wdst0 = frag + 16 * (L ^ (2 * q));             // + 256 i
         wdst1 = frag + 16 * ((L + 32) ^ (2 * q + 1));  // + 256 i
     }
-    int rd[SUB];  // this lane's slot in a W fragment of substep st (the image keeps the fragments in lane order)
+    int rd[SUB];  // this lane's slot in a W fragment of substep st
 #pragma unroll
-    for (int st = 0; st < SUB; ++st) rd[st] = WI ? 16 * lane : 16 * (lane ^ ((2 * st + lane / 32) & 7));
+    for (int st = 0; st < SUB; ++st) rd[st] = 16 * (lane ^ ((2 * st + lane / 32) & 7));
 
     const int ib = wn / 2, hh = wn % 2;
     const int nbj[2] = {4 * ib + hh, 4 * ib + 2 + hh};
@@ -506,14 +501,6 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
         for (int i = 0; i < WLD; ++i)
             r.w[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wres, woff, ((kbase + kt) / SPLIT) * K3 + i * wstride, 0));
     };
-    // WI: direct load i of wave w fills kilobyte w + 8 i of the W stage from the same kilobyte of the image
-    const int wimg_tile = tn * p.wsteps;
-    const auto issue_wi = [&](int kt, lds_byte* wd) {
-#pragma unroll
-        for (int i = 0; i < WLDI; ++i)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(wires, (__attribute__((address_space(3))) void*)(wd + (wave + 8 * i) * 1024), 16,
-                                                     tid * 16, (wimg_tile + (kbase + kt) / SPLIT) * WSTAGE + i * 8192, 0, 0);
-    };
     const auto issue_scales = [&](int g) {
         snext[0] = ssrc[0][g0 + g];
         snext[1] = ssrc[1][g0 + g];
@@ -531,8 +518,7 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
     // earlier one, among them the next step's X
     const auto barrier = [&]() {
         asm volatile("" ::: "memory");
-        if constexpr (WI) wait_vm_lgkm0<XLD>();  // only the X loads of step kt + 2 stay in flight
-        else wait_vm_lgkm0<2 + XLD + WLD>();
+        wait_vm_lgkm0<2 + XLD + WLD>();
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
     };
@@ -553,18 +539,12 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
     issue_x(0, xstage(I0{}));
     issue_x(min(1, KT - 1), xstage(I1{}));
     __builtin_amdgcn_sched_barrier(0);
-    if constexpr (WI) {
-        issue_wi(0, wstage(I0{}));
-        asm volatile("" ::: "memory");
-        wait_vm_lgkm0<0>();
-    } else {
-        issue_w(0, r0);
-        issue_w(min(1, KT - 1), r1);
-        __builtin_amdgcn_sched_barrier(0);
-        stage_w(wstage(I0{}), r0);
-        asm volatile("" ::: "memory");
-        wait_vm_lgkm0<WLD>();  // everything but step 1's W (X of steps 0 and 1 included)
-    }
+    issue_w(0, r0);
+    issue_w(min(1, KT - 1), r1);
+    __builtin_amdgcn_sched_barrier(0);
+    stage_w(wstage(I0{}), r0);
+    asm volatile("" ::: "memory");
+    wait_vm_lgkm0<WLD>();  // everything but step 1's W (X of steps 0 and 1 included)
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     // the Horner state (the first step's factor multiplies zero accumulators)
@@ -590,90 +570,42 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
             }
             issue_scales(min(kt / SPG + 1, groups - 1));
         }
-        if constexpr (WI) {
-            // step kt + 1's W stage (last read by step kt - 1), then step kt + 2's X
-            issue_wi(min(kt + 1, KT - 1), wstage(std::integral_constant<int, (j + 1) % 2>{}));
-            __builtin_amdgcn_sched_barrier(0);
-        }
         issue_x(min(kt + 2, KT - 1), xstage(std::integral_constant<int, (j + 2) % 3>{}));
         __builtin_amdgcn_sched_barrier(0);
-        if constexpr (!WI) issue_w(min(kt + 2, KT - 1), r_free);
+        issue_w(min(kt + 2, KT - 1), r_free);
         // keep the loads at the top of the step, in this order: the wait for a step's operands then leaves the later
         // steps' loads in flight
         __builtin_amdgcn_sched_barrier(0);
-        if constexpr (WI) {
-            // the fragments double-buffered: substep st + 1's reads are issued before substep st's MFMAs, so their
-            // latency hides behind the MFMAs (the register budget allows it without the weight staging registers)
-            u32x4 a[2][MB], b[2][2];
-            const auto read_frags = [&](int st, int sl) {
 #pragma unroll
-                for (int i = 0; i < MB; ++i)
-                    a[sl][i] = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(xs + (wm * MB + i) * 4096 + rx[st]);
+        for (int st = 0; st < SUB; ++st) {
+            u32x4 a[MB], b[2];
 #pragma unroll
-                for (int q = 0; q < 2; ++q)
-                    b[sl][q] = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(ws + (nbj[q] * SUB + st) * 1024 + rd[st]);
-            };
-            read_frags(0, 0);
+            for (int i = 0; i < MB; ++i)
+                a[i] = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(xs + (wm * MB + i) * 4096 + rx[st]);
 #pragma unroll
-            for (int st = 0; st < SUB; ++st) {
-                if (st + 1 < SUB) read_frags(st + 1, (st + 1) % 2);
+            for (int q = 0; q < 2; ++q)
+                b[q] = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(ws + (nbj[q] * SUB + st) * 1024 + rd[st]);
 #pragma unroll
-                for (int i = 0; i < MB; ++i)
+            for (int i = 0; i < MB; ++i)
 #pragma unroll
-                    for (int q = 0; q < 2; ++q) {
-                        if constexpr (first)
-                            if (st == 0) acc[i][q] = acc[i][q] * ratio[q];
-                        acc[i][q] = mfma32<XT>(a[st % 2][i], b[st % 2][q], acc[i][q]);
-                    }
-            }
-            // in this order: substep 0's reads; per substep the next substep's reads, then its MFMAs (at a group's
-            // first step, substep 0's MFMAs each after its block's 16 rescale multiplies)
+                for (int q = 0; q < 2; ++q) {
+                    // a group's Horner rescale of each accumulator block right before its first MFMA of the group:
+                    // the multiplies of one block overlap the MFMA of the previous one
+                    if constexpr (first)
+                        if (st == 0) acc[i][q] = acc[i][q] * ratio[q];
+                    acc[i][q] = mfma32<XT>(a[i], b[q], acc[i][q]);
+                }
+        }
+        if constexpr (first) {
+            // the first substep's fragment reads, then each block's 16 rescale multiplies and its MFMA, in turn
             __builtin_amdgcn_sched_group_barrier(0x100, MB + 2, 0);
 #pragma unroll
-            for (int st = 0; st < SUB; ++st) {
-                if (st + 1 < SUB) __builtin_amdgcn_sched_group_barrier(0x100, MB + 2, 0);
-                if (first && st == 0) {
-#pragma unroll
-                    for (int q = 0; q < 2 * MB; ++q) {
-                        __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);
-                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                    }
-                } else {
-                    __builtin_amdgcn_sched_group_barrier(0x008, 2 * MB, 0);
-                }
-            }
-        } else {
-#pragma unroll
-            for (int st = 0; st < SUB; ++st) {
-                u32x4 a[MB], b[2];
-#pragma unroll
-                for (int i = 0; i < MB; ++i)
-                    a[i] = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(xs + (wm * MB + i) * 4096 + rx[st]);
-#pragma unroll
-                for (int q = 0; q < 2; ++q)
-                    b[q] = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(ws + (nbj[q] * SUB + st) * 1024 + rd[st]);
-#pragma unroll
-                for (int i = 0; i < MB; ++i)
-#pragma unroll
-                    for (int q = 0; q < 2; ++q) {
-                        // a group's Horner rescale of each accumulator block right before its first MFMA of the group:
-                        // the multiplies of one block overlap the MFMA of the previous one
-                        if constexpr (first)
-                            if (st == 0) acc[i][q] = acc[i][q] * ratio[q];
-                        acc[i][q] = mfma32<XT>(a[i], b[q], acc[i][q]);
-                    }
-            }
-            if constexpr (first) {
-                // the first substep's fragment reads, then each block's 16 rescale multiplies and its MFMA, in turn
-                __builtin_amdgcn_sched_group_barrier(0x100, MB + 2, 0);
-#pragma unroll
-                for (int q = 0; q < 2 * MB; ++q) {
-                    __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                }
+            for (int q = 0; q < 2 * MB; ++q) {
+                __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
             }
         }
-        if constexpr (!WI) stage_w(wstage(std::integral_constant<int, (j + 1) % 2>{}), r_next);
+        stage_w(wstage(std::integral_constant<int, (j + 1) % 2>{}), r_next);
         barrier();
     };
     // the loop body is three groups (6 SPLIT steps: a multiple of the 3 X stages and 2 W stages), then at most two
@@ -754,12 +686,12 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
 
 // ---- large-M kernel, two wave groups in alternation (gemm_pp) --------------------------------------------------------
 //
-// The tile, waves, outputs, k order and Horner chain of gemm_big3<MB = 4, WI> (so the same bits), scheduled so that the
+// The tile, waves, outputs, k order and Horner chain of gemm_big3<MB> (so the same bits), scheduled so that the
 // MFMA units, the LDS and the VALU work at the same time instead of in turn. Waves 0-3 (group A, one per SIMD) and
 // 4-7 (group B) each alternate two slots per 64-wide step, separated by block barriers: L(k) issues the stage loads
-// of a later step and reads 16 of step k's 24 operand fragments (every W fragment, X of substeps 0 and 1); M(k) issues
+// of a later step and reads 20 of step k's 24 operand fragments (every W fragment, X of substeps 0 to 2); M(k) issues
 // the step's 32 MFMAs (at a group's first step each block's Horner rescale right before its first MFMA) and reads X of
-// substeps 2 and 3 behind the MFMAs of substeps 0 and 1 (all 24 fragments at once would not fit the registers).
+// substep 3 behind the MFMAs of the earlier substeps (all 24 fragments at once would not fit the registers).
 // Group B runs one slot behind group A (one extra barrier at its start, one at A's end), so in every slot one wave of
 // each SIMD multiplies while the other mostly reads. Slot 2k: A L(k), B M(k - 1); slot 2k + 1: A M(k), B L(k). An X
 // stage is read until the end of group B's M(k), slot 2k + 2, and reloaded from slot 2k + 3.
@@ -767,12 +699,14 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
 // W loads (step k + 1 at the start of L(k), due by the barrier that ends slot 2k + 1), group B all X loads (step k + 2
 // at the start of its L(k), slot 2k + 1, due by the barrier that ends slot 2k + 3). A stage is reloaded only after
 // the barrier that follows both groups' reads of it, and every L slot waits for its reads before its barrier.
-template <int XT, int EP, int YT, int SPLIT>
+template <int XT, int EP, int YT, int MB, int SPLIT>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) gemm_pp(const BigParams p) {
+    // MB m-blocks of 32 rows per wave: tiles of BM3 = 64 MB rows (256, or 128 for the last round of a launch)
     static_assert(SPLIT == 1 || (SPLIT == 2 && XT == SEPAL_HIP_BF16), "the hi + lo form is bf16");
-    constexpr int MB = 4, BN = 256, K3 = 64, SUB = K3 / 16, SPG = SPLIT * 128 / K3;
-    constexpr int XSTAGE = 256 * K3 * 2, WSTAGE = (BN / 32) * SUB * 1024;
-    constexpr int LDG = XSTAGE / 1024 / 4;  // direct loads per wave of its group per step (8)
+    static_assert(MB == 4 || MB == 2, "256- or 128-row tiles");
+    constexpr int BN = 256, K3 = 64, SUB = K3 / 16, SPG = SPLIT * 128 / K3, BM3 = 64 * MB;
+    constexpr int XSTAGE = BM3 * K3 * 2, WSTAGE = (BN / 32) * SUB * 1024;
+    constexpr int LDGX = XSTAGE / 1024 / 4, LDGW = WSTAGE / 1024 / 4;  // direct loads per wave of B (X) / A (W) per step
     __shared__ __align__(1024) unsigned char xs0[XSTAGE], xs1[XSTAGE], xs2[XSTAGE], ws0[WSTAGE], ws1[WSTAGE];
     const auto xstage = [&](auto it) -> lds_byte* {
         constexpr int i = decltype(it)::value;
@@ -790,9 +724,19 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
     const int wg = wave % 4;            // the wave's index in its group
     const bool group_b = wave >= 4;
     const int wm = wave % 2, wn = wave / 2;
-    int tm, tn;
-    tile_from_id(p.id0 + xcd_id(blockIdx.x, p.count), p.tiles_m, p.tiles_n, tm, tn);
-    const int m0 = tm * 256, n0 = tn * BN;
+    // MB 4: one logical 256 x 256 tile per block; MB 2: block b is half b / count of tile id0 + b % count (a half wholly
+    // past T has nothing to do, and leaves before any barrier)
+    int tm, tn, m0;
+    if constexpr (MB == 4) {
+        tile_from_id(p.id0 + xcd_id(blockIdx.x, p.count), p.tiles_m, p.tiles_n, tm, tn);
+        m0 = tm * 256;
+    } else {
+        const int bb = blockIdx.x;
+        tile_from_id(p.id0 + bb % p.count, p.tiles_m, p.tiles_n, tm, tn);
+        m0 = tm * 256 + (bb / p.count) * BM3;
+        if (m0 >= p.t) return;
+    }
+    const int n0 = tn * BN;
     const int KT = p.k / K3, groups = KT / SPG;
 
     const __amdgpu_buffer_rsrc_t xres = __builtin_amdgcn_make_buffer_rsrc(
@@ -825,11 +769,13 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
     const __amdgpu_buffer_rsrc_t lres = group_b ? xres : wires;
     const int lvoff = group_b ? xoff : wg * 1024 + lane * 16;
     const int lstride = group_b ? xstride : 4096;
+    const int nld = group_b ? LDGX : LDGW;
     const auto issue = [&](int soff, lds_byte* dst) __attribute__((always_inline)) {
 #pragma unroll
-        for (int i = 0; i < LDG; ++i)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(lres, (__attribute__((address_space(3))) void*)(dst + (wg + 4 * i) * 1024), 16,
-                                                     lvoff, soff + i * lstride, 0, 0);
+        for (int i = 0; i < LDGW; ++i)
+            if (LDGX == LDGW || i < nld)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(lres, (__attribute__((address_space(3))) void*)(dst + (wg + 4 * i) * 1024), 16,
+                                                         lvoff, soff + i * lstride, 0, 0);
     };
     const auto x_soff = [&](int kt) __attribute__((always_inline)) { return kt * K3 * 2; };
     const auto w_soff = [&](int kt) __attribute__((always_inline)) { return (wimg_tile + kt / SPLIT) * WSTAGE; };
@@ -856,7 +802,7 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
     float e[2] = {1.0f, 1.0f}, emax[2] = {0.0f, 0.0f};
-    u32x4 a[2][MB], b[SUB][2];
+    u32x4 a[3][MB], b[SUB][2];  // X fragments of substeps 0, 1, 2 (then 3 in the first), W of every substep
 
     using I0 = std::integral_constant<int, 0>;
     using I1 = std::integral_constant<int, 1>;
@@ -888,20 +834,21 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
         // the next group's scales after the stage loads (needed two steps later)
         if constexpr (first) issue_scales(min(kt / SPG + 1, groups - 1));
         __builtin_amdgcn_sched_barrier(0);
-        const auto read_x = [&](int st) __attribute__((always_inline)) {
+        const auto read_x = [&](int st, int sl) __attribute__((always_inline)) {
 #pragma unroll
             for (int i = 0; i < MB; ++i)
-                a[st % 2][i] = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(xs + (wm * MB + i) * 4096 + rx[st]);
+                a[sl][i] = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(xs + (wm * MB + i) * 4096 + rx[st]);
         };
-        // every W fragment of the step and the X fragments of substeps 0 and 1 (those of 2 and 3 are read in the M
-        // slot, into the registers substeps 0 and 1 free: the X stage is reloaded only two slots after the M slot)
+        // every W fragment of the step and the X fragments of substeps 0, 1 and 2 (those of substep 3 are read in the
+        // M slot, into the registers substep 0 frees: the X stage is reloaded only two slots after the M slot)
 #pragma unroll
         for (int st = 0; st < SUB; ++st)
 #pragma unroll
             for (int q = 0; q < 2; ++q)
                 b[st][q] = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(ws + (nbj[q] * SUB + st) * 1024 + 16 * lane);
-        read_x(0);
-        read_x(1);
+        read_x(0, 0);
+        read_x(1, 1);
+        read_x(2, 2);
         // the reads are complete before the barrier (a stage is reloaded right after the barrier that follows them).
         // Group B's X loads of step kt + 1 are due (group A reads them in the next slot); the loads issued after them
         // stay in flight: this slot's stage loads, and the scales issued after the stage loads at this step and the
@@ -910,39 +857,57 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
         asm volatile("" ::: "memory");
         {
             constexpr bool prev_first = (j + 6 - 1) % SPG == 0;
-            wait_vm_lgkm0<LDG + (first ? 2 : 0) + (prev_first ? 2 : 0)>();
+            constexpr int later = (first ? 2 : 0) + (prev_first ? 2 : 0);
+            if constexpr (LDGX == LDGW) {
+                wait_vm_lgkm0<LDGX + later>();
+            } else {
+                if (group_b) wait_vm_lgkm0<LDGX + later>();
+                else wait_vm_lgkm0<LDGW + later>();
+            }
         }
         barrier();
-        // ---- M(kt): the step's MFMAs
-#pragma unroll
-        for (int st = 0; st < SUB; ++st) {
-#pragma unroll
-            for (int i = 0; i < MB; ++i)
-#pragma unroll
-                for (int q = 0; q < 2; ++q) {
-                    // a group's Horner rescale of each block right before its first MFMA of the group
-                    if constexpr (first)
-                        if (st == 0) acc[i][q] = acc[i][q] * ratio[q];
-                    acc[i][q] = mfma32<XT>(a[st % 2][i], b[st][q], acc[i][q]);
-                }
-            if (st + 2 < SUB) read_x(st + 2);
-        }
-        // in this order: substep 0's MFMAs (at a group's first step each after its block's 16 rescale multiplies: the
-        // multiplies of one block overlap the MFMA of the previous one), substep 2's X reads, substep 1's MFMAs,
-        // substep 3's X reads, the rest (each read has the next substep's MFMAs to hide behind)
+        // ---- M(kt): the step's MFMAs; block bl = (i, q) = (bl / 2, bl % 2)
+        const auto mma = [&](int bl, int st, int sl) __attribute__((always_inline)) {
+            acc[bl / 2][bl % 2] = mfma32<XT>(a[sl][bl / 2], b[st][bl % 2], acc[bl / 2][bl % 2]);
+        };
         if constexpr (first) {
+            // each block's Horner rescale, then its substep 0 MFMA and the previous block's substep 1 MFMA: the two
+            // MFMAs cover the next block's 16 multiplies
 #pragma unroll
-            for (int q = 0; q < 2 * MB; ++q) {
-                __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            for (int bl = 0; bl < 2 * MB; ++bl) {
+                acc[bl / 2][bl % 2] = acc[bl / 2][bl % 2] * ratio[bl % 2];
+                mma(bl, 0, 0);
+                if (bl > 0) mma(bl - 1, 1, 1);
             }
+            mma(2 * MB - 1, 1, 1);
+            read_x(3, 0);
+#pragma unroll
+            for (int bl = 0; bl < 2 * MB; ++bl) mma(bl, 2, 2);
+#pragma unroll
+            for (int bl = 0; bl < 2 * MB; ++bl) mma(bl, 3, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+#pragma unroll
+            for (int bl = 1; bl < 2 * MB; ++bl) {
+                __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, MB, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 4 * MB, 0);
         } else {
+            // substep 0, then substep 3's X reads behind substeps 1 and 2
+#pragma unroll
+            for (int bl = 0; bl < 2 * MB; ++bl) mma(bl, 0, 0);
+            read_x(3, 0);
+#pragma unroll
+            for (int st = 1; st < SUB; ++st)
+#pragma unroll
+                for (int bl = 0; bl < 2 * MB; ++bl) mma(bl, st, st % 3);
             __builtin_amdgcn_sched_group_barrier(0x008, 2 * MB, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, MB, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 6 * MB, 0);
         }
-        __builtin_amdgcn_sched_group_barrier(0x100, MB, 0);
-        __builtin_amdgcn_sched_group_barrier(0x008, 2 * MB, 0);
-        __builtin_amdgcn_sched_group_barrier(0x100, MB, 0);
-        __builtin_amdgcn_sched_group_barrier(0x008, 4 * MB, 0);
         // group A's W loads of step kt + 1 are due (group A reads that stage in the next slot); group B's X loads of
         // step kt + 2 complete here too, a slot before they are due
         __builtin_amdgcn_sched_barrier(0);
@@ -1009,14 +974,11 @@ inline int device_cus() {
 template <int XT, int EP, int YT, int MB, int SPLIT>
 void launch_big3(const BigParams& p, hipStream_t stream) {
     const int blocks = p.dense ? p.nsub * p.splits : p.count * (256 / (64 * MB));
-    if (p.splits > 1) v2::gemm_big3<XT, EP, YT, MB, SPLIT, true, false><<<dim3(blocks), dim3(512), 0, stream>>>(p);
-    else if constexpr (MB >= 2) {
-        if (p.wimg != nullptr) v2::gemm_big3<XT, EP, YT, MB, SPLIT, false, true><<<dim3(blocks), dim3(512), 0, stream>>>(p);
-        else v2::gemm_big3<XT, EP, YT, MB, SPLIT, false, false><<<dim3(blocks), dim3(512), 0, stream>>>(p);
-    } else v2::gemm_big3<XT, EP, YT, MB, SPLIT, false, false><<<dim3(blocks), dim3(512), 0, stream>>>(p);
+    if (p.splits > 1) v2::gemm_big3<XT, EP, YT, MB, SPLIT, true><<<dim3(blocks), dim3(512), 0, stream>>>(p);
+    else v2::gemm_big3<XT, EP, YT, MB, SPLIT, false><<<dim3(blocks), dim3(512), 0, stream>>>(p);
 }
 
-// The weight image of gemm_big3's WI form: for every 256-column tile tn and weight step ks (64 values of k), the 32 KB
+// The weight image of gemm_pp: for every 256-column tile tn and weight step ks (64 values of k), the 32 KB
 // W stage in the order the fragment reads use it. Kilobyte 4 nb + st holds n-block nb (32 columns) at substep st (16
 // values of k); in it, lane l's 16 bytes are column 32 nb + l % 32 at k 16 st + 8 (l / 32) .. + 7, widened exactly to
 // the MFMA type (the same values the waves would widen into the stage). Columns past N are zero. One thread widens 128
@@ -1147,13 +1109,14 @@ void launch_big(const GemmArgs& a, hipStream_t stream) {
                 reinterpret_cast<const signed char*>(a.w), a.ld_w, static_cast<int>(a.n), p.wsteps, tn256, static_cast<unsigned char*>(a.wimage));
             check_launch("gemm_w8g weight image launch");
         }
-        if (p.wimg != nullptr) v2::gemm_pp<XT, EP, YT, SPLIT><<<dim3(p.count), dim3(512), 0, stream>>>(p);
+        if (p.wimg != nullptr) v2::gemm_pp<XT, EP, YT, 4, SPLIT><<<dim3(p.count), dim3(512), 0, stream>>>(p);
         else launch_big3<XT, EP, YT, 4, SPLIT>(p, stream);
         if (split) {
             BigParams q = p;
             q.id0 = full;
             q.count = rest;
-            launch_big3<XT, EP, YT, 2, SPLIT>(q, stream);
+            if (q.wimg != nullptr) v2::gemm_pp<XT, EP, YT, 2, SPLIT><<<dim3(2 * q.count), dim3(512), 0, stream>>>(q);
+            else launch_big3<XT, EP, YT, 2, SPLIT>(q, stream);
         }
     } else if (takes && !wide) {
         // fewer than two rounds of 256 x 256 tiles: the plan's tile height and K split
