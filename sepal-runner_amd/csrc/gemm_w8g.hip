@@ -1100,7 +1100,9 @@ void launch_big(const GemmArgs& a, hipStream_t stream) {
         p.count = split ? full : total;
         // the weights widened once into the image (one streaming pass), then loaded straight into LDS by every tile
         const std::size_t img = image_bytes(a.n, a.k);
-        if (a.wimage != nullptr && img != 0 && a.wimage_bytes >= img) {
+        // (gemm_pp reads the scales through a buffer descriptor with 32-bit offsets)
+        const bool scales32 = a.n * a.ld_s * 4 < (std::size_t{1} << 31);
+        if (a.wimage != nullptr && img != 0 && a.wimage_bytes >= img && scales32) {
             p.wimg = static_cast<const unsigned char*>(a.wimage);
             p.wimg_bytes = img;
             p.wsteps = static_cast<int>(a.k / 64);
