@@ -466,6 +466,43 @@ def test_w8g_swiglu_narrow_tiles_match_wide(sm):
     assert same_bits(y[:, :128], y256)
 
 
+@pytest.mark.parametrize("shape", [(2100, 16384, 640, "swiglu", "bf16"), (2100, 16384, 384, "store", "f32"),
+                                   (2400, 14992, 640, "add", "f16")])
+def test_w8g_image_kernel_step_tails(sm, shape):
+    """The large grids (at least two rounds of 256 x 256 tiles) run on the weight image with two wave groups in
+    alternation, whose loop body is six 64-wide steps: K of 5 groups (10 steps: one body and a two-group tail) and of 3
+    groups in the hi + lo form (12 steps), ragged rows and columns; every element against float64 of the dequantized
+    weights."""
+    t, n, k, ep, xdt = shape
+    rng = np.random.default_rng(t + n + k)
+    if xdt == "f32":
+        x = rng.standard_normal((t, k)).astype(np.float32)
+        xt = dev(x)
+    else:
+        dt = torch.bfloat16 if xdt == "bf16" else torch.float16
+        x = bf16_inputs(rng, (t, k))
+        xt = dev(x, dt)
+    w = (rng.standard_normal((n, k)) / np.sqrt(k)).astype(np.float32)
+    q, s = orc.quantize_group_r1(w)
+    qt, st = dev(q), dev(s)
+    ref = _deq_ref(xt.float(), qt, st, k)
+    say("w8g image kernel step tails", shape)
+    if ep == "swiglu":
+        f = torch.arange(n // 2, device=ref.device)
+        g, u = ref[:, 128 * (f // 64) + f % 64], ref[:, 128 * (f // 64) + 64 + f % 64]
+        y = host(sm.gemm_w8g(xt, qt, st, epilogue=sm.SWIGLU))
+        ref = host(g * torch.sigmoid(g) * u)
+    elif ep == "store":
+        y = host(sm.gemm_w8g(xt, qt, st))
+        ref = host(ref)
+    else:
+        base = torch.from_numpy(rng.standard_normal((t, n)).astype(np.float32)).cuda()
+        ya = base.clone()
+        sm.gemm_w8g(xt, qt, st, y=ya, epilogue=sm.ADD)
+        y, ref = host(ya), host(base.double() + ref)
+    assert max_rel_over_rms(y, ref) < 2e-3 and rel_rms(y, ref) < 1e-5, (max_rel_over_rms(y, ref), rel_rms(y, ref))
+
+
 # ---- float32 X (the reference's operand type, launch_gemm_simt(const float* x, ...)) ---------------------------------
 
 # (t, n, k, epilogue, config): the one-pass hi + lo kernel (64 x 256 quarters), the small-M path (two bf16 multiplies,
