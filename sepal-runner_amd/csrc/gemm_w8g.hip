@@ -786,10 +786,8 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
     };
     const auto barrier = [&]() __attribute__((always_inline)) {
         __builtin_amdgcn_sched_barrier(0);
-        __builtin_amdgcn_sched_barrier(0);
         asm volatile("" ::: "memory");
         __builtin_amdgcn_s_barrier();
-        __builtin_amdgcn_sched_barrier(0);
         asm volatile("" ::: "memory");
         __builtin_amdgcn_sched_barrier(0);
     };
@@ -849,22 +847,12 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
         read_x(0, 0);
         read_x(1, 1);
         read_x(2, 2);
-        // the reads are complete before the barrier (a stage is reloaded right after the barrier that follows them).
-        // Group B's X loads of step kt + 1 are due (group A reads them in the next slot); the loads issued after them
-        // stay in flight: this slot's stage loads, and the scales issued after the stage loads at this step and the
-        // step before. (Group A's older loads are complete already.)
+        // the reads are complete before the barrier (a stage is reloaded right after the barrier that follows them);
+        // this slot's stage loads and scales stay in flight (every older load completed at the end of the wave's
+        // previous M slot)
         __builtin_amdgcn_sched_barrier(0);
         asm volatile("" ::: "memory");
-        {
-            constexpr bool prev_first = (j + 6 - 1) % SPG == 0;
-            constexpr int later = (first ? 2 : 0) + (prev_first ? 2 : 0);
-            if constexpr (LDGX == LDGW) {
-                wait_vm_lgkm0<LDGX + later>();
-            } else {
-                if (group_b) wait_vm_lgkm0<LDGX + later>();
-                else wait_vm_lgkm0<LDGW + later>();
-            }
-        }
+        wait_vm_lgkm0<63>();
         barrier();
         // ---- M(kt): the step's MFMAs; block bl = (i, q) = (bl / 2, bl % 2)
         const auto mma = [&](int bl, int st, int sl) __attribute__((always_inline)) {
