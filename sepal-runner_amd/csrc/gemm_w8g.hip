@@ -336,14 +336,63 @@ __device__ __forceinline__ void wait_vm_lgkm0() {
 
 // The epilogue of a 256-column tile of the large-M kernels: wave `wave` holds MB x 2 blocks of 32 x 32 outputs (rows
 // m0 + 32 MB wm + 32 i.., columns n0 + 32 nbj[q]..), its Horner state e, and applies the last scale and the epilogue.
-template <int EP, int YT, int MB>
-__device__ __forceinline__ void tile_epilogue(const BigParams& p, const f32x16 (&acc)[MB][2], const float (&e)[2], int m0, int n0,
+// OVERLAP (the persistent gemm_pp, whose next tile's first loads are in flight): a whole tile's values are computed
+// first, in place, then the wave waits for its loads and issues the stores, which the next tile does not wait for;
+// an edge tile waits for the loads, stores, and waits for its stores. Plain Add epilogues read y, so they keep the
+// interleaved form.
+template <int EP, int YT, int MB, bool OVERLAP = false>
+__device__ __forceinline__ void tile_epilogue(const BigParams& p, f32x16 (&acc)[MB][2], const float (&e)[2], int m0, int n0,
                                               int wave, int lane) {
     constexpr int BM3 = 64 * MB, BN = 256;
     const int wm = wave % 2, wn = wave / 2, ib = wn / 2, hh = wn % 2;
     const int col[2] = {n0 + 32 * (4 * ib + hh) + lane % 32, n0 + 32 * (4 * ib + 2 + hh) + lane % 32};
     // A whole tile needs no bounds checks: the row and the wave's column base are wave-uniform (scalar registers) and
     // the lane adds a 32-bit offset, so a store costs no vector address arithmetic.
+    if constexpr (OVERLAP && EP != SEPAL_HIP_ADD) {
+        if (m0 + BM3 <= p.t && n0 + BN <= p.n) {
+            constexpr unsigned ES = YT == SEPAL_HIP_F32 ? 4 : 2;
+#pragma unroll
+            for (int i = 0; i < MB; ++i)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const float v0 = __fmul_rn(acc[i][0][r], e[0]), v1 = __fmul_rn(acc[i][1][r], e[1]);
+                    if constexpr (EP == SEPAL_HIP_SWIGLU) {
+                        acc[i][0][r] = swiglu_fast(v0, v1);
+                    } else {
+                        acc[i][0][r] = v0;
+                        acc[i][1][r] = v1;
+                    }
+                }
+            // the next tile's first loads (issued before this epilogue) are complete before the stores are queued
+            __builtin_amdgcn_sched_barrier(0);
+            asm volatile("" ::: "memory");
+            wait_vmcnt<0>();
+            asm volatile("" ::: "memory");
+            __builtin_amdgcn_sched_barrier(0);
+            const int wu = __builtin_amdgcn_readfirstlane(wave);
+            const int wmu = wu % 2, ibu = (wu / 2) / 2, hhu = (wu / 2) % 2;
+            const unsigned voff = (4u * static_cast<unsigned>(lane / 32) * static_cast<unsigned>(p.ld_y) + lane % 32) * ES;
+            char* const yb = static_cast<char*>(p.y);
+#pragma unroll
+            for (int i = 0; i < MB; ++i) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const std::size_t row = static_cast<std::size_t>(m0 + wmu * 32 * MB + i * 32 + 8 * (r / 4) + (r % 4));
+                    if constexpr (EP == SEPAL_HIP_SWIGLU) {
+                        char* const rp = yb + (row * p.ld_y + n0 / 2 + 64 * ibu + 32 * hhu) * ES;
+                        store_out<YT>(rp + voff, 0, acc[i][0][r]);
+                    } else {
+                        char* const rp0 = yb + (row * p.ld_y + n0 + 32 * (4 * ibu + hhu)) * ES;
+                        char* const rp1 = yb + (row * p.ld_y + n0 + 32 * (4 * ibu + 2 + hhu)) * ES;
+                        put_plain<EP, YT>(rp0 + voff, 0, acc[i][0][r]);
+                        put_plain<EP, YT>(rp1 + voff, 0, acc[i][1][r]);
+                    }
+                }
+            }
+            return;
+        }
+    }
+    if constexpr (OVERLAP) wait_vmcnt<0>();
     if (m0 + BM3 <= p.t && n0 + BN <= p.n) {
         constexpr unsigned ES = YT == SEPAL_HIP_F32 ? 4 : 2;
         const int wu = __builtin_amdgcn_readfirstlane(wave);
@@ -367,6 +416,7 @@ __device__ __forceinline__ void tile_epilogue(const BigParams& p, const f32x16 (
                 }
             }
         }
+        if constexpr (OVERLAP) wait_vmcnt<0>();
         return;
     }
 #pragma unroll
@@ -385,6 +435,7 @@ __device__ __forceinline__ void tile_epilogue(const BigParams& p, const f32x16 (
             }
         }
     }
+    if constexpr (OVERLAP) wait_vmcnt<0>();
 }
 
 template <int XT, int EP, int YT, int MB, int SPLIT, bool SK>
@@ -695,7 +746,9 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
 // Group B runs one slot behind group A (one extra barrier at its start, one at A's end), so in every slot one wave of
 // each SIMD multiplies while the other mostly reads. Slot 2k: A L(k), B M(k - 1); slot 2k + 1: A M(k), B L(k). An X
 // stage is read until the end of group B's M(k), slot 2k + 2, and reloaded from slot 2k + 3.
-// Stages: X of step k in X stage k mod 3, W of step k in W stage k mod 2 (from the weight image). Group A issues all
+// The full-tile launch is persistent (one block per CU over its XCD's tiles; the next tile's first loads are issued
+// before the current tile's epilogue). Stages: X of step k in X stage k mod 3, W of step k in W stage k mod 2 (from
+// the weight image). Group A issues all
 // W loads (step k + 1 at the start of L(k), due by the barrier that ends slot 2k + 1), group B all X loads (step k + 2
 // at the start of its L(k), slot 2k + 1, due by the barrier that ends slot 2k + 3). A stage is reloaded only after
 // the barrier that follows both groups' reads of it, and every L slot waits for its reads before its barrier.
@@ -724,19 +777,33 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
     const int wg = wave % 4;            // the wave's index in its group
     const bool group_b = wave >= 4;
     const int wm = wave % 2, wn = wave / 2;
-    // MB 4: one logical 256 x 256 tile per block; MB 2: block b is half b / count of tile id0 + b % count (a half wholly
-    // past T has nothing to do, and leaves before any barrier)
-    int tm, tn, m0;
+    // MB 4 (persistent): one block per CU; block b works through the contiguous range [lo, hi) of logical tiles of its
+    // XCD (b mod 8), every (gridDim.x / 8)-th from lo + b / 8, so the XCD's blocks run consecutive tiles at a time
+    // (they share its L2). MB 2: block b is half b / count of tile id0 + b % count (a half wholly past T has nothing to
+    // do, and leaves before any barrier).
+    int tm, tn, m0, n0, cur = 0, stride = 1, hi = 1;
     if constexpr (MB == 4) {
-        tile_from_id(p.id0 + xcd_id(blockIdx.x, p.count), p.tiles_m, p.tiles_n, tm, tn);
-        m0 = tm * 256;
-    } else {
-        const int bb = blockIdx.x;
-        tile_from_id(p.id0 + bb % p.count, p.tiles_m, p.tiles_n, tm, tn);
-        m0 = tm * 256 + (bb / p.count) * BM3;
-        if (m0 >= p.t) return;
+        const int nx = static_cast<int>(gridDim.x) / 8, xcd = blockIdx.x % 8;
+        const int q = p.count / 8, r = p.count % 8;
+        const int lo = xcd * q + min(xcd, r);
+        hi = lo + q + (xcd < r ? 1 : 0);
+        cur = lo + static_cast<int>(blockIdx.x) / 8;
+        stride = nx;
+        if (cur >= hi) return;
     }
-    const int n0 = tn * BN;
+    const auto tile_at = [&](int id) __attribute__((always_inline)) {
+        if constexpr (MB == 4) {
+            tile_from_id(p.id0 + id, p.tiles_m, p.tiles_n, tm, tn);
+            m0 = tm * 256;
+        } else {
+            const int bb = blockIdx.x;
+            tile_from_id(p.id0 + bb % p.count, p.tiles_m, p.tiles_n, tm, tn);
+            m0 = tm * 256 + (bb / p.count) * BM3;
+        }
+        n0 = tn * BN;
+    };
+    tile_at(cur);
+    if (m0 >= p.t) return;
     const int KT = p.k / K3, groups = KT / SPG;
 
     const __amdgpu_buffer_rsrc_t xres = __builtin_amdgcn_make_buffer_rsrc(
@@ -745,11 +812,7 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
         const_cast<unsigned char*>(p.wimg), 0, static_cast<int>(p.wimg_bytes), 0x00020000);
     // X (group B): direct load i of group wave g fills LDS kilobyte g + 4 i = rows 8 g + 32 i + {0..7}; lane l writes
     // slot l % 8 of row 8 g + 32 i + l / 8, which holds chunk (l % 8) ^ ((row / 2) & 7) = (l % 8) ^ ((4 g + l / 16) & 7)
-    int xoff;
-    {
-        const int r = 8 * wg + lane / 8, c = (lane % 8) ^ ((4 * wg + lane / 16) & 7);
-        xoff = (m0 + r) * static_cast<int>(p.ld_x) * 2 + 16 * c;
-    }
+    const int xrow = 8 * wg + lane / 8, xchunk = (lane % 8) ^ ((4 * wg + lane / 16) & 7);
     const int xstride = 32 * static_cast<int>(p.ld_x) * 2;
     int rx[SUB];
 #pragma unroll
@@ -760,14 +823,19 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
     const __amdgpu_buffer_rsrc_t sres = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<float*>(p.s), 0, static_cast<int>(static_cast<std::size_t>(p.n) * p.ld_s * 4), 0x00020000);
     // (columns past N read as 0: a zero scale keeps the Horner state; the second column is 64 columns on)
-    const int soff = (n0 + 32 * nbj[0] + lane % 32) * static_cast<int>(p.ld_s) * 4;
     const int soff1 = 64 * static_cast<int>(p.ld_s) * 4;
 
     // The wave's load role, chosen once (no branch in the loop): group B loads X, group A the weight image. Load i of
     // group wave g fills LDS kilobyte g + 4 i of the stage.
-    const int wimg_tile = tn * p.wsteps;
+    // the tile's offsets (set_tile)
+    int wimg_tile, lvoff, soff;
+    const auto set_tile = [&]() __attribute__((always_inline)) {
+        wimg_tile = tn * p.wsteps;
+        lvoff = group_b ? (m0 + xrow) * static_cast<int>(p.ld_x) * 2 + 16 * xchunk : wg * 1024 + lane * 16;
+        soff = (n0 + 32 * nbj[0] + lane % 32) * static_cast<int>(p.ld_s) * 4;
+    };
+    set_tile();
     const __amdgpu_buffer_rsrc_t lres = group_b ? xres : wires;
-    const int lvoff = group_b ? xoff : wg * 1024 + lane * 16;
     const int lstride = group_b ? xstride : 4096;
     const int nld = group_b ? LDGX : LDGW;
     const auto issue = [&](int soff, lds_byte* dst) __attribute__((always_inline)) {
@@ -793,27 +861,23 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
     };
 
     f32x16 acc[MB][2];
-#pragma unroll
-    for (int i = 0; i < MB; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-    float e[2] = {1.0f, 1.0f}, emax[2] = {0.0f, 0.0f};
+    float e[2], emax[2];
     u32x4 a[3][MB], b[SUB][2];  // X fragments of substeps 0, 1, 2 (then 3 in the first), W of every substep
 
     using I0 = std::integral_constant<int, 0>;
     using I1 = std::integral_constant<int, 1>;
-    issue_scales(0);
-    if (group_b) {
-        issue(x_soff(0), xstage(I0{}));
-        issue(x_soff(min(1, KT - 1)), xstage(I1{}));
-    } else {
-        issue(w_soff(0), wstage(I0{}));
-    }
+    // a tile's first loads: the first group's scales, X of steps 0 and 1 (group B), W of step 0 (group A)
+    const auto first_loads = [&]() __attribute__((always_inline)) {
+        issue_scales(0);
+        if (group_b) {
+            issue(x_soff(0), xstage(I0{}));
+            issue(x_soff(min(1, KT - 1)), xstage(I1{}));
+        } else {
+            issue(w_soff(0), wstage(I0{}));
+        }
+    };
+    first_loads();
     wait_vm_lgkm0<0>();
-    barrier();
-    if (group_b) barrier();  // B runs one slot behind A
 
     // Step kt (j = kt mod 6): slot L then slot M, each ended by a barrier.
     const auto step = [&](int kt, auto jt) __attribute__((always_inline)) {
@@ -907,19 +971,43 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
     const auto steps = [&]<int... J>(int k0, std::integer_sequence<int, J...>) __attribute__((always_inline)) {
         (step(k0 + J, std::integral_constant<int, J>{}), ...);
     };
-    int kt = 0;
-    for (; kt + U <= KT; kt += U) steps(kt, std::make_integer_sequence<int, U>{});
-    if (kt + SPG <= KT) {
-        steps(kt, std::make_integer_sequence<int, SPG>{});
-        if (kt + 2 * SPG <= KT) {
-            [&]<int... J>(std::integer_sequence<int, J...>) __attribute__((always_inline)) {
-                (step(kt + SPG + J, std::integral_constant<int, SPG + J>{}), ...);
-            }(std::make_integer_sequence<int, SPG>{});
+    // Tile loop. Per tile the barriers balance: group A 1 + 2 KT + 1, group B 1 + 1 + 2 KT. After the last one every
+    // wave has read the tile's stages for the last time and waited for every load it issued, so the next tile's first
+    // loads go out before this tile's epilogue, whose values are computed while they fly (MB 4).
+    for (;;) {
+#pragma unroll
+        for (int i = 0; i < MB; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+        e[0] = e[1] = 1.0f;
+        emax[0] = emax[1] = 0.0f;
+        barrier();
+        if (group_b) barrier();  // B runs one slot behind A
+        int kt = 0;
+        for (; kt + U <= KT; kt += U) steps(kt, std::make_integer_sequence<int, U>{});
+        if (kt + SPG <= KT) {
+            steps(kt, std::make_integer_sequence<int, SPG>{});
+            if (kt + 2 * SPG <= KT) {
+                [&]<int... J>(std::integer_sequence<int, J...>) __attribute__((always_inline)) {
+                    (step(kt + SPG + J, std::integral_constant<int, SPG + J>{}), ...);
+                }(std::make_integer_sequence<int, SPG>{});
+            }
         }
+        if (!group_b) barrier();  // matches group B's extra barrier
+        const int mc = m0, nc = n0;
+        cur += stride;
+        const bool more = MB == 4 && cur < hi;
+        if (more) {
+            tile_at(cur);
+            set_tile();
+            first_loads();
+        }
+        if constexpr (MB == 4) tile_epilogue<EP, YT, MB, true>(p, acc, e, mc, nc, wave, lane);
+        else tile_epilogue<EP, YT, MB>(p, acc, e, mc, nc, wave, lane);
+        if (!more) break;
     }
-    if (!group_b) barrier();  // matches group B's extra barrier
-    wait_vmcnt<0>();          // no direct load may still be writing LDS when the block ends
-    tile_epilogue<EP, YT, MB>(p, acc, e, m0, n0, wave, lane);
 }
 
 template <int WN>
@@ -1099,7 +1187,11 @@ void launch_big(const GemmArgs& a, hipStream_t stream) {
                 reinterpret_cast<const signed char*>(a.w), a.ld_w, static_cast<int>(a.n), p.wsteps, tn256, static_cast<unsigned char*>(a.wimage));
             check_launch("gemm_w8g weight image launch");
         }
-        if (p.wimg != nullptr) v2::gemm_pp<XT, EP, YT, 4, SPLIT><<<dim3(p.count), dim3(512), 0, stream>>>(p);
+        if (p.wimg != nullptr) {
+            // persistent: one block per CU (a multiple of the 8 XCDs)
+            const int grid = std::min(p.count, std::max(8, cus / 8 * 8));
+            v2::gemm_pp<XT, EP, YT, 4, SPLIT><<<dim3(grid), dim3(512), 0, stream>>>(p);
+        }
         else launch_big3<XT, EP, YT, 4, SPLIT>(p, stream);
         if (split) {
             BigParams q = p;
