@@ -68,6 +68,10 @@ struct Workspace {
     void* ptr = nullptr;
     std::size_t bytes = 0;
 };
+__global__ void zero_words_kernel(unsigned* p, std::size_t n) {
+    for (std::size_t i = blockIdx.x * 256ull + threadIdx.x; i < n; i += static_cast<std::size_t>(gridDim.x) * 256) p[i] = 0u;
+}
+
 std::mutex g_ws_mutex;
 std::map<std::pair<int, hipStream_t>, std::unique_ptr<Workspace>> g_ws;
 
@@ -94,7 +98,13 @@ Lease::Lease(std::size_t bytes, hipStream_t stream) {
         }
         const std::size_t grown = bytes < (std::size_t{64} << 20) ? (std::size_t{64} << 20) : bytes;
         if (hipMalloc(&w->ptr, grown) != hipSuccess) throw std::bad_alloc();
-        if (hipMemset(w->ptr, 0, grown) != hipSuccess) throw LaunchError("hipMemset of the workspace failed");
+        // The split-K counters must be zero before the first kernel that uses them. hipMemset would run on the null
+        // stream, which a non-blocking caller stream does not wait for (its first kernel could count in while the
+        // zeros are still being written, and a span's last block would never see the full count); a fill kernel on
+        // the workspace's own stream is ordered before every later use. (Only the counter zone needs zeros: every
+        // partial is written before it is read.)
+        zero_words_kernel<<<dim3(64), dim3(256), 0, stream>>>(static_cast<unsigned*>(w->ptr), kCounterBytes / 4);
+        if (hipGetLastError() != hipSuccess) throw LaunchError("the workspace's counter fill failed to launch");
         w->bytes = grown;
     }
     base_ = static_cast<char*>(w->ptr);
@@ -662,7 +672,12 @@ StackZones stack_zones(int kind, std::size_t t, std::size_t hidden, std::size_t 
     gu.k = dn.n = hidden;
     dn.k = inter;
     gu.epilogue = SEPAL_HIP_SWIGLU;
-    z.img = kind == 1 ? 0 : std::max(gemm_w8g_image_bytes(gu), gemm_w8g_image_bytes(dn));
+    gu.ld_s = hidden / 128;
+    dn.ld_s = inter / 128;
+    if (kind != 1) {
+        z.img = gemm_w8g_image_bytes(gu);
+        z.img_dn = gemm_w8g_image_bytes(dn);
+    }
     if (kind == 2) {
         GemmArgs dn;
         dn.x_type = SEPAL_HIP_F32;
@@ -674,7 +689,8 @@ StackZones stack_zones(int kind, std::size_t t, std::size_t hidden, std::size_t 
         split = gemm_w8g_scratch_bytes(dn);
     }
     z.off_img = z.off_split + up256(split);
-    z.end = z.off_img + z.img;
+    z.off_img_dn = z.off_img + z.img;
+    z.end = z.off_img_dn + z.img_dn;
     return z;
 }
 
@@ -733,8 +749,32 @@ void run_stack(const StackZones& z, int kind, std::size_t layers, std::size_t t,
         dn.epilogue = SEPAL_HIP_STORE;
         dn.scratch = ws;
         if (z.img != 0) {
-            gu.wimage = dn.wimage = ws + z.off_img;
-            gu.wimage_bytes = dn.wimage_bytes = z.img;
+            gu.wimage = ws + z.off_img;
+            gu.wimage_bytes = z.img;
+        }
+        if (z.img_dn != 0) {
+            dn.wimage = ws + z.off_img_dn;
+            dn.wimage_bytes = z.img_dn;
+        }
+        if (z.img != 0 && z.img_dn != 0) {
+            // both multiplies on images: the gate/up multiply's halves launch widens this layer's down weights, the
+            // down multiply's the next layer's gate/up weights (the first layer's gate/up widens its own)
+            gu.image_ready = l > 0;
+            gu.next_w = w_down[l];
+            gu.next_ld_w = inter;
+            gu.next_n = hidden;
+            gu.next_k = inter;
+            gu.next_f16 = kind == 0 ? 1 : 0;  // the down multiply's X: binary16 H (kind 0), or bf16 hi + lo pairs
+            gu.next_image = ws + z.off_img_dn;
+            dn.image_ready = true;
+            if (l + 1 < layers) {
+                dn.next_w = w_gate_up[l + 1];
+                dn.next_ld_w = hidden;
+                dn.next_n = 2 * inter;
+                dn.next_k = hidden;
+                dn.next_f16 = 0;
+                dn.next_image = ws + z.off_img;
+            }
         }
         if (kind != 1) {
             // w8g: H binary16 (kind 0) or float32 (kind 2, the down multiply on its bf16 hi + lo pairs)
@@ -799,10 +839,6 @@ constexpr int kMaxDevices = 64;
 std::mutex g_static_mutex;
 char* g_static_ptr[kMaxDevices] = {};
 
-__global__ void zero_words_kernel(unsigned* p, std::size_t n) {
-    for (std::size_t i = blockIdx.x * 256ull + threadIdx.x; i < n; i += static_cast<std::size_t>(gridDim.x) * 256) p[i] = 0u;
-}
-
 // The current device's static scratch. The first call on a device looks its address up (with that device current)
 // and enqueues, on `stream`, the clearing of the split-K counter zone, which is zero at rest from then on.
 char* static_scratch(hipStream_t stream) {
@@ -820,6 +856,7 @@ char* static_scratch(hipStream_t stream) {
         check_launch("mlp_stack_noalloc counter clearing launch");
         g_static_ptr[dev] = static_cast<char*>(ptr);
     }
+
     return g_static_ptr[dev];
 }
 
@@ -838,8 +875,8 @@ int32_t sepal_hip_mlp_stack_noalloc(int32_t kind, size_t layers, size_t t, size_
         const hipStream_t st = as_stream(stream);
         StackZones z = stack_zones(kind, t, hidden, inter, act_block);
         if (z.end > kStaticScratchBytes && z.img != 0) {
-            // without the weight image (the kernels widen the weights themselves; the same bits)
-            z.img = 0;
+            // without the weight images (the kernels widen the weights themselves; the same bits)
+            z.img = z.img_dn = 0;
             z.end = z.off_img;
         }
         require(z.end <= kStaticScratchBytes,

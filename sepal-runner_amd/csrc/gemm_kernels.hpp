@@ -41,6 +41,13 @@ struct GemmArgs {
     float* ytmp = nullptr;    // w8g with float32 X and SwiGLU off the one-pass kernel: the float32 sums [t, n]
     void* wimage = nullptr;   // w8g at large M: room for the widened weight image (gemm_w8g_image_bytes)
     std::size_t wimage_bytes = 0;
+    bool image_ready = false;  // the image already holds these weights (widened by the previous multiply of a stack)
+    // w8g at large M in a stack: the next multiply's weights, widened into next_image by the spare blocks of this
+    // multiply's last launch (or by a launch of its own after it); next_f16: widen to binary16, else bf16
+    const std::int8_t* next_w = nullptr;
+    std::size_t next_ld_w = 0, next_n = 0, next_k = 0;
+    int next_f16 = 0;
+    void* next_image = nullptr;
 };
 
 // q8 epilogue (internal, not in the public enum): SwiGLU, then the output quantized to int8 per row and 128 columns

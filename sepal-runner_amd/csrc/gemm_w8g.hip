@@ -43,6 +43,40 @@ __device__ __forceinline__ void widen16(const u32x4 v, unsigned (&o)[8]) {
     }
 }
 
+// Items [id0, total) of the weight image, every id_stride-th (the layout at widen_image_kernel): item id widens 128
+// bytes of one weight row (two 64-value steps) into 16 chunks of the image, exactly, to binary16 (f16) or bf16.
+__device__ __forceinline__ void widen_range(const signed char* __restrict__ w, std::size_t ld_w, int n, int wsteps, int tiles_n,
+                                            unsigned char* __restrict__ img, bool f16, std::size_t id0, std::size_t id_stride) {
+    const int pairs = wsteps / 2;
+    const std::size_t total = static_cast<std::size_t>(tiles_n) * pairs * 256;
+    for (std::size_t id = id0; id < total; id += id_stride) {
+        const int c = static_cast<int>(id % 32), nb = static_cast<int>((id / 32) % 8);
+        const int kp = static_cast<int>((id / 256) % pairs), tn = static_cast<int>(id / 256 / pairs);
+        const int row = tn * 256 + nb * 32 + c;
+        u32x4 v[8];
+        if (row < n) {
+            const u32x4* src = reinterpret_cast<const u32x4*>(w + static_cast<std::size_t>(row) * ld_w + 128 * kp);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] = src[i];
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] = u32x4{0u, 0u, 0u, 0u};
+        }
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            unsigned char* stage = img + (static_cast<std::size_t>(tn) * wsteps + 2 * kp + h) * 32768;
+#pragma unroll
+            for (int st = 0; st < 4; ++st) {
+                unsigned o[8];
+                if (f16) widen16<SEPAL_HIP_F16>(v[4 * h + st], o);
+                else widen16<SEPAL_HIP_BF16>(v[4 * h + st], o);
+                *reinterpret_cast<u32x4*>(stage + (nb * 4 + st) * 1024 + c * 16) = u32x4{o[0], o[1], o[2], o[3]};
+                *reinterpret_cast<u32x4*>(stage + (nb * 4 + st) * 1024 + (c + 32) * 16) = u32x4{o[4], o[5], o[6], o[7]};
+            }
+        }
+    }
+}
+
 template <int XT>
 __device__ __forceinline__ f32x16 mfma32(const u32x4 a, const u32x4 b, f32x16 c) {
     if constexpr (XT == SEPAL_HIP_BF16)
@@ -102,6 +136,12 @@ struct BigParams {
     const unsigned char* wimg = nullptr;
     std::size_t wimg_bytes = 0;
     int wsteps = 0;
+    // a second weight image widened by extra blocks of the halves launch (the blocks past the halves), for the next
+    // multiply of a stack: its weights, shape and destination
+    const signed char* jw = nullptr;
+    std::size_t j_ld = 0;
+    int j_n = 0, j_wsteps = 0, j_tiles_n = 0, j_f16 = 0, j_blocks = 0;
+    unsigned char* j_img = nullptr;
 };
 
 // Tile of logical id `id`: groups of GM M tiles sweep N with the same few X row panels.
@@ -782,6 +822,15 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
     // (they share its L2). MB 2: block b is half b / count of tile id0 + b % count (a half wholly past T has nothing to
     // do, and leaves before any barrier).
     int tm, tn, m0, n0, cur = 0, stride = 1, hi = 1;
+    if constexpr (MB == 2) {
+        // the blocks past the halves widen the stack's next weight image (they share no barrier with the others)
+        const int halves = 2 * p.count;
+        if (static_cast<int>(blockIdx.x) >= halves) {
+            widen_range(p.jw, p.j_ld, p.j_n, p.j_wsteps, p.j_tiles_n, p.j_img, p.j_f16 != 0,
+                        (blockIdx.x - halves) * 512ull + threadIdx.x, static_cast<std::size_t>(p.j_blocks) * 512);
+            return;
+        }
+    }
     if constexpr (MB == 4) {
         const int nx = static_cast<int>(gridDim.x) / 8, xcd = blockIdx.x % 8;
         const int q = p.count / 8, r = p.count % 8;
@@ -1059,42 +1108,26 @@ void launch_big3(const BigParams& p, hipStream_t stream) {
 // values of k); in it, lane l's 16 bytes are column 32 nb + l % 32 at k 16 st + 8 (l / 32) .. + 7, widened exactly to
 // the MFMA type (the same values the waves would widen into the stage). Columns past N are zero. One thread widens 128
 // bytes of one weight row (two steps) into 16 chunks; the threads of a wave write 512 contiguous bytes at a time.
-template <int XT>
 __global__ void __launch_bounds__(256) widen_image_kernel(const signed char* __restrict__ w, std::size_t ld_w, int n,
-                                                          int wsteps, int tiles_n, unsigned char* __restrict__ img) {
-    const int pairs = wsteps / 2;
-    const std::size_t total = static_cast<std::size_t>(tiles_n) * pairs * 256;
-    for (std::size_t id = blockIdx.x * 256ull + threadIdx.x; id < total; id += static_cast<std::size_t>(gridDim.x) * 256) {
-        const int c = static_cast<int>(id % 32), nb = static_cast<int>((id / 32) % 8);
-        const int kp = static_cast<int>((id / 256) % pairs), tn = static_cast<int>(id / 256 / pairs);
-        const int row = tn * 256 + nb * 32 + c;
-        u32x4 v[8];
-        if (row < n) {
-            const u32x4* src = reinterpret_cast<const u32x4*>(w + static_cast<std::size_t>(row) * ld_w + 128 * kp);
-#pragma unroll
-            for (int i = 0; i < 8; ++i) v[i] = src[i];
-        } else {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) v[i] = u32x4{0u, 0u, 0u, 0u};
-        }
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            unsigned char* stage = img + (static_cast<std::size_t>(tn) * wsteps + 2 * kp + h) * 32768;
-#pragma unroll
-            for (int st = 0; st < 4; ++st) {
-                unsigned o[8];
-                widen16<XT>(v[4 * h + st], o);
-                *reinterpret_cast<u32x4*>(stage + (nb * 4 + st) * 1024 + c * 16) = u32x4{o[0], o[1], o[2], o[3]};
-                *reinterpret_cast<u32x4*>(stage + (nb * 4 + st) * 1024 + (c + 32) * 16) = u32x4{o[4], o[5], o[6], o[7]};
-            }
-        }
-    }
+                                                          int wsteps, int tiles_n, unsigned char* __restrict__ img, int f16) {
+    widen_range(w, ld_w, n, wsteps, tiles_n, img, f16 != 0, blockIdx.x * 256ull + threadIdx.x, static_cast<std::size_t>(gridDim.x) * 256);
 }
 
 // Bytes of the weight image for an N x K multiply (0 when it would not fit 32-bit offsets).
 inline std::size_t image_bytes(std::size_t n, std::size_t k) {
     const std::size_t b = (n + 255) / 256 * (k / 64) * 32768;
     return b < (std::size_t{1} << 31) ? b : 0;
+}
+
+// One streaming pass that widens an N x K int8 weight matrix into its image (binary16 or bf16).
+inline void launch_widen(const std::int8_t* w, std::size_t ld_w, std::size_t n, std::size_t k, bool f16, void* img,
+                         hipStream_t stream) {
+    const int wsteps = static_cast<int>(k / 64), tiles_n = static_cast<int>((n + 255) / 256);
+    const std::size_t items = static_cast<std::size_t>(tiles_n) * (wsteps / 2) * 256;
+    widen_image_kernel<<<static_cast<int>(std::min<std::size_t>((items + 255) / 256, 8192)), 256, 0, stream>>>(
+        reinterpret_cast<const signed char*>(w), ld_w, static_cast<int>(n), wsteps, tiles_n, static_cast<unsigned char*>(img),
+        f16 ? 1 : 0);
+    check_launch("gemm_w8g weight image launch");
 }
 
 // Grids of fewer than two rounds of 256 x 256 tiles. The block tile is 64, 128 or 256 rows high (MB 1, 2, 4), and when
@@ -1162,6 +1195,7 @@ void launch_big(const GemmArgs& a, hipStream_t stream) {
     const bool takes = big3_takes(a, kx, a.ld_x);
     const bool wide = static_cast<long>(tiles_m) * tn256 >= 2 * 256 && (EP != SEPAL_HIP_SWIGLU || a.n % 256 == 0);
     p.tiles_m = tiles_m;
+    bool next_done = false;  // the next multiply's image (a stack's) widened by this call's halves launch
     if (wide && takes) {
         // The last, partial round of 256 x 256 tiles is the idle tail of the launch. When it is more than a quarter
         // full and its tiles fit one round as 128 x 256 halves, they go to a second launch of half-height tiles (the
@@ -1182,10 +1216,7 @@ void launch_big(const GemmArgs& a, hipStream_t stream) {
             p.wimg = static_cast<const unsigned char*>(a.wimage);
             p.wimg_bytes = img;
             p.wsteps = static_cast<int>(a.k / 64);
-            const std::size_t items = static_cast<std::size_t>(tn256) * (p.wsteps / 2) * 256;
-            widen_image_kernel<XT><<<static_cast<int>(std::min<std::size_t>((items + 255) / 256, 8192)), 256, 0, stream>>>(
-                reinterpret_cast<const signed char*>(a.w), a.ld_w, static_cast<int>(a.n), p.wsteps, tn256, static_cast<unsigned char*>(a.wimage));
-            check_launch("gemm_w8g weight image launch");
+            if (!a.image_ready) launch_widen(a.w, a.ld_w, a.n, a.k, XT == SEPAL_HIP_F16, a.wimage, stream);
         }
         if (p.wimg != nullptr) {
             // persistent: one block per CU (a multiple of the 8 XCDs)
@@ -1197,8 +1228,25 @@ void launch_big(const GemmArgs& a, hipStream_t stream) {
             BigParams q = p;
             q.id0 = full;
             q.count = rest;
-            if (q.wimg != nullptr) v2::gemm_pp<XT, EP, YT, 2, SPLIT><<<dim3(2 * q.count), dim3(512), 0, stream>>>(q);
-            else launch_big3<XT, EP, YT, 2, SPLIT>(q, stream);
+            if (q.wimg != nullptr) {
+                int extra = 0;
+                if (a.next_image != nullptr) {
+                    // the next multiply's image on the CUs the halves leave idle (at least 32 blocks)
+                    extra = std::max(32, cus - 2 * rest);
+                    q.jw = reinterpret_cast<const signed char*>(a.next_w);
+                    q.j_ld = a.next_ld_w;
+                    q.j_n = static_cast<int>(a.next_n);
+                    q.j_wsteps = static_cast<int>(a.next_k / 64);
+                    q.j_tiles_n = static_cast<int>((a.next_n + 255) / 256);
+                    q.j_f16 = a.next_f16;
+                    q.j_img = static_cast<unsigned char*>(a.next_image);
+                    q.j_blocks = extra;
+                    next_done = true;
+                }
+                v2::gemm_pp<XT, EP, YT, 2, SPLIT><<<dim3(2 * q.count + extra), dim3(512), 0, stream>>>(q);
+            } else {
+                launch_big3<XT, EP, YT, 2, SPLIT>(q, stream);
+            }
         }
     } else if (takes && !wide) {
         // fewer than two rounds of 256 x 256 tiles: the plan's tile height and K split
@@ -1227,6 +1275,9 @@ void launch_big(const GemmArgs& a, hipStream_t stream) {
         throw LaunchError("gemm_w8g: the hi + lo form runs on the 64-wide-step kernel only");
     }
     check_launch("gemm_w8g large-M kernel launch");
+    // the next multiply's image, when no halves launch took it
+    if (a.next_image != nullptr && !next_done)
+        launch_widen(a.next_w, a.next_ld_w, a.next_n, a.next_k, a.next_f16 != 0, a.next_image, stream);
 }
 
 // Whether a problem takes the small-M (weight-streaming) kernels: they write float32 (or SwiGLU outputs); a binary16

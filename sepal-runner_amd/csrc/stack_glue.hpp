@@ -22,7 +22,8 @@ struct StackZones {
     std::size_t off_h = 0, off_p = 0;                                          // H, the small forms' K-part sums
     std::size_t off_hmax = 0, off_qx = 0, off_sx = 0, off_qh = 0, off_sh = 0;  // q8: int8 operands and scales
     std::size_t off_split = 0;                                                 // kind 2: the hi + lo pairs of H
-    std::size_t off_img = 0, img = 0;  // w8g at large M: the widened weight image (0 bytes: the kernels widen)
+    // w8g at large M: the widened weight images of the gate/up and down weights (0 bytes: the kernels widen)
+    std::size_t off_img = 0, img = 0, off_img_dn = 0, img_dn = 0;
     std::size_t end = 0;
 };
 
