@@ -133,6 +133,26 @@ def test_c3_stack_full_size(sm):
     assert np.all(np.isfinite(y3))
 
 
+def test_c3_stack_float32_h_full_size(sm):
+    """C3 with H kept in float32 (mlp_stack kind 2: the down multiply on bf16 hi + lo pairs of H): two layers at
+    M = 15872 bit for bit against the same multiplies called one by one (each multiply's weight image, widened there
+    by the previous multiply's last launch, must hold the weights this one widens itself)."""
+    rng = np.random.default_rng(13)
+    x = bf16_inputs(rng, (M_LONG, H))
+    layers = [_layer_weights(sm, 2000 + l, rule=0) for l in range(2)]
+    say("C3 stack m 15872 float32 H, 2 layers vs composition")
+    xt = dev(x, torch.bfloat16)
+    y2 = host(sm.mlp_stack(2, xt, layers))
+    xc = dev(x, torch.bfloat16)
+    for li, (wgu, sgu, wd, sd) in enumerate(layers):
+        h = sm.gemm_w8g(xc, wgu, sgu, epilogue=sm.SWIGLU, y_dtype=torch.float32)
+        yc = sm.gemm_w8g(h, wd, sd)
+        if li + 1 < len(layers):
+            xc = sm.rmsnorm_rows(yc, y_dtype=torch.bfloat16)
+    assert same_bits(y2, host(yc))
+    assert np.all(np.isfinite(y2))
+
+
 def test_c4_per_token_full_size(sm):
     """C4 at its workload: the q8 stack with one activation scale per token at M = 15872, 1% of the input channels
     x20. Sampled rows of one layer bit for bit against the oracle's cpu-q8 chain; two layers bit for bit against the
