@@ -467,12 +467,12 @@ def test_w8g_swiglu_narrow_tiles_match_wide(sm):
 
 
 @pytest.mark.parametrize("shape", [(2100, 16384, 640, "swiglu", "bf16"), (2100, 16384, 384, "store", "f32"),
-                                   (2400, 14992, 640, "add", "f16")])
+                                   (2400, 14992, 640, "add", "f16"), (2100, 15616, 384, "store", "bf16")])
 def test_w8g_image_kernel_step_tails(sm, shape):
     """The large grids (at least two rounds of 256 x 256 tiles) run on the weight image with two wave groups in
     alternation, whose loop body is six 64-wide steps: K of 5 groups (10 steps: one body and a two-group tail) and of 3
-    groups in the hi + lo form (12 steps), ragged rows and columns; every element against float64 of the dequantized
-    weights."""
+    groups in the hi + lo form (12 steps), ragged rows and columns, and 549 tiles (the persistent launch's XCD ranges
+    of unequal length); every element against float64 of the dequantized weights."""
     t, n, k, ep, xdt = shape
     rng = np.random.default_rng(t + n + k)
     if xdt == "f32":
