@@ -782,6 +782,18 @@ void run_stack(const StackZones& z, int kind, std::size_t layers, std::size_t t,
             gu.x_type = SEPAL_HIP_BF16;
             gu.ld_x = hidden;
             gu.y_type = kind == 0 ? SEPAL_HIP_F16 : SEPAL_HIP_F32;
+            if (kind == 2 && gemm_w8g_pairs_chain(gu, dn)) {
+                // the gate/up epilogue writes H as the down multiply's bf16 hi + lo pairs (no split pass; the same
+                // pairs as the split of float32 H)
+                gu.y_type = kYPairs;
+                launch_gemm_w8g(gu, st);
+                dn.x = h;
+                dn.ld_x = 2 * inter;
+                dn.y_type = SEPAL_HIP_F32;
+                launch_gemm_w8g_pairs(dn, st);
+                if (l + 1 < layers) launch_rmsnorm(y, hidden, x, SEPAL_HIP_BF16, hidden, nullptr, t, hidden, eps, st);
+                continue;
+            }
             launch_gemm_w8g(gu, st);
             dn.x = h;
             dn.x_type = kind == 0 ? SEPAL_HIP_F16 : SEPAL_HIP_F32;

@@ -55,6 +55,14 @@ struct GemmArgs {
 constexpr int kSwigluQ8 = 16;
 
 void launch_gemm_w8g(const GemmArgs& a, hipStream_t stream);
+// w8g Y type (internal, not in the public enum): the SwiGLU output as bf16 hi + lo pairs in the row layout the float32-X
+// down multiply reads (y [t, 2 ld_y] bf16), the split of the float32 value as that multiply's own split pass makes it.
+constexpr int kYPairs = 17;
+// Whether a stack's gate/up multiply `gu` (SwiGLU) can write its H as kYPairs for the down multiply `dn` (float32 X):
+// both run on the large-M kernels, the down multiply on its one-pass hi + lo form.
+bool gemm_w8g_pairs_chain(const GemmArgs& gu, const GemmArgs& dn);
+// The down multiply of such a chain: dn.x holds the pairs (bf16 [t, 2 dn.k], row stride dn.ld_x values).
+void launch_gemm_w8g_pairs(const GemmArgs& dn, hipStream_t stream);
 // Scratch bytes launch_gemm_w8g needs at xsplit (then ytmp, 256-byte aligned, when non-zero) for this problem; 0 for a
 // 16-bit X.
 std::size_t gemm_w8g_scratch_bytes(const GemmArgs& a);

@@ -93,6 +93,22 @@ __device__ __forceinline__ f32x4 mfma16(const u32x4 a, const u32x4 b, f32x4 c) {
         return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
 }
 
+// The SwiGLU output f of `row` (the output's row stride ld_y values) as YT, or, for kYPairs, as its bf16 hi + lo
+// pair in the hi + lo row layout the 64-wide-step kernel reads (row stride 2 ld_y; value f at 128 (f / 64) + f % 64,
+// its lo 64 values on): the rounding of the split pass on the float32 value, so the down multiply's bits are those
+// of float32 H split by that pass.
+template <int YT>
+__device__ __forceinline__ void store_h(void* y, std::size_t row, std::size_t ld_y, int f, float v) {
+    if constexpr (YT == kYPairs) {
+        unsigned short* const d = static_cast<unsigned short*>(y) + row * 2 * ld_y + 128 * (f / 64) + f % 64;
+        const unsigned short h = f32_to_bf16_bits(v);
+        d[0] = h;
+        d[64] = f32_to_bf16_bits(__fsub_rn(v, bf16_bits_to_f32(h)));
+    } else {
+        store_out<YT>(y, row * ld_y + f, v);
+    }
+}
+
 // Epilogue of one output element (row, col) of the plain multiply: float32 Store / Add, or a binary16 Store (the
 // float32 value rounded to nearest even, as a separate conversion would).
 template <int EP, int YT>
@@ -418,7 +434,9 @@ __device__ __forceinline__ void tile_epilogue(const BigParams& p, f32x16 (&acc)[
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const std::size_t row = static_cast<std::size_t>(m0 + wmu * 32 * MB + i * 32 + 8 * (r / 4) + (r % 4));
-                    if constexpr (EP == SEPAL_HIP_SWIGLU) {
+                    if constexpr (EP == SEPAL_HIP_SWIGLU && YT == kYPairs) {
+                        store_h<YT>(p.y, row + 4 * (lane / 32), p.ld_y, n0 / 2 + 64 * ibu + 32 * hhu + lane % 32, acc[i][0][r]);
+                    } else if constexpr (EP == SEPAL_HIP_SWIGLU) {
                         char* const rp = yb + (row * p.ld_y + n0 / 2 + 64 * ibu + 32 * hhu) * ES;
                         store_out<YT>(rp + voff, 0, acc[i][0][r]);
                     } else {
@@ -445,7 +463,9 @@ __device__ __forceinline__ void tile_epilogue(const BigParams& p, f32x16 (&acc)[
             for (int r = 0; r < 16; ++r) {
                 const std::size_t row = static_cast<std::size_t>(m0 + wmu * 32 * MB + i * 32 + 8 * (r / 4) + (r % 4));
                 const float v0 = __fmul_rn(acc[i][0][r], e[0]), v1 = __fmul_rn(acc[i][1][r], e[1]);
-                if constexpr (EP == SEPAL_HIP_SWIGLU) {
+                if constexpr (EP == SEPAL_HIP_SWIGLU && YT == kYPairs) {
+                    store_h<YT>(p.y, row + 4 * (lane / 32), p.ld_y, n0 / 2 + 64 * ibu + 32 * hhu + lane % 32, swiglu_fast(v0, v1));
+                } else if constexpr (EP == SEPAL_HIP_SWIGLU) {
                     char* const rp = yb + (row * p.ld_y + n0 / 2 + 64 * ibu + 32 * hhu) * ES;
                     store_out<YT>(rp + voff, 0, swiglu_fast(v0, v1));
                 } else {
@@ -468,7 +488,7 @@ __device__ __forceinline__ void tile_epilogue(const BigParams& p, f32x16 (&acc)[
             const float v0 = __fmul_rn(acc[i][0][r], e[0]), v1 = __fmul_rn(acc[i][1][r], e[1]);
             if constexpr (EP == SEPAL_HIP_SWIGLU) {
                 const int f = n0 / 2 + 64 * ib + 32 * hh + lane % 32;
-                if (2 * f < p.n) store_out<YT>(p.y, static_cast<std::size_t>(row) * p.ld_y + f, swiglu_fast(v0, v1));
+                if (2 * f < p.n) store_h<YT>(p.y, static_cast<std::size_t>(row), p.ld_y, f, swiglu_fast(v0, v1));
             } else {
                 if (col[0] < p.n) put_plain<EP, YT>(p.y, static_cast<std::size_t>(row) * p.ld_y + col[0], v0);
                 if (col[1] < p.n) put_plain<EP, YT>(p.y, static_cast<std::size_t>(row) * p.ld_y + col[1], v1);
@@ -1267,12 +1287,12 @@ void launch_big(const GemmArgs& a, hipStream_t stream) {
         if (plan.mb == 4) launch_big3<XT, EP, YT, 4, SPLIT>(p, stream);
         else if (plan.mb == 2) launch_big3<XT, EP, YT, 2, SPLIT>(p, stream);
         else launch_big3<XT, EP, YT, 1, SPLIT>(p, stream);
-    } else if constexpr (SPLIT == 1) {
+    } else if constexpr (SPLIT == 1 && YT != kYPairs) {
         p.tiles_n = wide ? tn256 : static_cast<int>((a.n + 127) / 128);
         if (wide) launch_big2<XT, EP, YT, 4>(p, stream);
         else launch_big2<XT, EP, YT, 2>(p, stream);
     } else {
-        throw LaunchError("gemm_w8g: the hi + lo form runs on the 64-wide-step kernel only");
+        throw LaunchError("gemm_w8g: the hi + lo form (X or Y) runs on the 64-wide-step kernel only");
     }
     check_launch("gemm_w8g large-M kernel launch");
     // the next multiply's image, when no halves launch took it
@@ -1293,6 +1313,11 @@ inline bool small_path(const GemmArgs& a) {
 
 template <int XT, int EP, int YT, int SPLIT>
 void dispatch_path(const GemmArgs& a, hipStream_t stream) {
+    if constexpr (YT == kYPairs) {
+        // only the large-M kernels write the pairs (gemm_w8g_pairs_chain)
+        launch_big<XT, EP, YT, SPLIT>(a, stream);
+        return;
+    }
     if constexpr (SPLIT == 1) {
         // T <= 16 by default: the M <= 16 stack's pass kernels where they take the shape
         SmallGemmPlan plan;
@@ -1317,6 +1342,10 @@ void dispatch_ep(const GemmArgs& a, hipStream_t stream) {
         switch (a.y_type) {
         case SEPAL_HIP_F32: dispatch_path<XT, SEPAL_HIP_SWIGLU, SEPAL_HIP_F32, SPLIT>(a, stream); break;
         case SEPAL_HIP_BF16: dispatch_path<XT, SEPAL_HIP_SWIGLU, SEPAL_HIP_BF16, SPLIT>(a, stream); break;
+        case kYPairs:
+            if constexpr (XT == SEPAL_HIP_BF16 && SPLIT == 1) dispatch_path<XT, SEPAL_HIP_SWIGLU, kYPairs, SPLIT>(a, stream);
+            else throw LaunchError("gemm_w8g: hi + lo pair output needs a bf16 X");
+            break;
         default: dispatch_path<XT, SEPAL_HIP_SWIGLU, SEPAL_HIP_F16, SPLIT>(a, stream); break;
         }
     }
@@ -1422,6 +1451,22 @@ void launch_f32(const GemmArgs& a, hipStream_t stream) {
 }
 
 } // namespace w8g
+
+bool gemm_w8g_pairs_chain(const GemmArgs& gu, const GemmArgs& dn) {
+    GemmArgs d = dn;
+    d.x_type = SEPAL_HIP_F32;
+    d.y_type = SEPAL_HIP_F32;
+    GemmArgs g = gu;
+    g.y_type = SEPAL_HIP_F32;
+    return gu.epilogue == SEPAL_HIP_SWIGLU && gu.x_type == SEPAL_HIP_BF16 && gu.t > kSmallM && !w8g::small_path(g) &&
+           w8g::big3_takes(g, g.k, g.ld_x) && dn.k == gu.n / 2 && !w8g::small_path(d) && w8g::big3_takes(d, 2 * d.k, 2 * d.k);
+}
+
+void launch_gemm_w8g_pairs(const GemmArgs& dn, hipStream_t stream) {
+    GemmArgs b = dn;
+    b.x_type = SEPAL_HIP_BF16;
+    w8g::dispatch_ep<SEPAL_HIP_BF16, 2>(b, stream);
+}
 
 void launch_gemm_w8g(const GemmArgs& a, hipStream_t stream) {
     if (a.x_type == SEPAL_HIP_F32) w8g::launch_f32(a, stream);

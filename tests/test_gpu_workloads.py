@@ -153,6 +153,33 @@ def test_c3_stack_float32_h_full_size(sm):
     assert np.all(np.isfinite(y2))
 
 
+def test_float32_h_stack_ragged_rows(sm):
+    """The float32-H stack (kind 2) at 2100 rows with the model's shapes: the gate/up multiply on 256 x 256 tiles with a
+    ragged last row of tiles (52 rows), writing H straight as the down multiply's bf16 hi + lo pairs. Two layers bit
+    for bit against the multiplies called one by one (float32 H, split by the down multiply's own pass); layer 1 on
+    sampled rows, the ragged tile's included, against the float32-H oracle."""
+    rng = np.random.default_rng(17)
+    m = 2100
+    x = bf16_inputs(rng, (m, H))
+    layers = [_layer_weights(sm, 3000 + l, rule=0) for l in range(2)]
+    say("float32 H stack m 2100, 2 layers vs composition")
+    y2 = host(sm.mlp_stack(2, dev(x, torch.bfloat16), layers))
+    xc = dev(x, torch.bfloat16)
+    for li, (wgu, sgu, wd, sd) in enumerate(layers):
+        h = sm.gemm_w8g(xc, wgu, sgu, epilogue=sm.SWIGLU, y_dtype=torch.float32)
+        yc = sm.gemm_w8g(h, wd, sd)
+        if li + 1 < len(layers):
+            xc = sm.rmsnorm_rows(yc, y_dtype=torch.bfloat16)
+    assert same_bits(y2, host(yc))
+    say("float32 H stack m 2100 layer 1 vs oracle")
+    y1 = host(sm.mlp_stack(2, dev(x, torch.bfloat16), layers[:1]))
+    rows = np.sort(np.concatenate([[0, 2047, 2048, m - 1], rng.choice(np.arange(1, m - 1), size=28, replace=False)]))
+    ref = _w8g_block_oracle(x[rows], layers[0])
+    err = max_rel_over_rms(y1[rows], ref)
+    say("float32 H stack layer 1 max rel err", f"{err:.3e}")
+    assert err < 2e-4, err
+
+
 def test_c4_per_token_full_size(sm):
     """C4 at its workload: the q8 stack with one activation scale per token at M = 15872, 1% of the input channels
     x20. Sampled rows of one layer bit for bit against the oracle's cpu-q8 chain; two layers bit for bit against the
