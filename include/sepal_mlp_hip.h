@@ -242,7 +242,7 @@ SEPAL_HIP_API int32_t sepal_hip_packed_load(const char* path, int8_t* q, size_t 
  * (float32, written to y), and, when l + 1 < layers, x_{l+1} = bf16(RMSNorm(Y_l)) (identity weight, eps).
  * kind 0 = w8g (x bf16 [T, hidden]; H binary16: within the 2e-3 bar of the reference's float32 H, about 8e-4 at the
  * model's shape), kind 2 = w8g with H float32 as the reference keeps it (the down multiply on its bf16 hi + lo pairs,
- * twice that multiply's MFMA work), kind 1 = q8 (x bf16; activations quantised per act_block before each multiply;
+ * twice that multiply's MFMA work; above 64 rows the gate/up epilogue writes the pairs itself), kind 1 = q8 (x bf16; activations quantised per act_block before each multiply;
  * H float32). Weight arrays hold `layers` device pointers each: gate_up int8 [2*inter, hidden] + scales
  * [2*inter, hidden/128]; down int8 [hidden, inter] + scales [hidden, inter/128]. x is overwritten with the last layer's
  * input. Scratch (H, quantised activations, partial sums) comes from the workspace of (device, stream).
