@@ -798,6 +798,20 @@ def _gpu_composition(sm, kind, x, layers, act):
     return host(y)
 
 
+@pytest.mark.parametrize("t", [65, 300, 1500])
+def test_mlp_stack_float32_h_pairs(sm, t):
+    """kind 2 above 64 rows: the gate/up epilogue writes H as the down multiply's bf16 hi + lo pairs (small grids with
+    a K split, ragged last tiles); bit for bit against the steps called one by one, where the down multiply splits the
+    float32 H itself."""
+    say("mlp stack float32 H pairs t", t)
+    rng = np.random.default_rng(5000 + t)
+    hidden, inter = 512, 1280
+    layers = _stack_weights(sm, rng, 2, hidden, inter, rule=0)
+    x = bf16_inputs(rng, (t, hidden))
+    y = host(sm.mlp_stack(2, dev(x, torch.bfloat16), layers))
+    assert same_bits(y, _gpu_composition(sm, 2, x, layers, 128))
+
+
 @pytest.mark.parametrize("kind,act", [(0, 128), (2, 128), (1, 128), (1, 0)])
 @pytest.mark.parametrize("t", [16, 100])
 def test_mlp_stack(sm, kind, act, t):
