@@ -43,7 +43,13 @@ template <int RULE>
 __device__ __forceinline__ int quantize_value(float w, float scale, float inverse) {
     if constexpr (RULE == SEPAL_HIP_RULE_DIVIDE) {
         if (!(scale > 0.0f)) return 0;
-        const float r = __builtin_rintf(__fdiv_rn(w, scale));
+        // rint(w / scale) with the IEEE quotient. With inverse = rcp(scale) (within 1 ulp; 0 when not usable) and
+        // |w / scale| <= 127, t = w * inverse is within 2^-15 of the quotient; when t is more than 2^-12 from a
+        // half-integer, the quotient lies in the same rounding interval, so rint(t) is its rint. Otherwise (or for a
+        // NaN) the division decides.
+        const float t = __fmul_rn(w, inverse), rt = __builtin_rintf(t);
+        const float r = inverse != 0.0f && fabsf(fabsf(__fsub_rn(t, rt)) - 0.5f) > 0x1p-12f ? rt
+                                                                                         : __builtin_rintf(__fdiv_rn(w, scale));
         return static_cast<int>(fminf(fmaxf(r, -127.0f), 127.0f));
     } else {
         float r = __builtin_rintf(__fmul_rn(w, inverse));
@@ -91,6 +97,8 @@ __global__ void __launch_bounds__(256) quantize_group_kernel(const void* __restr
     float scale, inverse = 0.0f;
     if constexpr (RULE == SEPAL_HIP_RULE_DIVIDE) {
         scale = __fdiv_rn(m, 127.0f);
+        // (the fast path of quantize_value: scales whose reciprocal is a normal float; inf and NaN take the division)
+        if (scale >= 0x1p-100f && scale <= 0x1p100f) inverse = __builtin_amdgcn_rcpf(scale);
     } else {
         scale = m > 0.0f ? __fdiv_rn(m, 127.0f) : 1.0f;
         inverse = __fdiv_rn(1.0f, scale);

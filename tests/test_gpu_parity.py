@@ -71,6 +71,46 @@ def test_packer_r1_reference_case(sm):
     assert same_bits(host(q), qo) and same_bits(host(s), so)
 
 
+def test_packer_r1_half_integer_quotients(sm):
+    """The R1 rule's rint(w / scale) at and next to the rounding boundaries: groups with scale 1 and 0.5 holding exact
+    half-integer quotients (ties to even), groups whose values are (k + 1/2) * scale rounded and their float32
+    neighbours (quotients within an ulp of a boundary), and rows at 1e-30, 1e30 and 1e36 (scales whose reciprocal is
+    or is not a normal float); bit for bit against the oracle's IEEE division."""
+    say("packer R1 half-integer quotients")
+    rng = np.random.default_rng(77)
+    rows, k = 64, 512
+    w = (rng.standard_normal((rows, k)) * 0.3).astype(np.float32)
+    ks = np.arange(-126, 127, dtype=np.float32)
+    for r in range(8):
+        top = np.float32(127.0) if r % 2 == 0 else np.float32(63.5)  # scale 1 or 0.5
+        vals = (rng.choice(ks, 128) + np.float32(0.5)) * (top / np.float32(127.0))
+        vals[0] = top
+        w[r, :128] = vals
+    for r in range(8, 40):
+        g = r % 4
+        m = np.float32(rng.uniform(0.01, 5.0))
+        scale = np.float32(m / np.float32(127.0))
+        vals = ((rng.choice(ks, 128) + np.float32(0.5)) * scale).astype(np.float32)
+        step = r % 3
+        if step == 1:
+            vals = np.nextafter(vals, np.float32(np.inf))
+        elif step == 2:
+            vals = np.nextafter(vals, np.float32(-np.inf))
+        vals[0] = m
+        w[r, 128 * g:128 * (g + 1)] = vals
+    w[40:44] *= np.float32(1e-30)
+    w[44:48] *= np.float32(1e30)
+    w[48:52] *= np.float32(1e36)
+    q, s = sm.quantize_group_s8(dev(w))
+    qo, so = orc.quantize_group_r1(w)
+    assert same_bits(host(s), so)
+    assert same_bits(host(q), qo)
+    wh = w[:40].astype(np.float16)
+    q16, s16 = sm.quantize_group_s8(dev(wh))
+    qo16, so16 = orc.quantize_group_r1(wh.astype(np.float32))
+    assert same_bits(host(q16), qo16) and same_bits(host(s16), so16)
+
+
 @pytest.mark.parametrize("src", ["f16", "bf16", "f32"])
 @pytest.mark.parametrize("rule", [0, 1])
 def test_packer_types_and_rules(sm, src, rule):
