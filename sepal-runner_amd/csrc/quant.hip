@@ -58,13 +58,15 @@ __device__ __forceinline__ int quantize_value(float w, float scale, float invers
     }
 }
 
-template <int ST, int RULE>
+template <int ST, int RULE, int LANES>
 __global__ void __launch_bounds__(256) quantize_group_kernel(const void* __restrict__ src, std::size_t ld_src,
                                                              const void* __restrict__ src_up, std::int8_t* __restrict__ q,
                                                              std::size_t ld_q, float* __restrict__ s, std::size_t ld_s,
                                                              std::size_t rows, std::size_t groups, std::size_t inter) {
-    const std::size_t gid = (static_cast<std::size_t>(blockIdx.x) * 256 + threadIdx.x) / 16;
-    const int sub = threadIdx.x % 16;
+    // LANES lanes per (row, group); lane `sub` holds the 8-value chunks sub, sub + LANES, ...
+    constexpr int CH = 16 / LANES;
+    const std::size_t gid = (static_cast<std::size_t>(blockIdx.x) * 256 + threadIdx.x) / LANES;
+    const int sub = threadIdx.x % LANES;
     const bool live = gid < rows * groups;
     const std::size_t row = live ? gid / groups : 0, g = live ? gid % groups : 0;
     // source row: plain, or the 64-row gate/up interleave of the fused SwiGLU weights
@@ -78,20 +80,25 @@ __global__ void __launch_bounds__(256) quantize_group_kernel(const void* __restr
             base = src_up;
         }
     }
-    float v[8];
-    if (live) load8<ST>(base, srow * ld_src + g * 128 + sub * 8, v);
-    else
+    float v[CH][8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) v[i] = 0.0f;
+    for (int c = 0; c < CH; ++c) {
+        if (live) load8<ST>(base, srow * ld_src + g * 128 + (sub + LANES * c) * 8, v[c]);
+        else
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[c][i] = 0.0f;
+    }
     float m = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const float a = fabsf(v[i]);
-        m = a > m ? a : m;
-    }
+    for (int c = 0; c < CH; ++c)
 #pragma unroll
-    for (int o = 8; o > 0; o >>= 1) {
-        const float other = __shfl_xor(m, o, 16);
+        for (int i = 0; i < 8; ++i) {
+            const float a = fabsf(v[c][i]);
+            m = a > m ? a : m;
+        }
+#pragma unroll
+    for (int o = LANES / 2; o > 0; o >>= 1) {
+        const float other = __shfl_xor(m, o, LANES);
         m = other > m ? other : m;
     }
     float scale, inverse = 0.0f;
@@ -104,10 +111,14 @@ __global__ void __launch_bounds__(256) quantize_group_kernel(const void* __restr
         inverse = __fdiv_rn(1.0f, scale);
     }
     if (!live) return;
-    unsigned packed[2] = {0u, 0u};
 #pragma unroll
-    for (int i = 0; i < 8; ++i) packed[i / 4] |= (static_cast<unsigned>(quantize_value<RULE>(v[i], scale, inverse)) & 0xFFu) << (8 * (i % 4));
-    *reinterpret_cast<uint2*>(q + row * ld_q + g * 128 + sub * 8) = make_uint2(packed[0], packed[1]);
+    for (int c = 0; c < CH; ++c) {
+        unsigned packed[2] = {0u, 0u};
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            packed[i / 4] |= (static_cast<unsigned>(quantize_value<RULE>(v[c][i], scale, inverse)) & 0xFFu) << (8 * (i % 4));
+        *reinterpret_cast<uint2*>(q + row * ld_q + g * 128 + (sub + LANES * c) * 8) = make_uint2(packed[0], packed[1]);
+    }
     if (sub == 0) s[row * ld_s + g] = scale;
 }
 
@@ -573,12 +584,13 @@ template <int ST>
 void launch_group(const void* src, std::size_t ld_src, const void* src_up, std::int8_t* q, std::size_t ld_q, float* s,
                   std::size_t ld_s, std::size_t rows, std::size_t k, int rule, std::size_t inter, hipStream_t stream) {
     const std::size_t groups = k / 128;
-    const std::size_t blocks = (rows * groups * 16 + 255) / 256;
+    constexpr int kLanes = 8;
+    const std::size_t blocks = (rows * groups * kLanes + 255) / 256;
     if (rule == SEPAL_HIP_RULE_DIVIDE)
-        quantize_group_kernel<ST, SEPAL_HIP_RULE_DIVIDE><<<dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream>>>(
+        quantize_group_kernel<ST, SEPAL_HIP_RULE_DIVIDE, kLanes><<<dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream>>>(
             src, ld_src, src_up, q, ld_q, s, ld_s, rows, groups, inter);
     else
-        quantize_group_kernel<ST, SEPAL_HIP_RULE_RECIPROCAL><<<dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream>>>(
+        quantize_group_kernel<ST, SEPAL_HIP_RULE_RECIPROCAL, kLanes><<<dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream>>>(
             src, ld_src, src_up, q, ld_q, s, ld_s, rows, groups, inter);
     check_launch("quantize_group kernel launch");
 }
