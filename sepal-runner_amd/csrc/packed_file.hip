@@ -45,11 +45,22 @@ __global__ void __launch_bounds__(kThreads) lane_kernel(const unsigned char* __r
                                                         unsigned long long* __restrict__ lanes) {
     const std::size_t lane = static_cast<std::size_t>(blockIdx.x) * kThreads + threadIdx.x;
     const std::size_t words = (bytes + 7) / 8, full = bytes / 8;
+    const auto* w64 = reinterpret_cast<const unsigned long long*>(data);
     unsigned long long h = mix64(lane + 1);
-    for (std::size_t i = lane; i < words; i += kLanes) {
+    // the lane's whole words eight at a time, all eight loads in flight before the chain folds them in order
+    constexpr int B = 8;
+    std::size_t i = lane;
+    for (; i + (B - 1) * static_cast<std::size_t>(kLanes) < full; i += B * static_cast<std::size_t>(kLanes)) {
+        unsigned long long w[B];
+#pragma unroll
+        for (int j = 0; j < B; ++j) w[j] = w64[i + j * static_cast<std::size_t>(kLanes)];
+#pragma unroll
+        for (int j = 0; j < B; ++j) h = mix64(h ^ (w[j] + kGolden * (i + j * static_cast<std::size_t>(kLanes) + 1)));
+    }
+    for (; i < words; i += kLanes) {
         unsigned long long w = 0;
         if (i < full) {
-            w = reinterpret_cast<const unsigned long long*>(data)[i];
+            w = w64[i];
         } else {
             for (std::size_t b = 8 * i; b < bytes; ++b) w |= static_cast<unsigned long long>(data[b]) << (8 * (b - 8 * i));
         }

@@ -1230,6 +1230,9 @@ def test_weight_fingerprint_definition_and_sensitivity(sm):
     assert sm.weight_fingerprint(t[:-1]) != fp
     small = torch.from_numpy(raw[:5].copy()).cuda()
     assert sm.weight_fingerprint(small) == _fingerprint_np(raw[:5].tobytes())
+    # 10 words per lane (the kernel's batches of 8 loads, then the rest) and a 5-byte tail
+    big = rng.integers(0, 256, size=(5 << 20) + 5, dtype=np.uint8)
+    assert sm.weight_fingerprint(torch.from_numpy(big).cuda()) == _fingerprint_np(big.tobytes())
 
 
 def test_packed_file_round_trip_and_refusals(sm, tmp_path):
