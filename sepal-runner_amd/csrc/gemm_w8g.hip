@@ -43,37 +43,27 @@ __device__ __forceinline__ void widen16(const u32x4 v, unsigned (&o)[8]) {
     }
 }
 
-// Items [id0, total) of the weight image, every id_stride-th (the layout at widen_image_kernel): item id widens 128
-// bytes of one weight row (two 64-value steps) into 16 chunks of the image, exactly, to binary16 (f16) or bf16.
+// Items [id0, total) of the weight image, every id_stride-th (the layout at widen_image_kernel): item id widens one
+// 16-byte chunk (16 values of one substep) of one weight row into its two 16-byte slots of the image, exactly, to
+// binary16 (f16) or bf16. Eight consecutive items are the eight chunks of 128 bytes of one row (two 64-value steps),
+// so a wave reads 8 rows x 128 contiguous bytes and writes 128-byte runs.
 __device__ __forceinline__ void widen_range(const signed char* __restrict__ w, std::size_t ld_w, int n, int wsteps, int tiles_n,
                                             unsigned char* __restrict__ img, bool f16, std::size_t id0, std::size_t id_stride) {
     const int pairs = wsteps / 2;
-    const std::size_t total = static_cast<std::size_t>(tiles_n) * pairs * 256;
+    const std::size_t total = static_cast<std::size_t>(tiles_n) * pairs * 256 * 8;
     for (std::size_t id = id0; id < total; id += id_stride) {
-        const int c = static_cast<int>(id % 32), nb = static_cast<int>((id / 32) % 8);
-        const int kp = static_cast<int>((id / 256) % pairs), tn = static_cast<int>(id / 256 / pairs);
+        const int j = static_cast<int>(id % 8), c = static_cast<int>((id / 8) % 32), nb = static_cast<int>((id / 256) % 8);
+        const int kp = static_cast<int>((id / 2048) % pairs), tn = static_cast<int>(id / 2048 / pairs);
         const int row = tn * 256 + nb * 32 + c;
-        u32x4 v[8];
-        if (row < n) {
-            const u32x4* src = reinterpret_cast<const u32x4*>(w + static_cast<std::size_t>(row) * ld_w + 128 * kp);
-#pragma unroll
-            for (int i = 0; i < 8; ++i) v[i] = src[i];
-        } else {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) v[i] = u32x4{0u, 0u, 0u, 0u};
-        }
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            unsigned char* stage = img + (static_cast<std::size_t>(tn) * wsteps + 2 * kp + h) * 32768;
-#pragma unroll
-            for (int st = 0; st < 4; ++st) {
-                unsigned o[8];
-                if (f16) widen16<SEPAL_HIP_F16>(v[4 * h + st], o);
-                else widen16<SEPAL_HIP_BF16>(v[4 * h + st], o);
-                *reinterpret_cast<u32x4*>(stage + (nb * 4 + st) * 1024 + c * 16) = u32x4{o[0], o[1], o[2], o[3]};
-                *reinterpret_cast<u32x4*>(stage + (nb * 4 + st) * 1024 + (c + 32) * 16) = u32x4{o[4], o[5], o[6], o[7]};
-            }
-        }
+        u32x4 v = u32x4{0u, 0u, 0u, 0u};
+        if (row < n) v = *reinterpret_cast<const u32x4*>(w + static_cast<std::size_t>(row) * ld_w + 128 * kp + 16 * j);
+        const int h = j / 4, st = j % 4;
+        unsigned char* const stage = img + (static_cast<std::size_t>(tn) * wsteps + 2 * kp + h) * 32768;
+        unsigned o[8];
+        if (f16) widen16<SEPAL_HIP_F16>(v, o);
+        else widen16<SEPAL_HIP_BF16>(v, o);
+        *reinterpret_cast<u32x4*>(stage + (nb * 4 + st) * 1024 + c * 16) = u32x4{o[0], o[1], o[2], o[3]};
+        *reinterpret_cast<u32x4*>(stage + (nb * 4 + st) * 1024 + (c + 32) * 16) = u32x4{o[4], o[5], o[6], o[7]};
     }
 }
 
@@ -1126,8 +1116,8 @@ void launch_big3(const BigParams& p, hipStream_t stream) {
 // The weight image of gemm_pp: for every 256-column tile tn and weight step ks (64 values of k), the 32 KB
 // W stage in the order the fragment reads use it. Kilobyte 4 nb + st holds n-block nb (32 columns) at substep st (16
 // values of k); in it, lane l's 16 bytes are column 32 nb + l % 32 at k 16 st + 8 (l / 32) .. + 7, widened exactly to
-// the MFMA type (the same values the waves would widen into the stage). Columns past N are zero. One thread widens 128
-// bytes of one weight row (two steps) into 16 chunks; the threads of a wave write 512 contiguous bytes at a time.
+// the MFMA type (the same values the waves would widen into the stage). Columns past N are zero. One thread widens one
+// 16-byte chunk of one weight row (widen_range).
 __global__ void __launch_bounds__(256) widen_image_kernel(const signed char* __restrict__ w, std::size_t ld_w, int n,
                                                           int wsteps, int tiles_n, unsigned char* __restrict__ img, int f16) {
     widen_range(w, ld_w, n, wsteps, tiles_n, img, f16 != 0, blockIdx.x * 256ull + threadIdx.x, static_cast<std::size_t>(gridDim.x) * 256);
@@ -1143,8 +1133,8 @@ inline std::size_t image_bytes(std::size_t n, std::size_t k) {
 inline void launch_widen(const std::int8_t* w, std::size_t ld_w, std::size_t n, std::size_t k, bool f16, void* img,
                          hipStream_t stream) {
     const int wsteps = static_cast<int>(k / 64), tiles_n = static_cast<int>((n + 255) / 256);
-    const std::size_t items = static_cast<std::size_t>(tiles_n) * (wsteps / 2) * 256;
-    widen_image_kernel<<<static_cast<int>(std::min<std::size_t>((items + 255) / 256, 8192)), 256, 0, stream>>>(
+    const std::size_t items = static_cast<std::size_t>(tiles_n) * (wsteps / 2) * 256 * 8;
+    widen_image_kernel<<<static_cast<int>(std::min<std::size_t>((items + 255) / 256, 16384)), 256, 0, stream>>>(
         reinterpret_cast<const signed char*>(w), ld_w, static_cast<int>(n), wsteps, tiles_n, static_cast<unsigned char*>(img),
         f16 ? 1 : 0);
     check_launch("gemm_w8g weight image launch");
