@@ -72,11 +72,16 @@ def timed(torch, fn, steps, warmup, stream):
     return start.elapsed_time(stop) / steps
 
 
+_SIDE = []
+
+
 def graph_timed(torch, fn, reps=20, replays=10):
     """Microseconds of GPU time per call of fn(stream): `reps` calls captured in one HIP graph on a side stream (after
     warm-up calls there, which size the stream's workspace), replayed `replays` times between HIP events. Excludes
     the host's per-call overhead (the Python binding), which at these sizes exceeds the kernels' time."""
-    s = torch.cuda.Stream()
+    if not _SIDE:
+        _SIDE.append(torch.cuda.Stream())
+    s = _SIDE[0]  # one side stream for every measurement (the library keeps a workspace per stream)
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
         for _ in range(3):

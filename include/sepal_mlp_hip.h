@@ -53,6 +53,12 @@ enum { SEPAL_HIP_RULE_DIVIDE = 0, SEPAL_HIP_RULE_RECIPROCAL = 1 };
 SEPAL_HIP_API int32_t sepal_hip_api_version(void);
 SEPAL_HIP_API const char* sepal_hip_last_error(void);
 
+/* Frees the workspace the library keeps for (current device, `stream`), after waiting for that stream's work; the next
+ * call on the stream allocates a new one. Call it before hipStreamDestroy of a stream the library has used, as the
+ * reference frees an engine's memory at sepal_close (runner/src/capi/c_api.cpp:167). A stream without a
+ * workspace is a no-op. */
+SEPAL_HIP_API int32_t sepal_hip_release_workspace(void* stream);
+
 /* Load-time weight packer: int8 with one float32 scale per row and group of 128 values of k.
  * src [rows, ld_src] of src_type (fp16 and bf16 are widened to float32 exactly first); q [rows, ld_q] int8;
  * s [rows, ld_s] float32 (K/128 used). K a multiple of 128; ld_src, ld_q multiples of 16; 16-byte aligned src and q.
@@ -76,8 +82,12 @@ SEPAL_HIP_API int32_t sepal_hip_quantize_gate_up_s8(const void* gate, const void
  * float32. A float32 X is split into bf16 hi = bf16(x) and lo = bf16(x - hi) (|x - hi - lo| <= 2^-17 |x|), both
  * multiplied: twice the MFMA work of a 16-bit X, results within float32 rounding of the reference's chain; the split
  * takes 4 T K bytes of the workspace. Y float32 [T, ld_y] for STORE/ADD; for SWIGLU Y is [T, ld_y] of y_type
- * (F32, BF16 or F16) with N/2 columns. K a multiple of 128; N a multiple of 128 for SWIGLU, of 16 otherwise; ld_x,
- * ld_w multiples of 16; ld_y a multiple of 4; 16-byte aligned pointers. `config` -1 picks a path by T and N (at
+ * (F32, BF16 or F16) with N/2 columns. Shape rules are gemm_simt_supports' for int8-group weights: K a multiple of
+ * 128; N a multiple of 128 for SWIGLU, any N otherwise; ld_x and ld_y multiples of 4, ld_w of 16 (W rows of whole
+ * 16 bytes). Pointers: W and Y 16-byte aligned, a float32 X too (a 16-bit X may have any alignment). The kernels read
+ * 16-bit X rows of whole 16-byte chunks and store STORE / ADD outputs in 16-column tiles; other strides and the last
+ * N mod 16 columns are staged in the workspace (a contiguous copy of X; one zero-padded 16-row weight tile whose
+ * float32 outputs are stored or added into Y). `config` -1 picks a path by T and N (at
  * T <= 16 with a 16-bit X the M <= 16 stack's pass kernels where the shape fits them; small-M streaming at T <= 32 with
  * N < 8192; on the large-M path grids too small to fill the chip may split K over blocks; a row's bits then depend on
  * T); 0 forces the large-M
@@ -96,8 +106,9 @@ SEPAL_HIP_API int32_t sepal_hip_gemm_w8g_supports(int32_t x_type, size_t n, size
 
 /* Dynamic activation quantizer (rule RECIPROCAL): per row and block of `block` values (128, or cols for one scale per
  * token) amax = max|x|, s = amax > 0 ? amax / 127 : 1, q = clamp(nearbyint(x * (1 / s))). x [rows, ld_x] of x_type;
- * q int8 [rows, ld_q]; scales float32 [rows, ld_s] (cols/block used). cols a multiple of 128 (of 16 when block = cols);
- * strides multiples of 16, 16-byte aligned x and q.
+ * q int8 [rows, ld_q]; scales float32 [rows, ld_s] (cols/block used). block 128: cols a multiple of 128, strides
+ * multiples of 16, 16-byte aligned x and q. block = cols: any cols, strides and alignment (kernel_i8_y's packing takes
+ * any K).
  * Replaces the I8 branch of pack_acts (runner/src/cpu/gemm.cpp:285-306) and launch_quantize_rows_s8
  * (runner/cuda/src/gemm_s8_kernels.hpp:20-27; that one rounds by 127/amax, this one by the cpu-q8 rule). */
 SEPAL_HIP_API int32_t sepal_hip_quantize_rows_s8(const void* x, int32_t x_type, size_t ld_x, int8_t* q, size_t ld_q, float* scales,
@@ -141,8 +152,8 @@ SEPAL_HIP_API int32_t sepal_hip_channel_stats(const void* x, size_t ld_x, size_t
 
 /* The int8-activation multiply with per-channel scales: Y[t, n] = (float(sum over K of xq[t,k] * wq[n,k]) * sx[t]) *
  * sw[n], the sum exact in int32 (int8 MFMA over the whole K), then two float32 products in that order. Y float32 or
- * binary16 (y_type; round to nearest even) [T, ld_y]. K a multiple of 16 (as the reference's), strides of X and W
- * multiples of 16, 16-byte aligned X and W. Replaces launch_gemm_s8 (runner/cuda/src/gemm_s8_kernels.hpp:43-49). */
+ * binary16 (y_type; round to nearest even) [T, ld_y]. Shape rules of sepal_hip_gemm_s8_supports; 16-byte aligned
+ * X and W, 8-byte aligned Y. Replaces launch_gemm_s8 (runner/cuda/src/gemm_s8_kernels.hpp:43-49). */
 SEPAL_HIP_API int32_t sepal_hip_gemm_s8(const int8_t* xq, size_t ld_x, const float* sx, const int8_t* wq, size_t ld_w,
                                         const float* sw, void* y, int32_t y_type, size_t ld_y, size_t t, size_t n, size_t k,
                                         void* stream);
@@ -152,8 +163,10 @@ SEPAL_HIP_API int32_t sepal_hip_gemm_s8(const int8_t* xq, size_t ld_x, const flo
  * polynomial; gate and up rows in the 64-row interleave), bit for bit the reference's results. xq int8 [T, ld_x] with
  * xs float32 [T]; wq int8 [N, ld_w] with ws float32 [N]; both packed by sepal_hip_quantize_rows_s8 with block = K (its
  * rule is the reference's pack_acts and, for the weights, its Avx2 panel packer). Y float32 [T, ld_y], or y_type for
- * SWIGLU with N/2 columns. K a multiple of 16 (the reference takes any K); N any for STORE/ADD, a multiple of 128 for
- * SWIGLU; ld_x, ld_w multiples of 16; 16-byte aligned X and W.
+ * SWIGLU with N/2 columns. Any K, as the reference's; N any for STORE/ADD, a multiple of 128 for SWIGLU; ld_x, ld_w
+ * at least K; Y 4-byte aligned. The kernel reads 16-byte chunks: K off the 16-grid, or X / W rows that are not
+ * 16-byte multiples or aligned, run on zero-padded copies in the workspace (a zero byte adds an exact zero to the
+ * int32 sum: the same bits).
  * Replaces kernel_i8_y + finish_tile (runner/src/cpu/gemm_kernels_avx2.cpp:40-76, gemm.cpp:417-447) as gemm_packed runs
  * them (gemm.cpp:451-570) for weights packed for Isa::Avx2 or on a CPU without AVX-512 VNNI (pick_variant, gemm.cpp:56-69;
  * pack_acts' I8_Y branch gemm.cpp:286-306). */
@@ -162,8 +175,9 @@ SEPAL_HIP_API int32_t sepal_hip_gemm_q8y(const int8_t* xq, size_t ld_x, const fl
                                          int32_t epilogue, void* stream);
 
 /* 1 when sepal_hip_gemm_s8 / sepal_hip_gemm_w8a16 take these dimensions and strides (pointer alignment and the output
- * type are the caller's), else 0: N non-zero, K a non-zero multiple of 16 (gemm_s8) or 128 (gemm_w8a16), ld_x and ld_w
- * multiples of 16 and at least K, ld_y at least N. Replace gemm_s8_supports / gemm_w8a16_supports
+ * type are the caller's), else 0; the reference's predicates: K a non-zero multiple of 16, ld_x a multiple of 16
+ * (gemm_s8) or 8 (gemm_w8a16), ld_w a multiple of 16, ld_x and ld_w at least K, N and ld_y even, ld_y at least N.
+ * Replace gemm_s8_supports / gemm_w8a16_supports
  * (runner/cuda/src/gemm_s8_kernels.hpp:59-65), which the engine asks before it routes a matrix to the int8 multiplies
  * (cuda_engine.cpp:806). */
 SEPAL_HIP_API int32_t sepal_hip_gemm_s8_supports(size_t n, size_t k, size_t ld_x, size_t ld_w, size_t ld_y);
@@ -172,8 +186,10 @@ SEPAL_HIP_API int32_t sepal_hip_gemm_w8a16_supports(size_t n, size_t k, size_t l
 /* binary16 activations times int8 weights with per-channel scales: Y[t, n] = sw[n] * sum over K of x[t,k] * wq[n,k],
  * the weights widened exactly and multiplied with float32 accumulation (the gpu-w8g kernels with the channel's scale
  * in every group: within float32 rounding of one accumulator times sw). Y float32 or binary16 [T, ld_y] (binary16 is
- * the float32 result rounded to nearest even; at T <= 64 it goes through float32 in the workspace). Shape rules as
- * sepal_hip_gemm_s8; wq in the Plain layout.
+ * the float32 result rounded to nearest even; at T <= 64 it goes through float32 in the workspace). Shape rules of
+ * sepal_hip_gemm_w8a16_supports; 16-byte aligned X and W, 8-byte aligned Y; wq in the Plain layout. K off the
+ * 128-grid runs on zero-padded copies of X and W in the workspace (an exact zero per padded product), X rows that are
+ * not 32-byte multiples on a copy of X.
  * Replaces launch_gemm_w8a16 (runner/cuda/src/gemm_s8_kernels.hpp:51-57), the reference's gpu-q8w profile multiply. */
 SEPAL_HIP_API int32_t sepal_hip_gemm_w8a16(const void* x, size_t ld_x, const int8_t* wq, size_t ld_w, const float* sw, void* y,
                                            int32_t y_type, size_t ld_y, size_t t, size_t n, size_t k, void* stream);
@@ -263,8 +279,11 @@ SEPAL_HIP_API int32_t sepal_hip_mlp_stack(int32_t kind, size_t layers, size_t t,
  * in the reference: it is for callers that cannot allocate device memory (code under HIP graph capture, tight serving
  * loops, harnesses that forbid hipMalloc). A shape whose scratch exceeds 64 MiB is refused with SEPAL_HIP_EINVAL (at
  * the model's shape, hidden 2560 and intermediate 9728: up to 1721 rows for kind 0, about 2600 for kind 1 per 128,
- * about 430 for kind 2; the M <= 16 forms always fit). Every call on one device shares that device's array: calls that overlap on one device (other streams or
- * threads) race; serialise them. The first call on a device looks the array up and enqueues the clearing of its
+ * about 430 for kind 2; the M <= 16 forms always fit). Every call on one device shares that device's array and keeps
+ * the last call's contents. The library orders the calls: host threads take turns, and a call on another stream than
+ * the device's last one waits (hipStreamWaitEvent, no allocation) for that call's work. Under graph capture that wait
+ * is not made: a caller that captures or replays on several streams orders them itself (an event or a sync), or the
+ * calls race. The first call on a device looks the array up, creates its event and enqueues the clearing of the
  * counter zone on `stream`. */
 SEPAL_HIP_API int32_t sepal_hip_mlp_stack_noalloc(int32_t kind, size_t layers, size_t t, size_t hidden, size_t inter, void* x,
                                                   const int8_t* const* w_gate_up, const float* const* s_gate_up,

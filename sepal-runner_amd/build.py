@@ -19,7 +19,7 @@ OUT_DIR = os.path.join(HERE, "sepal_mlp")
 LIB = os.path.join(OUT_DIR, "libsepal_mlp_hip.so")
 OBJ_DIR = os.path.join(HERE, "_build")
 
-SOURCES = ["quant.hip", "gemm_w8g.hip", "gemm_q8.hip", "stream.hip", "stack_small.hip", "packed_file.hip", "capi.cpp"]
+SOURCES = ["quant.hip", "gemm_w8g.hip", "gemm_q8.hip", "stream.hip", "stack_small.hip", "packed_file.hip", "edge.hip", "capi.cpp"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [
     "--offload-arch=gfx950", "-O3", "-fPIC", "-std=c++20", "-fvisibility=hidden",

@@ -128,6 +128,105 @@ void check_gemm_common(const char* who, const void* x, std::size_t ld_x, const v
     require(n < 0x7FFFFFFFu && k < 0x7FFFFFFFu, w_ + ": dimension beyond 2^31");
 }
 
+// gemm_simt_supports for int8-group weights (runner/cuda/src/gemm_simt_kernels.cu:303-310): K a multiple of 128, X rows
+// of whole 4-value multiples, W rows of whole 16 bytes, Y rows of 4-value multiples; SwiGLU N a multiple of 128, Store /
+// Add any N.
+bool w8g_shape_ok(std::size_t n, std::size_t k, std::size_t ld_x, std::size_t ld_w, std::size_t ld_y, int epilogue) {
+    if (k == 0 || n == 0 || k % 128 != 0 || ld_x % 4 != 0 || ld_x < k || ld_w < k || ld_y % 4 != 0 || ld_w % 16 != 0) return false;
+    if (epilogue == SEPAL_HIP_SWIGLU) return n % 128 == 0 && ld_y >= n / 2;
+    return ld_y >= n;
+}
+
+inline std::size_t up256(std::size_t b) { return (b + 255) / 256 * 256; }
+
+// Scratch of one launch_gemm_w8g call beyond the counter zone: its split / sum buffers, then the weight image.
+std::size_t w8g_call_bytes(const GemmArgs& a) { return up256(gemm_w8g_scratch_bytes(a)) + gemm_w8g_image_bytes(a); }
+
+void w8g_call(GemmArgs a, char* ws, char* zone, hipStream_t st) {
+    const std::size_t extra = up256(gemm_w8g_scratch_bytes(a));
+    const std::size_t img = gemm_w8g_image_bytes(a);
+    a.scratch = ws;
+    a.xsplit = zone;
+    a.ytmp = reinterpret_cast<float*>(zone + gemm_w8g_split_bytes(a));
+    a.wimage = img != 0 ? zone + extra : nullptr;
+    a.wimage_bytes = img;
+    launch_gemm_w8g(a, st);
+}
+
+// One w8g multiply for every shape w8g_shape_ok takes. The kernels read 16-bit X in 16-byte row chunks and write Store
+// / Add outputs in 16-column tiles; the rest is staged (edge.hip): a 16-bit X whose rows are not 16-byte multiples (or
+// aligned) is copied to a contiguous [t, k] buffer, and the last N mod 16 columns run as one zero-padded 16-row weight
+// tile whose float32 outputs are then stored or added into Y. `a` holds the caller's arguments.
+struct W8gAnyLayout {
+    std::size_t x_bytes = 0, call = 0, wt = 0, st = 0, yt = 0, total = 0;
+    std::size_t n16 = 0, rest = 0;
+};
+
+W8gAnyLayout w8g_any_layout(const GemmArgs& a) {
+    W8gAnyLayout L;
+    const bool sixteen = a.x_type != SEPAL_HIP_F32;
+    if (sixteen && (a.ld_x % 16 != 0 || !aligned16(a.x))) L.x_bytes = up256(a.t * a.k * 2);
+    L.rest = a.epilogue == SEPAL_HIP_SWIGLU ? 0 : a.n % 16;
+    L.n16 = a.n - L.rest;
+    GemmArgs m = a, tl = a;
+    if (L.x_bytes != 0) m.ld_x = tl.ld_x = a.k;
+    m.n = L.n16;
+    tl.n = 16;
+    tl.ld_w = a.k;
+    tl.ld_s = a.k / 128;
+    tl.y_type = SEPAL_HIP_F32;
+    tl.ld_y = 16;
+    tl.epilogue = SEPAL_HIP_STORE;
+    L.call = std::max(L.n16 != 0 ? w8g_call_bytes(m) : 0, L.rest != 0 ? w8g_call_bytes(tl) : 0);
+    if (L.rest != 0) {
+        L.wt = up256(16 * a.k);
+        L.st = up256(16 * (a.k / 128) * 4);
+        L.yt = up256(a.t * 16 * 4);
+    }
+    L.total = L.x_bytes + L.call + L.wt + L.st + L.yt;
+    return L;
+}
+
+void w8g_any(GemmArgs a, const W8gAnyLayout& L, char* ws, char* zone, hipStream_t st) {
+    char* p = zone;
+    if (L.x_bytes != 0) {
+        launch_pad_rows(a.x, a.ld_x * 2, p, a.k * 2, a.t, a.k * 2, st);
+        a.x = p;
+        a.ld_x = a.k;
+        p += L.x_bytes;
+    }
+    char* call = p;
+    p += L.call;
+    if (L.n16 != 0) {
+        GemmArgs m = a;
+        m.n = L.n16;
+        w8g_call(m, ws, call, st);
+    }
+    if (L.rest == 0) return;
+    auto* wt = reinterpret_cast<std::int8_t*>(p);
+    auto* sc = reinterpret_cast<float*>(p + L.wt);
+    auto* yt = reinterpret_cast<float*>(p + L.wt + L.st);
+    const std::size_t groups = a.k / 128;
+    // the last rows of W and their scales, then zero rows up to 16
+    launch_pad_rows(a.w + L.n16 * a.ld_w, a.ld_w, wt, a.k, L.rest, a.k, st);
+    launch_pad_rows(nullptr, 0, wt + L.rest * a.k, a.k, 16 - L.rest, 0, st);
+    launch_pad_rows(a.s + L.n16 * a.ld_s, a.ld_s * 4, sc, groups * 4, L.rest, groups * 4, st);
+    launch_pad_rows(nullptr, 0, sc + L.rest * groups, groups * 4, 16 - L.rest, 0, st);
+    GemmArgs tl = a;
+    tl.w = wt;
+    tl.ld_w = a.k;
+    tl.s = sc;
+    tl.ld_s = groups;
+    tl.n = 16;
+    tl.y = yt;
+    tl.y_type = SEPAL_HIP_F32;
+    tl.ld_y = 16;
+    tl.epilogue = SEPAL_HIP_STORE;
+    w8g_call(tl, ws, call, st);
+    const std::size_t eb = a.y_type == SEPAL_HIP_F32 ? 4 : 2;
+    launch_put_cols(yt, 16, static_cast<char*>(a.y) + L.n16 * eb, a.y_type, a.ld_y, a.t, L.rest, a.epilogue == SEPAL_HIP_ADD, st);
+}
+
 } // namespace
 } // namespace sepal::hip
 
@@ -136,6 +235,30 @@ using namespace sepal::hip;
 extern "C" {
 
 int32_t sepal_hip_api_version(void) { return SEPAL_HIP_API_VERSION; }
+
+int32_t sepal_hip_release_workspace(void* stream) {
+    return guarded([&] {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess) throw LaunchError("hipGetDevice failed");
+        const hipStream_t st = as_stream(stream);
+        std::lock_guard<std::mutex> lock(g_ws_mutex);
+        auto it = g_ws.find({dev, st});
+        if (it == g_ws.end()) return;
+        {
+            // (waits for a call that is still enqueueing on this stream, then for the stream's work)
+            std::lock_guard<std::mutex> held(it->second->m);
+            if (it->second->ptr != nullptr) {
+                if (hipStreamSynchronize(st) != hipSuccess) throw LaunchError("release_workspace: hipStreamSynchronize failed");
+                if (hipFree(it->second->ptr) != hipSuccess) throw LaunchError("release_workspace: hipFree failed");
+                it->second->ptr = nullptr;
+                it->second->bytes = 0;
+            }
+        }
+        g_ws.erase(it);
+    });
+}
+
+
 
 const char* sepal_hip_last_error(void) { return g_error.c_str(); }
 
@@ -173,10 +296,8 @@ int32_t sepal_hip_quantize_gate_up_s8(const void* gate, const void* up, int32_t 
 int32_t sepal_hip_gemm_w8g_supports(int32_t x_type, size_t n, size_t k, size_t ld_x, size_t ld_w, size_t ld_y,
                                     int32_t epilogue) {
     if (!valid_type(x_type)) return 0;
-    if (n == 0 || k == 0 || k % 128 != 0 || ld_x < k || ld_w < k || ld_x % 16 != 0 || ld_w % 16 != 0 || ld_y % 4 != 0) return 0;
-    if (epilogue == SEPAL_HIP_SWIGLU) return n % 128 == 0 && ld_y >= n / 2 ? 1 : 0;
-    if (epilogue != SEPAL_HIP_STORE && epilogue != SEPAL_HIP_ADD) return 0;
-    return n % 16 == 0 && ld_y >= n ? 1 : 0;
+    if (epilogue != SEPAL_HIP_STORE && epilogue != SEPAL_HIP_ADD && epilogue != SEPAL_HIP_SWIGLU) return 0;
+    return w8g_shape_ok(n, k, ld_x, ld_w, ld_y, epilogue) ? 1 : 0;
 }
 
 int32_t sepal_hip_gemm_w8g(const void* x, int32_t x_type, size_t ld_x, const int8_t* w, size_t ld_w, const float* s,
@@ -185,9 +306,19 @@ int32_t sepal_hip_gemm_w8g(const void* x, int32_t x_type, size_t ld_x, const int
     return guarded([&] {
         require(valid_type(x_type), "gemm_w8g: X must be float32, bf16 or binary16");
         require(valid_type(y_type), "gemm_w8g: unknown output type");
+        require(epilogue == SEPAL_HIP_STORE || epilogue == SEPAL_HIP_ADD || epilogue == SEPAL_HIP_SWIGLU, "gemm_w8g: unknown epilogue");
         require(epilogue == SEPAL_HIP_SWIGLU || y_type == SEPAL_HIP_F32, "gemm_w8g: Store and Add write float32");
         require(config >= -1 && config <= 2, "gemm_w8g: config must be -1, 0, 1 or 2");
-        check_gemm_common("gemm_w8g", x, ld_x, w, ld_w, s, ld_s, y, ld_y, n, k, epilogue);
+        require(x != nullptr && w != nullptr && s != nullptr && y != nullptr, "gemm_w8g: null pointer");
+        // the message of launch_gemm_simt (runner/cuda/src/gemm_simt_kernels.cu:314-318)
+        require(w8g_shape_ok(n, k, ld_x, ld_w, ld_y, epilogue),
+                "gemm_w8g: unsupported shape [" + std::to_string(t) + " x " + std::to_string(k) + "] by [" + std::to_string(n) +
+                    " x " + std::to_string(k) + "] (K a multiple of 128; strides multiples of 4 values and W rows of 16 "
+                    "bytes; SwiGLU needs N a multiple of 128)");
+        require(ld_s >= k / 128, "gemm_w8g: the scale row stride must hold K/128 scales");
+        require((x_type != SEPAL_HIP_F32 || aligned16(x)) && aligned16(w) && aligned16(y),
+                "gemm_w8g: float32 X, W and Y must be 16-byte aligned");
+        require(n < 0x7FFFFFFFu && k < 0x7FFFFFFFu, "gemm_w8g: dimension beyond 2^31");
         if (t == 0) return;
         require(t < 0x7FFFFFFFu, "gemm_w8g: dimension beyond 2^31");
         if (config >= 1) require(t <= kSmallM, "gemm_w8g: the small-M path takes at most 64 rows");
@@ -209,15 +340,9 @@ int32_t sepal_hip_gemm_w8g(const void* x, int32_t x_type, size_t ld_x, const int
         a.config = config == 2 ? 1 : config;
         a.force_splits = config == 2 ? 1 : 0;
         const hipStream_t st = as_stream(stream);
-        const std::size_t extra = (gemm_w8g_scratch_bytes(a) + 255) / 256 * 256;
-        const std::size_t img = gemm_w8g_image_bytes(a);
-        Lease ws(kScratchOffset + extra + img, st);
-        a.scratch = ws.base();
-        a.xsplit = ws.base() + kScratchOffset;
-        a.ytmp = reinterpret_cast<float*>(ws.base() + kScratchOffset + gemm_w8g_split_bytes(a));
-        a.wimage = img != 0 ? ws.base() + kScratchOffset + extra : nullptr;
-        a.wimage_bytes = img;
-        launch_gemm_w8g(a, st);
+        const W8gAnyLayout L = w8g_any_layout(a);
+        Lease ws(kScratchOffset + L.total, st);
+        w8g_any(a, L, ws.base(), ws.base() + kScratchOffset, st);
     });
 }
 
@@ -228,10 +353,14 @@ int32_t sepal_hip_quantize_rows_s8(const void* x, int32_t x_type, size_t ld_x, i
         require(block == 128 || block == cols, "quantize_rows_s8: block must be 128 or cols");
         if (rows == 0 || cols == 0) return;
         require(x != nullptr && q != nullptr && scales != nullptr, "quantize_rows_s8: null pointer");
-        require(block == 128 ? cols % 128 == 0 : cols % 16 == 0, "quantize_rows_s8: cols must be a multiple of 128 (of 16 per token)");
-        require(ld_x >= cols && ld_q >= cols && ld_x % 16 == 0 && ld_q % 16 == 0 && ld_s >= cols / block,
-                "quantize_rows_s8: strides must be multiples of 16 and hold the row");
-        require(aligned16(x) && aligned16(q), "quantize_rows_s8: pointers must be 16-byte aligned");
+        require(ld_x >= cols && ld_q >= cols && ld_s >= cols / block, "quantize_rows_s8: strides must hold the row");
+        if (block == 128) {
+            // per 128 (pack_acts I8_Z): whole groups of 16-byte chunks
+            require(cols % 128 == 0, "quantize_rows_s8: cols must be a multiple of 128");
+            require(ld_x % 16 == 0 && ld_q % 16 == 0, "quantize_rows_s8: strides must be multiples of 16");
+            require(aligned16(x) && aligned16(q), "quantize_rows_s8: pointers must be 16-byte aligned");
+        }
+        // (one scale per row takes any length, stride and alignment: kernel_i8_y's packing, runner/src/cpu/gemm.cpp:286-306)
         launch_quantize_rows(x, x_type, ld_x, q, ld_q, scales, ld_s, rows, cols, block, as_stream(stream));
     });
 }
@@ -310,40 +439,42 @@ int32_t sepal_hip_channel_stats(const void* x, size_t ld_x, size_t rows, size_t 
 }
 
 namespace {
-// The shape rules of sepal_hip_gemm_s8 (k_step 16) and sepal_hip_gemm_w8a16 (k_step 128).
-bool s8_family_shape_ok(size_t n, size_t k, size_t ld_x, size_t ld_w, size_t ld_y, size_t k_step) {
-    return n != 0 && k != 0 && k % k_step == 0 && ld_x >= k && ld_w >= k && ld_x % 16 == 0 && ld_w % 16 == 0 && ld_y >= n &&
-           n < 0x7FFFFFFFu;
-}
-
-void check_s8_family(const char* who, const void* x, size_t ld_x, const void* w, size_t ld_w, const float* sw, const void* y,
-                     int32_t y_type, size_t ld_y, size_t n, size_t k, size_t k_step) {
-    const std::string w_ = who;
-    require(x != nullptr && w != nullptr && sw != nullptr && y != nullptr, w_ + ": null pointer");
-    require(y_type == SEPAL_HIP_F32 || y_type == SEPAL_HIP_F16, w_ + ": the output is float32 or binary16");
-    require(n != 0 && k != 0 && k % k_step == 0,
-            w_ + (k_step == 128 ? ": K must be a non-zero multiple of 128 (this library's group step) and N non-zero"
-                                : ": K must be a non-zero multiple of 16 and N non-zero"));
-    require(ld_x >= k && ld_w >= k && ld_x % 16 == 0 && ld_w % 16 == 0, w_ + ": row strides of X and W must be multiples of 16 and at least K");
-    require(ld_y >= n, w_ + ": ld_y must be at least N");
-    require(aligned16(x) && aligned16(w) && aligned8(y), w_ + ": X and W must be 16-byte aligned, Y 8-byte aligned");
+// The checks of launch_gemm_s8 (runner/cuda/src/gemm_s8_kernels.cu:522-531), after its T = 0 / N = 0 no-op.
+void check_s8(const void* x, size_t ld_x, const float* sx, const void* w, size_t ld_w, const float* sw, const void* y,
+              int32_t y_type, size_t ld_y, size_t n, size_t k) {
+    require(x != nullptr && w != nullptr && sx != nullptr && sw != nullptr && y != nullptr, "gemm_s8: null pointer");
+    require(y_type == SEPAL_HIP_F32 || y_type == SEPAL_HIP_F16, "gemm_s8: the output is float32 or binary16");
+    require(k != 0 && k % 16 == 0 && ld_x >= k && ld_w >= k && ld_x % 16 == 0 && ld_w % 16 == 0 && n % 2 == 0 && ld_y % 2 == 0 &&
+                ld_y >= n,
+            "gemm_s8: K and the row strides of X and W must be multiples of 16 (strides at least K), N and the row stride "
+            "of Y even (at least N)");
+    require(aligned16(x) && aligned16(w) && aligned8(y) && reinterpret_cast<std::uintptr_t>(sx) % 4 == 0 &&
+                reinterpret_cast<std::uintptr_t>(sw) % 4 == 0,
+            "gemm_s8: X and W must be 16-byte aligned, Y 8-byte aligned, the scales 4-byte aligned");
 }
 } // namespace
 
+// gemm_s8_supports (runner/cuda/src/gemm_s8_kernels.hpp:59-61), the same predicate.
 int32_t sepal_hip_gemm_s8_supports(size_t n, size_t k, size_t ld_x, size_t ld_w, size_t ld_y) {
-    return s8_family_shape_ok(n, k, ld_x, ld_w, ld_y, 16) ? 1 : 0;
+    return k != 0 && k % 16 == 0 && ld_x % 16 == 0 && ld_w % 16 == 0 && ld_x >= k && ld_w >= k && n % 2 == 0 && ld_y % 2 == 0 &&
+                   ld_y >= n
+               ? 1
+               : 0;
 }
 
+// gemm_w8a16_supports (runner/cuda/src/gemm_s8_kernels.hpp:62-64), the same predicate.
 int32_t sepal_hip_gemm_w8a16_supports(size_t n, size_t k, size_t ld_x, size_t ld_w, size_t ld_y) {
-    return s8_family_shape_ok(n, k, ld_x, ld_w, ld_y, 128) ? 1 : 0;
+    return k != 0 && k % 16 == 0 && ld_x % 8 == 0 && ld_w % 16 == 0 && ld_x >= k && ld_w >= k && n % 2 == 0 && ld_y % 2 == 0 &&
+                   ld_y >= n
+               ? 1
+               : 0;
 }
 
 int32_t sepal_hip_gemm_s8(const int8_t* xq, size_t ld_x, const float* sx, const int8_t* wq, size_t ld_w, const float* sw,
                           void* y, int32_t y_type, size_t ld_y, size_t t, size_t n, size_t k, void* stream) {
     return guarded([&] {
-        check_s8_family("gemm_s8", xq, ld_x, wq, ld_w, sw, y, y_type, ld_y, n, k, 16);
-        require(sx != nullptr, "gemm_s8: null pointer");
-        if (t == 0) return;
+        if (t == 0 || n == 0) return;
+        check_s8(xq, ld_x, sx, wq, ld_w, sw, y, y_type, ld_y, n, k);
         require(t < 0x7FFFFFFFu && n < 0x7FFFFFFFu, "gemm_s8: dimension beyond 2^31");
         GemmArgs a;
         a.x = xq;
@@ -373,15 +504,14 @@ int32_t sepal_hip_gemm_q8y(const int8_t* xq, size_t ld_x, const float* xs, const
         require(epilogue == SEPAL_HIP_STORE || epilogue == SEPAL_HIP_ADD || epilogue == SEPAL_HIP_SWIGLU, "gemm_q8y: unknown epilogue");
         require(valid_type(y_type), "gemm_q8y: unknown output type");
         require(epilogue == SEPAL_HIP_SWIGLU || y_type == SEPAL_HIP_F32, "gemm_q8y: Store and Add write float32");
-        require(n != 0 && k != 0 && k % 16 == 0, "gemm_q8y: K must be a non-zero multiple of 16 and N non-zero");
-        require(ld_x >= k && ld_w >= k && ld_x % 16 == 0 && ld_w % 16 == 0,
-                "gemm_q8y: row strides of X and W must be multiples of 16 and at least K");
+        require(n != 0 && k != 0, "gemm_q8y: K and N must be non-zero");
+        require(ld_x >= k && ld_w >= k, "gemm_q8y: row strides of X and W must be at least K");
         if (epilogue == SEPAL_HIP_SWIGLU) require(n % 128 == 0 && ld_y >= n / 2, "gemm_q8y: SwiGLU needs N a multiple of 128 and ld_y >= N/2");
         else require(ld_y >= n, "gemm_q8y: ld_y must be at least N");
-        require(aligned16(xq) && aligned16(wq) && reinterpret_cast<std::uintptr_t>(y) % 4 == 0,
-                "gemm_q8y: X and W must be 16-byte aligned, Y 4-byte aligned");
+        require(reinterpret_cast<std::uintptr_t>(y) % 4 == 0, "gemm_q8y: Y must be 4-byte aligned");
         if (t == 0) return;
         require(t < 0x7FFFFFFFu && n < 0x7FFFFFFFu && k < 0x7FFFFFFFu, "gemm_q8y: dimension beyond 2^31");
+        const hipStream_t st = as_stream(stream);
         GemmArgs a;
         a.x = xq;
         a.ld_x = ld_x;
@@ -399,59 +529,99 @@ int32_t sepal_hip_gemm_q8y(const int8_t* xq, size_t ld_x, const float* xs, const
         a.n = n;
         a.k = k;
         a.epilogue = epilogue;
-        launch_gemm_q8y(a, as_stream(stream));
+        // kernel_i8_y takes any K (runner/src/cpu/gemm_kernels_avx2.cpp:40-76). The kernel reads whole 16-byte chunks,
+        // so K off the 16-grid, or rows that are not 16-byte multiples or aligned, run on zero-padded copies: a zero
+        // byte adds an exact zero to the int32 sum, so the sums and every output bit are the unpadded ones.
+        if (k % 16 != 0 || ld_x % 16 != 0 || ld_w % 16 != 0 || !aligned16(xq) || !aligned16(wq)) {
+            const std::size_t kp = (k + 15) / 16 * 16, xb = up256(t * kp);
+            Lease lease(kScratchOffset + xb + up256(n * kp), st);
+            char* xp = lease.base() + kScratchOffset;
+            char* wp = xp + xb;
+            launch_pad_rows(xq, ld_x, xp, kp, t, k, st);
+            launch_pad_rows(wq, ld_w, wp, kp, n, k, st);
+            a.x = xp;
+            a.ld_x = kp;
+            a.w = reinterpret_cast<const std::int8_t*>(wp);
+            a.ld_w = kp;
+            a.k = kp;
+            a.act_block = kp;
+            launch_gemm_q8y(a, st);
+            return;
+        }
+        launch_gemm_q8y(a, st);
     });
 }
 
 int32_t sepal_hip_gemm_w8a16(const void* x, size_t ld_x, const int8_t* wq, size_t ld_w, const float* sw, void* y,
                              int32_t y_type, size_t ld_y, size_t t, size_t n, size_t k, void* stream) {
     return guarded([&] {
-        check_s8_family("gemm_w8a16", x, ld_x, wq, ld_w, sw, y, y_type, ld_y, n, k, 128);
-        if (t == 0) return;
-        require(t < 0x7FFFFFFFu && n < 0x7FFFFFFFu, "gemm_w8a16: dimension beyond 2^31");
+        // (the order of launch_gemm_w8a16's checks, runner/cuda/src/gemm_s8_kernels.cu:550-557)
+        if (t == 0 || n == 0) return;
+        require(x != nullptr && wq != nullptr && sw != nullptr && y != nullptr, "gemm_w8a16: null pointer");
+        require(y_type == SEPAL_HIP_F32 || y_type == SEPAL_HIP_F16, "gemm_w8a16: the output is float32 or binary16");
+        require(sepal_hip_gemm_w8a16_supports(n, k, ld_x, ld_w, ld_y) == 1,
+                "gemm_w8a16: unsupported shape (K a multiple of 16, ld_x of 8, ld_w of 16, N and ld_y even, strides at "
+                "least K and N)");
+        require(aligned16(x) && aligned16(wq) && aligned8(y) && reinterpret_cast<std::uintptr_t>(sw) % 4 == 0,
+                "gemm_w8a16: X and W must be 16-byte aligned, Y 8-byte aligned, the scales 4-byte aligned");
+        require(t < 0x7FFFFFFFu && n < 0x7FFFFFFFu && k < 0x7FFFFFFFu, "gemm_w8a16: dimension beyond 2^31");
         const hipStream_t st = as_stream(stream);
-        // the per-channel scale as per-group scales in the workspace, then the w8g multiply (binary16 X, Store). Above
-        // the small-M size a binary16 output comes straight from the large-M kernels; below it, through float32 row
-        // chunks of at most 64 MB and a conversion (the same rounding; a row's bits do not depend on the batch).
-        const std::size_t groups = k / 128, s_bytes = (n * groups * 4 + 255) / 256 * 256;
-        const bool direct = y_type == SEPAL_HIP_F32 || t > static_cast<std::size_t>(kSmallM);
-        const std::size_t chunk = direct ? t : std::max<std::size_t>(1, (std::size_t{64} << 20) / (n * 4));
+        // The per-channel scale as per-group scales, then the w8g multiply (binary16 X, Store). K off the 128-grid runs
+        // on zero-padded copies of X and W (an exact zero per padded product), X rows that are not 32-byte multiples on
+        // a copy of X. Above the small-M size a binary16 output comes straight from the large-M kernels; below it (or
+        // for Y rows the kernels cannot store), through float32 row chunks of at most 64 MB and a conversion (the same
+        // rounding; a row's bits do not depend on the batch).
+        const std::size_t kp = (k + 127) / 128 * 128, groups = kp / 128;
+        const bool pad_k = kp != k, stage_x = pad_k || ld_x % 16 != 0;
+        const std::size_t s_bytes = up256(n * groups * 4);
+        const std::size_t xs_bytes = stage_x ? up256(t * kp * 2) : 0;
+        const std::size_t wp_bytes = pad_k ? up256(n * kp) : 0;
+        const bool direct = (y_type == SEPAL_HIP_F32 || t > static_cast<std::size_t>(kSmallM)) && ld_y % 4 == 0 && aligned16(y);
+        const std::size_t ldt = (n + 3) / 4 * 4;
+        const std::size_t chunk = direct ? t : std::max<std::size_t>(1, (std::size_t{64} << 20) / (ldt * 4));
         const std::size_t rows = std::min(t, chunk);
-        GemmArgs probe;
-        probe.t = rows;
-        probe.n = n;
-        probe.k = k;
-        const std::size_t img = direct ? gemm_w8g_image_bytes(probe) : 0;
-        const std::size_t tmp_bytes = direct ? 0 : (rows * n * 4 + 255) / 256 * 256;
-        Lease lease(kScratchOffset + s_bytes + tmp_bytes + img, st);
-        char* ws = lease.base();
-        float* s = reinterpret_cast<float*>(ws + kScratchOffset);
-        float* tmp = reinterpret_cast<float*>(ws + kScratchOffset + s_bytes);
-        launch_broadcast_scales(sw, s, n, groups, st);
-        for (std::size_t r0 = 0; r0 < t; r0 += rows) {
-            const std::size_t tr = std::min(rows, t - r0);
+        const std::size_t tmp_bytes = direct ? 0 : up256(rows * ldt * 4);
+        const auto args = [&](const void* xs, const std::int8_t* w, const float* s, char* tmp, std::size_t r0, std::size_t tr) {
             GemmArgs a;
-            a.x = static_cast<const std::uint16_t*>(x) + r0 * ld_x;
+            a.x = static_cast<const std::uint16_t*>(xs) + r0 * (stage_x ? kp : ld_x);
             a.x_type = SEPAL_HIP_F16;
-            a.ld_x = ld_x;
-            a.w = wq;
-            a.ld_w = ld_w;
+            a.ld_x = stage_x ? kp : ld_x;
+            a.w = w;
+            a.ld_w = pad_k ? kp : ld_w;
             a.s = s;
             a.ld_s = groups;
             a.y = direct ? static_cast<void*>(static_cast<char*>(y) + r0 * ld_y * (y_type == SEPAL_HIP_F32 ? 4 : 2))
                          : static_cast<void*>(tmp);
             a.y_type = direct ? y_type : SEPAL_HIP_F32;
-            a.ld_y = direct ? ld_y : n;
+            a.ld_y = direct ? ld_y : ldt;
             a.t = tr;
             a.n = n;
-            a.k = k;
+            a.k = kp;
             a.epilogue = SEPAL_HIP_STORE;
             a.config = tr > static_cast<std::size_t>(kSmallM) ? 0 : -1;  // no K split: a row's bits do not depend on the batch
-            a.scratch = ws;
-            a.wimage = img != 0 ? ws + kScratchOffset + s_bytes + tmp_bytes : nullptr;
-            a.wimage_bytes = img;
-            launch_gemm_w8g(a, st);
-            if (!direct) launch_f32_to_f16(tmp, n, static_cast<std::uint16_t*>(y) + r0 * ld_y, ld_y, tr, n, st);
+            return a;
+        };
+        // (the layout of the first, largest chunk bounds every later one)
+        const W8gAnyLayout L0 = w8g_any_layout(args(stage_x ? nullptr : x, wq, sw, nullptr, 0, rows));
+        Lease lease(kScratchOffset + s_bytes + xs_bytes + wp_bytes + tmp_bytes + L0.total, st);
+        char* ws = lease.base();
+        char* p = ws + kScratchOffset;
+        float* s = reinterpret_cast<float*>(p);
+        char* xs = p + s_bytes;
+        auto* wp = reinterpret_cast<std::int8_t*>(xs + xs_bytes);
+        char* tmp = xs + xs_bytes + wp_bytes;
+        char* zone = tmp + tmp_bytes;
+        launch_broadcast_scales(sw, s, n, groups, st);
+        if (stage_x) launch_pad_rows(x, ld_x * 2, xs, kp * 2, t, k * 2, st);
+        if (pad_k) launch_pad_rows(wq, ld_w, wp, kp, n, k, st);
+        for (std::size_t r0 = 0; r0 < t; r0 += rows) {
+            const std::size_t tr = std::min(rows, t - r0);
+            const GemmArgs a = args(stage_x ? static_cast<const void*>(xs) : x, pad_k ? wp : wq, s, tmp, r0, tr);
+            w8g_any(a, w8g_any_layout(a), ws, zone, st);
+            if (!direct)
+                launch_put_cols(reinterpret_cast<const float*>(tmp), ldt,
+                                static_cast<char*>(y) + r0 * ld_y * (y_type == SEPAL_HIP_F32 ? 4 : 2), y_type, ld_y, tr, n,
+                                false, st);
         }
     });
 }
@@ -850,15 +1020,20 @@ static __device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
 constexpr int kMaxDevices = 64;
 std::mutex g_static_mutex;
 char* g_static_ptr[kMaxDevices] = {};
+// Calls on one device share its array. Each call's work is recorded in the device's event, and a call on another stream
+// than the last waits for it on the device, so calls on different streams run one after the other (graph capture
+// excepted: there the caller orders the streams). g_static_mutex is held from the wait to the record.
+hipEvent_t g_static_done[kMaxDevices] = {};
+hipStream_t g_static_last[kMaxDevices] = {};
+bool g_static_used[kMaxDevices] = {};
 
 // The current device's static scratch. The first call on a device looks its address up (with that device current)
 // and enqueues, on `stream`, the clearing of the split-K counter zone, which is zero at rest from then on.
-char* static_scratch(hipStream_t stream) {
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) throw LaunchError("hipGetDevice failed");
-    if (dev < 0 || dev >= kMaxDevices) throw LaunchError("mlp_stack_noalloc: device index beyond the library's table");
-    std::lock_guard<std::mutex> lock(g_static_mutex);
+// The caller holds g_static_mutex.
+char* static_scratch(int dev, hipStream_t stream) {
     if (g_static_ptr[dev] == nullptr) {
+        if (hipEventCreateWithFlags(&g_static_done[dev], hipEventDisableTiming) != hipSuccess)
+            throw LaunchError("mlp_stack_noalloc: hipEventCreateWithFlags failed");
         void* ptr = nullptr;
         const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
         if (e != hipSuccess || ptr == nullptr)
@@ -894,7 +1069,22 @@ int32_t sepal_hip_mlp_stack_noalloc(int32_t kind, size_t layers, size_t t, size_
         require(z.end <= kStaticScratchBytes,
                 "mlp_stack_noalloc: this shape needs " + std::to_string(z.end) + " bytes of scratch, beyond the " +
                     std::to_string(kStaticScratchBytes) + " of the static scratch (call with fewer rows)");
-        run_stack(z, kind, layers, t, hidden, inter, x, w_gate_up, s_gate_up, w_down, s_down, y, eps, static_scratch(st), st);
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess) throw LaunchError("hipGetDevice failed");
+        if (dev < 0 || dev >= kMaxDevices) throw LaunchError("mlp_stack_noalloc: device index beyond the library's table");
+        std::lock_guard<std::mutex> lock(g_static_mutex);
+        char* base = static_scratch(dev, st);
+        hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(st, &cap) != hipSuccess) throw LaunchError("mlp_stack_noalloc: hipStreamIsCapturing failed");
+        const bool eager = cap == hipStreamCaptureStatusNone;
+        if (eager && g_static_used[dev] && g_static_last[dev] != st && hipStreamWaitEvent(st, g_static_done[dev], 0) != hipSuccess)
+            throw LaunchError("mlp_stack_noalloc: hipStreamWaitEvent failed");
+        run_stack(z, kind, layers, t, hidden, inter, x, w_gate_up, s_gate_up, w_down, s_down, y, eps, base, st);
+        if (eager) {
+            if (hipEventRecord(g_static_done[dev], st) != hipSuccess) throw LaunchError("mlp_stack_noalloc: hipEventRecord failed");
+            g_static_last[dev] = st;
+            g_static_used[dev] = true;
+        }
     });
 }
 

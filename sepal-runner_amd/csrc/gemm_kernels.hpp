@@ -103,6 +103,13 @@ void launch_rmsnorm_quantize(const float* x, std::size_t ld_x, std::uint16_t* y_
                              std::size_t cols, std::size_t block, double eps, hipStream_t stream);
 void launch_f32_to_bf16(const float* src, std::uint16_t* dst, std::size_t count, hipStream_t stream);
 
+// Edge shapes (edge.hip): a zero-padded copy of `rows` rows of `bytes` bytes (src may be null when bytes is 0) into rows
+// of ld_dst_bytes (a multiple of 4); and y[:, 0:cols] = tmp (or += tmp for add; y float32 or binary16, rounded).
+void launch_pad_rows(const void* src, std::size_t ld_src_bytes, void* dst, std::size_t ld_dst_bytes, std::size_t rows,
+                     std::size_t bytes, hipStream_t stream);
+void launch_put_cols(const float* tmp, std::size_t ld_tmp, void* y, int y_type, std::size_t ld_y, std::size_t rows,
+                     std::size_t cols, bool add, hipStream_t stream);
+
 // Packed-weight files (packed_file.hip): the device fingerprint of a byte range (`lanes` holds
 // fingerprint_scratch_bytes()), and the synchronous save / load of one packed matrix.
 void launch_fingerprint(const void* data, std::size_t bytes, std::uint64_t* out, void* lanes, hipStream_t stream);

@@ -206,6 +206,43 @@ __global__ void __launch_bounds__(256) quantize_rows_token_kernel(const void* __
     }
 }
 
+// The same rule for rows of any length and stride (kernel_i8_y's packing takes any K, runner/src/cpu/gemm.cpp:
+// 286-306): element loads, the row maximum by the same block reduction (a maximum does not depend on order), then each
+// value quantized on its own, so the bits are those of the vector kernel.
+template <int ST>
+__global__ void __launch_bounds__(256) quantize_rows_token_any_kernel(const void* __restrict__ x, std::size_t ld_x,
+                                                                      std::int8_t* __restrict__ q, std::size_t ld_q,
+                                                                      float* __restrict__ scales, std::size_t ld_s, int cols) {
+    __shared__ float red[4];
+    const std::size_t row = blockIdx.x;
+    const auto at = [&](int c) -> float {
+        const std::size_t i = row * ld_x + c;
+        if constexpr (ST == SEPAL_HIP_F32) return static_cast<const float*>(x)[i];
+        else if constexpr (ST == SEPAL_HIP_BF16) return bf16_bits_to_f32(static_cast<const unsigned short*>(x)[i]);
+        else return f16_bits_to_f32(static_cast<const unsigned short*>(x)[i]);
+    };
+    float m = 0.0f;
+    for (int c = threadIdx.x; c < cols; c += 256) {
+        const float a = fabsf(at(c));
+        m = a > m ? a : m;
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float other = __shfl_xor(m, o, 64);
+        m = other > m ? other : m;
+    }
+    if (threadIdx.x % 64 == 0) red[threadIdx.x / 64] = m;
+    __syncthreads();
+    m = red[0];
+#pragma unroll
+    for (int i = 1; i < 4; ++i) m = red[i] > m ? red[i] : m;
+    const float scale = m > 0.0f ? __fdiv_rn(m, 127.0f) : 1.0f;
+    const float inverse = __fdiv_rn(1.0f, scale);
+    if (threadIdx.x == 0) scales[row * ld_s] = scale;
+    for (int c = threadIdx.x; c < cols; c += 256)
+        q[row * ld_q + c] = static_cast<std::int8_t>(quantize_value<SEPAL_HIP_RULE_RECIPROCAL>(at(c), scale, inverse));
+}
+
 // One row per wave, four rows per block. The row is read coalesced (16 bytes per lane, every load of a segment in flight
 // at once) into LDS, then lanes 0..31 run the reference's 32 accumulator chains from LDS: lane L is accumulator register
 // L / 8, lane L % 8, and adds x[c]^2 for c = L, L + 32, ... in order (then, for a tail of 8 to 31 columns, lanes 0..7
@@ -614,6 +651,17 @@ void launch_quantize_rows(const void* x, int x_type, std::size_t ld_x, std::int8
         return;
     }
     const dim3 grid(static_cast<unsigned>(rows));
+    const std::size_t eb = x_type == SEPAL_HIP_F32 ? 4 : 2;
+    if (cols % 16 != 0 || ld_x % 16 != 0 || ld_q % 16 != 0 || reinterpret_cast<std::uintptr_t>(x) % 16 != 0 ||
+        reinterpret_cast<std::uintptr_t>(q) % 16 != 0 || (ld_x * eb) % 16 != 0) {
+        switch (x_type) {
+        case SEPAL_HIP_F32: quant::quantize_rows_token_any_kernel<SEPAL_HIP_F32><<<grid, dim3(256), 0, stream>>>(x, ld_x, q, ld_q, scales, ld_s, static_cast<int>(cols)); break;
+        case SEPAL_HIP_BF16: quant::quantize_rows_token_any_kernel<SEPAL_HIP_BF16><<<grid, dim3(256), 0, stream>>>(x, ld_x, q, ld_q, scales, ld_s, static_cast<int>(cols)); break;
+        default: quant::quantize_rows_token_any_kernel<SEPAL_HIP_F16><<<grid, dim3(256), 0, stream>>>(x, ld_x, q, ld_q, scales, ld_s, static_cast<int>(cols)); break;
+        }
+        check_launch("quantize_rows kernel launch");
+        return;
+    }
     switch (x_type) {
     case SEPAL_HIP_F32: quant::quantize_rows_token_kernel<SEPAL_HIP_F32><<<grid, dim3(256), 0, stream>>>(x, ld_x, q, ld_q, scales, ld_s, static_cast<int>(cols)); break;
     case SEPAL_HIP_BF16: quant::quantize_rows_token_kernel<SEPAL_HIP_BF16><<<grid, dim3(256), 0, stream>>>(x, ld_x, q, ld_q, scales, ld_s, static_cast<int>(cols)); break;

@@ -71,6 +71,7 @@ def library() -> C.CDLL:
         L.sepal_hip_gemm_q8y.argtypes = [vp, sz, vp, vp, sz, vp, vp, i32, sz, sz, sz, sz, i32, vp]
         L.sepal_hip_column_absmax.argtypes = [vp, sz, vp, sz, sz, vp]
         L.sepal_hip_channel_stats.argtypes = [vp, sz, sz, sz, vp, vp, vp]
+        L.sepal_hip_release_workspace.argtypes = [vp]
         for name in ("sepal_hip_quantize_group_s8", "sepal_hip_quantize_gate_up_s8", "sepal_hip_gemm_w8g",
                      "sepal_hip_quantize_rows_s8", "sepal_hip_gemm_q8", "sepal_hip_q8_group_sums",
                      "sepal_hip_rmsnorm_rows", "sepal_hip_float_to_bf16", "sepal_hip_mlp_stack",
@@ -78,7 +79,7 @@ def library() -> C.CDLL:
                      "sepal_hip_rmsnorm_quantize_rows", "sepal_hip_gemm_q8_swiglu_quantize",
                      "sepal_hip_weight_fingerprint", "sepal_hip_packed_save", "sepal_hip_packed_load",
                      "sepal_hip_s8_quantize_rows", "sepal_hip_gemm_s8", "sepal_hip_gemm_w8a16", "sepal_hip_gemm_q8y",
-                     "sepal_hip_column_absmax", "sepal_hip_channel_stats"):
+                     "sepal_hip_column_absmax", "sepal_hip_channel_stats", "sepal_hip_release_workspace"):
             getattr(L, name).restype = i32
         L.sepal_hip_gemm_w8g_supports.restype = i32
         L.sepal_hip_gemm_s8_supports.restype = i32
@@ -344,6 +345,12 @@ def packed_load(path: str, q, s, source_fp: int, rule: int = RULE_DIVIDE, layout
         return False
     _check(rc)
     return True
+
+
+def release_workspace(stream=None) -> None:
+    """Frees the library's workspace of (current device, stream) after waiting for the stream (before the stream is
+    destroyed, or to give the memory back)."""
+    _check(library().sepal_hip_release_workspace(_stream(stream)))
 
 
 def float_to_bf16(x, stream=None):

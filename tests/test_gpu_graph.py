@@ -25,6 +25,16 @@ def sm():
     return sepal_mlp
 
 
+_SIDE = []
+
+
+def _side():
+    """One side stream for every test of the module (the library keeps a workspace per stream)."""
+    if not _SIDE:
+        _SIDE.append(torch.cuda.Stream())
+    return _SIDE[0]
+
+
 # T = 1 and 16: the pass kernels; 48: the large-M plan with a K split; 896: split-K down, planned gate/up
 @pytest.mark.parametrize("t", [1, 16, 48, 896])
 def test_captured_mlp_block_replays(sm, t):
@@ -57,7 +67,7 @@ def test_captured_mlp_block_replays(sm, t):
         hq, hs = sm.quantize_rows_s8(hf, block=I, stream=st)
         sm.gemm_q8(hq, hs, qd, qsd, y=z, act_block=I, stream=st)
 
-    side = torch.cuda.Stream()
+    side = _side()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
         for _ in range(2):
