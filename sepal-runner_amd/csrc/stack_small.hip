@@ -6,9 +6,10 @@
 // At 16 tokens each layer is a single pass over 77 MB of int8 weights and scales, so the kernels are shaped to keep
 // every CU streaming its share of weights for the whole kernel:
 //   tiles  (gate/up, SwiGLU): one block of 16 waves per CU, and each block owns whole 16-row weight tiles (8 gate rows
-//          and the 8 up rows of the same features) over the full K, 4 or 5 tiles per CU at the model's shape. Every
-//          wave first stages one X row in LDS; then 4 loader waves stage the block's scales while the 12 worker waves
-//          already have every weight load of their pairs in flight; the block's (tile, group) pairs are split evenly
+//          and the 8 up rows of the same features) over the full K, 4 or 5 tiles per CU at the model's shape. 4 loader
+//          waves stage the 16 X rows straight into LDS (their requests issued before any weight request) and the
+//          block's scales, while the 12 worker waves already have every weight load of their pairs in flight and wait
+//          for the loaders' flag; the block's (tile, group) pairs are split evenly
 //          over the workers, and their partial tiles are added in LDS in worker order, then SwiGLU. Weight loads take
 //          whole 128-byte lines (8 rows per instruction) and pass through a per-worker LDS transpose into the MFMA
 //          layout.
@@ -41,6 +42,9 @@ __device__ __forceinline__ f32x4 mfma16(int xt, const u32x4 a, const u32x4 b, f3
         return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
 }
+
+typedef __attribute__((address_space(3))) void lds_void;
+typedef const __attribute__((address_space(1))) void global_void;
 
 // Activation type of the gpu-q8w stack: int8 X (and int8 H, quantized by the down pass's loaders) on int8 MFMAs.
 constexpr int kActI8 = 8;
@@ -184,54 +188,70 @@ __global__ void __launch_bounds__(kThreads) pass_kernel(const PassParams p) {
     __shared__ unsigned row_max[16];  // q8 gate/up, per token: |H| maxima of this block's outputs (float bits)
     if (tid == 0) ready = 0u;
     if (tid < 16) row_max[tid] = 0u;
-    // ---- every wave stages one row of X (rows past T repeat row T - 1 and feed only outputs that are never stored)
-    // before any weight load is issued: behind a weight burst these loads would wait in the memory queues (M = 16
-    // stack: w8g 1.240 -> 1.197 ms per pass; q8 1.46 -> 1.30 ms) ----
-    const int xr = min(wave, p.t - 1);
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the counter is zero before the barrier below lets any wave count
+    // ---- X (rows past T repeat row T - 1 and feed only outputs that are never stored). The loader waves stage all 16
+    // rows straight from global memory into LDS (direct loads, no registers; 4 rows a wave), and their requests are
+    // issued before any weight request of the block (a bare barrier orders the issue, not the arrival): behind a
+    // weight burst these loads would wait in the memory queues, and waiting for them before the burst (as a block
+    // barrier would) leaves the weight stream idle for their round trip. The workers wait for the loaders' flag. The
+    // q8 down pass quantizes H while it stages it, every wave one row, ahead of the burst. ----
+    constexpr bool kEarly = !(XT == kActI8 && !SWIGLU);  // X loads in flight under the weight issue
+    float xsv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    // the loaders' share of the block's weight scales (row runs of gpt words)
+    float sv[kScaleLoads];
+    const auto load_scales = [&] {
+#pragma unroll
+        for (int e = 0; e < kScaleLoads; ++e) {
+            const int idx = min(tid + e * 64 * kLoaders, total * 16 - 1);
+            const int tl = idx / (16 * gpt), rem = idx % (16 * gpt);
+            const int row = min(tile_row<SWIGLU>(tile0 + tl, rem / gpt), p.n - 1);
+            sv[e] = p.s[static_cast<std::size_t>(row) * p.ld_s + g_lo + rem % gpt];
+        }
+    };
     if constexpr (XT == kActI8 && !SWIGLU) {
         // q8 down: H float32 quantized as the activation quantizer does (rule RECIPROCAL, scale = max / 127), per 128
         // columns or with the row maximum of the gate/up pass's partial maxima (per token)
         if (gpt <= 14) stage_h_q8<7, 1>(p, lds, xsc, xpitch, g_lo, gpt, wave, 1, lane);
         else stage_h_q8<12, 1>(p, lds, xsc, xpitch, g_lo, gpt, wave, 1, lane);
-    } else if constexpr (Q8) {
-        // q8 gate/up: int8 rows (16-byte chunks of 16 columns) and the rows' activation scales
-        const int cq = kw / 16;
-        const unsigned char* xrow = reinterpret_cast<const unsigned char*>(p.x) + static_cast<std::size_t>(xr) * p.ld_x + 128 * g_lo;
-        u32x4 xv[kXChunks / 2];
-#pragma unroll
-        for (int e = 0; e < kXChunks / 2; ++e) xv[e] = *reinterpret_cast<const u32x4*>(xrow + 16 * min(lane + 64 * e, cq - 1));
-        const int nsc = p.per_token ? 1 : gpt;
-        const float xsv = p.xs[static_cast<std::size_t>(xr) * p.ld_xs + (p.per_token ? 0 : g_lo + min(lane, nsc - 1))];
-#pragma unroll
-        for (int e = 0; e < kXChunks / 2; ++e)
-            if (lane + 64 * e < cq) *reinterpret_cast<u32x4*>(lds + wave * xpitch + 16 * (lane + 64 * e)) = xv[e];
-        if (lane < nsc) xsc[p.per_token ? wave : wave * gpt + lane] = xsv;
+        __syncthreads();
     } else {
-        const int cpr = kw / 8;
-        const unsigned short* xrow = p.x + static_cast<std::size_t>(xr) * p.ld_x + 128 * g_lo;
-        u32x4 xv[kXChunks];
+        if (wave < kLoaders) {
+            const int chunks = Q8 ? kw / 16 : kw / 8;  // 16-byte chunks of a row
+            const int esz = Q8 ? 1 : 2;
 #pragma unroll
-        for (int e = 0; e < kXChunks; ++e) xv[e] = *reinterpret_cast<const u32x4*>(xrow + 8 * min(lane + 64 * e, cpr - 1));
+            for (int j = 0; j < 4; ++j) {
+                const int r = 4 * wave + j, xr = min(r, p.t - 1);
+                const unsigned char* xrow = reinterpret_cast<const unsigned char*>(p.x) + (static_cast<std::size_t>(xr) * p.ld_x + 128 * g_lo) * esz;
 #pragma unroll
-        for (int e = 0; e < kXChunks; ++e)
-            if (lane + 64 * e < cpr) *reinterpret_cast<u32x4*>(lds + wave * xpitch + 16 * (lane + 64 * e)) = xv[e];
+                for (int e = 0; e < (Q8 ? kXChunks / 2 : kXChunks); ++e)
+                    if (lane + 64 * e < chunks)
+                        __builtin_amdgcn_global_load_lds((global_void*)(xrow + 16 * (lane + 64 * e)),
+                                                         (lds_void*)(lds + r * xpitch + 1024 * e), 16, 0, 0);
+                if constexpr (Q8) {
+                    const int nsc = p.per_token ? 1 : gpt;
+                    xsv[j] = p.xs[static_cast<std::size_t>(xr) * p.ld_xs + (p.per_token ? 0 : g_lo + min(lane, nsc - 1))];
+                }
+            }
+        }
+        __builtin_amdgcn_s_barrier();  // the loaders' X requests are issued before any weight request
     }
-    __syncthreads();
 
     if (wave < kLoaders) {
-        // ---- loaders: the block's weight scales (row runs of gpt words) ----
-        const int lt = tid;      // 0 .. 64 kLoaders - 1
-        float sv[kScaleLoads];
-#pragma unroll
-        for (int e = 0; e < kScaleLoads; ++e) {
-            const int idx = min(lt + e * 64 * kLoaders, total * 16 - 1);
-            const int tl = idx / (16 * gpt), rem = idx % (16 * gpt);
-            const int row = min(tile_row<SWIGLU>(tile0 + tl, rem / gpt), p.n - 1);
-            sv[e] = p.s[static_cast<std::size_t>(row) * p.ld_s + g_lo + rem % gpt];
-        }
+        // ---- loaders: the block's weight scales into LDS (issued beside the workers' weights: ahead of them they
+        // measured slower), then X (the q8 activation scales too) has landed ----
+        load_scales();
 #pragma unroll
         for (int e = 0; e < kScaleLoads; ++e)
-            if (lt + e * 64 * kLoaders < total * 16) scl[lt + e * 64 * kLoaders] = sv[e];
+            if (tid + e * 64 * kLoaders < total * 16) scl[tid + e * 64 * kLoaders] = sv[e];
+        if constexpr (kEarly) {
+            if constexpr (Q8) {
+                const int nsc = p.per_token ? 1 : gpt;
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    if (lane < nsc) xsc[p.per_token ? 4 * wave + j : (4 * wave + j) * gpt + lane] = xsv[j];
+            }
+            __builtin_amdgcn_s_waitcnt(0);  // vmcnt(0) lgkmcnt(0): the direct X loads have landed in LDS
+        }
         __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS writes are done
         if (lane == 0) __hip_atomic_fetch_add(&ready, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
     } else {
@@ -259,12 +279,6 @@ __global__ void __launch_bounds__(kThreads) pass_kernel(const PassParams p) {
             int slot = qs / gpt - first_tile, g = g_lo + qs % gpt;
 #pragma unroll
             for (int i = 0; i < kPairs; ++i) {
-                const signed char* src = wrow[0] + 128 * g;
-#pragma unroll
-                for (int j = 1; j < kSlots; ++j)
-                    if (slot == j) src = wrow[j] + 128 * g;
-                wb[i][0] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src));
-                wb[i][1] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + kRowStep * p.ld_w));
                 pslot[i] = slot;
                 pg[i] = g;
                 if (q0 + i + 1 < q1) {
@@ -274,6 +288,15 @@ __global__ void __launch_bounds__(kThreads) pass_kernel(const PassParams p) {
                     }
                 }
             }
+        }
+#pragma unroll
+        for (int i = 0; i < kPairs; ++i) {
+            const signed char* src = wrow[0] + 128 * pg[i];
+#pragma unroll
+            for (int j = 1; j < kSlots; ++j)
+                if (pslot[i] == j) src = wrow[j] + 128 * pg[i];
+            wb[i][0] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src));
+            wb[i][1] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + kRowStep * p.ld_w));
         }
         // ---- X and the scales are staged ----
         while (__hip_atomic_load(&ready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < static_cast<unsigned>(kLoaders))
