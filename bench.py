@@ -336,6 +336,20 @@ def main():
     extra = {"c3_down_kernel": {"ms": round(ms_dn, 4), "tflops": round(dn_tflops, 1),
                                 "frac_bf16_peak": round(dn_tflops / PEAK["bf16_tflops"], 4)}}
     if not args.no_extra:
+        # ---- the practical ceiling of these shapes: hipBLASLt's plain bf16 GEMM (torch.matmul, no dequantization, no
+        # group scales, no epilogue) at the C3 gate/up and down shapes, X [M, K] times W[N, K]^T, timed the same way ----
+        ceil = {}
+        for name, n_c, k_c in (("gate_up", 2 * I, H), ("down", H, I)):
+            a_c = torch.randn(M_BIG, k_c, device="cuda").bfloat16()
+            w_c = torch.randn(n_c, k_c, device="cuda").bfloat16()
+            o_c = torch.empty(M_BIG, n_c, dtype=torch.bfloat16, device="cuda")
+            ms_c = timed(torch, lambda: torch.matmul(a_c, w_c.t(), out=o_c), 10, 3, stream)
+            tf_c = 2.0 * M_BIG * n_c * k_c / (ms_c * 1e-3) / 1e12
+            ceil[name] = {"ms": round(ms_c, 4), "tflops": round(tf_c, 1), "frac_bf16_peak": round(tf_c / PEAK["bf16_tflops"], 4)}
+            del a_c, w_c, o_c
+        ceil["note"] = "torch.matmul bf16 (hipBLASLt), [15872 x K] x [N x K]^T, bf16 out"
+        extra["bf16_gemm_ceiling"] = ceil
+        log(f"bf16 GEMM ceiling (torch.matmul): {ceil}")
         # ---- C3 with H kept in float32 (mlp_stack kind 2: the down multiply on bf16 hi + lo pairs) ----
         def step_c3_f32h():
             x.copy_(x0)

@@ -208,7 +208,9 @@ SEPAL_HIP_API int32_t sepal_hip_gemm_q8_swiglu_quantize(const int8_t* xq, size_t
                                           size_t k, int32_t config, void* stream);
 
 /* The exact int32 per-group sums of the q8 multiply, sums[g][t][n] = sum over k in group g of xq[t,k] * w[n,k]
- * (int8 MFMA, the same kernel body as sepal_hip_gemm_q8's large-M path). For checking the integer part bit for bit. */
+ * (int8 MFMA), from the kernels the q8 multiplies run at that size: at T <= 16 the M <= 16 stack's pass kernels (the
+ * gate/up pass for N a multiple of 128, else the K-parts pass) where a pass plan takes the shape, else the large-M
+ * kernel body of sepal_hip_gemm_q8. For checking the integer part bit for bit. */
 SEPAL_HIP_API int32_t sepal_hip_q8_group_sums(const int8_t* xq, size_t ld_x, const int8_t* w, size_t ld_w, int32_t* sums, size_t t,
                                 size_t n, size_t k, void* stream);
 

@@ -698,7 +698,10 @@ int32_t sepal_hip_q8_group_sums(const int8_t* xq, size_t ld_x, const int8_t* w, 
         a.n = n;
         a.k = k;
         a.sums = sums;
-        launch_q8_group_sums(a, as_stream(stream));
+        const hipStream_t st = as_stream(stream);
+        Lease ws(kScratchOffset, st);
+        a.scratch = ws.base();
+        launch_q8_group_sums(a, st);
     });
 }
 

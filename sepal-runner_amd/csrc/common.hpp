@@ -144,6 +144,15 @@ __device__ __forceinline__ float swiglu_cephes(float g, float u) {
     return __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, e)), u);
 }
 
+// silu(g) * u of the gpu-q8w multiplies. With one activation scale per 128 values (cpu-q8's I8_Z blocking) the
+// cpu-q8 epilogue bit for bit; with one scale per token, a form with no reference bits to match, the fast one (the
+// float results are held to the parity bar; the int32 group sums stay exact).
+template <bool PER_TOKEN>
+__device__ __forceinline__ float swiglu_q8(float g, float u) {
+    if constexpr (PER_TOKEN) return swiglu_fast(g, u);
+    else return swiglu_cephes(g, u);
+}
+
 // ---- group scales in Horner form ---------------------------------------------------------------------------------------
 
 // One Horner step of the w8g group scales. The MFMAs add each group's partial sum P_g straight into the running sum U,

@@ -140,6 +140,9 @@ void launch_small_gemm_w8g(const GemmArgs& a, const SmallGemmPlan& plan, hipStre
 // The q8 form for the SwiGLU multiply (float32 H): the gate/up pass of the q8 stack.
 bool small_gemm_plan_q8(const GemmArgs& a, SmallGemmPlan& plan);
 void launch_small_gemm_q8(const GemmArgs& a, const SmallGemmPlan& plan, hipStream_t stream);
+// The exact int32 group sums (a.sums [K/128][T][N]) from the pass kernels' int8 MFMAs at T <= 16 (the gate/up pass
+// when N is a multiple of 128, else the K-parts pass); false when no pass plan takes the shape.
+bool small_q8_group_sums(const GemmArgs& a, hipStream_t stream);
 // ... and for the Store / Add multiply (float32 Y through K-parts and the parts sum).
 bool small_gemm_plan_q8_parts(const GemmArgs& a, SmallGemmPlan& plan);
 void launch_small_gemm_q8_parts(const GemmArgs& a, const SmallGemmPlan& plan, hipStream_t stream);

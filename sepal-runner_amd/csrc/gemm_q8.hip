@@ -115,7 +115,9 @@ typedef const __attribute__((address_space(1))) void global_void;
 // The chain modes' epilogue of a 128 x 256 tile: acc[i][q][r] holds the chain of output (row m0 + wm 64 + 32 i +
 // 8 (r / 4) + 4 (lane / 32) + r % 4, column col[q]); per token it is multiplied by the row's activation scale here.
 // hb: LDS scratch of 32 KB (kSwigluQ8 only; free when called).
-template <int EP, int YT, bool PER_TOKEN>
+// FAST_SILU: the SwiGLU of the per-token chain (swiglu_q8<true>); the per-128 chain and the AVX2 int8 multiply's
+// whole-K form keep the cpu-q8 silu.
+template <int EP, int YT, bool PER_TOKEN, bool FAST_SILU = PER_TOKEN>
 __device__ __forceinline__ void chain_epilogue(const Params& p, float (&acc)[2][2][16], int m0, int n0, int wm, int ib, int hh,
                                                int lane, int tid, const int (&col)[2], float* hb) {
     constexpr int BM = 128;
@@ -143,7 +145,7 @@ __device__ __forceinline__ void chain_epilogue(const Params& p, float (&acc)[2][
                             v0 = __fmul_rn(v0, xs);
                             v1 = __fmul_rn(v1, xs);
                         }
-                        hb[rl * 64 + (((c / 4) ^ (rl % 16)) * 4) + c % 4] = swiglu_cephes(v0, v1);
+                        hb[rl * 64 + (((c / 4) ^ (rl % 16)) * 4) + c % 4] = swiglu_q8<FAST_SILU>(v0, v1);
                     }
             }
             __syncthreads();
@@ -215,7 +217,7 @@ __device__ __forceinline__ void chain_epilogue(const Params& p, float (&acc)[2][
                 }
                 if constexpr (EP == SEPAL_HIP_SWIGLU) {
                     char* const rp = yb + (row * p.ld_y + n0 / 2 + 64 * ibu + 32 * hhu) * ES;
-                    store_out<YT>(rp + voff, 0, swiglu_cephes(v0, v1));
+                    store_out<YT>(rp + voff, 0, swiglu_q8<FAST_SILU>(v0, v1));
                 } else {
                     // put writes float32
                     const unsigned foff = (lrow * static_cast<unsigned>(p.ld_y) + lane % 32) * 4u;
@@ -241,7 +243,7 @@ __device__ __forceinline__ void chain_epilogue(const Params& p, float (&acc)[2][
             }
             if constexpr (EP == SEPAL_HIP_SWIGLU) {
                 const int f = n0 / 2 + 64 * ib + 32 * hh + lane % 32;
-                if (2 * f < p.n) store_out<YT>(p.y, static_cast<std::size_t>(row) * p.ld_y + f, swiglu_cephes(v0, v1));
+                if (2 * f < p.n) store_out<YT>(p.y, static_cast<std::size_t>(row) * p.ld_y + f, swiglu_q8<FAST_SILU>(v0, v1));
             } else {
                 if (col[0] < p.n) put<EP, YT>(p.y, p.ld_y, row, col[0], v0);
                 if (col[1] < p.n) put<EP, YT>(p.y, p.ld_y, row, col[1], v1);
@@ -502,7 +504,7 @@ __global__ void __launch_bounds__(512) gemm_big(const Params p) {
                 for (int r = 0; r < 16; ++r) acc[i][j][r] = __fmul_rn(static_cast<float>(tot[i][j][r]), wsrow[j][0]);
     }
 
-    chain_epilogue<EP, YT, PER_TOKEN>(p, acc, m0, n0, wm, ib, hh, lane, tid, col, reinterpret_cast<float*>(lw0));
+    chain_epilogue<EP, YT, PER_TOKEN, PER_TOKEN && MODE == MODE_CHAIN>(p, acc, m0, n0, wm, ib, hh, lane, tid, col, reinterpret_cast<float*>(lw0));
 }
 
 // ---- the chain modes, one 32 x 32 block at a time (gemm_chain) -----------------------------------------------------
@@ -1065,6 +1067,9 @@ void launch_gemm_q8y(const GemmArgs& a, hipStream_t stream) {
 }
 
 void launch_q8_group_sums(const GemmArgs& a, hipStream_t stream) {
+    // at T <= 16 (config -1) the M <= 16 stack's pass kernels, whose int8 MFMAs the q8 stack and the single q8 calls at
+    // those sizes run; else the large-M kernel body
+    if (a.config < 0 && small_q8_group_sums(a, stream)) return;
     q8::launch_big<SEPAL_HIP_STORE, SEPAL_HIP_F32, true, q8::MODE_SUMS>(a, stream);
 }
 

@@ -81,6 +81,7 @@ struct PassParams {
     const float* hmax;        // down, per token: the gate/up pass's partial row maxima of |H| [T, hmax_blocks]
     int hmax_blocks;
     float* pmax;              // gate/up, per token: this pass's partial row maxima [T, gridDim.x]
+    std::int32_t* sums;       // q8, when set: only the exact int32 group sums, sums[g][T][N] (no chain, no epilogue)
 };
 
 // Weight row of column c (0..15) of a tile. SwiGLU tiles take 8 gate rows and the 8 up rows of the same features in the
@@ -342,6 +343,18 @@ __global__ void __launch_bounds__(kThreads) pass_kernel(const PassParams p) {
                     const u32x4 a = *reinterpret_cast<const u32x4*>(lds + (lane % 16) * xpitch + kofs + 64 * h + 16 * (lane / 16));
                     acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i32x4, a), __builtin_bit_cast(i32x4, wv), acc, 0, 0, 0);
                 }
+                if (p.sums != nullptr) {
+                    // the pair's group sums as they are: lane l holds token rows 4 (l / 16) + r of weight row
+                    // (tile column) l % 16
+                    const int wrow_n = tile_row<SWIGLU>(tile0 + first_tile + pslot[i], lane % 16);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int row = 4 * (lane / 16) + r;
+                        if (row < p.t && wrow_n < p.n)
+                            p.sums[(static_cast<std::size_t>(pg[i]) * p.t + row) * p.n + wrow_n] = acc[r];
+                    }
+                    continue;
+                }
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const float s_r = p.per_token ? sc : __fmul_rn(sc, xsc[(4 * (lane / 16) + r) * gpt + q % gpt]);
@@ -371,6 +384,7 @@ __global__ void __launch_bounds__(kThreads) pass_kernel(const PassParams p) {
         if (n_pairs > 0) flush(cur_slot);
     }
 
+    if (p.sums != nullptr) return;  // (uniform) the group sums are written
     // ---- per block-local tile: the workers that cover it, q / per over the tile's pairs; per worker: its first tile ----
     __shared__ int cover_lo[kWaves], cover_hi[kWaves], worker_first[kWorkers];
     if (tid < ntiles) {
@@ -389,7 +403,7 @@ __global__ void __launch_bounds__(kThreads) pass_kernel(const PassParams p) {
         return v;
     };
     if constexpr (Q8 && SWIGLU) {
-        // H = swiglu_cephes(gate, up) in float32 (the gpu-q8w epilogue), and, per token, this block's row maxima of |H|
+        // H = SwiGLU(gate, up) in float32 (the gpu-q8w epilogue), and, per token, this block's row maxima of |H|
         float* hy = static_cast<float*>(p.y);
         for (int id = tid; id < ntiles * 16 * 8; id += kThreads) {
             const int tl = id / 128, r = (id / 8) % 16, i = id % 8;
@@ -401,7 +415,8 @@ __global__ void __launch_bounds__(kThreads) pass_kernel(const PassParams p) {
                 g = __fmul_rn(g, xsc[r]);
                 u = __fmul_rn(u, xsc[r]);
             }
-            const float hv = swiglu_cephes(g, u);
+            // (per token, a form with no reference bits, the fast silu, as the large-M q8 kernels use it)
+            const float hv = p.per_token ? swiglu_fast(g, u) : swiglu_cephes(g, u);
             hy[static_cast<std::size_t>(r) * p.ld_y + f] = hv;
             if (p.per_token) atomicMax(&row_max[r], __float_as_uint(fabsf(hv)));
         }
@@ -914,6 +929,47 @@ void launch_small_gemm_q8(const GemmArgs& a, const SmallGemmPlan& plan, hipStrea
     p.per_token = a.act_block == a.k && a.k != 128 ? 1 : 0;
     p.pmax = reinterpret_cast<float*>(static_cast<char*>(a.scratch) + kCounterBytes);  // unused by the caller
     launch_pass<kActI8, true, SEPAL_HIP_F32>(p, plan.lds, stream);
+}
+
+bool small_q8_group_sums(const GemmArgs& a, hipStream_t stream) {
+    using namespace stack;
+    if (a.t == 0 || a.t > 16 || a.scratch == nullptr || a.sums == nullptr) return false;
+    // the gate/up pass (its 64-row interleaved tiles) when N is a multiple of 128, else the K-parts pass; no scales
+    // are applied (the loaders read a placeholder in the workspace)
+    GemmArgs b = a;
+    b.x_type = SEPAL_HIP_BF16;
+    b.y_type = SEPAL_HIP_F32;
+    b.epilogue = a.n % 128 == 0 ? SEPAL_HIP_SWIGLU : SEPAL_HIP_STORE;
+    SmallGemmPlan plan;
+    if (!small_gemm_plan(b, plan)) {
+        if (b.epilogue == SEPAL_HIP_STORE) return false;
+        b.epilogue = SEPAL_HIP_STORE;
+        if (!small_gemm_plan(b, plan)) return false;
+    }
+    const bool swiglu = b.epilogue == SEPAL_HIP_SWIGLU;
+    if (!swiglu && (a.k / 128 + plan.parts - 1) / plan.parts > 24) return false;
+    const float* dummy = reinterpret_cast<const float*>(static_cast<const char*>(a.scratch) + kCounterBytes);
+    PassParams p{};
+    p.x = static_cast<const unsigned short*>(a.x);
+    p.ld_x = a.ld_x;
+    p.w = reinterpret_cast<const signed char*>(a.w);
+    p.ld_w = a.ld_w;
+    p.s = dummy;
+    p.ld_s = 0;
+    p.t = static_cast<int>(a.t);
+    p.n = static_cast<int>(a.n);
+    p.k = static_cast<int>(a.k);
+    p.parts = plan.parts;
+    p.per_block = plan.per_block;
+    p.tiles = static_cast<int>(a.n / 16);
+    p.blocks_per_part = (p.tiles + p.per_block - 1) / p.per_block;
+    p.xs = dummy;
+    p.ld_xs = 0;
+    p.per_token = 1;
+    p.sums = a.sums;
+    if (swiglu) launch_pass<kActI8, true, SEPAL_HIP_F32>(p, plan.lds, stream);
+    else launch_pass<kActI8X, false, SEPAL_HIP_F32>(p, plan.lds, stream);
+    return true;
 }
 
 bool small_gemm_plan_q8_parts(const GemmArgs& a, SmallGemmPlan& plan) {

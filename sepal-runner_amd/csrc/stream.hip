@@ -76,7 +76,9 @@ __device__ __forceinline__ int span_col(int span, int c) {
     }
 }
 
-template <int EP, int YT, bool CEPHES>
+// SILU: 0 the w8g form (HIP's expf / log1pf), 1 the cpu-q8 form (per-128 activation scales), 2 the fast form (q8 with
+// one activation scale per token)
+template <int EP, int YT, int SILU>
 __device__ __forceinline__ void epilogue(const Params& p, const float* tile, int ldt, int rows, int span) {
     // tile [rows][kSpan] floats in LDS; threads write consecutive columns of a row (coalesced)
     if constexpr (EP == SEPAL_HIP_SWIGLU) {
@@ -85,7 +87,7 @@ __device__ __forceinline__ void epilogue(const Params& p, const float* tile, int
             const int f = 64 * (span / 2) + 32 * (span % 2) + c;  // feature of gate row span_col(span, c)
             if (r >= p.t || 2 * f >= p.n) continue;
             const float g = tile[r * ldt + c], u = tile[r * ldt + c + 32];
-            store_out<YT>(p.y, static_cast<std::size_t>(r) * p.ld_y + f, CEPHES ? swiglu_cephes(g, u) : swiglu_libm(g, u));
+            store_out<YT>(p.y, static_cast<std::size_t>(r) * p.ld_y + f, SILU == 1 ? swiglu_cephes(g, u) : (SILU == 2 ? swiglu_fast(g, u) : swiglu_libm(g, u)));
         }
     } else {
         float* y = static_cast<float*>(p.y);
@@ -289,7 +291,7 @@ __global__ void __launch_bounds__(256) gemm_stream(const Params p) {
         }
         __syncthreads();
     }
-    epilogue<EP, YT, K::q8>(p, tile, ldt, ROWS, span);
+    epilogue<EP, YT, K::q8 ? (K::per_token ? 2 : 1) : 0>(p, tile, ldt, ROWS, span);
 }
 
 // ---- launch ----------------------------------------------------------------------------------------------------------

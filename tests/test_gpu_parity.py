@@ -719,7 +719,8 @@ def test_q8_swiglu_bit_exact(sm, case):
 @pytest.mark.parametrize("act", ["128", "token"])
 def test_q8_swiglu_quantize_fused(sm, case, act):
     """gate/up with the int8 re-quantization of H in the epilogue equals gemm_q8 (SwiGLU, float32 H) followed by the
-    activation quantizer (block 128), bit for bit, on both paths; the large path also equals the oracle chain."""
+    activation quantizer (block 128), bit for bit, on both paths; with per-128 input scales the large path also equals
+    the oracle chain."""
     t, n, k = case
     rng = np.random.default_rng(11 * t + n + k)
     x = bf16_inputs(rng, (t, k), outlier_frac=0.01)
@@ -736,7 +737,8 @@ def test_q8_swiglu_quantize_fused(sm, case, act):
         hq_ref, hs_ref = sm.quantize_rows_s8(h, block=128)
         hq, hs = sm.gemm_q8_swiglu_quantize(xq, xs, wq, ws, act_block=ab, config=cfg)
         assert same_bits(host(hq), host(hq_ref)) and same_bits(host(hs), host(hs_ref))
-        if cfg == 0 or t > 64:
+        if (cfg == 0 or t > 64) and act == "128":
+            # (per token the SwiGLU is the fast form, so H is within the bar of the oracle's, not its bits)
             href = orc.gemm_q8(host(xq), host(xs), host(wq), host(ws), epilogue=orc.SWIGLU, act_block=ab)
             qo, so = orc.quantize_block_r2(href, block=128)
             assert same_bits(host(hq), qo) and same_bits(host(hs), so)
@@ -774,6 +776,25 @@ def test_q8_group_sums_exact_with_outliers(sm):
     xe = torch.full((130, 256), -127, dtype=torch.int8, device="cuda")
     we = torch.full((32, 256), -127, dtype=torch.int8, device="cuda")
     assert np.all(host(sm.q8_group_sums(xe, we)) == 128 * 127 * 127)
+
+
+@pytest.mark.parametrize("t,n,k", [(1, 19456, 2560), (16, 19456, 2560), (1, 2560, 9728), (16, 2560, 9728), (5, 1024, 512)])
+def test_q8_small_m_group_sums_exact(sm, t, n, k):
+    """At T <= 16 the group sums come from the M <= 16 stack's pass kernels (the gate/up pass with its interleaved
+    tiles for N a multiple of 128 and K <= 3072; the K-parts pass at the down shape): the int32 sums those kernels'
+    int8 MFMAs form, bit for bit against brute force, at the model's K of 2560 and 9728, with outlier channels; the
+    extremes (every product 127 x 127) do not overflow."""
+    say("q8 small-M group sums", t, n, k)
+    rng = np.random.default_rng(t + n + k)
+    x = bf16_inputs(rng, (t, k), outlier_frac=0.01)
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    xq, _ = sm.quantize_rows_s8(dev(x, torch.bfloat16), block=k)
+    wq, _ = sm.quantize_group_s8(dev(w), rule=1)
+    sums = host(sm.q8_group_sums(xq, wq))
+    assert np.array_equal(sums, orc.group_sums(host(xq), host(wq)))
+    xe = torch.full((t, k), -127, dtype=torch.int8, device="cuda")
+    we = torch.full((n, k), 127, dtype=torch.int8, device="cuda")
+    assert np.all(host(sm.q8_group_sums(xe, we)) == -128 * 127 * 127)
 
 
 # ---- the stack -----------------------------------------------------------------------------------------------------------
@@ -864,15 +885,17 @@ def test_mlp_stack(sm, kind, act, t):
     y = host(sm.mlp_stack(kind, xt, layers, act_block=act))
     # the one-call stack is exactly its steps called one by one
     assert same_bits(y, _gpu_composition(sm, kind, x, layers, act))
-    if kind == 1 and t > 64:
+    if kind == 1 and t > 64 and act == 128:
         # x holds the last layer's input (for q8 written by the fused RMSNorm + quantize pass)
         assert same_bits(host(xt), orc.bf16_round(orc.rmsnorm_rows(_oracle_stack(kind, x, layers[:2], act))))
     # one layer (no rounding of an intermediate activation to bf16) against the oracle at the parity bar
     y1 = host(sm.mlp_stack(kind, dev(x, torch.bfloat16), layers[:1], act_block=act))
     ref1 = _oracle_stack(kind, x, layers[:1], act)
     ref = _oracle_stack(kind, x, layers, act)
-    if kind == 1 and t > 64:
-        assert same_bits(y1, ref1) and same_bits(y, ref)  # the large-M q8 path is the reference's arithmetic
+    if kind == 1 and t > 64 and act == 128:
+        # the large-M q8 path per 128 is the reference's arithmetic (per token, a form the reference does not have,
+        # the SwiGLU is the fast one and the floats are held to the parity bar)
+        assert same_bits(y1, ref1) and same_bits(y, ref)
     else:
         say("errors: one layer max rel", f"{max_rel_over_rms(y1, ref1):.3e}", "three layers rel rms", f"{rel_rms(y, ref):.3e}")
         assert max_rel_over_rms(y1, ref1) < 2e-3, max_rel_over_rms(y1, ref1)

