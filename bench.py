@@ -349,7 +349,41 @@ def main():
             del a_c, w_c, o_c
         ceil["note"] = "torch.matmul bf16 (hipBLASLt), [15872 x K] x [N x K]^T, bf16 out"
         extra["bf16_gemm_ceiling"] = ceil
+        # ... and its plain int8 GEMM (torch._int_mm, int32 out: no scales, no chain) for C4's shapes
+        ceil8 = {}
+        try:
+            for name, n_c, k_c in (("gate_up", 2 * I, H), ("down", H, I)):
+                a_c = torch.randint(-127, 128, (M_BIG, k_c), device="cuda", dtype=torch.int8)
+                w_c = torch.randint(-127, 128, (n_c, k_c), device="cuda", dtype=torch.int8)
+                ms_c = timed(torch, lambda: torch._int_mm(a_c, w_c.t()), 10, 3, stream)
+                to_c = 2.0 * M_BIG * n_c * k_c / (ms_c * 1e-3) / 1e12
+                ceil8[name] = {"ms": round(ms_c, 4), "tops": round(to_c, 1), "frac_int8_peak": round(to_c / PEAK["int8_tops"], 4)}
+                del a_c, w_c
+            ceil8["note"] = "torch._int_mm int8 x int8 -> int32 (hipBLASLt), [15872 x K] x [N x K]^T"
+        except Exception as e:  # an int8 GEMM the installed torch does not provide is reported as such
+            ceil8 = {"error": str(e)[:200]}
+        extra["int8_gemm_ceiling"] = ceil8
+        log(f"int8 GEMM ceiling (torch._int_mm): {ceil8}")
         log(f"bf16 GEMM ceiling (torch.matmul): {ceil}")
+        # ---- C3 on load-time weight images (sepal_hip_mlp_stack_images): the weights widened once, outside the timed
+        # region, into the images the large-M kernels read; the same bits as the headline step ----
+        images = [(sm.w8g_make_image(l[0], torch.bfloat16), sm.w8g_make_image(l[2], torch.float16)) for l in layers]
+        torch.cuda.synchronize()
+
+        def step_c3_img():
+            x.copy_(x0)
+            sm.mlp_stack_images(0, x, layers, images, y=y)
+
+        ms_c3i = timed(torch, step_c3_img, args.steps, args.warmup, stream)
+        tops_c3i = ops_step / (ms_c3i * 1e-3) / 1e12
+        extra["c3_w8g_load_time_images"] = {"ms_per_step": round(ms_c3i, 3), "tops": round(tops_c3i, 1),
+                                            "frac_bf16_peak": round(tops_c3i / PEAK["bf16_tflops"], 4),
+                                            "image_bytes": int(sum(a.numel() + b.numel() for a, b in images)),
+                                            "note": "weights widened once at load into bf16 / binary16 images of the "
+                                                    "kernels' LDS stages (2x the int8 bytes, kept beside them)"}
+        log(f"C3 w8g stack on load-time images: {ms_c3i:.2f} ms/step, {tops_c3i:.1f} TOPS")
+        del images
+        torch.cuda.empty_cache()
         # ---- C3 with H kept in float32 (mlp_stack kind 2: the down multiply on bf16 hi + lo pairs) ----
         def step_c3_f32h():
             x.copy_(x0)

@@ -275,6 +275,29 @@ SEPAL_HIP_API int32_t sepal_hip_mlp_stack(int32_t kind, size_t layers, size_t t,
                             const int8_t* const* w_gate_up, const float* const* s_gate_up, const int8_t* const* w_down,
                             const float* const* s_down, float* y, size_t act_block, double eps, void* stream);
 
+/* Load-time weight images of the large-M w8g kernels. Above about two rounds of 256 x 256 output tiles the w8g multiply
+ * widens its int8 weights, exactly, into an image of the kernel's LDS stages before it multiplies (in the workspace,
+ * every call; inside sepal_hip_mlp_stack the previous multiply's last launch widens the next one's). The weights do not
+ * change between calls, so a caller with the memory may keep the images instead: twice the int8 bytes per matrix
+ * (99.6 MB for the 19456 x 2560 gate/up weights, 49.8 MB for the 2560 x 9728 down weights).
+ * sepal_hip_w8g_image_bytes: the bytes of the image of an int8 [n, k] matrix (0 when the image form does not apply).
+ * sepal_hip_w8g_make_image: widens w [n, ld_w] into img for X of x_type (F16: a binary16 image; BF16 and F32: bf16).
+ * No counterpart in the reference (it dequantizes in registers every call, runner/cuda/src/gemm_simt_kernels.cu:172-178);
+ * for callers that keep weights resident across many large-M calls (prefill). */
+SEPAL_HIP_API size_t sepal_hip_w8g_image_bytes(size_t n, size_t k);
+SEPAL_HIP_API int32_t sepal_hip_w8g_make_image(const int8_t* w, size_t ld_w, size_t n, size_t k, int32_t x_type, void* img,
+                                               size_t img_bytes, void* stream);
+
+/* sepal_hip_mlp_stack (kind 0 or 2) on load-time images: img_gate_up[l] the bf16 image of layer l's gate/up weights,
+ * img_down[l] the image of its down weights (binary16 for kind 0, whose H is binary16; bf16 for kind 2), each made by
+ * sepal_hip_w8g_make_image. The same bits as sepal_hip_mlp_stack; the multiplies that run the image kernels read the
+ * images instead of widening the weights, and the workspace holds no images. */
+SEPAL_HIP_API int32_t sepal_hip_mlp_stack_images(int32_t kind, size_t layers, size_t t, size_t hidden, size_t inter, void* x,
+                                                 const int8_t* const* w_gate_up, const float* const* s_gate_up,
+                                                 const int8_t* const* w_down, const float* const* s_down,
+                                                 const void* const* img_gate_up, const void* const* img_down, float* y,
+                                                 double eps, void* stream);
+
 /* sepal_hip_mlp_stack with no allocation of any kind: the same arguments, work and bits, with every scratch buffer in
  * a static device array of 64 MiB that the library holds on each device it runs on until the process ends (the split-K
  * counter zone, then the stack's intermediates as sepal_hip_mlp_stack lays them out in its workspace). No counterpart

@@ -870,7 +870,8 @@ StackZones stack_zones(int kind, std::size_t t, std::size_t hidden, std::size_t 
 // One call of the stack on the scratch at `ws` (laid out by stack_zones).
 void run_stack(const StackZones& z, int kind, std::size_t layers, std::size_t t, std::size_t hidden, std::size_t inter,
                void* x, const int8_t* const* w_gate_up, const float* const* s_gate_up, const int8_t* const* w_down,
-               const float* const* s_down, float* y, double eps, char* ws, hipStream_t st) {
+               const float* const* s_down, float* y, double eps, char* ws, hipStream_t st, const void* const* img_gate_up,
+               const void* const* img_down) {
     if (z.form == StackZones::SMALL_W8G) {
         // three launches per layer: whole-K gate/up tiles per CU, the down multiply in K-parts, the finish pass
         for (std::size_t l = 0; l < layers; ++l)
@@ -928,6 +929,15 @@ void run_stack(const StackZones& z, int kind, std::size_t layers, std::size_t t,
         if (z.img_dn != 0) {
             dn.wimage = ws + z.off_img_dn;
             dn.wimage_bytes = z.img_dn;
+        }
+        if (img_gate_up != nullptr) {
+            // load-time images: nothing to widen
+            gu.wimage = const_cast<void*>(img_gate_up[l]);
+            gu.wimage_bytes = w8g_image_bytes_nk(2 * inter, hidden);
+            gu.image_ready = true;
+            dn.wimage = const_cast<void*>(img_down[l]);
+            dn.wimage_bytes = w8g_image_bytes_nk(hidden, inter);
+            dn.image_ready = true;
         }
         if (z.img != 0 && z.img_dn != 0) {
             // both multiplies on images: the gate/up multiply's halves launch widens this layer's down weights, the
@@ -1088,6 +1098,48 @@ int32_t sepal_hip_mlp_stack_noalloc(int32_t kind, size_t layers, size_t t, size_
             g_static_last[dev] = st;
             g_static_used[dev] = true;
         }
+    });
+}
+
+size_t sepal_hip_w8g_image_bytes(size_t n, size_t k) { return n == 0 || k == 0 ? 0 : w8g_image_bytes_nk(n, k); }
+
+int32_t sepal_hip_w8g_make_image(const int8_t* w, size_t ld_w, size_t n, size_t k, int32_t x_type, void* img,
+                                 size_t img_bytes, void* stream) {
+    return guarded([&] {
+        require(w != nullptr && img != nullptr, "w8g_make_image: null pointer");
+        require(valid_type(x_type), "w8g_make_image: X must be float32, bf16 or binary16");
+        require(n != 0 && k != 0 && k % 128 == 0 && ld_w >= k && ld_w % 16 == 0 && aligned16(w),
+                "w8g_make_image: K must be a non-zero multiple of 128, W rows of whole 16 bytes (16-byte aligned)");
+        const std::size_t need = w8g_image_bytes_nk(n, k);
+        require(need != 0, "w8g_make_image: the image of this shape would exceed 2^31 bytes");
+        require(img_bytes >= need && aligned16(img), "w8g_make_image: img must hold sepal_hip_w8g_image_bytes(n, k) bytes, 16-byte aligned");
+        launch_w8g_image(w, ld_w, n, k, x_type == SEPAL_HIP_F16, img, as_stream(stream));
+    });
+}
+
+int32_t sepal_hip_mlp_stack_images(int32_t kind, size_t layers, size_t t, size_t hidden, size_t inter, void* x,
+                                   const int8_t* const* w_gate_up, const float* const* s_gate_up,
+                                   const int8_t* const* w_down, const float* const* s_down, const void* const* img_gate_up,
+                                   const void* const* img_down, float* y, double eps, void* stream) {
+    return guarded([&] {
+        check_stack_args(kind, hidden, inter, x, w_gate_up, s_gate_up, w_down, s_down, y, 128);
+        require(kind == 0 || kind == 2, "mlp_stack_images: kind must be 0 or 2 (the w8g stacks)");
+        require(img_gate_up != nullptr && img_down != nullptr, "mlp_stack_images: null image array");
+        require(w8g_image_bytes_nk(2 * inter, hidden) != 0 && w8g_image_bytes_nk(hidden, inter) != 0,
+                "mlp_stack_images: the images of this shape would exceed 2^31 bytes");
+        if (layers == 0 || t == 0) return;
+        for (std::size_t l = 0; l < layers; ++l)
+            require(img_gate_up[l] != nullptr && img_down[l] != nullptr && aligned16(img_gate_up[l]) && aligned16(img_down[l]),
+                    "mlp_stack_images: null or misaligned image");
+        const hipStream_t st = as_stream(stream);
+        StackZones z = stack_zones(kind, t, hidden, inter, 128);
+        if (z.form == StackZones::GENERAL) {
+            z.img = z.img_dn = 0;  // the caller's images replace the workspace's
+            z.end = z.off_img;
+        }
+        Lease ws(z.end, st);
+        run_stack(z, kind, layers, t, hidden, inter, x, w_gate_up, s_gate_up, w_down, s_down, y, eps, ws.base(), st,
+                  z.form == StackZones::GENERAL ? img_gate_up : nullptr, z.form == StackZones::GENERAL ? img_down : nullptr);
     });
 }
 

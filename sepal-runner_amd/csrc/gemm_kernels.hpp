@@ -69,6 +69,11 @@ std::size_t gemm_w8g_scratch_bytes(const GemmArgs& a);
 // Bytes of the widened weight image the large-M w8g kernels use for this problem (0: they widen in the kernel). The
 // image is written by every call, so it only needs to be scratch.
 std::size_t gemm_w8g_image_bytes(const GemmArgs& a);
+// The weight image as a load-time form: its bytes for an N x K matrix (0 when its offsets would exceed 32 bits) and
+// the widening pass (binary16 when f16, else bf16) into `img`.
+std::size_t w8g_image_bytes_nk(std::size_t n, std::size_t k);
+void launch_w8g_image(const std::int8_t* w, std::size_t ld_w, std::size_t n, std::size_t k, bool f16, void* img,
+                      hipStream_t stream);
 // The part of gemm_w8g_scratch_bytes that is the split buffer (ytmp follows it).
 inline std::size_t gemm_w8g_split_bytes(const GemmArgs& a) { return (a.t * a.k * 4 + 255) / 256 * 256; }
 void launch_stream_w8g(const GemmArgs& a, hipStream_t stream);

@@ -1471,6 +1471,13 @@ std::size_t gemm_w8g_image_bytes(const GemmArgs& a) {
     return w8g::image_bytes(a.n, a.k);
 }
 
+std::size_t w8g_image_bytes_nk(std::size_t n, std::size_t k) { return k % 64 == 0 ? w8g::image_bytes(n, k) : 0; }
+
+void launch_w8g_image(const std::int8_t* w, std::size_t ld_w, std::size_t n, std::size_t k, bool f16, void* img,
+                      hipStream_t stream) {
+    w8g::launch_widen(w, ld_w, n, k, f16, img, stream);
+}
+
 std::size_t gemm_w8g_scratch_bytes(const GemmArgs& a) {
     if (a.x_type != SEPAL_HIP_F32) return 0;
     const auto up256 = [](std::size_t b) { return (b + 255) / 256 * 256; };

@@ -72,6 +72,10 @@ def library() -> C.CDLL:
         L.sepal_hip_column_absmax.argtypes = [vp, sz, vp, sz, sz, vp]
         L.sepal_hip_channel_stats.argtypes = [vp, sz, sz, sz, vp, vp, vp]
         L.sepal_hip_release_workspace.argtypes = [vp]
+        L.sepal_hip_w8g_image_bytes.argtypes = [sz, sz]
+        L.sepal_hip_w8g_image_bytes.restype = sz
+        L.sepal_hip_w8g_make_image.argtypes = [vp, sz, sz, sz, i32, vp, sz, vp]
+        L.sepal_hip_mlp_stack_images.argtypes = [i32, sz, sz, sz, sz, vp, vp, vp, vp, vp, vp, vp, vp, d, vp]
         for name in ("sepal_hip_quantize_group_s8", "sepal_hip_quantize_gate_up_s8", "sepal_hip_gemm_w8g",
                      "sepal_hip_quantize_rows_s8", "sepal_hip_gemm_q8", "sepal_hip_q8_group_sums",
                      "sepal_hip_rmsnorm_rows", "sepal_hip_float_to_bf16", "sepal_hip_mlp_stack",
@@ -79,7 +83,8 @@ def library() -> C.CDLL:
                      "sepal_hip_rmsnorm_quantize_rows", "sepal_hip_gemm_q8_swiglu_quantize",
                      "sepal_hip_weight_fingerprint", "sepal_hip_packed_save", "sepal_hip_packed_load",
                      "sepal_hip_s8_quantize_rows", "sepal_hip_gemm_s8", "sepal_hip_gemm_w8a16", "sepal_hip_gemm_q8y",
-                     "sepal_hip_column_absmax", "sepal_hip_channel_stats", "sepal_hip_release_workspace"):
+                     "sepal_hip_column_absmax", "sepal_hip_channel_stats", "sepal_hip_release_workspace",
+                     "sepal_hip_w8g_make_image", "sepal_hip_mlp_stack_images"):
             getattr(L, name).restype = i32
         L.sepal_hip_gemm_w8g_supports.restype = i32
         L.sepal_hip_gemm_s8_supports.restype = i32
@@ -345,6 +350,36 @@ def packed_load(path: str, q, s, source_fp: int, rule: int = RULE_DIVIDE, layout
         return False
     _check(rc)
     return True
+
+
+def w8g_make_image(w, x_dtype, stream=None):
+    """The load-time image of int8 weights w [N, K] for the large-M w8g kernels, for X of x_dtype (torch.float16: a
+    binary16 image; bfloat16 / float32: bf16). A uint8 device tensor of sepal_hip_w8g_image_bytes(N, K) bytes."""
+    torch = _torch()
+    n, k = w.shape
+    nbytes = library().sepal_hip_w8g_image_bytes(n, k)
+    if nbytes == 0:
+        raise SepalHipInvalid("the image form does not apply to this shape")
+    img = torch.empty(nbytes, dtype=torch.uint8, device=w.device)
+    _check(library().sepal_hip_w8g_make_image(_ptr(w), _ld(w), n, k, _type_of(torch.empty(0, dtype=x_dtype)), _ptr(img),
+                                              nbytes, _stream(stream)))
+    return img
+
+
+def mlp_stack_images(kind: int, x, layers, images, y=None, eps: float = 1e-6, stream=None):
+    """mlp_stack (kind 0 or 2) on load-time images: images is a list of (img_gate_up, img_down) per layer."""
+    torch = _torch()
+    t, hidden = x.shape
+    inter = layers[0][2].shape[1]
+    y = torch.empty(t, hidden, dtype=torch.float32, device=x.device) if y is None else y
+
+    def arr(seq, i):
+        return (C.c_void_p * len(seq))(*[e[i].data_ptr() for e in seq])
+
+    _check(library().sepal_hip_mlp_stack_images(kind, len(layers), t, hidden, inter, _ptr(x), arr(layers, 0), arr(layers, 1),
+                                                arr(layers, 2), arr(layers, 3), arr(images, 0), arr(images, 1), _ptr(y),
+                                                eps, _stream(stream)))
+    return y
 
 
 def release_workspace(stream=None) -> None:

@@ -180,6 +180,26 @@ def test_float32_h_stack_ragged_rows(sm):
     assert err < 2e-4, err
 
 
+@pytest.mark.parametrize("kind,m", [(0, 15872), (2, 15872), (0, 2100)])
+def test_stack_on_load_time_images(sm, kind, m):
+    """mlp_stack_images: the w8g stack on images made once by w8g_make_image gives the bits of mlp_stack, which widens
+    the weights into its workspace every call; at M = 15872 both multiplies run the image kernels, at M = 2100 the
+    gate/up multiply does and the down multiply (a small grid) ignores its image."""
+    say("stack on load-time images kind", kind, "m", m)
+    rng = np.random.default_rng(kind + m)
+    x = bf16_inputs(rng, (m, H))
+    layers = [_layer_weights(sm, 3000 + l, rule=0) for l in range(2)]
+    dn_dtype = torch.float16 if kind == 0 else torch.bfloat16
+    images = [(sm.w8g_make_image(l[0], torch.bfloat16), sm.w8g_make_image(l[2], dn_dtype)) for l in layers]
+    xa, xb = dev(x, torch.bfloat16), dev(x, torch.bfloat16)
+    ya = host(sm.mlp_stack(kind, xa, layers))
+    yb = host(sm.mlp_stack_images(kind, xb, layers, images))
+    assert same_bits(yb, ya)
+    assert torch.equal(xa, xb)
+    assert sm.library().sepal_hip_w8g_image_bytes(2 * I, H) == 2 * I * H * 2
+    assert sm.library().sepal_hip_w8g_image_bytes(H, I) == H * I * 2
+
+
 def test_c4_per_token_full_size(sm):
     """C4 at its workload: the q8 stack with one activation scale per token at M = 15872, 1% of the input channels
     x20. Sampled rows of one layer against the oracle's cpu-q8 chain within the parity bar (per token, a form the
