@@ -18,8 +18,9 @@
 //            groups in alternation) and the half tiles of gemm_big3 load straight into LDS. Otherwise the weights are
 //            widened per tile by the waves when staged into LDS. gemm_big3:
 //            256 x 256 tiles (128 x 256 halves for a launch's last partial round; for grids of fewer than 512 large
-//            tiles, blocks of 64, 128 or 256 rows and, by default, K split over blocks, by plan_small_grid), K in steps
-//            of 64, X straight from global memory into LDS. gemm_big2 (when an offset does not fit 32 bits, or a
+//            tiles, blocks of 64, 128 or 256 rows and, by default, K split over blocks with the partials added by the
+//            last block of a tile or by planes_sum_kernel, and the leading whole 256-row tiles run apart from the rows
+//            after them, by plan_small_grid), K in steps of 64, X straight from global memory into LDS. gemm_big2 (when an offset does not fit 32 bits, or a
 //            SwiGLU N is not a multiple of 256): 256 x 128 or 256 x 256 tiles, K in steps of 32.
 //   small M: at T <= 16 the M <= 16 stack's pass kernels (stack_small.hip) where the shape fits them; else, at
 //            T <= 32 with N < 8192, stream.hip (the weights streamed once, HBM-bound); else the large-M plan.
@@ -137,6 +138,9 @@ struct BigParams {
     // split-K launches run the live block tiles sub0 .. sub0 + nsub - 1 of the dense order: block tile s at rows
     // (s mod sub_m) BM3 and columns (s / sub_m) 256, sub_m = ceil(T / BM3)
     int dense = 0, sub_m = 0, sub0 = 0, nsub = 0;
+    // split-K into planes: instead of the hand-off, split s writes its float32 partial (the same values) row-major to
+    // part + s * t * n (row stride n), and planes_sum_kernel adds the planes in split order and runs the epilogue
+    int planes = 0;
     // gemm_pp: the widened W stage of 256-column tile tn and weight step ks (64 values of k) is the 32 KB at wimg +
     // (tn * wsteps + ks) * 32768, in the LDS order the fragment reads use
     const unsigned char* wimg = nullptr;
@@ -491,7 +495,8 @@ __device__ __forceinline__ void tile_epilogue(const BigParams& p, f32x16 (&acc)[
 template <int XT, int EP, int YT, int MB, int SPLIT, bool SK>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) gemm_big3(const BigParams p) {
     // MB m-blocks of 32 rows per wave: tiles of BM3 = 64 MB rows (256, or 128 for the tail rows of a launch).
-    // SK: split-K (the block's K range is its split of the groups; BigParams::splits).
+    // SK: the dense order (only block tiles with rows to do), the K range split over BigParams::splits blocks (1: the
+    // whole K, no hand-off).
     // SPLIT 2: X is a float32 operand as a bf16 hi + lo pair, stored as one bf16 row of 2K values (64-value chunk j of
     // k is chunk 2j (hi) and 2j + 1 (lo)); steps 2j and 2j + 1 multiply the same weights, so p.k counts the 2K values
     // and the weight offset of step kt is kt / 2 chunks.
@@ -514,7 +519,7 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
 
     const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
     const int wm = wave % 2, wn = wave / 2;
-    // Split-K (the dense order): logical id -> block tile sub0 + id / S (sub-rows fastest, so consecutive ids share
+    // The dense order (SK): logical id -> block tile sub0 + id / S (sub-rows fastest, so consecutive ids share
     // the weight tile) and split id mod S; the splits of one block tile take consecutive logical ids, which stay on
     // one XCD (shared L2). Otherwise MB 4: one logical 256 x 256 tile per block; MB 2 or 1: block b is part b / count
     // (BM3 rows) of tile id0 + b % count; a part wholly past T has nothing to do.
@@ -728,13 +733,20 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
     // no direct load may still be writing LDS when the block ends
     wait_vmcnt<0>();
 
-    if constexpr (SK) {
+    if constexpr (SK) if (p.splits > 1) {
         // This split's sums s_g P_g over its groups, value v of thread tid at part[((sub S + split) 32 MB + v) 512 + tid].
         // The hand-off between the splits of a block tile uses no device-wide fence (on gfx950 one writes back and
         // invalidates the L2 of the XCD): the partials are written and read with device-scope relaxed atomics, which go
         // to the device coherence point; each thread waits for its stores to complete before the barrier, and only
         // then does one thread count the block in. The last block to arrive adds the S partials in split order (its
         // own read back like the others), so the result does not depend on the arrival order.
+        if (p.planes) {
+            BigParams q = p;
+            q.y = p.part + static_cast<std::size_t>(split) * p.t * p.n;
+            q.ld_y = static_cast<std::size_t>(p.n);
+            tile_epilogue<SEPAL_HIP_STORE, SEPAL_HIP_F32, MB>(q, acc, e, m0, n0, wave, lane);
+            return;
+        }
         constexpr int NV = MB * 32;
         float* mine = p.part + (static_cast<std::size_t>(sub) * p.splits + split) * NV * 512 + tid;
 #pragma unroll
@@ -1106,10 +1118,65 @@ inline int device_cus() {
     return cus;
 }
 
+// The planes of a split-K launch added in split order, then the epilogue: the additions and epilogue operations of
+// the hand-off (sum = plane 0, then sum + plane s; x 1; the tile epilogue's conversion), so the same bits. A thread
+// takes 4 consecutive outputs of one row: Store / Add columns c..c+3, or SwiGLU features f..f+3, whose gate and up
+// columns are 128 (f / 64) + f % 64 and 64 past it (the gate/up interleave of a 256-column tile). VEC: n % 4 == 0
+// (16-byte plane reads).
+template <int EP, int YT, bool VEC>
+__global__ void __launch_bounds__(256) planes_sum_kernel(const float* __restrict__ part, int splits, int t, int n, void* y,
+                                                         std::size_t ld_y) {
+    const int outs = EP == SEPAL_HIP_SWIGLU ? n / 2 : n;
+    const int per_row = (outs + 3) / 4;
+    const long id = static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (id >= static_cast<long>(t) * per_row) return;
+    const int row = static_cast<int>(id / per_row), c0 = static_cast<int>(id % per_row) * 4;
+    const std::size_t plane = static_cast<std::size_t>(t) * n;
+    const auto sum4 = [&](int col, float (&s)[4]) {
+        const float* src = part + static_cast<std::size_t>(row) * n + col;
+        for (int sp = 0; sp < splits; ++sp, src += plane) {
+            float v[4];
+            if constexpr (VEC) {
+                const float4 f = *reinterpret_cast<const float4*>(src);
+                v[0] = f.x, v[1] = f.y, v[2] = f.z, v[3] = f.w;
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) v[j] = col + j < n ? src[j] : 0.0f;
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) s[j] = sp == 0 ? v[j] : __fadd_rn(s[j], v[j]);
+        }
+    };
+    if constexpr (EP == SEPAL_HIP_SWIGLU) {
+        float g[4], u[4];
+        const int gc = 128 * (c0 / 64) + c0 % 64;
+        sum4(gc, g);
+        sum4(gc + 64, u);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            if (c0 + j < outs) store_h<YT>(y, static_cast<std::size_t>(row), ld_y, c0 + j, swiglu_fast(__fmul_rn(g[j], 1.0f), __fmul_rn(u[j], 1.0f)));
+    } else {
+        float s[4];
+        sum4(c0, s);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            if (c0 + j < outs) put_plain<EP, YT>(y, static_cast<std::size_t>(row) * ld_y + c0 + j, __fmul_rn(s[j], 1.0f));
+    }
+}
+
+template <int EP, int YT>
+void launch_planes_sum(const float* part, int splits, int t, int n, void* y, std::size_t ld_y, hipStream_t stream) {
+    const int outs = EP == SEPAL_HIP_SWIGLU ? n / 2 : n;
+    const long threads = static_cast<long>(t) * ((outs + 3) / 4);
+    const dim3 grid(static_cast<unsigned>((threads + 255) / 256));
+    if (n % 4 == 0) planes_sum_kernel<EP, YT, true><<<grid, dim3(256), 0, stream>>>(part, splits, t, n, y, ld_y);
+    else planes_sum_kernel<EP, YT, false><<<grid, dim3(256), 0, stream>>>(part, splits, t, n, y, ld_y);
+}
+
 template <int XT, int EP, int YT, int MB, int SPLIT>
 void launch_big3(const BigParams& p, hipStream_t stream) {
     const int blocks = p.dense ? p.nsub * p.splits : p.count * (256 / (64 * MB));
-    if (p.splits > 1) v2::gemm_big3<XT, EP, YT, MB, SPLIT, true><<<dim3(blocks), dim3(512), 0, stream>>>(p);
+    if (p.dense) v2::gemm_big3<XT, EP, YT, MB, SPLIT, true><<<dim3(blocks), dim3(512), 0, stream>>>(p);
     else v2::gemm_big3<XT, EP, YT, MB, SPLIT, false><<<dim3(blocks), dim3(512), 0, stream>>>(p);
 }
 
@@ -1147,43 +1214,77 @@ inline void launch_widen(const std::int8_t* w, std::size_t ld_w, std::size_t n, 
 // (config 0).
 struct SmallGridPlan {
     int mb = 1, splits = 1;
+    bool planes = false;      // split-K through planes and planes_sum_kernel instead of the in-kernel hand-off
+    // row split: the floor(T / 256) x 256 leading rows as unsplit 256 x 256 tiles, then the remaining rows as a grid of
+    // their own with (mb2, splits2, planes2)
+    bool rows = false;
+    int mb2 = 1, splits2 = 1;
+    bool planes2 = false;
 };
 
-inline SmallGridPlan plan_small_grid(const GemmArgs& a, int tiles_n, int groups, bool allow_split) {
-    // Fitted to times measured on MI355X (the MLP shapes, M from 65 to 4096, every plan): the time per 128-value group
-    // of a lone block of 64, 128 or 256 rows (MB 1, 2, 4); the rate at which the blocks' operand reads are served;
-    // and the split hand-off, a fixed cost plus the last block's reads of the S partials of its tile (one block's
-    // coherent reads are slow). More than 6 splits measured slower than 6 in every case. (Splitting only the last
-    // partial round's block tiles never won under this model at the MLP shapes: those grids are bound by the operand
-    // reads, not by the idle CUs of the last round.)
-    constexpr double us_per_group[5] = {0.0, 1.46, 1.84, 0.0, 3.05};
-    constexpr double operand_bytes_per_us = 6.0e6, handoff_us = 8.0, tail_bytes_per_us = 8.0e4;
-    const int cus = device_cus();
-    SmallGridPlan best;
-    double best_cost = 1e30;
-    for (int mb : {4, 2, 1}) {
-        const int rows = 64 * mb;
-        const long subs = static_cast<long>((a.t + rows - 1) / rows) * tiles_n;  // block tiles with rows to do
-        for (int sp = 1; sp <= 6 && sp <= groups; ++sp) {
-            if (sp > 1) {
-                if (!allow_split || a.scratch == nullptr) break;
-                const std::size_t part = static_cast<std::size_t>(subs) * sp * rows * 256 * sizeof(float);
-                if (subs * static_cast<long>(sizeof(unsigned)) > static_cast<long>(kCounterBytes) || part > kPartialBytes) break;
-            }
-            const long blocks = subs * sp, rounds = (blocks + cus - 1) / cus;
-            const int per_block = (groups + sp - 1) / sp;
-            const double compute = static_cast<double>(rounds) * per_block * us_per_group[mb];
-            const double operand = static_cast<double>(blocks) * per_block * 128.0 * (2.0 * rows + 256.0) / operand_bytes_per_us;
-            double cost = compute > operand ? compute : operand;
-            if (sp > 1) cost += handoff_us + static_cast<double>(sp) * rows * 256 * sizeof(float) / tail_bytes_per_us;
-            if (cost < best_cost) {
-                best_cost = cost;
-                best.mb = mb;
-                best.splits = sp;
-            }
-        }
+// Modelled time (us) of one grid of t rows: fitted to times measured on MI355X (the MLP shapes, M from 65 to 12288,
+// every plan): the time per 128-value group of a lone block of 64, 128 or 256 rows (MB 1, 2, 4); the rate at which
+// the blocks' operand reads are served; the in-kernel split hand-off, a fixed cost plus the last block's reads of the
+// S partials of its tile (one block's coherent reads are slow); or the planes' finisher, a launch plus the S planes
+// read and the output written at the rate of a plain streaming kernel. Negative: the plan does not fit the scratch.
+inline double grid_cost(long t, int tiles_n, int groups, int mb, int sp, bool planes, int cus) {
+    constexpr double us_per_group[5] = {0.0, 1.65, 2.44, 0.0, 4.60};
+    constexpr double operand_bytes_per_us = 9.27e6, handoff_us = 5.7, tail_bytes_per_us = 8.8e4;
+    constexpr double finish_us = 2.5, stream_bytes_per_us = 3.45e6;
+    const int rows = 64 * mb;
+    const long subs = (t + rows - 1) / rows * tiles_n;  // block tiles with rows to do
+    const double plane = static_cast<double>(t) * tiles_n * 256 * sizeof(float);
+    if (sp > 1) {
+        if (planes && plane * sp > static_cast<double>(kPartialBytes)) return -1.0;
+        if (!planes && (subs * static_cast<long>(sizeof(unsigned)) > static_cast<long>(kCounterBytes) ||
+                        static_cast<double>(subs) * sp * rows * 256 * sizeof(float) > static_cast<double>(kPartialBytes)))
+            return -1.0;
     }
-    return best;
+    const long blocks = subs * sp, rounds = (blocks + cus - 1) / cus;
+    const int per_block = (groups + sp - 1) / sp;
+    const double compute = static_cast<double>(rounds) * per_block * us_per_group[mb];
+    const double operand = static_cast<double>(blocks) * per_block * 128.0 * (2.0 * rows + 256.0) / operand_bytes_per_us;
+    double cost = compute > operand ? compute : operand;
+    if (sp > 1)
+        cost += planes ? finish_us + (sp + 1) * plane / stream_bytes_per_us
+                       : handoff_us + static_cast<double>(sp) * rows * 256 * sizeof(float) / tail_bytes_per_us;
+    return cost;
+}
+
+// The plan of least modelled time: one grid over all rows, or (T above 256 and not a multiple of it) the leading whole
+// 256-row tiles unsplit, then the remaining rows as a grid of their own (at M = 896, gate/up 19456 x 2560: 3 x 76
+// whole tiles, one round, then 128 rows in 128-row blocks split 3 ways: 107 us against 149-156 us for any one grid;
+// the model predicts both within 5%).
+inline SmallGridPlan plan_small_grid(const GemmArgs& a, int tiles_n, int groups, bool allow_split) {
+    const int cus = device_cus();
+    const bool can_split = allow_split && a.scratch != nullptr;
+    const auto best_grid = [&](long t, int& mb_out, int& sp_out, bool& pl_out) {
+        double best = 1e30;
+        for (int mb : {4, 2, 1})
+            for (int sp = 1; sp <= 8 && sp <= groups && (sp == 1 || can_split); ++sp)
+                for (int pl = 0; pl < (sp > 1 ? 2 : 1); ++pl) {
+                    const double c = grid_cost(t, tiles_n, groups, mb, sp, pl != 0, cus);
+                    if (c >= 0.0 && c < best) {
+                        best = c;
+                        mb_out = mb;
+                        sp_out = sp;
+                        pl_out = pl != 0;
+                    }
+                }
+        return best;
+    };
+    SmallGridPlan plan;
+    const double one = best_grid(static_cast<long>(a.t), plan.mb, plan.splits, plan.planes);
+    const long lead = static_cast<long>(a.t) / 256 * 256;
+    if (lead > 0 && lead < static_cast<long>(a.t)) {
+        constexpr double launch_us = 3.2;
+        SmallGridPlan r;
+        r.rows = true;
+        const double two = grid_cost(lead, tiles_n, groups, 4, 1, false, cus) + launch_us +
+                           best_grid(static_cast<long>(a.t) - lead, r.mb2, r.splits2, r.planes2);
+        if (two < one) plan = r;
+    }
+    return plan;
 }
 
 // gemm_big3 addresses X and W with 32-bit offsets (rows up to one tile past the end included) and writes SwiGLU outputs
@@ -1191,6 +1292,39 @@ inline SmallGridPlan plan_small_grid(const GemmArgs& a, int tiles_n, int groups,
 bool big3_takes(const GemmArgs& a, std::size_t kx, std::size_t ld_x) {
     const bool offsets32 = (a.t + 256) * ld_x * 2 < (std::size_t{1} << 31) && (a.n + 256) * a.ld_w < (std::size_t{1} << 31);
     return offsets32 && kx <= ld_x && (a.epilogue != SEPAL_HIP_SWIGLU || a.n % 256 == 0);
+}
+
+// Bytes between consecutive rows of Y of type YT (kYPairs: the hi + lo row of 2 ld_y bf16 values).
+template <int YT>
+constexpr std::size_t y_row_bytes(std::size_t ld_y) {
+    return YT == SEPAL_HIP_F32 || YT == kYPairs ? 4 * ld_y : 2 * ld_y;
+}
+
+// One gemm_big3 grid over the rows of p (p.tiles_n set): block tiles of 64 mb rows, K split over `splits` blocks
+// (through the hand-off, or through planes and planes_sum_kernel).
+template <int XT, int EP, int YT, int SPLIT>
+void launch_grid(const GemmArgs& a, BigParams p, int mb, int splits, bool planes, hipStream_t stream) {
+    p.tiles_m = (p.t + 255) / 256;
+    p.id0 = 0;
+    p.count = p.tiles_m * p.tiles_n;
+    // the dense order (only block tiles with rows to do are launched) for split grids and for blocks below 256 rows
+    if (splits > 1 || mb < 4) {
+        const int rows = 64 * mb;
+        p.dense = 1;
+        p.sub_m = (p.t + rows - 1) / rows;
+        p.nsub = p.sub_m * p.tiles_n;
+        p.splits = splits;
+        p.planes = planes ? 1 : 0;
+        p.counters = static_cast<unsigned*>(a.scratch);
+        p.part = reinterpret_cast<float*>(static_cast<char*>(a.scratch) + kCounterBytes);
+    }
+    if (mb == 4) launch_big3<XT, EP, YT, 4, SPLIT>(p, stream);
+    else if (mb == 2) launch_big3<XT, EP, YT, 2, SPLIT>(p, stream);
+    else launch_big3<XT, EP, YT, 1, SPLIT>(p, stream);
+    if (splits > 1 && planes) {
+        check_launch("gemm_w8g split-K launch");
+        launch_planes_sum<EP, YT>(p.part, splits, p.t, p.n, p.y, p.ld_y, stream);
+    }
 }
 
 template <int XT, int EP, int YT, int SPLIT>
@@ -1261,22 +1395,25 @@ void launch_big(const GemmArgs& a, hipStream_t stream) {
     } else if (takes && !wide) {
         // fewer than two rounds of 256 x 256 tiles: the plan's tile height and K split
         p.tiles_n = tn256;
-        p.id0 = 0;
-        p.count = tiles_m * tn256;
         const SmallGridPlan plan = plan_small_grid(a, tn256, static_cast<int>(a.k / 128), a.config < 0);
-        if (plan.splits > 1) {
-            // split-K runs the live block tiles in the dense order
-            const int rows = 64 * plan.mb;
-            p.dense = 1;
-            p.sub_m = static_cast<int>((a.t + rows - 1) / rows);
-            p.nsub = p.sub_m * tn256;
-            p.splits = plan.splits;
-            p.counters = static_cast<unsigned*>(a.scratch);
-            p.part = reinterpret_cast<float*>(static_cast<char*>(a.scratch) + kCounterBytes);
+        const int lead = plan.rows ? static_cast<int>(a.t / 256) * 256 : 0;
+        if (lead > 0) {
+            BigParams q = p;
+            q.t = lead;
+            q.x_bytes = (static_cast<std::size_t>(lead - 1) * a.ld_x + kx) * 2;
+            launch_grid<XT, EP, YT, SPLIT>(a, q, 4, 1, false, stream);
         }
-        if (plan.mb == 4) launch_big3<XT, EP, YT, 4, SPLIT>(p, stream);
-        else if (plan.mb == 2) launch_big3<XT, EP, YT, 2, SPLIT>(p, stream);
-        else launch_big3<XT, EP, YT, 1, SPLIT>(p, stream);
+        if (lead < static_cast<int>(a.t)) {
+            BigParams q = p;
+            if (lead > 0) {
+                q.t = static_cast<int>(a.t) - lead;
+                q.x = p.x + static_cast<std::size_t>(lead) * a.ld_x;
+                q.y = static_cast<char*>(p.y) + static_cast<std::size_t>(lead) * y_row_bytes<YT>(a.ld_y);
+                q.x_bytes = (static_cast<std::size_t>(q.t - 1) * a.ld_x + kx) * 2;
+            }
+            if (plan.rows) launch_grid<XT, EP, YT, SPLIT>(a, q, plan.mb2, plan.splits2, plan.planes2, stream);
+            else launch_grid<XT, EP, YT, SPLIT>(a, q, plan.mb, plan.splits, plan.planes, stream);
+        }
     } else if constexpr (SPLIT == 1 && YT != kYPairs) {
         p.tiles_n = wide ? tn256 : static_cast<int>((a.n + 127) / 128);
         if (wide) launch_big2<XT, EP, YT, 4>(p, stream);

@@ -314,6 +314,49 @@ def test_w8g_split_k_mlp_shapes(sm, t):
         assert max_rel_over_rms(host(y.float()), host(y0.float()).astype(np.float64)) < 2e-3
 
 
+@pytest.mark.parametrize("t,n,k,ep,ydt", [
+    (33, 2560, 9728, "store", "f32"), (200, 2560, 9728, "store", "f32"), (700, 2560, 9728, "add", "f32"),
+    (1024, 2560, 9728, "store", "f32"), (64, 2560, 4096, "add", "f32"), (100, 19456, 2560, "swiglu", "f32"),
+    (300, 19456, 2560, "swiglu", "bf16"), (896, 19456, 2560, "swiglu", "f16"), (1300, 12288, 2560, "store", "f32"),
+    (1300, 9728, 2560, "add", "f32"), (1100, 19456, 2560, "swiglu", "f16")])
+def test_w8g_small_grid_plans(sm, t, n, k, ep, ydt):
+    """The small-grid plans at the model's weight shapes: K split through planes (the splits' float32 partials written
+    row-major, then added in split order by a finisher that runs the epilogue: Store, Add, SwiGLU into float32, binary16
+    or bf16) or through the last block's hand-off, the leading whole 256-row tiles apart from the rows after them (at
+    M = 896 gate/up: 768 rows unsplit, then 128 rows with a K split), and 64- / 128-row blocks in the dense order. Every
+    element against float64 of the dequantized weights within the bar, and the same bits on a second call."""
+    say("w8g small-grid plan", t, n, k, ep, ydt)
+    g = torch.Generator(device="cuda").manual_seed(7 * t + n + k)
+    w = (torch.randn(n, k, generator=g, device="cuda") * 0.02).half()
+    q, s = sm.quantize_group_s8(w)
+    x = torch.randn(t, k, generator=g, device="cuda").bfloat16()
+    epi = {"store": sm.STORE, "add": sm.ADD, "swiglu": sm.SWIGLU}[ep]
+    dt = {"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16}[ydt]
+    ref = _deq_ref(x, q, s, k)
+    if ep == "swiglu":
+        z = ref.view(t, n // 128, 2, 64)
+        gate, up = z[:, :, 0, :].reshape(t, n // 2), z[:, :, 1, :].reshape(t, n // 2)
+        ref = gate / (1.0 + torch.exp(-gate)) * up
+    ref = ref.cpu().numpy()
+    if ep == "add":
+        base = torch.randn(t, n, generator=g, device="cuda")
+        y = base.clone()
+        sm.gemm_w8g(x, q, s, y=y, epilogue=epi)
+        y2 = base.clone()
+        sm.gemm_w8g(x, q, s, y=y2, epilogue=epi)
+        got = host(y) - host(base).astype(np.float64)
+    else:
+        y = sm.gemm_w8g(x, q, s, epilogue=epi, y_dtype=dt)
+        y2 = sm.gemm_w8g(x, q, s, epilogue=epi, y_dtype=dt)
+        got = host(y.float())
+    assert torch.equal(y, y2), (t, n, k, ep)
+    if ydt == "bf16":
+        assert_within_one_bf16_step(got, ref)
+    else:
+        err = max_rel_over_rms(got, ref)
+        assert err < 2e-3, (t, n, k, ep, ydt, err)
+
+
 @pytest.mark.parametrize("t", [1, 7, 16])
 @pytest.mark.parametrize("xdt", ["bf16", "f16"])
 def test_w8g_single_call_pass_kernels(sm, t, xdt):
@@ -859,7 +902,7 @@ def _gpu_composition(sm, kind, x, layers, act):
     return host(y)
 
 
-@pytest.mark.parametrize("t", [65, 300, 1500])
+@pytest.mark.parametrize("t", [65, 300, 896, 1500])
 def test_mlp_stack_float32_h_pairs(sm, t):
     """kind 2 above 64 rows: the gate/up epilogue writes H as the down multiply's bf16 hi + lo pairs (small grids with
     a K split, ragged last tiles); bit for bit against the steps called one by one, where the down multiply splits the
