@@ -828,9 +828,9 @@ StackZones stack_zones(int kind, std::size_t t, std::size_t hidden, std::size_t 
         z.end = z.off_sx + up256(t * (hidden / z.ab_h) * 4);
         return z;
     }
-    // general: H [t, inter] (binary16 for w8g; float32 for kind 2, and for q8 unless the gate/up epilogue quantizes
-    // it); q8 also the int8 layer input and int8 H with their scales; kind 2 the hi + lo pairs of H for the down
-    // multiply
+    // general: H [t, inter] (binary16 for w8g and for q8 with one scale per token; float32 for kind 2, and for q8 per
+    // 128 unless the gate/up epilogue quantizes it); q8 also the int8 layer input and int8 H with their scales; kind 2
+    // the hi + lo pairs of H for the down multiply
     z.fused_h = kind == 1 && z.ab_i == 128 && !q8_streams(t, 2 * inter);
     const std::size_t h_bytes = kind == 0 ? t * inter * 2 : (z.fused_h ? 0 : t * inter * 4);
     z.off_qx = z.off_h + up256(h_bytes);
@@ -1003,8 +1003,12 @@ void run_stack(const StackZones& z, int kind, std::size_t layers, std::size_t t,
             gu.ld_ys = inter / 128;
             launch_gemm_q8_swiglu_q8(gu, st);
         } else {
+            // H binary16 when one scale per token follows (the reference's GPU int8 path quantizes its binary16
+            // activations per row, runner/cuda/src/cuda_engine.cpp:1098-1102); float32 per 128, as cpu-q8 keeps it
+            const int h_type = z.per_token ? SEPAL_HIP_F16 : SEPAL_HIP_F32;
+            gu.y_type = h_type;
             launch_gemm_q8(gu, st);
-            launch_quantize_rows(h, SEPAL_HIP_F32, inter, qh, inter, sh, inter / z.ab_i, t, inter, z.ab_i, st);
+            launch_quantize_rows(h, h_type, inter, qh, inter, sh, inter / z.ab_i, t, inter, z.ab_i, st);
         }
         dn.x = qh;
         dn.ld_x = inter;

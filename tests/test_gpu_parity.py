@@ -10,7 +10,7 @@ import sys
 import numpy as np
 import pytest
 
-from helpers import bf16_inputs, max_rel_over_rms, rel_rms, same_bits
+from helpers import bf16_inputs, max_rel_over_rms, per_token_layer_stages, rel_rms, same_bits
 from oracle import orc
 
 pytestmark = pytest.mark.gpu
@@ -845,8 +845,11 @@ def test_q8_small_m_group_sums_exact(sm, t, n, k):
 # Drift of a three-layer stack (each layer's input re-rounded to bf16) against the oracle, which keeps H in float32 as
 # the reference does: the binary16 H of kind 0 costs ~8e-4 of the 2e-3 single-layer bar, and the bf16 re-rounding
 # between layers carries that to ~3e-3 rel rms after three layers; kind 2 (float32 H as bf16 hi + lo) stays at the
-# float32-rounding level of one layer and within 2e-3 after three.
+# float32-rounding level of one layer and within 2e-3 after three. The q8 stack with one scale per token keeps H in
+# binary16 before its quantization (as the reference's GPU int8 path does), so the rare activation that crosses an
+# int8 rounding boundary against the oracle's moves by a whole int8 step, and three layers carry that to ~4.4e-3.
 STACK3_DRIFT = {0: 4e-3, 2: 2e-3}
+STACK3_DRIFT_Q8_TOKEN = 1e-2
 
 
 def _stack_weights(sm, rng, layers, hidden, inter, rule):
@@ -861,7 +864,9 @@ def _stack_weights(sm, rng, layers, hidden, inter, rule):
     return out
 
 
-def _oracle_stack(kind, x, layers, act_block):
+def _oracle_stack(kind, x, layers, act_block, h16=False):
+    """h16: H rounded to binary16 before its per-token quantization (the general q8 path, as the reference's GPU int8
+    path quantizes binary16 activations, runner/cuda/src/cuda_engine.cpp:1098-1102; the M <= 16 stack keeps float32)."""
     x = x.copy()
     y = None
     for li, (wgu, sgu, wd, sd) in enumerate(layers):
@@ -875,6 +880,8 @@ def _oracle_stack(kind, x, layers, act_block):
             xq, xs = orc.quantize_block_r2(x, block=ab_h)
             h = orc.gemm_q8(xq, xs, wgu, sgu, epilogue=orc.SWIGLU, act_block=ab_h)
             ab_i = 128 if act_block == 128 else h.shape[1]
+            if h16 and act_block != 128:
+                h = h.astype(np.float16).astype(np.float32)
             hq, hs = orc.quantize_block_r2(h, block=ab_i)
             y = orc.gemm_q8(hq, hs, wd, sd, act_block=ab_i)
         if li + 1 < len(layers):
@@ -893,7 +900,9 @@ def _gpu_composition(sm, kind, x, layers, act):
         else:
             ab_h = 128 if act == 128 else x.shape[1]
             xq, xs = sm.quantize_rows_s8(xt, block=ab_h)
-            h = sm.gemm_q8(xq, xs, wgu, sgu, epilogue=sm.SWIGLU, act_block=ab_h)
+            # (one scale per token: H binary16, on the general path these shapes take)
+            h = sm.gemm_q8(xq, xs, wgu, sgu, epilogue=sm.SWIGLU, act_block=ab_h,
+                           y_dtype=torch.float32 if act == 128 else torch.float16)
             ab_i = 128 if act == 128 else h.shape[1]
             hq, hs = sm.quantize_rows_s8(h, block=ab_i)
             y = sm.gemm_q8(hq, hs, wd, sd, act_block=ab_i)
@@ -933,12 +942,16 @@ def test_mlp_stack(sm, kind, act, t):
         assert same_bits(host(xt), orc.bf16_round(orc.rmsnorm_rows(_oracle_stack(kind, x, layers[:2], act))))
     # one layer (no rounding of an intermediate activation to bf16) against the oracle at the parity bar
     y1 = host(sm.mlp_stack(kind, dev(x, torch.bfloat16), layers[:1], act_block=act))
-    ref1 = _oracle_stack(kind, x, layers[:1], act)
-    ref = _oracle_stack(kind, x, layers, act)
+    ref1 = _oracle_stack(kind, x, layers[:1], act, h16=True)
+    ref = _oracle_stack(kind, x, layers, act, h16=True)
     if kind == 1 and t > 64 and act == 128:
         # the large-M q8 path per 128 is the reference's arithmetic (per token, a form the reference does not have,
         # the SwiGLU is the fast one and the floats are held to the parity bar)
         assert same_bits(y1, ref1) and same_bits(y, ref)
+    elif kind == 1 and act == 0:
+        say("errors: one layer rel rms", f"{rel_rms(y1, ref1):.3e}", "three layers rel rms", f"{rel_rms(y, ref):.3e}")
+        assert same_bits(per_token_layer_stages(sm, x, layers[0]), y1)
+        assert rel_rms(y1, ref1) < 2e-3 and rel_rms(y, ref) < STACK3_DRIFT_Q8_TOKEN, (rel_rms(y1, ref1), rel_rms(y, ref))
     else:
         say("errors: one layer max rel", f"{max_rel_over_rms(y1, ref1):.3e}", "three layers rel rms", f"{rel_rms(y, ref):.3e}")
         assert max_rel_over_rms(y1, ref1) < 2e-3, max_rel_over_rms(y1, ref1)
