@@ -1375,8 +1375,15 @@ void launch_big(const GemmArgs& a, hipStream_t stream) {
             if (q.wimg != nullptr) {
                 int extra = 0;
                 if (a.next_image != nullptr) {
-                    // the next multiply's image on the CUs the halves leave idle (at least 32 blocks)
-                    extra = std::max(32, cus - 2 * rest);
+                    // the next multiply's image on blocks dispatched after the halves. When the CUs the halves
+                    // leave idle can widen it within the halves' time (measured: ~2.1 us per 128-value group for a
+                    // half, ~25 GB/s of image traffic per widening CU), they alone do (the down multiply's halves,
+                    // 164 us, against 150 MB); otherwise four blocks per CU, so that every CU joins as its half ends
+                    // (the gate/up multiply's halves, ~42 us, against 75 MB: 75 -> 60 us)
+                    const int idle = std::max(32, cus - 2 * rest);
+                    const double halves_us = 2.1 * static_cast<double>(a.k / 128);
+                    const double widen_us = 3.0 * static_cast<double>(a.next_n) * a.next_k / (idle * 25.0e3);
+                    extra = widen_us <= halves_us ? idle : 4 * cus;
                     q.jw = reinterpret_cast<const signed char*>(a.next_w);
                     q.j_ld = a.next_ld_w;
                     q.j_n = static_cast<int>(a.next_n);
