@@ -507,19 +507,28 @@ __global__ void __launch_bounds__(512) gemm_big(const Params p) {
     chain_epilogue<EP, YT, PER_TOKEN, PER_TOKEN && MODE == MODE_CHAIN>(p, acc, m0, n0, wm, ib, hh, lane, tid, col, reinterpret_cast<float*>(lw0));
 }
 
-// ---- the chain modes, one 32 x 32 block at a time (gemm_chain) -----------------------------------------------------
+// ---- the chain with one activation scale per token: two wave groups in alternation (gemm_chain) ---------------------
 //
-// The tile, waves, LDS stages and swizzle of gemm_big's chain mode, in another order. At the top of group g, after the
-// barrier that publishes its stage, each wave reads all 16 operand fragments of the group into registers (stage g is
-// then free, and group g + 2's loads are issued into the stage of group g - 1). It then runs its four 32 x 32 blocks
-// one after the other: the block's four MFMAs (one per 32-wide substep) give its exact int32 group sums, and while
-// they run, the previous block's sums go through their link of the float chain. The chain thus trails the MFMAs by one
-// block, and only two blocks of int32 sums are ever live (the group's sums of all four blocks, as in gemm_big, would
-// not leave room for the fragments). The links run in the same order with the same operands as gemm_big's, so the
-// results are the same bits. The direct loads go through buffer descriptors (a 32-bit lane offset: the row, clamped to
-// the last row, and the swizzled chunk; the group's offset in the scalar offset; the LDS destination in scalar
-// registers), so issuing a group's loads costs no vector instruction. The launcher uses this kernel when every
-// offset fits 32 bits.
+// The 128 x 256 tile of gemm_big's chain mode: 8 waves of 64 x 64 outputs (2 x 2 blocks of MFMA 32x32x32 i8), K in
+// steps of one group (128 bytes) through three LDS stages of 128-byte rows (chunk c of row r at c ^ sw8(r)), filled
+// straight from global memory through buffer descriptors (a 32-bit lane offset: the row, clamped to the last row, and
+// the swizzled chunk; the group's offset in the scalar offset; the LDS destination in scalar registers). Each block's
+// four MFMAs give its exact int32 group sums, and the cpu-q8 chain links them into the float accumulators
+// (acc = f_0 ws_0, then acc = fma(f_g, ws_g, acc); times the token's scale in the epilogue), each output's links in
+// group order, so the results do not depend on how the work is scheduled.
+// Schedule: waves 0-3 (group A, one per SIMD) and 4-7 (group B) each alternate two slots per group, separated by
+// block barriers, so that in every slot one wave of each SIMD reads the LDS while the other runs MFMAs and the chain's
+// VALU work (with every wave reading after the same barrier and then multiplying, the two waves of a SIMD waited for
+// the LDS together and then competed for the MFMA and VALU units together: 8% slower at C4). L(g) issues the wave's
+// share of group g + 2's direct loads (2 of the activations' and 4 of the weights' 1 KB loads, and its two weight
+// scales) into the stage of group g - 1 and reads all 16 operand fragments of group g; M(g) runs the group's four
+// blocks, each block's MFMAs with the link of the block two before it (whose sums were complete a block ago, so the
+// link's converts and fused multiply-adds interleave with the MFMAs). Group B runs one slot behind group A: slot 2g is
+// A L(g) and B M(g - 1), slot 2g + 1 is A M(g) and B L(g). Stage g mod 3 is last read in slot 2g + 1 and reloaded
+// (with group g + 3) from slot 2g + 2. At the end of L(g) a wave waits for its share of group g + 1 (issued in its
+// previous L slot), so both shares are complete by the barrier that ends slot 2g + 1, before group g + 1 is first
+// read; every wave issues, reads and waits alike (only B's extra barrier at the start and A's at the end differ), so
+// the kernel has no branch between the groups' code. The launcher uses this kernel when every offset fits 32 bits.
 struct ChainParams {
     Params p;
     unsigned x_bytes, w_bytes, ws_bytes, xs_bytes;  // extents of X, W and their scales (buffer ranges)
@@ -527,13 +536,12 @@ struct ChainParams {
 
 template <int EP, int YT, bool PER_TOKEN>
 __global__ void __launch_bounds__(512) gemm_chain(const ChainParams cp) {
+    static_assert(PER_TOKEN, "one activation scale per token (the chain's scale is the weight scale alone)");
     const Params& p = cp.p;
     constexpr int BM = 128, BN = 256;
-    constexpr int XDMA = BM / 64, WDMA = BN / 64;
-    constexpr int NSC = PER_TOKEN ? 2 : 3;  // scale loads per thread and group
+    constexpr int XDMA = BM / 64, WDMA = BN / 64, NLD = XDMA + WDMA + 2;  // a wave's loads per group (with 2 scales)
     __shared__ __align__(1024) u32x4 lx0[BM * 8], lx1[BM * 8], lx2[BM * 8];
     __shared__ __align__(1024) u32x4 lw0[BN * 8], lw1[BN * 8], lw2[BN * 8];
-    __shared__ float lds_xs[3][BM];  // per-128 activation scales of group g in buffer g mod 3
     typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
     const auto xstage = [&](auto it) -> lds_u32x4* {
         constexpr int i = decltype(it)::value;
@@ -550,6 +558,7 @@ __global__ void __launch_bounds__(512) gemm_chain(const ChainParams cp) {
 
     const int tid = threadIdx.x, lane = tid % 64;
     const int wave = __builtin_amdgcn_readfirstlane(tid / 64);  // wave-uniform: LDS destinations stay scalar
+    const bool group_b = wave >= 4;
     const int wm = wave % 2, wn = wave / 2;
     int tm, tn;
     tile_of(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
@@ -559,10 +568,9 @@ __global__ void __launch_bounds__(512) gemm_chain(const ChainParams cp) {
     const __amdgpu_buffer_rsrc_t xres = __builtin_amdgcn_make_buffer_rsrc(const_cast<signed char*>(p.x), 0, static_cast<int>(cp.x_bytes), 0x00020000);
     const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(const_cast<signed char*>(p.w), 0, static_cast<int>(cp.w_bytes), 0x00020000);
     const __amdgpu_buffer_rsrc_t wsres = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(p.ws), 0, static_cast<int>(cp.ws_bytes), 0x00020000);
-    const __amdgpu_buffer_rsrc_t xsres = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(p.xs), 0, static_cast<int>(cp.xs_bytes), 0x00020000);
-    // direct load e of wave w fills LDS kilobyte w + 8 e = rows 8 w + 64 e + {0..7}; lane l writes slot l % 8 of row
-    // 8 w + 64 e + l / 8, which holds chunk (l % 8) ^ sw8(row) = (l % 8) ^ ((4 w + l / 16) & 7); rows past T or N
-    // repeat the last row (never stored)
+    // a wave's share of a group's loads: direct load e fills LDS kilobyte
+    // wave + 8 e = rows 8 wave + 64 e + {0..7}; lane l writes slot l % 8 of row 8 wave + 64 e + l / 8, which holds chunk
+    // (l % 8) ^ sw8(row) = (l % 8) ^ ((4 wave + l / 16) & 7); rows past T or N repeat the last row (never stored)
     const int chunk = (lane % 8) ^ ((4 * wave + lane / 16) & 7);
     int xoff[XDMA], woff[WDMA];
 #pragma unroll
@@ -571,8 +579,6 @@ __global__ void __launch_bounds__(512) gemm_chain(const ChainParams cp) {
 #pragma unroll
     for (int e = 0; e < WDMA; ++e)
         woff[e] = min(n0 + 8 * wave + 64 * e + lane / 8, p.n - 1) * static_cast<int>(p.ld_w) + 16 * chunk;
-    const int xs_off = PER_TOKEN ? 0 : min(m0 + (tid % BM), p.t - 1) * static_cast<int>(p.ld_xs) * 4;
-
     const int ib = wn / 2, hh = wn % 2;
     const int colrel[2] = {128 * ib + 32 * hh + lane % 32, 128 * ib + 64 + 32 * hh + lane % 32};
     int col[2];
@@ -580,9 +586,6 @@ __global__ void __launch_bounds__(512) gemm_chain(const ChainParams cp) {
     for (int j = 0; j < 2; ++j) col[j] = n0 + colrel[j];
     const int ws_off0 = min(col[0], p.n - 1) * static_cast<int>(p.ld_ws) * 4;
     const int ws_off1 = min(col[1], p.n - 1) * static_cast<int>(p.ld_ws) * 4;
-    // fragment reads (u32x4 units): lane l of m-block i, substep st reads row wm 64 + 32 i + l % 32, chunk 2 st + l / 32
-    // at slot chunk ^ sw8(row); of n-block q, row colrel[q]. Rows 32 apart (m-blocks) and 64 apart (n-blocks) share
-    // sw8, so one offset per substep serves both, the second block at a constant distance.
     int ra[4], rb[4];
     {
         const int rowa = wm * 64 + lane % 32, rowb = colrel[0];
@@ -595,9 +598,10 @@ __global__ void __launch_bounds__(512) gemm_chain(const ChainParams cp) {
     }
 
     struct Set {
-        float xs, ws[2];
+        float ws[2];
     };
-    Set s0, s1, s2;  // group g's scales in set g mod 3
+    Set s0, s1, s2;  // group g's weight scales in set g mod 3
+    // the wave's loads of group g: its share of one operand's stage, then its two weight scales
     const auto issue = [&](int g, lds_u32x4* xd, lds_u32x4* wd, Set& s) {
         const int k0 = g * 128;
 #pragma unroll
@@ -608,10 +612,15 @@ __global__ void __launch_bounds__(512) gemm_chain(const ChainParams cp) {
         for (int e = 0; e < WDMA; ++e)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(wres, (__attribute__((address_space(3))) void*)(wd + (wave + 8 * e) * 64), 16,
                                                      woff[e], k0, 0, 0);
-        if constexpr (!PER_TOKEN)
-            s.xs = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(xsres, xs_off, (g >> p.act_shift) * 4, 0));
         s.ws[0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(wsres, ws_off0, g * 4, 0));
         s.ws[1] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(wsres, ws_off1, g * 4, 0));
+    };
+    const auto barrier = [&]() __attribute__((always_inline)) {
+        __builtin_amdgcn_sched_barrier(0);
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
     };
 
     float acc[2][2][16];
@@ -622,46 +631,29 @@ __global__ void __launch_bounds__(512) gemm_chain(const ChainParams cp) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
     const i32x16 zero16 = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-    i32x16 T0, T1;  // int32 sums of the blocks in flight (block b of a group in T(b mod 2))
-
-    // link of the chain for block (i, q): acc += sums * scale (the first group's link multiplies)
-    const auto link = [&](const i32x16& S, int i, int q, float ws, int xbuf, bool first) {
+    // int32 sums of the blocks in flight: block n = 4 g + b (group g, block b) in T[n mod 3] (with three groups a turn
+    // the index is a constant: (4 (g mod 3) + b) mod 3)
+    i32x16 T[3];
+    u32x4 a[2][4], b[2][4];
+    const auto link = [&](const i32x16& S, int i, int q, float ws, bool first) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            float sc = ws;
-            if constexpr (!PER_TOKEN) sc = __fmul_rn(ws, lds_xs[xbuf][wm * 64 + i * 32 + 8 * (r / 4) + 4 * (lane / 32) + (r % 4)]);
             const float f = static_cast<float>(S[r]);
-            acc[i][q][r] = first ? __fmul_rn(f, sc) : __builtin_fmaf(f, sc, acc[i][q][r]);
+            acc[i][q][r] = first ? __fmul_rn(f, ws) : __builtin_fmaf(f, ws, acc[i][q][r]);
         }
     };
 
-    // Group g, stage j = g mod 3 (its scales in set j): wait for the group's loads, put its per-128 activation scales in
-    // LDS, barrier; read its 16 fragments; copy group g - 1's weight scales out of set (g + 2) mod 3 and issue group
-    // g + 2's loads there (clamped; past the end they repeat into stages nothing reads again, so the wait counts stay
-    // exact); then blocks 0..3, each block's MFMAs with the previous block's link (block 3 of group g - 1 at block 0).
-    float pw0 = 0.0f, pw1 = 0.0f;  // group g - 1's weight scales
-    const auto group_step = [&](int g, auto jt, auto prev_t) {
+    // L(g), stage j = g mod 3: group g + 2's loads (clamped: past the end they repeat into stages nothing reads again,
+    // so the wait counts stay exact) into the stage and scale set of group g - 1, then group g's 16 fragments; the
+    // reads are complete before the barrier
+    const auto slot_l = [&](int g, auto jt) __attribute__((always_inline)) {
         constexpr int j = decltype(jt)::value;
-        // 0: group 0 (no previous group; its own links multiply); 1: group 1 (group 0's block 3 links by a
-        // multiply); 2: later groups
-        constexpr int pmode = decltype(prev_t)::value;
-        constexpr bool first = pmode == 0;
-        Set& cur = j == 0 ? s0 : (j == 1 ? s1 : s2);
-        Set& prev = j == 0 ? s2 : (j == 1 ? s0 : s1);  // group g - 1's set, reused for group g + 2
-        asm volatile("" ::: "memory");
-        wait_vm_lgkm0<XDMA + WDMA + NSC>();  // everything but group g + 1's loads
-        if constexpr (!PER_TOKEN)
-            if (tid < BM) lds_xs[g % 3][tid] = cur.xs;
-        __builtin_amdgcn_s_barrier();
-        asm volatile("" ::: "memory");
-        // group g + 2's loads into the stage and set of group g - 1 (read before the barrier; its weight scales
-        // copied out first)
-        const float cws0 = pw0, cws1 = pw1;
+        Set& nxt = j == 0 ? s2 : (j == 1 ? s0 : s1);
         issue(min(g + 2, groups - 1), xstage(std::integral_constant<int, (j + 2) % 3>{}),
-              wstage(std::integral_constant<int, (j + 2) % 3>{}), prev);
+              wstage(std::integral_constant<int, (j + 2) % 3>{}), nxt);
+        __builtin_amdgcn_sched_barrier(0);
         const lds_u32x4* tx = xstage(std::integral_constant<int, j>{});
         const lds_u32x4* tw = wstage(std::integral_constant<int, j>{});
-        u32x4 a[2][4], b[2][4];
 #pragma unroll
         for (int st = 0; st < 4; ++st) {
             a[0][st] = tx[ra[st]];
@@ -672,42 +664,88 @@ __global__ void __launch_bounds__(512) gemm_chain(const ChainParams cp) {
             a[1][st] = tx[ra[st] + 256];
             b[1][st] = tw[rb[st] + 512];
         }
+        __builtin_amdgcn_sched_barrier(0);
+        asm volatile("" ::: "memory");
+        wait_vm_lgkm0<NLD>();  // and the wave's loads of group g + 1 (its loads of group g + 2 stay in flight)
+        barrier();
+    };
+    // M(g): blocks 0..3, each block's four MFMAs with the link of the block two before it (blocks 2 and 3 of group
+    // g - 1 at blocks 0 and 1): those sums were complete a block ago, so the link's converts and fused multiply-adds
+    // interleave with the MFMAs instead of waiting for the last one; every output's links still run in group order. The
+    // last group's blocks 2 and 3 are linked after its M slot.
+    float pw0 = 0.0f, pw1 = 0.0f;  // group g - 1's weight scales
+    const auto slot_m = [&](auto jt, auto prev_t) __attribute__((always_inline)) {
+        constexpr int j = decltype(jt)::value;
+        // 0: group 0 (no previous group; its own links multiply); 1: group 1 (group 0's blocks 2 and 3 link by a
+        // multiply); 2: later groups
+        constexpr int pmode = decltype(prev_t)::value;
+        constexpr bool first = pmode == 0;
+        Set& cur = j == 0 ? s0 : (j == 1 ? s1 : s2);
         const float gws0 = cur.ws[0], gws1 = cur.ws[1];
 #pragma unroll
         for (int blk = 0; blk < 4; ++blk) {
             const int i = blk / 2, q = blk % 2;
-            i32x16& S = blk % 2 == 0 ? T0 : T1;
+            i32x16& S = T[(4 * j + blk) % 3];
 #pragma unroll
             for (int st = 0; st < 4; ++st) S = mfma_i8_32(a[i][st], b[q][st], st == 0 ? zero16 : S);
-            if (blk == 0) {
-                if constexpr (pmode > 0) link(T1, 1, 1, cws1, (g + 2) % 3, pmode == 1);
-            } else {
-                const int pi = (blk - 1) / 2, pq = (blk - 1) % 2;
-                link(blk % 2 == 0 ? T1 : T0, pi, pq, pq == 0 ? gws0 : gws1, g % 3, first);
+            if (blk >= 2) {
+                const int pq = (blk - 2) % 2;
+                link(T[(4 * j + blk - 2) % 3], (blk - 2) / 2, pq, pq == 0 ? gws0 : gws1, first);
+            } else if constexpr (pmode > 0) {
+                link(T[(4 * j + blk + 1) % 3], 1, blk, blk == 0 ? pw0 : pw1, pmode == 1);
             }
         }
         pw0 = gws0;
         pw1 = gws1;
+        barrier();
     };
+
     using I0 = std::integral_constant<int, 0>;
     using I1 = std::integral_constant<int, 1>;
     using I2 = std::integral_constant<int, 2>;
     issue(0, xstage(I0{}), wstage(I0{}), s0);
     issue(min(1, groups - 1), xstage(I1{}), wstage(I1{}), s1);
-    // group 0, group 1, then three groups per iteration (stage and scale set g mod 3)
-    group_step(0, I0{}, I0{});
-    if (groups > 1) group_step(1, I1{}, I1{});
-    int g = 2;
-    for (; g + 3 <= groups; g += 3) {
-        group_step(g, I2{}, I2{});
-        group_step(g + 1, I0{}, I2{});
-        group_step(g + 2, I1{}, I2{});
+    wait_vm_lgkm0<NLD>();  // group 0's loads
+    barrier();
+    if (group_b) barrier();  // B runs one slot behind A
+    // group g in stage and scale set g mod 3; M of group 0 and group 1 by their own modes, then three groups a turn
+    slot_l(0, I0{});
+    slot_m(I0{}, I0{});
+    int g = 1;
+    if (groups > 1) {
+        slot_l(1, I1{});
+        slot_m(I1{}, I1{});
+        g = 2;
     }
-    if (g < groups) group_step(g, I2{}, I2{});
-    if (g + 1 < groups) group_step(g + 1, I0{}, I2{});
-    // the last group's block 3
-    link(T1, 1, 1, pw1, (groups - 1) % 3, groups == 1);
-    // the repeated loads of the last steps may still be writing LDS: drain them before the block reuses or leaves it
+    for (; g + 3 <= groups; g += 3) {
+        slot_l(g, I2{});
+        slot_m(I2{}, I2{});
+        slot_l(g + 1, I0{});
+        slot_m(I0{}, I2{});
+        slot_l(g + 2, I1{});
+        slot_m(I1{}, I2{});
+    }
+    if (g < groups) {
+        slot_l(g, I2{});
+        slot_m(I2{}, I2{});
+    }
+    if (g + 1 < groups) {
+        slot_l(g + 1, I0{});
+        slot_m(I0{}, I2{});
+    }
+    if (!group_b) barrier();  // matches group B's extra barrier
+    // the last group's blocks 2 and 3 (group groups - 1, stage index (groups - 1) mod 3)
+    const auto last_links = [&](auto jt) __attribute__((always_inline)) {
+        constexpr int j = decltype(jt)::value;
+        link(T[(4 * j + 2) % 3], 1, 0, pw0, groups == 1);
+        link(T[(4 * j + 3) % 3], 1, 1, pw1, groups == 1);
+    };
+    switch ((groups - 1) % 3) {
+    case 0: last_links(I0{}); break;
+    case 1: last_links(I1{}); break;
+    default: last_links(I2{}); break;
+    }
+    // the repeated loads of the last groups may still be writing LDS: drain them before the block reuses or leaves it
     wait_vm_lgkm0<0>();
     __syncthreads();
     chain_epilogue<EP, YT, PER_TOKEN>(p, acc, m0, n0, wm, ib, hh, lane, tid, col, reinterpret_cast<float*>(lw0));
