@@ -560,32 +560,48 @@ __global__ void __launch_bounds__(512) gemm_chain(const ChainParams cp) {
     const int wave = __builtin_amdgcn_readfirstlane(tid / 64);  // wave-uniform: LDS destinations stay scalar
     const bool group_b = wave >= 4;
     const int wm = wave % 2, wn = wave / 2;
-    int tm, tn;
-    tile_of(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
-    const int m0 = tm * BM, n0 = tn * BN;
+    // persistent: one block per CU; block b works through the contiguous range [lo, hi) of logical tiles of its XCD
+    // (b mod 8), every (gridDim.x / 8)-th from lo + b / 8, so the XCD's blocks run consecutive tiles at a time (they
+    // share its L2)
+    const int total = p.tiles_m * p.tiles_n;
+    int cur, hi, stride;
+    {
+        const int nx = static_cast<int>(gridDim.x) / 8, xcd = static_cast<int>(blockIdx.x) % 8;
+        const int q = total / 8, r = total % 8;
+        const int lo = xcd * q + min(xcd, r);
+        hi = lo + q + (xcd < r ? 1 : 0);
+        cur = lo + static_cast<int>(blockIdx.x) / 8;
+        stride = nx;
+    }
+    if (cur >= hi || stride < 1) return;  // (the launcher's grid is a positive multiple of 8, so stride >= 1)
     const int groups = p.k / 128;
 
     const __amdgpu_buffer_rsrc_t xres = __builtin_amdgcn_make_buffer_rsrc(const_cast<signed char*>(p.x), 0, static_cast<int>(cp.x_bytes), 0x00020000);
     const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(const_cast<signed char*>(p.w), 0, static_cast<int>(cp.w_bytes), 0x00020000);
     const __amdgpu_buffer_rsrc_t wsres = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(p.ws), 0, static_cast<int>(cp.ws_bytes), 0x00020000);
-    // a wave's share of a group's loads: direct load e fills LDS kilobyte
-    // wave + 8 e = rows 8 wave + 64 e + {0..7}; lane l writes slot l % 8 of row 8 wave + 64 e + l / 8, which holds chunk
-    // (l % 8) ^ sw8(row) = (l % 8) ^ ((4 wave + l / 16) & 7); rows past T or N repeat the last row (never stored)
+    // a wave's share of a group's loads: direct load e fills LDS kilobyte wave + 8 e = rows 8 wave + 64 e + {0..7};
+    // lane l writes slot l % 8 of row 8 wave + 64 e + l / 8, which holds chunk (l % 8) ^ sw8(row) = (l % 8) ^
+    // ((4 wave + l / 16) & 7); rows past T or N repeat the last row (never stored)
     const int chunk = (lane % 8) ^ ((4 * wave + lane / 16) & 7);
-    int xoff[XDMA], woff[WDMA];
-#pragma unroll
-    for (int e = 0; e < XDMA; ++e)
-        xoff[e] = min(m0 + 8 * wave + 64 * e + lane / 8, p.t - 1) * static_cast<int>(p.ld_x) + 16 * chunk;
-#pragma unroll
-    for (int e = 0; e < WDMA; ++e)
-        woff[e] = min(n0 + 8 * wave + 64 * e + lane / 8, p.n - 1) * static_cast<int>(p.ld_w) + 16 * chunk;
     const int ib = wn / 2, hh = wn % 2;
     const int colrel[2] = {128 * ib + 32 * hh + lane % 32, 128 * ib + 64 + 32 * hh + lane % 32};
-    int col[2];
+    // the tile's origin and the offsets that depend on it
+    int m0, n0, xoff[XDMA], woff[WDMA], ws_off0, ws_off1;
+    const auto set_tile = [&]() __attribute__((always_inline)) {
+        int tm, tn;
+        tile_from_id(cur, p.tiles_m, p.tiles_n, tm, tn);
+        m0 = tm * BM;
+        n0 = tn * BN;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) col[j] = n0 + colrel[j];
-    const int ws_off0 = min(col[0], p.n - 1) * static_cast<int>(p.ld_ws) * 4;
-    const int ws_off1 = min(col[1], p.n - 1) * static_cast<int>(p.ld_ws) * 4;
+        for (int e = 0; e < XDMA; ++e)
+            xoff[e] = min(m0 + 8 * wave + 64 * e + lane / 8, p.t - 1) * static_cast<int>(p.ld_x) + 16 * chunk;
+#pragma unroll
+        for (int e = 0; e < WDMA; ++e)
+            woff[e] = min(n0 + 8 * wave + 64 * e + lane / 8, p.n - 1) * static_cast<int>(p.ld_w) + 16 * chunk;
+        ws_off0 = min(n0 + colrel[0], p.n - 1) * static_cast<int>(p.ld_ws) * 4;
+        ws_off1 = min(n0 + colrel[1], p.n - 1) * static_cast<int>(p.ld_ws) * 4;
+    };
+    set_tile();
     int ra[4], rb[4];
     {
         const int rowa = wm * 64 + lane % 32, rowb = colrel[0];
@@ -624,12 +640,6 @@ __global__ void __launch_bounds__(512) gemm_chain(const ChainParams cp) {
     };
 
     float acc[2][2][16];
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
     const i32x16 zero16 = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
     // int32 sums of the blocks in flight: block n = 4 g + b (group g, block b) in T[n mod 3] (with three groups a turn
     // the index is a constant: (4 (g mod 3) + b) mod 3)
@@ -703,52 +713,85 @@ __global__ void __launch_bounds__(512) gemm_chain(const ChainParams cp) {
     using I0 = std::integral_constant<int, 0>;
     using I1 = std::integral_constant<int, 1>;
     using I2 = std::integral_constant<int, 2>;
-    issue(0, xstage(I0{}), wstage(I0{}), s0);
-    issue(min(1, groups - 1), xstage(I1{}), wstage(I1{}), s1);
-    wait_vm_lgkm0<NLD>();  // group 0's loads
-    barrier();
-    if (group_b) barrier();  // B runs one slot behind A
-    // group g in stage and scale set g mod 3; M of group 0 and group 1 by their own modes, then three groups a turn
-    slot_l(0, I0{});
-    slot_m(I0{}, I0{});
-    int g = 1;
-    if (groups > 1) {
-        slot_l(1, I1{});
-        slot_m(I1{}, I1{});
-        g = 2;
-    }
-    for (; g + 3 <= groups; g += 3) {
-        slot_l(g, I2{});
-        slot_m(I2{}, I2{});
-        slot_l(g + 1, I0{});
-        slot_m(I0{}, I2{});
-        slot_l(g + 2, I1{});
-        slot_m(I1{}, I2{});
-    }
-    if (g < groups) {
-        slot_l(g, I2{});
-        slot_m(I2{}, I2{});
-    }
-    if (g + 1 < groups) {
-        slot_l(g + 1, I0{});
-        slot_m(I0{}, I2{});
-    }
-    if (!group_b) barrier();  // matches group B's extra barrier
-    // the last group's blocks 2 and 3 (group groups - 1, stage index (groups - 1) mod 3)
-    const auto last_links = [&](auto jt) __attribute__((always_inline)) {
-        constexpr int j = decltype(jt)::value;
-        link(T[(4 * j + 2) % 3], 1, 0, pw0, groups == 1);
-        link(T[(4 * j + 3) % 3], 1, 1, pw1, groups == 1);
+    // a tile's first loads: groups 0 and 1 in stages and scale sets 0 and 1
+    const auto first_loads = [&]() __attribute__((always_inline)) {
+        issue(0, xstage(I0{}), wstage(I0{}), s0);
+        issue(min(1, groups - 1), xstage(I1{}), wstage(I1{}), s1);
     };
-    switch ((groups - 1) % 3) {
-    case 0: last_links(I0{}); break;
-    case 1: last_links(I1{}); break;
-    default: last_links(I2{}); break;
+    first_loads();
+    // Tile loop. Per tile the barriers balance (group A: 1 + 2 groups + 1, group B: 1 + 1 + 2 groups); after the last
+    // one every wave has read the tile's stages for the last time, so once a wave has waited for its own loads (the
+    // clamped repeats of the last groups) it issues the next tile's first loads, which fly while this tile's epilogue
+    // runs (its outputs go straight to global memory). The SwiGLU -> int8 epilogue uses weight stage 0 as scratch, so
+    // there the next tile's loads follow it.
+    for (;;) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+        wait_vm_lgkm0<NLD>();  // group 0's loads
+        barrier();
+        if (group_b) barrier();  // B runs one slot behind A
+        // group g in stage and scale set g mod 3; M of group 0 and group 1 by their own modes, then three groups a turn
+        slot_l(0, I0{});
+        slot_m(I0{}, I0{});
+        int g = 1;
+        if (groups > 1) {
+            slot_l(1, I1{});
+            slot_m(I1{}, I1{});
+            g = 2;
+        }
+        for (; g + 3 <= groups; g += 3) {
+            slot_l(g, I2{});
+            slot_m(I2{}, I2{});
+            slot_l(g + 1, I0{});
+            slot_m(I0{}, I2{});
+            slot_l(g + 2, I1{});
+            slot_m(I1{}, I2{});
+        }
+        if (g < groups) {
+            slot_l(g, I2{});
+            slot_m(I2{}, I2{});
+        }
+        if (g + 1 < groups) {
+            slot_l(g + 1, I0{});
+            slot_m(I0{}, I2{});
+        }
+        if (!group_b) barrier();  // matches group B's extra barrier
+        // the last group's blocks 2 and 3 (group groups - 1, stage index (groups - 1) mod 3)
+        const auto last_links = [&](auto jt) __attribute__((always_inline)) {
+            constexpr int j = decltype(jt)::value;
+            link(T[(4 * j + 2) % 3], 1, 0, pw0, groups == 1);
+            link(T[(4 * j + 3) % 3], 1, 1, pw1, groups == 1);
+        };
+        switch ((groups - 1) % 3) {
+        case 0: last_links(I0{}); break;
+        case 1: last_links(I1{}); break;
+        default: last_links(I2{}); break;
+        }
+        wait_vm_lgkm0<0>();  // this wave's repeated loads of the last groups have landed
+        const int mc = m0, nc = n0;
+        const int col[2] = {nc + colrel[0], nc + colrel[1]};
+        cur += stride;
+        const bool more = cur < hi;
+        if constexpr (EP == kSwigluQ8) {
+            __syncthreads();
+            chain_epilogue<EP, YT, PER_TOKEN>(p, acc, mc, nc, wm, ib, hh, lane, tid, col, reinterpret_cast<float*>(lw0));
+            __syncthreads();  // weight stage 0 (the epilogue's scratch) is free again
+            if (!more) break;
+            set_tile();
+            first_loads();
+        } else {
+            if (more) {
+                set_tile();
+                first_loads();
+            }
+            chain_epilogue<EP, YT, PER_TOKEN>(p, acc, mc, nc, wm, ib, hh, lane, tid, col, reinterpret_cast<float*>(lw0));
+            if (!more) break;
+        }
     }
-    // the repeated loads of the last groups may still be writing LDS: drain them before the block reuses or leaves it
-    wait_vm_lgkm0<0>();
-    __syncthreads();
-    chain_epilogue<EP, YT, PER_TOKEN>(p, acc, m0, n0, wm, ib, hh, lane, tid, col, reinterpret_cast<float*>(lw0));
 }
 
 // ---- gemm_s8 (per-channel W8A8, int32 sums over the whole K): 256 x 256 tiles ----------------------------------------
@@ -955,6 +998,19 @@ inline Params make_params(const GemmArgs& a) {
     return p;
 }
 
+// Compute units of the current device (cached per device).
+inline int device_cus() {
+    static int cached[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0) throw LaunchError("gemm_s8: hipGetDevice failed");
+    if (dev < 64 && cached[dev] > 0) return cached[dev];
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+        throw LaunchError("gemm_s8: device query failed");
+    if (dev < 64) cached[dev] = cus;
+    return cus;
+}
+
 template <int EP, int YT, bool PT, int MODE>
 void launch_big(const GemmArgs& a, hipStream_t stream) {
     Params p = make_params(a);
@@ -968,7 +1024,12 @@ void launch_big(const GemmArgs& a, hipStream_t stream) {
         if (x_bytes < lim && w_bytes < lim && ws_bytes < lim && xs_bytes < lim) {
             const ChainParams cp{p, static_cast<unsigned>(x_bytes), static_cast<unsigned>(w_bytes),
                                  static_cast<unsigned>(ws_bytes), static_cast<unsigned>(xs_bytes)};
-            gemm_chain<EP, YT, PT><<<dim3(p.tiles_m * p.tiles_n), dim3(512), 0, stream>>>(cp);
+            // persistent: at most one block per CU, a whole number of blocks per XCD (the kernel's stride through its
+            // XCD's tiles is grid / 8, so it must be at least 1; blocks whose range is empty leave at once)
+            const int tiles = p.tiles_m * p.tiles_n;
+            const int grid = 8 * std::max(1, std::min((tiles + 7) / 8, device_cus() / 8));
+            if (grid % 8 != 0 || grid < 8) throw LaunchError("gemm_q8: persistent grid must be a positive multiple of 8");
+            gemm_chain<EP, YT, PT><<<dim3(grid), dim3(512), 0, stream>>>(cp);
             check_launch("gemm_q8 large-M kernel launch");
             return;
         }
@@ -1027,18 +1088,6 @@ void launch_gemm_q8_swiglu_q8(const GemmArgs& a, hipStream_t stream) {
 
 namespace q8 {
 
-// Compute units of the current device (cached per device).
-inline int device_cus() {
-    static int cached[64] = {};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0) throw LaunchError("gemm_s8: hipGetDevice failed");
-    if (dev < 64 && cached[dev] > 0) return cached[dev];
-    int cus = 0;
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-        throw LaunchError("gemm_s8: device query failed");
-    if (dev < 64) cached[dev] = cus;
-    return cus;
-}
 
 // 256 x 256 tiles when they fill the chip at least once, K is a multiple of 128 and every offset fits 32 bits; the last partial round, when
 // more than a quarter full and small enough, as 128 x 256 halves in a second launch.
