@@ -320,14 +320,15 @@ __global__ void __launch_bounds__(kThreads) pass_kernel(const PassParams p) {
 #pragma unroll
         for (int i = 0; i < kPairs; ++i) {
             if (i >= n_pairs) continue;
-            const int q = q0 + i;
-            if (i > 0 && q % gpt == 0) {  // a new tile (wave-uniform)
+            // (the walk above: pair i is group pg[i] of tile slot pslot[i]; a new tile starts where it wrapped to g_lo)
+            const int gq = pg[i] - g_lo;  // = (q0 + i) mod gpt, without a division per pair
+            if (i > 0 && gq == 0) {  // a new tile (wave-uniform)
                 flush(cur_slot);
                 ++cur_slot;
                 cur = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
             }
             const float sc = scl[((first_tile + pslot[i]) * 16 + lane % 16) * gpt + (pg[i] - g_lo)];
-            const int kofs = 128 * (q % gpt);
+            const int kofs = 128 * gq;
             f32x4 prt = {0.0f, 0.0f, 0.0f, 0.0f};
             *reinterpret_cast<u32x4*>(tb + wr_lo) = wb[i][0];
             *reinterpret_cast<u32x4*>(tb + wr_hi) = wb[i][1];
@@ -357,7 +358,7 @@ __global__ void __launch_bounds__(kThreads) pass_kernel(const PassParams p) {
                 }
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    const float s_r = p.per_token ? sc : __fmul_rn(sc, xsc[(4 * (lane / 16) + r) * gpt + q % gpt]);
+                    const float s_r = p.per_token ? sc : __fmul_rn(sc, xsc[(4 * (lane / 16) + r) * gpt + gq]);
                     cur[r] = __builtin_fmaf(static_cast<float>(acc[r]), s_r, cur[r]);
                 }
                 continue;
