@@ -409,6 +409,16 @@ def main():
         log(f"C5 w8g M=16 stack: {ms_c5:.3f} ms/pass, {gbs_c5:.0f} GB/s ({gbs_c5 / PEAK['hbm_gbs'] * 100:.1f}% of HBM)")
         extra["c5_w8g_m16"] = {"ms_per_pass": round(ms_c5, 4), "gbs": round(gbs_c5, 1),
                                "frac_hbm": round(gbs_c5 / PEAK["hbm_gbs"], 4), "bytes_per_pass": C5_BYTES}
+        # the same pass on stream-layout weights (made once at load; same bits, no LDS transpose in the kernels)
+        slayers = [(sm.w8g_make_stream_layout(a, True), b, sm.w8g_make_stream_layout(c, False), d)
+                   for a, b, c, d in layers]
+        ms_c5s = timed(torch, lambda: (xs_.copy_(xs0), sm.mlp_stack_stream(xs_, slayers, y=ys)), 20, 3, stream)
+        gbs_c5s = C5_BYTES / (ms_c5s * 1e-3) / 1e9
+        log(f"C5 w8g M=16 stack, stream layout: {ms_c5s:.3f} ms/pass, {gbs_c5s:.0f} GB/s")
+        extra["c5_w8g_m16_stream_layout"] = {"ms_per_pass": round(ms_c5s, 4), "gbs": round(gbs_c5s, 1),
+                                             "frac_hbm": round(gbs_c5s / PEAK["hbm_gbs"], 4)}
+        del slayers
+        torch.cuda.empty_cache()
         # ---- the load-time packer ----
         g = torch.Generator(device="cuda").manual_seed(7)
         src = (torch.randn(I, H, generator=g, device="cuda") * 0.02).half()

@@ -871,12 +871,12 @@ StackZones stack_zones(int kind, std::size_t t, std::size_t hidden, std::size_t 
 void run_stack(const StackZones& z, int kind, std::size_t layers, std::size_t t, std::size_t hidden, std::size_t inter,
                void* x, const int8_t* const* w_gate_up, const float* const* s_gate_up, const int8_t* const* w_down,
                const float* const* s_down, float* y, double eps, char* ws, hipStream_t st, const void* const* img_gate_up,
-               const void* const* img_down) {
+               const void* const* img_down, bool stream_w) {
     if (z.form == StackZones::SMALL_W8G) {
         // three launches per layer: whole-K gate/up tiles per CU, the down multiply in K-parts, the finish pass
         for (std::size_t l = 0; l < layers; ++l)
             launch_small_layer(z.plan, t, hidden, inter, x, w_gate_up[l], s_gate_up[l], w_down[l], s_down[l], ws + z.off_h,
-                               reinterpret_cast<float*>(ws + z.off_p), y, l + 1 < layers ? x : nullptr, eps, st);
+                               reinterpret_cast<float*>(ws + z.off_p), y, l + 1 < layers ? x : nullptr, eps, st, stream_w);
         return;
     }
     if (z.form == StackZones::SMALL_Q8) {
@@ -1144,6 +1144,40 @@ int32_t sepal_hip_mlp_stack_images(int32_t kind, size_t layers, size_t t, size_t
         Lease ws(z.end, st);
         run_stack(z, kind, layers, t, hidden, inter, x, w_gate_up, s_gate_up, w_down, s_down, y, eps, ws.base(), st,
                   z.form == StackZones::GENERAL ? img_gate_up : nullptr, z.form == StackZones::GENERAL ? img_down : nullptr);
+    });
+}
+
+size_t sepal_hip_w8g_stream_layout_bytes(size_t n, size_t k) {
+    return n != 0 && k != 0 && n % 16 == 0 && k % 128 == 0 ? n * k : 0;
+}
+
+int32_t sepal_hip_w8g_make_stream_layout(const int8_t* w, size_t ld_w, size_t n, size_t k, int32_t interleave, void* out,
+                                         size_t out_bytes, void* stream) {
+    return guarded([&] {
+        require(w != nullptr && out != nullptr, "w8g_make_stream_layout: null pointer");
+        require(n != 0 && k != 0 && n % 16 == 0 && k % 128 == 0, "w8g_make_stream_layout: N must be a multiple of 16 and K of 128");
+        require(!interleave || n % 128 == 0, "w8g_make_stream_layout: the gate/up interleave takes N a multiple of 128");
+        require(ld_w >= k && ld_w % 16 == 0 && aligned16(w), "w8g_make_stream_layout: W rows of whole 16 bytes (16-byte aligned)");
+        require(out_bytes >= n * k && aligned16(out), "w8g_make_stream_layout: out must hold n * k bytes, 16-byte aligned");
+        launch_stream_layout(w, ld_w, n, k, interleave != 0, static_cast<int8_t*>(out), as_stream(stream));
+    });
+}
+
+int32_t sepal_hip_mlp_stack_stream(size_t layers, size_t t, size_t hidden, size_t inter, void* x,
+                                   const int8_t* const* w_gate_up, const float* const* s_gate_up, const int8_t* const* w_down,
+                                   const float* const* s_down, float* y, double eps, void* stream) {
+    return guarded([&] {
+        check_stack_args(0, hidden, inter, x, w_gate_up, s_gate_up, w_down, s_down, y, 128);
+        if (layers == 0 || t == 0) return;
+        for (std::size_t l = 0; l < layers; ++l)
+            require(aligned16(w_gate_up[l]) && aligned16(w_down[l]), "mlp_stack_stream: weights must be 16-byte aligned");
+        const hipStream_t st = as_stream(stream);
+        const StackZones z = stack_zones(0, t, hidden, inter, 128);
+        require(z.form == StackZones::SMALL_W8G,
+                "mlp_stack_stream: the stream layout is read by the M <= 16 passes only (T <= 16 at a shape they take)");
+        Lease ws(z.end, st);
+        run_stack(z, 0, layers, t, hidden, inter, x, w_gate_up, s_gate_up, w_down, s_down, y, eps, ws.base(), st, nullptr,
+                  nullptr, true);
     });
 }
 

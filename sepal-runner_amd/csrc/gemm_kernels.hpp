@@ -152,10 +152,16 @@ bool small_q8_group_sums(const GemmArgs& a, hipStream_t stream);
 bool small_gemm_plan_q8_parts(const GemmArgs& a, SmallGemmPlan& plan);
 void launch_small_gemm_q8_parts(const GemmArgs& a, const SmallGemmPlan& plan, hipStream_t stream);
 // x bf16 [t, hidden] -> h binary16 [t, inter] -> part float32 [parts][t][hidden] -> y float32 [t, hidden] and, when
-// xn is set, xn bf16 [t, hidden] = RMSNorm(y) (cpu-q8 order, identity weight).
+// xn is set, xn bf16 [t, hidden] = RMSNorm(y) (cpu-q8 order, identity weight). stream_w: w_gu and w_d in the stream
+// layout (launch_stream_layout; the same bits).
 void launch_small_layer(const SmallStackPlan& plan, std::size_t t, std::size_t hidden, std::size_t inter, const void* x,
                         const std::int8_t* w_gu, const float* s_gu, const std::int8_t* w_d, const float* s_d, void* h,
-                        float* part, float* y, void* xn, double eps, hipStream_t stream);
+                        float* part, float* y, void* xn, double eps, hipStream_t stream, bool stream_w = false);
+// The stream layout of an int8 [n, k] weight matrix for the M <= 16 passes (n a multiple of 16, k of 128; n * k
+// bytes): each (16-row tile, 128-value group) pair's 2 KB contiguous, in the MFMA operand order of the pass kernels.
+// interleave: the gate/up matrix (tiles of 8 gate and 8 up rows, the 64-row interleave).
+void launch_stream_layout(const std::int8_t* w, std::size_t ld_w, std::size_t n, std::size_t k, bool interleave, std::int8_t* out,
+                          hipStream_t stream);
 // The gpu-q8w form: int8 x [t, hidden] with its scales (one per token, or per 128 columns) -> H float32 [t, inter]
 // (per token also hmax [t, ceil(inter / 8 / tiles_per_block)], the partial row maxima of |H|) -> part -> y; when xq_next is
 // set, the next layer's input bf16(RMSNorm(y)) goes to xn (bf16) and, quantized, to xq_next / xs_next.

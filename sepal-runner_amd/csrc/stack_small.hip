@@ -165,7 +165,9 @@ __device__ __forceinline__ void stage_h_q8(const PassParams& p, unsigned char* l
 // block's scales in LDS and raise an LDS flag; waves kLoaders .. 15 (the workers) issue every weight load of their
 // pairs at once, wait for the flag, and multiply. The weights are in flight while the scales arrive, and no worker's
 // load issue (which stalls when the memory queues are full) holds up a barrier.
-template <int XT, bool SWIGLU, int YT>
+// STREAM: the weights in the stream layout (make_stream_layout): each (tile, group) pair's 2 KB contiguous, already in
+// the MFMA operand order, so a pair is two 1 KB loads and needs no LDS transpose.
+template <int XT, bool SWIGLU, int YT, bool STREAM = false>
 __global__ void __launch_bounds__(kThreads) pass_kernel(const PassParams p) {
     extern __shared__ __align__(16) unsigned char lds[];
     __shared__ unsigned ready;
@@ -292,12 +294,21 @@ __global__ void __launch_bounds__(kThreads) pass_kernel(const PassParams p) {
         }
 #pragma unroll
         for (int i = 0; i < kPairs; ++i) {
-            const signed char* src = wrow[0] + 128 * pg[i];
+            if constexpr (STREAM) {
+                // pair (tile, group): 2 KB at (tile * groups + group) * 2048, half h at + 1024 h, lane l's 16 bytes at
+                // + 16 l: weight row tile_row(tile, l % 16), k = 128 group + 64 h + 16 (l / 16) .. + 15
+                const std::size_t blk = static_cast<std::size_t>(tile0 + first_tile + pslot[i]) * groups + pg[i];
+                const signed char* src = p.w + blk * 2048 + 16 * lane;
+                wb[i][0] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src));
+                wb[i][1] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + 1024));
+            } else {
+                const signed char* src = wrow[0] + 128 * pg[i];
 #pragma unroll
-            for (int j = 1; j < kSlots; ++j)
-                if (pslot[i] == j) src = wrow[j] + 128 * pg[i];
-            wb[i][0] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src));
-            wb[i][1] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + kRowStep * p.ld_w));
+                for (int j = 1; j < kSlots; ++j)
+                    if (pslot[i] == j) src = wrow[j] + 128 * pg[i];
+                wb[i][0] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src));
+                wb[i][1] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + kRowStep * p.ld_w));
+            }
         }
         // ---- X and the scales are staged ----
         while (__hip_atomic_load(&ready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < static_cast<unsigned>(kLoaders))
@@ -330,8 +341,16 @@ __global__ void __launch_bounds__(kThreads) pass_kernel(const PassParams p) {
             const float sc = scl[((first_tile + pslot[i]) * 16 + lane % 16) * gpt + (pg[i] - g_lo)];
             const int kofs = 128 * gq;
             f32x4 prt = {0.0f, 0.0f, 0.0f, 0.0f};
-            *reinterpret_cast<u32x4*>(tb + wr_lo) = wb[i][0];
-            *reinterpret_cast<u32x4*>(tb + wr_hi) = wb[i][1];
+            if constexpr (!STREAM) {
+                *reinterpret_cast<u32x4*>(tb + wr_lo) = wb[i][0];
+                *reinterpret_cast<u32x4*>(tb + wr_hi) = wb[i][1];
+            }
+            // the MFMA operand of half h: lane l's 16 bytes of weight row l % 16, k = 64 h + 16 (l / 16) .. + 15
+            const auto wop = [&](int h) __attribute__((always_inline)) -> u32x4 {
+                if constexpr (STREAM) return wb[i][h];
+                const int rr = lane % 16, cc = 4 * h + lane / 16;
+                return *reinterpret_cast<const u32x4*>(tb + rr * 128 + ((cc + rr / 2) % 8) * 16);
+            };
             if constexpr (Q8) {
                 // the int8 weights go to the MFMA as they are: the exact int32 group sum, then the cpu-q8 float chain
                 // (runner/src/cpu/gemm_kernels_avx512.cpp:67-115): t = fma(f_g, ws_g, t) with one scale per token
@@ -339,8 +358,7 @@ __global__ void __launch_bounds__(kThreads) pass_kernel(const PassParams p) {
                 i32x4 acc = {0, 0, 0, 0};
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
-                    const int rr = lane % 16, cc = 4 * h + lane / 16;
-                    const u32x4 wv = *reinterpret_cast<const u32x4*>(tb + rr * 128 + ((cc + rr / 2) % 8) * 16);
+                    const u32x4 wv = wop(h);
                     const u32x4 a = *reinterpret_cast<const u32x4*>(lds + (lane % 16) * xpitch + kofs + 64 * h + 16 * (lane / 16));
                     acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i32x4, a), __builtin_bit_cast(i32x4, wv), acc, 0, 0, 0);
                 }
@@ -365,8 +383,7 @@ __global__ void __launch_bounds__(kThreads) pass_kernel(const PassParams p) {
             }
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
-                const int rr = lane % 16, cc = 4 * h + lane / 16;
-                const u32x4 wv = *reinterpret_cast<const u32x4*>(tb + rr * 128 + ((cc + rr / 2) % 8) * 16);
+                const u32x4 wv = wop(h);
                 unsigned o[8];
 #pragma unroll
                 for (int c = 0; c < 4; ++c) {
@@ -453,6 +470,25 @@ __global__ void __launch_bounds__(kThreads) pass_kernel(const PassParams p) {
             y[(static_cast<std::size_t>(part) * p.t + r) * p.ld_y + col] = sum_tile(tl, r * 16 + c);
         }
     }
+}
+
+// The stream layout of an int8 [n, k] weight matrix for the M <= 16 passes (n a multiple of 16, k of 128): pair (tile,
+// group) is 2 KB at (tile * (k / 128) + group) * 2048; its half h, at + 1024 h, holds for lane l the 16 bytes of weight
+// row tile_row(tile, l % 16) at k = 128 group + 64 h + 16 (l / 16) .. + 15 (the MFMA operand the pass kernels form
+// through their LDS transpose). interleave: gate/up tiles of 8 gate and the 8 up rows of the same features. One thread
+// moves one 16-byte item.
+__global__ void __launch_bounds__(256) stream_layout_kernel(const signed char* __restrict__ w, std::size_t ld_w, int n, int k,
+                                                            int interleave, signed char* __restrict__ out) {
+    const std::size_t id = static_cast<std::size_t>(blockIdx.x) * 256 + threadIdx.x;
+    const int groups = k / 128;
+    const std::size_t items = static_cast<std::size_t>(n / 16) * groups * 128;
+    if (id >= items) return;
+    const int l = static_cast<int>(id % 64), h = static_cast<int>((id / 64) % 2);
+    const std::size_t blk = id / 128;
+    const int g = static_cast<int>(blk % groups), tile = static_cast<int>(blk / groups);
+    const int row = interleave ? tile_row<true>(tile, l % 16) : tile_row<false>(tile, l % 16);
+    const u32x4 v = *reinterpret_cast<const u32x4*>(w + static_cast<std::size_t>(row) * ld_w + 128 * g + 64 * h + 16 * (l / 16));
+    *reinterpret_cast<u32x4*>(out + id * 16) = v;
 }
 
 // y[r][c] = sum over the P parts (in order) of P[part][r][c]; then, if xn is set, xn[r] = bf16(RMSNorm(y[r])) with the
@@ -696,7 +732,7 @@ bool small_stack_plan(std::size_t t, std::size_t hidden, std::size_t inter, Smal
 
 void launch_small_layer(const SmallStackPlan& plan, std::size_t t, std::size_t hidden, std::size_t inter, const void* x,
                         const std::int8_t* w_gu, const float* s_gu, const std::int8_t* w_d, const float* s_d, void* h,
-                        float* part, float* y, void* xn, double eps, hipStream_t stream) {
+                        float* part, float* y, void* xn, double eps, hipStream_t stream, bool stream_w) {
     using namespace stack;
     // gate/up: x bf16 [t, hidden] -> H binary16 [t, inter]
     PassParams a{};
@@ -715,10 +751,10 @@ void launch_small_layer(const SmallStackPlan& plan, std::size_t t, std::size_t h
     a.parts = 1;
     a.per_block = plan.tiles_per_block;
     a.blocks_per_part = (a.tiles + a.per_block - 1) / a.per_block;
-    const auto ka = pass_kernel<SEPAL_HIP_BF16, true, SEPAL_HIP_F16>;
-    static std::size_t raised_a = 0;
+    const auto ka = stream_w ? pass_kernel<SEPAL_HIP_BF16, true, SEPAL_HIP_F16, true> : pass_kernel<SEPAL_HIP_BF16, true, SEPAL_HIP_F16>;
+    static std::size_t raised_a[2] = {0, 0};
     const std::size_t lds_a = pass_lds(2 * hidden);
-    raise_lds(ka, lds_a, raised_a);
+    raise_lds(ka, lds_a, raised_a[stream_w ? 1 : 0]);
     ka<<<dim3(a.blocks_per_part), dim3(kThreads), lds_a, stream>>>(a);
     check_launch("small-M stack gate/up launch");
     // down: H [t, inter] -> P [parts][t][hidden]
@@ -738,11 +774,11 @@ void launch_small_layer(const SmallStackPlan& plan, std::size_t t, std::size_t h
     d.parts = plan.parts;
     d.per_block = plan.units_per_block;
     d.blocks_per_part = (d.tiles + d.per_block - 1) / d.per_block;
-    const auto kd = pass_kernel<SEPAL_HIP_F16, false, SEPAL_HIP_F32>;
-    static std::size_t raised_d = 0;
+    const auto kd = stream_w ? pass_kernel<SEPAL_HIP_F16, false, SEPAL_HIP_F32, true> : pass_kernel<SEPAL_HIP_F16, false, SEPAL_HIP_F32>;
+    static std::size_t raised_d[2] = {0, 0};
     const std::size_t gpt = (inter / 128 + plan.parts - 1) / plan.parts;
     const std::size_t lds_d = pass_lds(gpt * 256);
-    raise_lds(kd, lds_d, raised_d);
+    raise_lds(kd, lds_d, raised_d[stream_w ? 1 : 0]);
     kd<<<dim3(d.parts * d.blocks_per_part), dim3(kThreads), lds_d, stream>>>(d);
     check_launch("small-M stack down launch");
     // y = sum of the parts; next layer's input
@@ -750,6 +786,16 @@ void launch_small_layer(const SmallStackPlan& plan, std::size_t t, std::size_t h
     check_launch("small-M stack finish launch");
 }
 
+
+void launch_stream_layout(const std::int8_t* w, std::size_t ld_w, std::size_t n, std::size_t k, bool interleave, std::int8_t* out,
+                          hipStream_t stream) {
+    if (n % 16 != 0 || k % 128 != 0 || n == 0 || k == 0) throw LaunchError("stream layout: n must be a multiple of 16 and k of 128");
+    const std::size_t items = n / 16 * (k / 128) * 128;
+    stack::stream_layout_kernel<<<dim3(static_cast<unsigned>((items + 255) / 256)), dim3(256), 0, stream>>>(
+        reinterpret_cast<const signed char*>(w), ld_w, static_cast<int>(n), static_cast<int>(k), interleave ? 1 : 0,
+        reinterpret_cast<signed char*>(out));
+    check_launch("stream layout launch");
+}
 
 void launch_small_layer_q8(const SmallStackPlan& plan, std::size_t t, std::size_t hidden, std::size_t inter,
                            const std::int8_t* xq, const float* xs, bool per_token, const std::int8_t* w_gu, const float* s_gu,

@@ -76,6 +76,10 @@ def library() -> C.CDLL:
         L.sepal_hip_w8g_image_bytes.restype = sz
         L.sepal_hip_w8g_make_image.argtypes = [vp, sz, sz, sz, i32, vp, sz, vp]
         L.sepal_hip_mlp_stack_images.argtypes = [i32, sz, sz, sz, sz, vp, vp, vp, vp, vp, vp, vp, vp, d, vp]
+        L.sepal_hip_w8g_stream_layout_bytes.argtypes = [sz, sz]
+        L.sepal_hip_w8g_stream_layout_bytes.restype = sz
+        L.sepal_hip_w8g_make_stream_layout.argtypes = [vp, sz, sz, sz, i32, vp, sz, vp]
+        L.sepal_hip_mlp_stack_stream.argtypes = [sz, sz, sz, sz, vp, vp, vp, vp, vp, vp, d, vp]
         for name in ("sepal_hip_quantize_group_s8", "sepal_hip_quantize_gate_up_s8", "sepal_hip_gemm_w8g",
                      "sepal_hip_quantize_rows_s8", "sepal_hip_gemm_q8", "sepal_hip_q8_group_sums",
                      "sepal_hip_rmsnorm_rows", "sepal_hip_float_to_bf16", "sepal_hip_mlp_stack",
@@ -84,7 +88,8 @@ def library() -> C.CDLL:
                      "sepal_hip_weight_fingerprint", "sepal_hip_packed_save", "sepal_hip_packed_load",
                      "sepal_hip_s8_quantize_rows", "sepal_hip_gemm_s8", "sepal_hip_gemm_w8a16", "sepal_hip_gemm_q8y",
                      "sepal_hip_column_absmax", "sepal_hip_channel_stats", "sepal_hip_release_workspace",
-                     "sepal_hip_w8g_make_image", "sepal_hip_mlp_stack_images"):
+                     "sepal_hip_w8g_make_image", "sepal_hip_mlp_stack_images", "sepal_hip_w8g_make_stream_layout",
+                     "sepal_hip_mlp_stack_stream"):
             getattr(L, name).restype = i32
         L.sepal_hip_gemm_w8g_supports.restype = i32
         L.sepal_hip_gemm_s8_supports.restype = i32
@@ -364,6 +369,36 @@ def w8g_make_image(w, x_dtype, stream=None):
     _check(library().sepal_hip_w8g_make_image(_ptr(w), _ld(w), n, k, _type_of(torch.empty(0, dtype=x_dtype)), _ptr(img),
                                               nbytes, _stream(stream)))
     return img
+
+
+def w8g_make_stream_layout(w, interleave: bool, stream=None):
+    """The load-time stream layout of int8 weights w [N, K] for the M <= 16 w8g stack (interleave: a gate/up matrix in
+    the 64-row interleave). An int8 device tensor of N * K bytes."""
+    torch = _torch()
+    n, k = w.shape
+    nbytes = library().sepal_hip_w8g_stream_layout_bytes(n, k)
+    if nbytes == 0:
+        raise SepalHipInvalid("the stream layout takes N a multiple of 16 and K of 128")
+    out = torch.empty(nbytes, dtype=torch.int8, device=w.device)
+    _check(library().sepal_hip_w8g_make_stream_layout(_ptr(w), _ld(w), n, k, 1 if interleave else 0, _ptr(out), nbytes,
+                                                      _stream(stream)))
+    return out
+
+
+def mlp_stack_stream(x, layers, y=None, eps: float = 1e-6, stream=None):
+    """mlp_stack kind 0 (w8g) at T <= 16 on stream-layout weights: layers is a list of (w_gate_up_stream, s_gate_up,
+    w_down_stream, s_down), the weights made by w8g_make_stream_layout. Same bits as mlp_stack."""
+    torch = _torch()
+    t, hidden = x.shape
+    inter = layers[0][3].shape[1] * 128  # the down scales: [hidden, inter / 128]
+    y = torch.empty(t, hidden, dtype=torch.float32, device=x.device) if y is None else y
+
+    def arr(i):
+        return (C.c_void_p * len(layers))(*[e[i].data_ptr() for e in layers])
+
+    _check(library().sepal_hip_mlp_stack_stream(len(layers), t, hidden, inter, _ptr(x), arr(0), arr(1), arr(2), arr(3),
+                                                _ptr(y), eps, _stream(stream)))
+    return y
 
 
 def mlp_stack_images(kind: int, x, layers, images, y=None, eps: float = 1e-6, stream=None):
