@@ -412,7 +412,7 @@ def main():
         # the same pass on stream-layout weights (made once at load; same bits, no LDS transpose in the kernels)
         slayers = [(sm.w8g_make_stream_layout(a, True), b, sm.w8g_make_stream_layout(c, False), d)
                    for a, b, c, d in layers]
-        ms_c5s = timed(torch, lambda: (xs_.copy_(xs0), sm.mlp_stack_stream(xs_, slayers, y=ys)), 20, 3, stream)
+        ms_c5s = timed(torch, lambda: (xs_.copy_(xs0), sm.mlp_stack_stream(0, xs_, slayers, y=ys)), 20, 3, stream)
         gbs_c5s = C5_BYTES / (ms_c5s * 1e-3) / 1e9
         log(f"C5 w8g M=16 stack, stream layout: {ms_c5s:.3f} ms/pass, {gbs_c5s:.0f} GB/s")
         extra["c5_w8g_m16_stream_layout"] = {"ms_per_pass": round(ms_c5s, 4), "gbs": round(gbs_c5s, 1),
@@ -486,6 +486,13 @@ def main():
         extra["c5_q8w_m16"] = {"ms_per_pass": round(ms_c4_16, 4), "gbs": round(gbs_q16, 1),
                                "frac_hbm": round(gbs_q16 / PEAK["hbm_gbs"], 4)}
         log(f"C5 q8w M=16 stack: {ms_c4_16:.3f} ms/pass, {gbs_q16:.0f} GB/s")
+        sq = [(sm.w8g_make_stream_layout(a, True), b, sm.w8g_make_stream_layout(c, False), d) for a, b, c, d in qlayers]
+        ms_q16s = timed(torch, lambda: (xs_.copy_(xs0), sm.mlp_stack_stream(1, xs_, sq, y=ys, act_block=0)), 20, 3, stream)
+        gbs_q16s = C5_BYTES / (ms_q16s * 1e-3) / 1e9
+        extra["c5_q8w_m16_stream_layout"] = {"ms_per_pass": round(ms_q16s, 4), "gbs": round(gbs_q16s, 1),
+                                             "frac_hbm": round(gbs_q16s / PEAK["hbm_gbs"], 4)}
+        log(f"C5 q8w M=16 stack, stream layout: {ms_q16s:.3f} ms/pass, {gbs_q16s:.0f} GB/s")
+        del sq
         del qlayers
         torch.cuda.empty_cache()
         # ---- the model's other int8 weight groups (dn_in / attn_in [12288 or 10240, 2560], attn_out [2560, 4096]):

@@ -298,24 +298,24 @@ SEPAL_HIP_API int32_t sepal_hip_mlp_stack_images(int32_t kind, size_t layers, si
                                                  const void* const* img_gate_up, const void* const* img_down, float* y,
                                                  double eps, void* stream);
 
-/* Load-time stream layout of the M <= 16 w8g stack's weights. At T <= 16 each layer streams its int8 weights once through
+/* Load-time stream layout of the M <= 16 stack's weights (w8g and q8w: the same int8 format). At T <= 16 each layer streams its int8 weights once through
  * the pass kernels, in (16-row tile, 128-value group) pairs of 2 KB; in the row-major packed format a pair's 16 rows
  * are 16 separate 128-byte lines, which the kernels pass through LDS into the MFMA operand order. The stream layout
  * stores each pair's 2 KB contiguous in that order (the same n * k bytes, permuted), so the kernels load it as two
  * 1 KB runs and skip the transpose. sepal_hip_w8g_stream_layout_bytes: n * k (0 unless n % 16 == 0 and k % 128 == 0).
  * sepal_hip_w8g_make_stream_layout: w [n, ld_w] into out; interleave 1 for a gate/up matrix (the 64-row interleave,
- * n a multiple of 128), 0 for a down matrix. sepal_hip_mlp_stack_stream: sepal_hip_mlp_stack kind 0 (w8g) on the stream
- * layouts of every layer's gate/up and down weights (the scales as they are), with the same bits; it runs the M <= 16
- * form only and refuses a T or shape that form does not take. No counterpart in the reference (its decode path reads
+ * n a multiple of 128), 0 for a down matrix. sepal_hip_mlp_stack_stream: sepal_hip_mlp_stack (kind 0 w8g or 1 q8w,
+ * act_block as there) on the stream layouts of every layer's gate/up and down weights (the scales as they are), with
+ * the same bits; it runs the M <= 16 forms only and refuses a T or shape they do not take. No counterpart in the reference (its decode path reads
  * the packed format, runner/cuda/src/gemm_simt_kernels.cu:303-332); for callers that keep weights resident for
  * decode. */
 SEPAL_HIP_API size_t sepal_hip_w8g_stream_layout_bytes(size_t n, size_t k);
 SEPAL_HIP_API int32_t sepal_hip_w8g_make_stream_layout(const int8_t* w, size_t ld_w, size_t n, size_t k, int32_t interleave,
                                                        void* out, size_t out_bytes, void* stream);
-SEPAL_HIP_API int32_t sepal_hip_mlp_stack_stream(size_t layers, size_t t, size_t hidden, size_t inter, void* x,
-                                                 const int8_t* const* w_gate_up, const float* const* s_gate_up,
+SEPAL_HIP_API int32_t sepal_hip_mlp_stack_stream(int32_t kind, size_t layers, size_t t, size_t hidden, size_t inter,
+                                                 void* x, const int8_t* const* w_gate_up, const float* const* s_gate_up,
                                                  const int8_t* const* w_down, const float* const* s_down, float* y,
-                                                 double eps, void* stream);
+                                                 size_t act_block, double eps, void* stream);
 
 /* sepal_hip_mlp_stack with no allocation of any kind: the same arguments, work and bits, with every scratch buffer in
  * a static device array of 64 MiB that the library holds on each device it runs on until the process ends (the split-K

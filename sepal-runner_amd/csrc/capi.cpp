@@ -889,7 +889,7 @@ void run_stack(const StackZones& z, int kind, std::size_t layers, std::size_t t,
             launch_small_layer_q8(z.plan, t, hidden, inter, qx, sx, z.per_token, w_gate_up[l], s_gate_up[l], w_down[l],
                                   s_down[l], reinterpret_cast<float*>(ws + z.off_h), reinterpret_cast<float*>(ws + z.off_hmax),
                                   reinterpret_cast<float*>(ws + z.off_p), y, l + 1 < layers ? qx : nullptr, sx,
-                                  l + 1 < layers ? x : nullptr, eps, st);
+                                  l + 1 < layers ? x : nullptr, eps, st, stream_w);
         return;
     }
     void* h = ws + z.off_h;
@@ -1163,20 +1163,21 @@ int32_t sepal_hip_w8g_make_stream_layout(const int8_t* w, size_t ld_w, size_t n,
     });
 }
 
-int32_t sepal_hip_mlp_stack_stream(size_t layers, size_t t, size_t hidden, size_t inter, void* x,
+int32_t sepal_hip_mlp_stack_stream(int32_t kind, size_t layers, size_t t, size_t hidden, size_t inter, void* x,
                                    const int8_t* const* w_gate_up, const float* const* s_gate_up, const int8_t* const* w_down,
-                                   const float* const* s_down, float* y, double eps, void* stream) {
+                                   const float* const* s_down, float* y, size_t act_block, double eps, void* stream) {
     return guarded([&] {
-        check_stack_args(0, hidden, inter, x, w_gate_up, s_gate_up, w_down, s_down, y, 128);
+        require(kind == 0 || kind == 1, "mlp_stack_stream: kind must be 0 (w8g) or 1 (q8w)");
+        check_stack_args(kind, hidden, inter, x, w_gate_up, s_gate_up, w_down, s_down, y, act_block);
         if (layers == 0 || t == 0) return;
         for (std::size_t l = 0; l < layers; ++l)
             require(aligned16(w_gate_up[l]) && aligned16(w_down[l]), "mlp_stack_stream: weights must be 16-byte aligned");
         const hipStream_t st = as_stream(stream);
-        const StackZones z = stack_zones(0, t, hidden, inter, 128);
-        require(z.form == StackZones::SMALL_W8G,
+        const StackZones z = stack_zones(kind, t, hidden, inter, act_block);
+        require(z.form == StackZones::SMALL_W8G || z.form == StackZones::SMALL_Q8,
                 "mlp_stack_stream: the stream layout is read by the M <= 16 passes only (T <= 16 at a shape they take)");
         Lease ws(z.end, st);
-        run_stack(z, 0, layers, t, hidden, inter, x, w_gate_up, s_gate_up, w_down, s_down, y, eps, ws.base(), st, nullptr,
+        run_stack(z, kind, layers, t, hidden, inter, x, w_gate_up, s_gate_up, w_down, s_down, y, eps, ws.base(), st, nullptr,
                   nullptr, true);
     });
 }

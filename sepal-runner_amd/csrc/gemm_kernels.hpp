@@ -164,10 +164,12 @@ void launch_stream_layout(const std::int8_t* w, std::size_t ld_w, std::size_t n,
                           hipStream_t stream);
 // The gpu-q8w form: int8 x [t, hidden] with its scales (one per token, or per 128 columns) -> H float32 [t, inter]
 // (per token also hmax [t, ceil(inter / 8 / tiles_per_block)], the partial row maxima of |H|) -> part -> y; when xq_next is
-// set, the next layer's input bf16(RMSNorm(y)) goes to xn (bf16) and, quantized, to xq_next / xs_next.
+// set, the next layer's input bf16(RMSNorm(y)) goes to xn (bf16) and, quantized, to xq_next / xs_next. stream_w: the
+// weights in the stream layout, as for launch_small_layer.
 void launch_small_layer_q8(const SmallStackPlan& plan, std::size_t t, std::size_t hidden, std::size_t inter,
                            const std::int8_t* xq, const float* xs, bool per_token, const std::int8_t* w_gu, const float* s_gu,
                            const std::int8_t* w_d, const float* s_d, float* h, float* hmax, float* part, float* y,
-                           std::int8_t* xq_next, float* xs_next, void* xn, double eps, hipStream_t stream);
+                           std::int8_t* xq_next, float* xs_next, void* xn, double eps, hipStream_t stream,
+                           bool stream_w = false);
 
 } // namespace sepal::hip

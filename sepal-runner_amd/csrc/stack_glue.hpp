@@ -31,8 +31,8 @@ StackZones stack_zones(int kind, std::size_t t, std::size_t hidden, std::size_t 
 
 // One call of the stack on the scratch at `ws` (laid out by stack_zones; its counter zone zero at rest). img_gate_up /
 // img_down (null, or one load-time weight image per layer): the w8g multiplies read them instead of widening the
-// weights into the workspace's images (z.img and z.img_dn are then 0). stream_w: the M <= 16 w8g form's weights are
-// in the stream layout (launch_stream_layout).
+// weights into the workspace's images (z.img and z.img_dn are then 0). stream_w: the M <= 16 forms' weights (w8g and
+// q8) are in the stream layout (launch_stream_layout).
 void run_stack(const StackZones& z, int kind, std::size_t layers, std::size_t t, std::size_t hidden, std::size_t inter,
                void* x, const int8_t* const* w_gate_up, const float* const* s_gate_up, const int8_t* const* w_down,
                const float* const* s_down, float* y, double eps, char* ws, hipStream_t st,

@@ -79,7 +79,7 @@ def library() -> C.CDLL:
         L.sepal_hip_w8g_stream_layout_bytes.argtypes = [sz, sz]
         L.sepal_hip_w8g_stream_layout_bytes.restype = sz
         L.sepal_hip_w8g_make_stream_layout.argtypes = [vp, sz, sz, sz, i32, vp, sz, vp]
-        L.sepal_hip_mlp_stack_stream.argtypes = [sz, sz, sz, sz, vp, vp, vp, vp, vp, vp, d, vp]
+        L.sepal_hip_mlp_stack_stream.argtypes = [i32, sz, sz, sz, sz, vp, vp, vp, vp, vp, vp, sz, d, vp]
         for name in ("sepal_hip_quantize_group_s8", "sepal_hip_quantize_gate_up_s8", "sepal_hip_gemm_w8g",
                      "sepal_hip_quantize_rows_s8", "sepal_hip_gemm_q8", "sepal_hip_q8_group_sums",
                      "sepal_hip_rmsnorm_rows", "sepal_hip_float_to_bf16", "sepal_hip_mlp_stack",
@@ -385,9 +385,9 @@ def w8g_make_stream_layout(w, interleave: bool, stream=None):
     return out
 
 
-def mlp_stack_stream(x, layers, y=None, eps: float = 1e-6, stream=None):
-    """mlp_stack kind 0 (w8g) at T <= 16 on stream-layout weights: layers is a list of (w_gate_up_stream, s_gate_up,
-    w_down_stream, s_down), the weights made by w8g_make_stream_layout. Same bits as mlp_stack."""
+def mlp_stack_stream(kind: int, x, layers, y=None, act_block: int = 128, eps: float = 1e-6, stream=None):
+    """mlp_stack (kind 0 w8g or 1 q8) at T <= 16 on stream-layout weights: layers is a list of (w_gate_up_stream,
+    s_gate_up, w_down_stream, s_down), the weights made by w8g_make_stream_layout. Same bits as mlp_stack."""
     torch = _torch()
     t, hidden = x.shape
     inter = layers[0][3].shape[1] * 128  # the down scales: [hidden, inter / 128]
@@ -396,8 +396,8 @@ def mlp_stack_stream(x, layers, y=None, eps: float = 1e-6, stream=None):
     def arr(i):
         return (C.c_void_p * len(layers))(*[e[i].data_ptr() for e in layers])
 
-    _check(library().sepal_hip_mlp_stack_stream(len(layers), t, hidden, inter, _ptr(x), arr(0), arr(1), arr(2), arr(3),
-                                                _ptr(y), eps, _stream(stream)))
+    _check(library().sepal_hip_mlp_stack_stream(kind, len(layers), t, hidden, inter, _ptr(x), arr(0), arr(1), arr(2),
+                                                arr(3), _ptr(y), act_block, eps, _stream(stream)))
     return y
 
 

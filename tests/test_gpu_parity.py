@@ -1044,24 +1044,25 @@ def test_mlp_stack_small_q8_full_size(sm, act):
     assert rel_rms(y, _oracle_stack(1, x, layers, act)) < 2e-3
 
 
+@pytest.mark.parametrize("kind,act_block", [(0, 128), (1, 0), (1, 128)])
 @pytest.mark.parametrize("t", [1, 5, 16])
-def test_mlp_stack_stream_layout(sm, t):
-    """The M <= 16 w8g stack on stream-layout weights (each (tile, group) pair's 2 KB contiguous in the MFMA operand
-    order, no LDS transpose) gives the same bits as on the packed weights, at the model's shape over three layers; a
-    T the M <= 16 form does not take is refused."""
-    say("mlp stack stream layout t", t)
-    rng = np.random.default_rng(300 + t)
-    layers = _stack_weights(sm, rng, 3, 2560, 9728, rule=0)
+def test_mlp_stack_stream_layout(sm, t, kind, act_block):
+    """The M <= 16 stack (w8g, and q8 with both activation-scale modes) on stream-layout weights (each (tile, group)
+    pair's 2 KB contiguous in the MFMA operand order, no LDS transpose) gives the same bits as on the packed weights, at
+    the model's shape over three layers; a T the M <= 16 forms do not take is refused."""
+    say("mlp stack stream layout t", t, "kind", kind, "act_block", act_block)
+    rng = np.random.default_rng(300 + t + 10 * kind + act_block)
+    layers = _stack_weights(sm, rng, 3, 2560, 9728, rule=1 if kind == 1 else 0)
     slayers = [(sm.w8g_make_stream_layout(wgu, True), sgu, sm.w8g_make_stream_layout(wd, False), sd)
                for wgu, sgu, wd, sd in layers]
     x = bf16_inputs(rng, (t, 2560))
     xa, xb = dev(x, torch.bfloat16), dev(x, torch.bfloat16)
-    ya = host(sm.mlp_stack(0, xa, layers))
-    yb = host(sm.mlp_stack_stream(xb, slayers))
+    ya = host(sm.mlp_stack(kind, xa, layers, act_block=act_block))
+    yb = host(sm.mlp_stack_stream(kind, xb, slayers, act_block=act_block))
     assert same_bits(ya, yb)
     assert torch.equal(xa, xb)
     with pytest.raises(sm.SepalHipInvalid):
-        sm.mlp_stack_stream(dev(bf16_inputs(rng, (17, 2560)), torch.bfloat16), slayers)
+        sm.mlp_stack_stream(kind, dev(bf16_inputs(rng, (17, 2560)), torch.bfloat16), slayers, act_block=act_block)
 
 
 def test_mlp_stack_small_path_full_size(sm):
