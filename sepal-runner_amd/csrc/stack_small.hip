@@ -530,9 +530,16 @@ __global__ void __launch_bounds__(1024) finish_kernel(const float* __restrict__ 
         float a = 0.0f;
         const int full = n / 32 * 32;
         if (tid < 32) {
-            // eight reads in flight, then their eight links of the chain, in order (one read at a time left the wave
-            // waiting on LDS latency at every link)
+            // forty reads in flight, then their forty links of the chain, in order (one LDS round trip per 1280
+            // columns instead of one per 256)
             int c = 0;
+            for (; c + 1280 <= full; c += 1280) {
+                float v[40];
+#pragma unroll
+                for (int u = 0; u < 40; ++u) v[u] = row_buf[c + 32 * u + L];
+#pragma unroll
+                for (int u = 0; u < 40; ++u) a = __builtin_fmaf(v[u], v[u], a);
+            }
             for (; c + 256 <= full; c += 256) {
                 float v[8];
 #pragma unroll
