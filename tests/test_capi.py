@@ -158,6 +158,34 @@ def test_q8_and_quantizer_refusals():
     assert L.sepal_hip_q8_group_sums(FAKE, 256, FAKE, 256, FAKE, 0, 128, 256, None) == sm.OK
 
 
+def test_stream_layout_refusals():
+    """The load-time stream layout and the stack that reads it refuse bad shapes, pointers and kinds before any device
+    work; the size query is n * k on the grid the layout takes and 0 off it."""
+    L = sm.library()
+    assert L.sepal_hip_w8g_stream_layout_bytes(19456, 2560) == 19456 * 2560
+    assert L.sepal_hip_w8g_stream_layout_bytes(100, 2560) == 0   # N not a multiple of 16
+    assert L.sepal_hip_w8g_stream_layout_bytes(64, 200) == 0     # K not a multiple of 128
+    ok = (FAKE, 256, 256, 256, 0, FAKE, 256 * 256, None)
+    bad = [
+        (None,) + ok[1:],                                  # null weights
+        ok[:2] + (100,) + ok[3:],                          # N not a multiple of 16
+        ok[:3] + (200,) + ok[4:],                          # K not a multiple of 128
+        ok[:1] + (128,) + ok[2:],                          # ld_w below K
+        ok[:2] + (144,) + ok[3:4] + (1,) + ok[5:6] + (144 * 256,) + ok[7:],  # gate/up interleave with N % 128 != 0
+        ok[:6] + (256 * 256 - 1,) + ok[7:],                # output too small
+        ok[:5] + (FAKE + 4,) + ok[6:],                     # output misaligned
+    ]
+    for args in bad:
+        assert L.sepal_hip_w8g_make_stream_layout(*args) == sm.EINVAL, args
+    one = lambda v: (C.c_void_p * 1)(v)
+    args = [0, 1, 4, 256, 512, FAKE, one(FAKE), one(FAKE), one(FAKE), one(FAKE), FAKE, 128, 1e-6, None]
+    assert L.sepal_hip_mlp_stack_stream(2, *args[1:]) == sm.EINVAL      # kind 2 has no stream form
+    assert "kind" in _err()
+    assert L.sepal_hip_mlp_stack_stream(0, *args[1:5], None, *args[6:]) == sm.EINVAL  # null x
+    assert L.sepal_hip_mlp_stack_stream(0, *args[1:6], one(FAKE + 4), *args[7:]) == sm.EINVAL  # misaligned weights
+    assert L.sepal_hip_mlp_stack_stream(0, 0, *args[2:]) == sm.OK       # no layers: a no-op
+
+
 def test_fused_producer_refusals():
     L = sm.library()
     # RMSNorm -> int8: block must be 128 or cols; cols a multiple of 128; misaligned q; eps positive

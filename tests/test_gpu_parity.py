@@ -1065,6 +1065,24 @@ def test_mlp_stack_stream_layout(sm, t, kind, act_block):
         sm.mlp_stack_stream(kind, dev(bf16_inputs(rng, (17, 2560)), torch.bfloat16), slayers, act_block=act_block)
 
 
+@pytest.mark.parametrize("hidden,inter,t", [(512, 1024, 3), (1024, 2048, 11), (768, 1536, 16)])
+@pytest.mark.parametrize("kind,act_block", [(0, 128), (1, 0), (1, 128)])
+def test_mlp_stack_stream_layout_shapes(sm, hidden, inter, t, kind, act_block):
+    """The stream layout at other plans of the M <= 16 forms (fewer groups per tile, other K-part counts, ragged T):
+    the same bits as the packed weights."""
+    say("mlp stack stream layout shapes", hidden, inter, t, kind, act_block)
+    rng = np.random.default_rng(hidden + t + kind + act_block)
+    layers = _stack_weights(sm, rng, 2, hidden, inter, rule=1 if kind == 1 else 0)
+    slayers = [(sm.w8g_make_stream_layout(wgu, True), sgu, sm.w8g_make_stream_layout(wd, False), sd)
+               for wgu, sgu, wd, sd in layers]
+    x = bf16_inputs(rng, (t, hidden))
+    xa, xb = dev(x, torch.bfloat16), dev(x, torch.bfloat16)
+    ya = host(sm.mlp_stack(kind, xa, layers, act_block=act_block))
+    yb = host(sm.mlp_stack_stream(kind, xb, slayers, act_block=act_block))
+    assert same_bits(ya, yb)
+    assert torch.equal(xa, xb)
+
+
 def test_mlp_stack_small_path_full_size(sm):
     """The M = 16 stack at the model's shape (H 2560, I 9728), two layers, against the oracle."""
     say("mlp stack small path full size")
