@@ -531,12 +531,15 @@ def main():
                                             rule=sm.RULE_RECIPROCAL)
         qwd, qsd = sm.quantize_group_s8((torch.randn(H, I, generator=g2, device="cuda") * 0.02).half(),
                                         rule=sm.RULE_RECIPROCAL)
+        wgu_sl, wd_sl = sm.w8g_make_stream_layout(wgu, True), sm.w8g_make_stream_layout(wd, False)
         for t_dec in (1, 16):
             xd = bf16_x(torch, t_dec, 9)
             hd = torch.empty(t_dec, I, dtype=torch.bfloat16, device="cuda")
             yd = torch.empty(t_dec, H, dtype=torch.float32, device="cuda")
             us_gu = graph_timed(torch, lambda st: sm.gemm_w8g(xd, wgu, sgu, y=hd, epilogue=sm.SWIGLU, stream=st))
             us_dn = graph_timed(torch, lambda st: sm.gemm_w8g(hd, wd, sd, y=yd, stream=st))
+            us_gu_s = graph_timed(torch, lambda st: sm.gemm_w8g_stream(xd, wgu_sl, sgu, y=hd, epilogue=sm.SWIGLU, stream=st))
+            us_dn_s = graph_timed(torch, lambda st: sm.gemm_w8g_stream(hd, wd_sl, sd, y=yd, stream=st))
             xq_d, xs_d = sm.quantize_rows_s8(xd, block=H)
             hq_d = torch.zeros(t_dec, I, dtype=torch.int8, device="cuda")
             hs_d = torch.ones(t_dec, 1, dtype=torch.float32, device="cuda")
@@ -547,11 +550,12 @@ def main():
             block_bytes = C5_BYTES / LAYERS
             dec[f"t{t_dec}"] = {"w8g_gate_up_us": round(us_gu, 2), "w8g_down_us": round(us_dn, 2),
                                 "w8g_block_gbs": round(block_bytes / ((us_gu + us_dn) * 1e-6) / 1e9, 1),
+                                "w8g_stream_layout_gate_up_us": round(us_gu_s, 2), "w8g_stream_layout_down_us": round(us_dn_s, 2),
                                 "q8_gate_up_us": round(us_qgu, 2), "q8_down_us": round(us_qdn, 2),
                                 "q8_block_gbs": round(block_bytes / ((us_qgu + us_qdn) * 1e-6) / 1e9, 1)}
         extra["decode_single_calls"] = dec
         log(f"decode single calls (GPU time per call): {dec}")
-        del qwgu, qsgu, qwd, qsd
+        del qwgu, qsgu, qwd, qsd, wgu_sl, wd_sl
         # ---- the per-channel int8 family (the reference's launch_gemm_s8 / launch_gemm_w8a16) at the MLP shapes ----
         s8 = {}
         for n_o, k_o in ((2 * I, H), (H, I)):

@@ -316,6 +316,18 @@ SEPAL_HIP_API int32_t sepal_hip_mlp_stack_stream(int32_t kind, size_t layers, si
                                                  void* x, const int8_t* const* w_gate_up, const float* const* s_gate_up,
                                                  const int8_t* const* w_down, const float* const* s_down, float* y,
                                                  size_t act_block, double eps, void* stream);
+/* Single multiplies at T <= 16 on stream-layout weights (a decode step calls gate/up and down one by one): the same
+ * arguments, rules and bits as sepal_hip_gemm_w8g / sepal_hip_gemm_q8 at config -1 on the packed matrix, with w the
+ * matrix's stream layout (made with interleave 1 for a SwiGLU gate/up matrix, 0 otherwise; no row stride). X of
+ * sepal_hip_gemm_w8g_stream is bf16 or binary16 with rows of whole 16 values, 16-byte aligned; sepal_hip_gemm_q8_stream
+ * writes float32. Each refuses T > 16 and a shape the M <= 16 kernels do not take. No counterpart in the reference
+ * (runner/cuda/src/gemm_simt_kernels.cu:303-332 reads the packed format). */
+SEPAL_HIP_API int32_t sepal_hip_gemm_w8g_stream(const void* x, int32_t x_type, size_t ld_x, const int8_t* w, const float* s,
+                                                size_t ld_s, void* y, int32_t y_type, size_t ld_y, size_t t, size_t n,
+                                                size_t k, int32_t epilogue, void* stream);
+SEPAL_HIP_API int32_t sepal_hip_gemm_q8_stream(const int8_t* xq, size_t ld_x, const float* xs, size_t ld_xs, size_t act_block,
+                                               const int8_t* w, const float* ws, size_t ld_ws, void* y, int32_t y_type,
+                                               size_t ld_y, size_t t, size_t n, size_t k, int32_t epilogue, void* stream);
 
 /* sepal_hip_mlp_stack with no allocation of any kind: the same arguments, work and bits, with every scratch buffer in
  * a static device array of 64 MiB that the library holds on each device it runs on until the process ends (the split-K

@@ -1182,6 +1182,81 @@ int32_t sepal_hip_mlp_stack_stream(int32_t kind, size_t layers, size_t t, size_t
     });
 }
 
+int32_t sepal_hip_gemm_w8g_stream(const void* x, int32_t x_type, size_t ld_x, const int8_t* w, const float* s, size_t ld_s,
+                                  void* y, int32_t y_type, size_t ld_y, size_t t, size_t n, size_t k, int32_t epilogue,
+                                  void* stream) {
+    return guarded([&] {
+        require(x_type == SEPAL_HIP_BF16 || x_type == SEPAL_HIP_F16, "gemm_w8g_stream: X must be bf16 or binary16");
+        require(valid_type(y_type), "gemm_w8g_stream: unknown output type");
+        require(epilogue == SEPAL_HIP_SWIGLU || y_type == SEPAL_HIP_F32, "gemm_w8g_stream: Store and Add write float32");
+        check_gemm_common("gemm_w8g_stream", x, ld_x, w, k, s, ld_s, y, ld_y, n, k, epilogue);
+        if (t == 0) return;
+        require(t <= 16, "gemm_w8g_stream: the stream layout is read by the M <= 16 kernels only (T <= 16)");
+        GemmArgs a;
+        a.x = x;
+        a.x_type = x_type;
+        a.ld_x = ld_x;
+        a.w = w;
+        a.ld_w = k;
+        a.w_stream = true;
+        a.s = s;
+        a.ld_s = ld_s;
+        a.y = y;
+        a.y_type = y_type;
+        a.ld_y = ld_y;
+        a.t = t;
+        a.n = n;
+        a.k = k;
+        a.epilogue = epilogue;
+        SmallGemmPlan plan;
+        require(small_gemm_plan(a, plan), "gemm_w8g_stream: a shape the M <= 16 kernels do not take");
+        const hipStream_t st = as_stream(stream);
+        Lease ws(kScratchOffset, st);
+        a.scratch = ws.base();
+        launch_small_gemm_w8g(a, plan, st);
+    });
+}
+
+int32_t sepal_hip_gemm_q8_stream(const int8_t* xq, size_t ld_x, const float* xs, size_t ld_xs, size_t act_block,
+                                 const int8_t* w, const float* ws, size_t ld_ws, void* y, int32_t y_type, size_t ld_y,
+                                 size_t t, size_t n, size_t k, int32_t epilogue, void* stream) {
+    return guarded([&] {
+        require(y_type == SEPAL_HIP_F32, "gemm_q8_stream: the M <= 16 q8 kernels write float32");
+        check_gemm_common("gemm_q8_stream", xq, ld_x, w, k, ws, ld_ws, y, ld_y, n, k, epilogue);
+        require(act_block == 128 || act_block == k, "gemm_q8_stream: act_block must be 128 or K");
+        require(xs != nullptr && ld_xs >= k / act_block, "gemm_q8_stream: activation scales missing or stride too small");
+        if (t == 0) return;
+        require(t <= 16, "gemm_q8_stream: the stream layout is read by the M <= 16 kernels only (T <= 16)");
+        GemmArgs a;
+        a.x = xq;
+        a.ld_x = ld_x;
+        a.xs = xs;
+        a.ld_xs = ld_xs;
+        a.act_block = act_block;
+        a.w = w;
+        a.ld_w = k;
+        a.w_stream = true;
+        a.s = ws;
+        a.ld_s = ld_ws;
+        a.y = y;
+        a.y_type = y_type;
+        a.ld_y = ld_y;
+        a.t = t;
+        a.n = n;
+        a.k = k;
+        a.epilogue = epilogue;
+        SmallGemmPlan plan;
+        const bool swiglu = epilogue == SEPAL_HIP_SWIGLU;
+        require(swiglu ? small_gemm_plan_q8(a, plan) : small_gemm_plan_q8_parts(a, plan),
+                "gemm_q8_stream: a shape the M <= 16 kernels do not take");
+        const hipStream_t st = as_stream(stream);
+        Lease lease(kScratchOffset, st);
+        a.scratch = lease.base();
+        if (swiglu) launch_small_gemm_q8(a, plan, st);
+        else launch_small_gemm_q8_parts(a, plan, st);
+    });
+}
+
 int32_t sepal_hip_mlp_stack(int32_t kind, size_t layers, size_t t, size_t hidden, size_t inter, void* x,
                             const int8_t* const* w_gate_up, const float* const* s_gate_up, const int8_t* const* w_down,
                             const float* const* s_down, float* y, size_t act_block, double eps, void* stream) {

@@ -28,6 +28,7 @@ struct GemmArgs {
     int epilogue = SEPAL_HIP_STORE;
     int config = -1;
     int force_splits = 0;  // small-M: > 0 forces the number of K splits (tests)
+    bool w_stream = false;  // M <= 16 pass kernels only: w in the stream layout (launch_stream_layout; ld_w unused)
     // q8 only
     const float* xs = nullptr;
     std::size_t ld_xs = 0;

@@ -890,13 +890,20 @@ void launch_parts_sum(int parts, bool add, std::size_t t, std::size_t n, const f
     else stack::parts_sum_kernel<P, false><<<grid, 256, 0, stream>>>(part, static_cast<int>(t), static_cast<int>(n), y, ld_y);
 }
 
-template <int XT, bool SWIGLU, int YT>
+template <int XT, bool SWIGLU, int YT, bool STREAM = false>
 void launch_pass(const stack::PassParams& p, std::size_t lds, hipStream_t stream) {
-    const auto kernel = stack::pass_kernel<XT, SWIGLU, YT>;
+    const auto kernel = stack::pass_kernel<XT, SWIGLU, YT, STREAM>;
     static std::size_t raised = 0;
     raise_lds(kernel, lds, raised);
     kernel<<<dim3(p.parts * p.blocks_per_part), dim3(stack::kThreads), lds, stream>>>(p);
     check_launch("small-M multiply pass launch");
+}
+
+// The pass on the packed weights, or on their stream layout when the caller passed that.
+template <int XT, bool SWIGLU, int YT>
+void launch_pass_w(const GemmArgs& a, const stack::PassParams& p, std::size_t lds, hipStream_t stream) {
+    if (a.w_stream) launch_pass<XT, SWIGLU, YT, true>(p, lds, stream);
+    else launch_pass<XT, SWIGLU, YT>(p, lds, stream);
 }
 
 } // namespace
@@ -982,7 +989,7 @@ void launch_small_gemm_q8(const GemmArgs& a, const SmallGemmPlan& plan, hipStrea
     p.ld_xs = a.ld_xs;
     p.per_token = a.act_block == a.k && a.k != 128 ? 1 : 0;
     p.pmax = reinterpret_cast<float*>(static_cast<char*>(a.scratch) + kCounterBytes);  // unused by the caller
-    launch_pass<kActI8, true, SEPAL_HIP_F32>(p, plan.lds, stream);
+    launch_pass_w<kActI8, true, SEPAL_HIP_F32>(a, p, plan.lds, stream);
 }
 
 bool small_q8_group_sums(const GemmArgs& a, hipStream_t stream) {
@@ -1059,7 +1066,7 @@ void launch_small_gemm_q8_parts(const GemmArgs& a, const SmallGemmPlan& plan, hi
     p.xs = a.xs;
     p.ld_xs = a.ld_xs;
     p.per_token = a.act_block == a.k && a.k != 128 ? 1 : 0;
-    launch_pass<kActI8X, false, SEPAL_HIP_F32>(p, plan.lds, stream);
+    launch_pass_w<kActI8X, false, SEPAL_HIP_F32>(a, p, plan.lds, stream);
     launch_parts_sum(plan.parts, a.epilogue == SEPAL_HIP_ADD, a.t, a.n, part, static_cast<float*>(a.y), a.ld_y, stream);
     check_launch("small-M multiply parts sum launch");
 }
@@ -1086,13 +1093,16 @@ void launch_small_gemm_w8g(const GemmArgs& a, const SmallGemmPlan& plan, hipStre
         const bool bf = a.x_type == SEPAL_HIP_BF16;
         switch (a.y_type) {
         case SEPAL_HIP_F32:
-            bf ? launch_pass<SEPAL_HIP_BF16, true, SEPAL_HIP_F32>(p, plan.lds, stream) : launch_pass<SEPAL_HIP_F16, true, SEPAL_HIP_F32>(p, plan.lds, stream);
+            bf ? launch_pass_w<SEPAL_HIP_BF16, true, SEPAL_HIP_F32>(a, p, plan.lds, stream)
+               : launch_pass_w<SEPAL_HIP_F16, true, SEPAL_HIP_F32>(a, p, plan.lds, stream);
             break;
         case SEPAL_HIP_BF16:
-            bf ? launch_pass<SEPAL_HIP_BF16, true, SEPAL_HIP_BF16>(p, plan.lds, stream) : launch_pass<SEPAL_HIP_F16, true, SEPAL_HIP_BF16>(p, plan.lds, stream);
+            bf ? launch_pass_w<SEPAL_HIP_BF16, true, SEPAL_HIP_BF16>(a, p, plan.lds, stream)
+               : launch_pass_w<SEPAL_HIP_F16, true, SEPAL_HIP_BF16>(a, p, plan.lds, stream);
             break;
         default:
-            bf ? launch_pass<SEPAL_HIP_BF16, true, SEPAL_HIP_F16>(p, plan.lds, stream) : launch_pass<SEPAL_HIP_F16, true, SEPAL_HIP_F16>(p, plan.lds, stream);
+            bf ? launch_pass_w<SEPAL_HIP_BF16, true, SEPAL_HIP_F16>(a, p, plan.lds, stream)
+               : launch_pass_w<SEPAL_HIP_F16, true, SEPAL_HIP_F16>(a, p, plan.lds, stream);
             break;
         }
         return;
@@ -1103,8 +1113,8 @@ void launch_small_gemm_w8g(const GemmArgs& a, const SmallGemmPlan& plan, hipStre
     p.ld_y = a.n;
     p.tiles = static_cast<int>(a.n / 16);
     p.blocks_per_part = (p.tiles + p.per_block - 1) / p.per_block;
-    if (a.x_type == SEPAL_HIP_BF16) launch_pass<SEPAL_HIP_BF16, false, SEPAL_HIP_F32>(p, plan.lds, stream);
-    else launch_pass<SEPAL_HIP_F16, false, SEPAL_HIP_F32>(p, plan.lds, stream);
+    if (a.x_type == SEPAL_HIP_BF16) launch_pass_w<SEPAL_HIP_BF16, false, SEPAL_HIP_F32>(a, p, plan.lds, stream);
+    else launch_pass_w<SEPAL_HIP_F16, false, SEPAL_HIP_F32>(a, p, plan.lds, stream);
     launch_parts_sum(plan.parts, a.epilogue == SEPAL_HIP_ADD, a.t, a.n, part, static_cast<float*>(a.y), a.ld_y, stream);
     check_launch("small-M multiply parts sum launch");
 }

@@ -80,6 +80,8 @@ def library() -> C.CDLL:
         L.sepal_hip_w8g_stream_layout_bytes.restype = sz
         L.sepal_hip_w8g_make_stream_layout.argtypes = [vp, sz, sz, sz, i32, vp, sz, vp]
         L.sepal_hip_mlp_stack_stream.argtypes = [i32, sz, sz, sz, sz, vp, vp, vp, vp, vp, vp, sz, d, vp]
+        L.sepal_hip_gemm_w8g_stream.argtypes = [vp, i32, sz, vp, vp, sz, vp, i32, sz, sz, sz, sz, i32, vp]
+        L.sepal_hip_gemm_q8_stream.argtypes = [vp, sz, vp, sz, sz, vp, vp, sz, vp, i32, sz, sz, sz, sz, i32, vp]
         for name in ("sepal_hip_quantize_group_s8", "sepal_hip_quantize_gate_up_s8", "sepal_hip_gemm_w8g",
                      "sepal_hip_quantize_rows_s8", "sepal_hip_gemm_q8", "sepal_hip_q8_group_sums",
                      "sepal_hip_rmsnorm_rows", "sepal_hip_float_to_bf16", "sepal_hip_mlp_stack",
@@ -89,7 +91,7 @@ def library() -> C.CDLL:
                      "sepal_hip_s8_quantize_rows", "sepal_hip_gemm_s8", "sepal_hip_gemm_w8a16", "sepal_hip_gemm_q8y",
                      "sepal_hip_column_absmax", "sepal_hip_channel_stats", "sepal_hip_release_workspace",
                      "sepal_hip_w8g_make_image", "sepal_hip_mlp_stack_images", "sepal_hip_w8g_make_stream_layout",
-                     "sepal_hip_mlp_stack_stream"):
+                     "sepal_hip_mlp_stack_stream", "sepal_hip_gemm_w8g_stream", "sepal_hip_gemm_q8_stream"):
             getattr(L, name).restype = i32
         L.sepal_hip_gemm_w8g_supports.restype = i32
         L.sepal_hip_gemm_s8_supports.restype = i32
@@ -197,6 +199,20 @@ def gemm_w8g(x, w, s, y=None, epilogue: int = STORE, y_dtype=None, config: int =
     return y
 
 
+def gemm_w8g_stream(x, w_stream, s, y=None, epilogue: int = STORE, y_dtype=None, stream=None):
+    """gemm_w8g at T <= 16 on a stream-layout matrix (w8g_make_stream_layout; interleave for SwiGLU): the same bits as
+    gemm_w8g on the packed matrix. x [T, K] bf16/fp16; s float32 [N, K/128]."""
+    torch = _torch()
+    t, k = x.shape
+    n = s.shape[0]
+    cols = n // 2 if epilogue == SWIGLU else n
+    if y is None:
+        y = torch.empty(t, cols, dtype=y_dtype or torch.float32, device=x.device)
+    _check(library().sepal_hip_gemm_w8g_stream(_ptr(x), _type_of(x), _ld(x), _ptr(w_stream), _ptr(s), _ld(s), _ptr(y),
+                                               _type_of(y), _ld(y), t, n, k, epilogue, _stream(stream)))
+    return y
+
+
 def quantize_rows_s8(x, block: int = 128, stream=None):
     """Dynamic activation quantizer (cpu-q8 rule): int8 q [T, K] and scales [T, K/block]."""
     torch = _torch()
@@ -269,6 +285,19 @@ def gemm_q8(xq, xs, w, ws, y=None, epilogue: int = STORE, act_block: int = 128, 
     _check(library().sepal_hip_gemm_q8(_ptr(xq), _ld(xq), _ptr(xs), _ld(xs), act_block, _ptr(w), _ld(w), _ptr(ws),
                                        _ld(ws), _ptr(y), _type_of(y), _ld(y), t, n, k, epilogue, config,
                                        _stream(stream)))
+    return y
+
+
+def gemm_q8_stream(xq, xs, w_stream, ws, y=None, epilogue: int = STORE, act_block: int = 128, stream=None):
+    """gemm_q8 at T <= 16 on a stream-layout matrix (float32 y): the same bits as gemm_q8 on the packed matrix."""
+    torch = _torch()
+    t, k = xq.shape
+    n = ws.shape[0]
+    cols = n // 2 if epilogue == SWIGLU else n
+    if y is None:
+        y = torch.empty(t, cols, dtype=torch.float32, device=xq.device)
+    _check(library().sepal_hip_gemm_q8_stream(_ptr(xq), _ld(xq), _ptr(xs), _ld(xs), act_block, _ptr(w_stream), _ptr(ws),
+                                              _ld(ws), _ptr(y), _type_of(y), _ld(y), t, n, k, epilogue, _stream(stream)))
     return y
 
 

@@ -184,6 +184,15 @@ def test_stream_layout_refusals():
     assert L.sepal_hip_mlp_stack_stream(0, *args[1:5], None, *args[6:]) == sm.EINVAL  # null x
     assert L.sepal_hip_mlp_stack_stream(0, *args[1:6], one(FAKE + 4), *args[7:]) == sm.EINVAL  # misaligned weights
     assert L.sepal_hip_mlp_stack_stream(0, 0, *args[2:]) == sm.OK       # no layers: a no-op
+    # single multiplies: X types the pass kernels take, T <= 16, float32 q8 output
+    assert L.sepal_hip_gemm_w8g_stream(FAKE, sm.F32, 256, FAKE, FAKE, 2, FAKE, sm.F32, 128, 4, 128, 256, sm.STORE, None) == sm.EINVAL
+    assert L.sepal_hip_gemm_w8g_stream(FAKE, sm.BF16, 256, FAKE, FAKE, 2, FAKE, sm.F32, 128, 17, 128, 256, sm.STORE, None) == sm.EINVAL
+    assert "T <= 16" in _err()
+    assert L.sepal_hip_gemm_w8g_stream(FAKE, sm.BF16, 264, FAKE, FAKE, 2, FAKE, sm.F32, 128, 4, 128, 256, sm.STORE, None) == sm.EINVAL
+    assert L.sepal_hip_gemm_w8g_stream(FAKE, sm.BF16, 256, FAKE, FAKE, 2, FAKE, sm.F32, 128, 0, 128, 256, sm.STORE, None) == sm.OK
+    assert L.sepal_hip_gemm_q8_stream(FAKE, 256, FAKE, 2, 128, FAKE, FAKE, 2, FAKE, sm.F16, 128, 4, 256, 256, sm.SWIGLU, None) == sm.EINVAL
+    assert L.sepal_hip_gemm_q8_stream(FAKE, 256, FAKE, 2, 64, FAKE, FAKE, 2, FAKE, sm.F32, 128, 4, 128, 256, sm.STORE, None) == sm.EINVAL
+    assert L.sepal_hip_gemm_q8_stream(FAKE, 256, FAKE, 2, 128, FAKE, FAKE, 2, FAKE, sm.F32, 128, 17, 128, 256, sm.STORE, None) == sm.EINVAL
 
 
 def test_fused_producer_refusals():

@@ -1083,6 +1083,51 @@ def test_mlp_stack_stream_layout_shapes(sm, hidden, inter, t, kind, act_block):
     assert torch.equal(xa, xb)
 
 
+@pytest.mark.parametrize("t", [1, 7, 16])
+def test_gemm_stream_layout_single_calls(sm, t):
+    """Single multiplies at T <= 16 on stream-layout weights give the bits of the same call on the packed matrix: w8g
+    gate/up SwiGLU (bf16 X; float32, bf16 and binary16 H), w8g down Store and Add (binary16 X), a shape off the MLP's,
+    and q8 gate/up and down with one scale per token and per 128 columns."""
+    say("gemm stream layout single calls t", t)
+    rng = np.random.default_rng(400 + t)
+    H, I = 2560, 9728
+    gate = (rng.standard_normal((I, H)) * 0.02).astype(np.float16)
+    up = (rng.standard_normal((I, H)) * 0.02).astype(np.float16)
+    down = (rng.standard_normal((H, I)) * 0.02).astype(np.float16)
+    wgu, sgu = sm.quantize_gate_up_s8(dev(gate), dev(up))
+    wd, sd = sm.quantize_group_s8(dev(down))
+    sgu_w, sd_w = sm.w8g_make_stream_layout(wgu, True), sm.w8g_make_stream_layout(wd, False)
+    x = dev(bf16_inputs(rng, (t, H)), torch.bfloat16)
+    for yd in (torch.float32, torch.bfloat16, torch.float16):
+        a = host(sm.gemm_w8g(x, wgu, sgu, epilogue=sm.SWIGLU, y_dtype=yd).float())
+        b = host(sm.gemm_w8g_stream(x, sgu_w, sgu, epilogue=sm.SWIGLU, y_dtype=yd).float())
+        assert same_bits(a, b), yd
+    h = dev(rng.standard_normal((t, I)).astype(np.float16), torch.float16)
+    assert same_bits(host(sm.gemm_w8g(h, wd, sd)), host(sm.gemm_w8g_stream(h, sd_w, sd)))
+    y0 = dev(rng.standard_normal((t, H)).astype(np.float32))
+    ya, yb = y0.clone(), y0.clone()
+    sm.gemm_w8g(h, wd, sd, y=ya, epilogue=sm.ADD)
+    sm.gemm_w8g_stream(h, sd_w, sd, y=yb, epilogue=sm.ADD)
+    assert same_bits(host(ya), host(yb))
+    # a shape off the MLP's: N = 1040 (65 tiles), K = 512 (the M <= 16 kernels take K of 4 groups and more)
+    wo, so = sm.quantize_group_s8(dev((rng.standard_normal((1040, 512)) * 0.02).astype(np.float16)))
+    xo = dev(bf16_inputs(rng, (t, 512)), torch.bfloat16)
+    assert same_bits(host(sm.gemm_w8g(xo, wo, so)), host(sm.gemm_w8g_stream(xo, sm.w8g_make_stream_layout(wo, False), so)))
+    # q8 (reciprocal-rule weights): gate/up SwiGLU and down Store, per token and per 128
+    qgu, qsgu = sm.quantize_gate_up_s8(dev(gate), dev(up), rule=sm.RULE_RECIPROCAL)
+    qd, qsd = sm.quantize_group_s8(dev(down), rule=sm.RULE_RECIPROCAL)
+    qgu_w, qd_w = sm.w8g_make_stream_layout(qgu, True), sm.w8g_make_stream_layout(qd, False)
+    for blk_x, blk_h in ((H, I), (128, 128)):
+        xq, xs = sm.quantize_rows_s8(x, block=blk_x)
+        a = host(sm.gemm_q8(xq, xs, qgu, qsgu, epilogue=sm.SWIGLU, act_block=blk_x))
+        b = host(sm.gemm_q8_stream(xq, xs, qgu_w, qsgu, epilogue=sm.SWIGLU, act_block=blk_x))
+        assert same_bits(a, b), blk_x
+        hq, hs = sm.quantize_rows_s8(h, block=blk_h)
+        a = host(sm.gemm_q8(hq, hs, qd, qsd, act_block=blk_h))
+        b = host(sm.gemm_q8_stream(hq, hs, qd_w, qsd, act_block=blk_h))
+        assert same_bits(a, b), blk_h
+
+
 def test_mlp_stack_small_path_full_size(sm):
     """The M = 16 stack at the model's shape (H 2560, I 9728), two layers, against the oracle."""
     say("mlp stack small path full size")
