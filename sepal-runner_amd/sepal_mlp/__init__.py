@@ -401,8 +401,8 @@ def w8g_make_image(w, x_dtype, stream=None):
 
 
 def w8g_make_stream_layout(w, interleave: bool, stream=None):
-    """The load-time stream layout of int8 weights w [N, K] for the M <= 16 w8g stack (interleave: a gate/up matrix in
-    the 64-row interleave). An int8 device tensor of N * K bytes."""
+    """The load-time stream layout of int8 weights w [N, K] for the M <= 16 kernels (mlp_stack_stream, gemm_w8g_stream,
+    gemm_q8_stream; interleave: a gate/up matrix in the 64-row interleave). An int8 device tensor of N * K bytes."""
     torch = _torch()
     n, k = w.shape
     nbytes = library().sepal_hip_w8g_stream_layout_bytes(n, k)
