@@ -275,6 +275,10 @@ def profile_kernels():
     y16 = torch.empty(M_SMALL, H, dtype=torch.float32, device="cuda")
     for _ in range(2):
         sm.mlp_stack(0, xs16, layers, y=y16)
+    # ... and two passes on the load-time stream layout of the same weights
+    slayers = [(sm.w8g_make_stream_layout(a, True), b, sm.w8g_make_stream_layout(c, False), d) for a, b, c, d in layers]
+    for _ in range(2):
+        sm.mlp_stack_stream(0, xs16, slayers, y=y16)
     torch.cuda.synchronize()
     log("profile-kernels: done")
 
