@@ -163,8 +163,9 @@ void launch_small_layer(const SmallStackPlan& plan, std::size_t t, std::size_t h
 // interleave: the gate/up matrix (tiles of 8 gate and 8 up rows, the 64-row interleave).
 void launch_stream_layout(const std::int8_t* w, std::size_t ld_w, std::size_t n, std::size_t k, bool interleave, std::int8_t* out,
                           hipStream_t stream);
-// The gpu-q8w form: int8 x [t, hidden] with its scales (one per token, or per 128 columns) -> H float32 [t, inter]
-// (per token also hmax [t, ceil(inter / 8 / tiles_per_block)], the partial row maxima of |H|) -> part -> y; when xq_next is
+// The gpu-q8w form: int8 x [t, hidden] with its scales (one per token, or per 128 columns) -> H [t, inter] in h, float32
+// per 128 columns, binary16 per token as the large-M per-token stack keeps it (per token also hmax [t, ceil(inter / 8 /
+// tiles_per_block)], the partial row maxima of |H|) -> part -> y; when xq_next is
 // set, the next layer's input bf16(RMSNorm(y)) goes to xn (bf16) and, quantized, to xq_next / xs_next. stream_w: the
 // weights in the stream layout, as for launch_small_layer.
 void launch_small_layer_q8(const SmallStackPlan& plan, std::size_t t, std::size_t hidden, std::size_t inter,

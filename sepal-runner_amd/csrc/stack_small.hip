@@ -77,7 +77,9 @@ struct PassParams {
     const float* xs;          // gate/up: X scales [T, ld_xs], one per token or per 128 columns
     std::size_t ld_xs;
     int per_token;            // 1: one activation scale per token; 0: one per 128 columns
-    const float* xf;          // down: H float32 [T, ld_x], quantized here
+    const float* xf;          // down: H float32 [T, ld_x], quantized here (per 128 columns)
+    int h16;                  // the stack's per-token form: the gate/up pass writes H in binary16 (its row maxima over
+                              // the rounded values), and the down pass stages binary16 H from x
     const float* hmax;        // down, per token: the gate/up pass's partial row maxima of |H| [T, hmax_blocks]
     int hmax_blocks;
     float* pmax;              // gate/up, per token: this pass's partial row maxima [T, gridDim.x]
@@ -111,10 +113,23 @@ __device__ __forceinline__ void stage_h_q8(const PassParams& p, unsigned char* l
 #pragma unroll
         for (int h = 0; h < ROWS; ++h) {
             const int rs = min(row0 + rr + h, p.t - 1);
-            const float* hrow = p.xf + static_cast<std::size_t>(rs) * p.ld_x + 128 * g_lo;
+            if (p.h16) {
+                // binary16 H: four values per lane in 8 bytes, widened exactly
+                const unsigned short* hrow = p.x + static_cast<std::size_t>(rs) * p.ld_x + 128 * g_lo;
 #pragma unroll
-            for (int e = 0; e < NQ; ++e)
-                hv[h][e] = *reinterpret_cast<const float4*>(hrow + 128 * min(2 * e + lane / 32, gpt - 1) + 4 * (lane % 32));
+                for (int e = 0; e < NQ; ++e) {
+                    const uint2 b = *reinterpret_cast<const uint2*>(hrow + 128 * min(2 * e + lane / 32, gpt - 1) + 4 * (lane % 32));
+                    hv[h][e] = make_float4(f16_bits_to_f32(static_cast<unsigned short>(b.x & 0xFFFFu)),
+                                           f16_bits_to_f32(static_cast<unsigned short>(b.x >> 16)),
+                                           f16_bits_to_f32(static_cast<unsigned short>(b.y & 0xFFFFu)),
+                                           f16_bits_to_f32(static_cast<unsigned short>(b.y >> 16)));
+                }
+            } else {
+                const float* hrow = p.xf + static_cast<std::size_t>(rs) * p.ld_x + 128 * g_lo;
+#pragma unroll
+                for (int e = 0; e < NQ; ++e)
+                    hv[h][e] = *reinterpret_cast<const float4*>(hrow + 128 * min(2 * e + lane / 32, gpt - 1) + 4 * (lane % 32));
+            }
             if (p.per_token) {
 #pragma unroll
                 for (int i = 0; i < kMaxPartials; ++i)
@@ -212,8 +227,9 @@ __global__ void __launch_bounds__(kThreads) pass_kernel(const PassParams p) {
         }
     };
     if constexpr (XT == kActI8 && !SWIGLU) {
-        // q8 down: H float32 quantized as the activation quantizer does (rule RECIPROCAL, scale = max / 127), per 128
-        // columns or with the row maximum of the gate/up pass's partial maxima (per token)
+        // q8 down: H (float32 per 128 columns; binary16 in the stack's per-token form) quantized as the activation
+        // quantizer does (rule RECIPROCAL, scale = max / 127), per 128 columns or with the row maximum of the gate/up
+        // pass's partial maxima (per token)
         if (gpt <= 14) stage_h_q8<7, 1>(p, lds, xsc, xpitch, g_lo, gpt, wave, 1, lane);
         else stage_h_q8<12, 1>(p, lds, xsc, xpitch, g_lo, gpt, wave, 1, lane);
         __syncthreads();
@@ -421,7 +437,8 @@ __global__ void __launch_bounds__(kThreads) pass_kernel(const PassParams p) {
         return v;
     };
     if constexpr (Q8 && SWIGLU) {
-        // H = SwiGLU(gate, up) in float32 (the gpu-q8w epilogue), and, per token, this block's row maxima of |H|
+        // H = SwiGLU(gate, up) in float32 (the gpu-q8w epilogue; binary16 when h16 is set), and, per token, this
+        // block's row maxima of |H|
         float* hy = static_cast<float*>(p.y);
         for (int id = tid; id < ntiles * 16 * 8; id += kThreads) {
             const int tl = id / 128, r = (id / 8) % 16, i = id % 8;
@@ -435,8 +452,15 @@ __global__ void __launch_bounds__(kThreads) pass_kernel(const PassParams p) {
             }
             // (per token, a form with no reference bits, the fast silu, as the large-M q8 kernels use it)
             const float hv = p.per_token ? swiglu_fast(g, u) : swiglu_cephes(g, u);
-            hy[static_cast<std::size_t>(r) * p.ld_y + f] = hv;
-            if (p.per_token) atomicMax(&row_max[r], __float_as_uint(fabsf(hv)));
+            if (p.h16) {
+                // binary16 H, as the large-M per-token stack writes it; the maxima are over the rounded values
+                const unsigned short hb = f32_to_f16_bits(hv);
+                static_cast<unsigned short*>(p.y)[static_cast<std::size_t>(r) * p.ld_y + f] = hb;
+                atomicMax(&row_max[r], __float_as_uint(fabsf(f16_bits_to_f32(hb))));
+            } else {
+                hy[static_cast<std::size_t>(r) * p.ld_y + f] = hv;
+                if (p.per_token) atomicMax(&row_max[r], __float_as_uint(fabsf(hv)));
+            }
         }
         if (p.per_token) {
             __syncthreads();
@@ -809,7 +833,8 @@ void launch_small_layer_q8(const SmallStackPlan& plan, std::size_t t, std::size_
                            const std::int8_t* w_d, const float* s_d, float* h, float* hmax, float* part, float* y,
                            std::int8_t* xq_next, float* xs_next, void* xn, double eps, hipStream_t stream, bool stream_w) {
     using namespace stack;
-    // gate/up: int8 X [t, hidden] (+ scales) -> H float32 [t, inter] (+ per token: partial row maxima of |H|)
+    // gate/up: int8 X [t, hidden] (+ scales) -> H [t, inter], float32 per 128 columns, binary16 per token (+ per token:
+    // partial row maxima of |H|)
     PassParams a{};
     a.x = reinterpret_cast<const unsigned short*>(xq);
     a.ld_x = hidden;  // bytes
@@ -829,6 +854,7 @@ void launch_small_layer_q8(const SmallStackPlan& plan, std::size_t t, std::size_
     a.xs = xs;
     a.ld_xs = per_token ? 1 : hidden / 128;
     a.per_token = per_token ? 1 : 0;
+    a.h16 = per_token ? 1 : 0;
     a.pmax = hmax;
     const auto ka = stream_w ? pass_kernel<kActI8, true, SEPAL_HIP_F32, true> : pass_kernel<kActI8, true, SEPAL_HIP_F32>;
     static std::size_t raised_a[2] = {0, 0};
@@ -854,6 +880,8 @@ void launch_small_layer_q8(const SmallStackPlan& plan, std::size_t t, std::size_
     d.per_block = plan.units_per_block;
     d.blocks_per_part = (d.tiles + d.per_block - 1) / d.per_block;
     d.per_token = per_token ? 1 : 0;
+    d.h16 = per_token ? 1 : 0;
+    d.x = reinterpret_cast<const unsigned short*>(h);
     d.hmax = hmax;
     d.hmax_blocks = a.blocks_per_part;
 

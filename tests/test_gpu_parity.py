@@ -886,8 +886,8 @@ def _stack_weights(sm, rng, layers, hidden, inter, rule):
 
 
 def _oracle_stack(kind, x, layers, act_block, h16=False):
-    """h16: H rounded to binary16 before its per-token quantization (the general q8 path, as the reference's GPU int8
-    path quantizes binary16 activations, runner/cuda/src/cuda_engine.cpp:1098-1102; the M <= 16 stack keeps float32)."""
+    """h16: H rounded to binary16 before its per-token quantization (every per-token stack, as the reference's GPU int8
+    path quantizes binary16 activations, runner/cuda/src/cuda_engine.cpp:1098-1102)."""
     x = x.copy()
     y = None
     for li, (wgu, sgu, wd, sd) in enumerate(layers):
@@ -1011,7 +1011,10 @@ def test_mlp_stack_small_path(sm, t):
 @pytest.mark.parametrize("t,act", [(1, 0), (5, 128), (16, 0), (16, 128)])
 def test_mlp_stack_small_q8(sm, t, act):
     """M <= 16 gpu-q8w stack (int8 MFMAs, H quantized by the down pass while staged, the next layer's input quantized
-    by the finish pass) against the oracle's q8 chain: same int8 products, float sums in another order (tolerance)."""
+    by the finish pass) against the oracle's q8 chain: same int8 products, float sums in another order (tolerance).
+    Per token H is binary16, as on the large-M path (the oracle rounds its H the same way); a binary16 H that rounds
+    the other way from the oracle's moves an int8 step now and then, so that mode is held in relative rms per layer
+    and to the per-token drift bar over three layers."""
     say("mlp stack small q8 t", t, "act", act)
     rng = np.random.default_rng(91 + t + act)
     hidden, inter, nl = 512, 1024, 3
@@ -1020,14 +1023,17 @@ def test_mlp_stack_small_q8(sm, t, act):
     x[:, ::97] *= 20.0  # outlier channels, as the q8 benchmark's activations
     x = orc.bf16_round(x)
     xt = dev(x, torch.bfloat16)
+    h16 = act == 0
+    bar3 = STACK3_DRIFT_Q8_TOKEN if h16 else 2e-3
     y = host(sm.mlp_stack(1, xt, layers, act_block=act))
-    ref = _oracle_stack(1, x, layers, act)
-    assert rel_rms(y, ref) < 2e-3, rel_rms(y, ref)
-    y2 = _oracle_stack(1, x, layers[:2], act)
-    assert rel_rms(host(xt).astype(np.float32), orc.bf16_round(orc.rmsnorm_rows(y2))) < 2e-3
+    ref = _oracle_stack(1, x, layers, act, h16=h16)
+    assert rel_rms(y, ref) < bar3, rel_rms(y, ref)
+    y2 = _oracle_stack(1, x, layers[:2], act, h16=h16)
+    assert rel_rms(host(xt).astype(np.float32), orc.bf16_round(orc.rmsnorm_rows(y2))) < bar3
     y1 = host(sm.mlp_stack(1, dev(x, torch.bfloat16), layers[:1], act_block=act))
-    ref1 = _oracle_stack(1, x, layers[:1], act)
-    assert max_rel_over_rms(y1, ref1) < 2e-3, max_rel_over_rms(y1, ref1)
+    ref1 = _oracle_stack(1, x, layers[:1], act, h16=h16)
+    err1 = rel_rms(y1, ref1) if h16 else max_rel_over_rms(y1, ref1)
+    assert err1 < 2e-3, err1
 
 
 @pytest.mark.parametrize("act", [0, 128])
@@ -1037,11 +1043,13 @@ def test_mlp_stack_small_q8_full_size(sm, act):
     rng = np.random.default_rng(6 + act)
     layers = _stack_weights(sm, rng, 2, 2560, 9728, rule=1)
     x = bf16_inputs(rng, (16, 2560))
+    h16 = act == 0  # per token: binary16 H (the oracle rounds its H the same way)
     y1 = host(sm.mlp_stack(1, dev(x, torch.bfloat16), layers[:1], act_block=act))
-    ref1 = _oracle_stack(1, x, layers[:1], act)
-    assert max_rel_over_rms(y1, ref1) < 2e-3, max_rel_over_rms(y1, ref1)
+    ref1 = _oracle_stack(1, x, layers[:1], act, h16=h16)
+    err1 = rel_rms(y1, ref1) if h16 else max_rel_over_rms(y1, ref1)
+    assert err1 < 2e-3, err1
     y = host(sm.mlp_stack(1, dev(x, torch.bfloat16), layers, act_block=act))
-    assert rel_rms(y, _oracle_stack(1, x, layers, act)) < 2e-3
+    assert rel_rms(y, _oracle_stack(1, x, layers, act, h16=h16)) < 2e-3
 
 
 @pytest.mark.parametrize("kind,act_block", [(0, 128), (1, 0), (1, 128)])
