@@ -100,6 +100,47 @@ __device__ __forceinline__ int tile_row(int tile, int c) {
 
 constexpr int kXChunks = 6;  // 16-byte X chunks per lane of a staged row: 64 x 6 x 8 = 3072 columns at most
 
+// The same for the stack's per-token form, whose H is binary16 (h16): one scale per row (the maximum of the gate/up
+// pass's partial maxima), so no group maxima; each lane widens and quantizes 8 values of a 16-byte load (16 lanes per
+// 128 columns, NQ loads per row cover 4 NQ groups).
+template <int NQ>
+__device__ __forceinline__ void stage_h16_q8(const PassParams& p, unsigned char* lds, float* xsc, int xpitch, int g_lo, int gpt,
+                                             int row0, int nrows, int lane) {
+    constexpr int kMaxPartials = 4;  // 64 lanes x 4: the gate/up grid has at most 256 blocks
+#pragma unroll 1
+    for (int rr = 0; rr < nrows; ++rr) {
+        const int r = row0 + rr, rs = min(r, p.t - 1);
+        const unsigned short* hrow = p.x + static_cast<std::size_t>(rs) * p.ld_x + 128 * g_lo;
+        uint4 hb[NQ];
+#pragma unroll
+        for (int e = 0; e < NQ; ++e)
+            hb[e] = *reinterpret_cast<const uint4*>(hrow + 128 * min(4 * e + lane / 16, gpt - 1) + 8 * (lane % 16));
+        float pm[kMaxPartials];
+#pragma unroll
+        for (int i = 0; i < kMaxPartials; ++i)
+            pm[i] = p.hmax[static_cast<std::size_t>(rs) * p.hmax_blocks + min(lane + 64 * i, p.hmax_blocks - 1)];
+        float m = fmaxf(fmaxf(pm[0], pm[1]), fmaxf(pm[2], pm[3]));
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+        const float rscale = m > 0.0f ? __fdiv_rn(m, 127.0f) : 1.0f;
+        const float rinv = __fdiv_rn(1.0f, rscale);
+        if (lane == 0) xsc[r] = rscale;
+#pragma unroll
+        for (int e = 0; e < NQ; ++e) {
+            if (4 * e >= gpt) break;  // uniform
+            const int g = 4 * e + lane / 16;
+            const unsigned w[4] = {hb[e].x, hb[e].y, hb[e].z, hb[e].w};
+            unsigned packed[2] = {0u, 0u};
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float v = f16_bits_to_f32(static_cast<unsigned short>((w[j / 2] >> (16 * (j % 2))) & 0xFFFFu));
+                packed[j / 4] |= (static_cast<unsigned>(quantize_act(v, rinv)) & 0xFFu) << (8 * (j % 4));
+            }
+            if (g < gpt) *reinterpret_cast<uint2*>(lds + r * xpitch + 128 * g + 8 * (lane % 16)) = make_uint2(packed[0], packed[1]);
+        }
+    }
+}
+
 // The q8 down pass's staging of H rows 4 w .. 4 w + 3 (w = loader wave), ROWS rows per round trip: NQ float4 loads
 // per lane and row cover 2 NQ blocks of 128 columns (NQ = ceil(gpt / 2) rounded up to an instantiated size).
 template <int NQ, int ROWS>
@@ -113,23 +154,10 @@ __device__ __forceinline__ void stage_h_q8(const PassParams& p, unsigned char* l
 #pragma unroll
         for (int h = 0; h < ROWS; ++h) {
             const int rs = min(row0 + rr + h, p.t - 1);
-            if (p.h16) {
-                // binary16 H: four values per lane in 8 bytes, widened exactly
-                const unsigned short* hrow = p.x + static_cast<std::size_t>(rs) * p.ld_x + 128 * g_lo;
+            const float* hrow = p.xf + static_cast<std::size_t>(rs) * p.ld_x + 128 * g_lo;
 #pragma unroll
-                for (int e = 0; e < NQ; ++e) {
-                    const uint2 b = *reinterpret_cast<const uint2*>(hrow + 128 * min(2 * e + lane / 32, gpt - 1) + 4 * (lane % 32));
-                    hv[h][e] = make_float4(f16_bits_to_f32(static_cast<unsigned short>(b.x & 0xFFFFu)),
-                                           f16_bits_to_f32(static_cast<unsigned short>(b.x >> 16)),
-                                           f16_bits_to_f32(static_cast<unsigned short>(b.y & 0xFFFFu)),
-                                           f16_bits_to_f32(static_cast<unsigned short>(b.y >> 16)));
-                }
-            } else {
-                const float* hrow = p.xf + static_cast<std::size_t>(rs) * p.ld_x + 128 * g_lo;
-#pragma unroll
-                for (int e = 0; e < NQ; ++e)
-                    hv[h][e] = *reinterpret_cast<const float4*>(hrow + 128 * min(2 * e + lane / 32, gpt - 1) + 4 * (lane % 32));
-            }
+            for (int e = 0; e < NQ; ++e)
+                hv[h][e] = *reinterpret_cast<const float4*>(hrow + 128 * min(2 * e + lane / 32, gpt - 1) + 4 * (lane % 32));
             if (p.per_token) {
 #pragma unroll
                 for (int i = 0; i < kMaxPartials; ++i)
@@ -230,8 +258,14 @@ __global__ void __launch_bounds__(kThreads) pass_kernel(const PassParams p) {
         // q8 down: H (float32 per 128 columns; binary16 in the stack's per-token form) quantized as the activation
         // quantizer does (rule RECIPROCAL, scale = max / 127), per 128 columns or with the row maximum of the gate/up
         // pass's partial maxima (per token)
-        if (gpt <= 14) stage_h_q8<7, 1>(p, lds, xsc, xpitch, g_lo, gpt, wave, 1, lane);
-        else stage_h_q8<12, 1>(p, lds, xsc, xpitch, g_lo, gpt, wave, 1, lane);
+        if (p.h16) {
+            if (gpt <= 16) stage_h16_q8<4>(p, lds, xsc, xpitch, g_lo, gpt, wave, 1, lane);
+            else stage_h16_q8<6>(p, lds, xsc, xpitch, g_lo, gpt, wave, 1, lane);
+        } else if (gpt <= 14) {
+            stage_h_q8<7, 1>(p, lds, xsc, xpitch, g_lo, gpt, wave, 1, lane);
+        } else {
+            stage_h_q8<12, 1>(p, lds, xsc, xpitch, g_lo, gpt, wave, 1, lane);
+        }
         __syncthreads();
     } else {
         if (wave < kLoaders) {
