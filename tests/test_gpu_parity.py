@@ -1136,6 +1136,41 @@ def test_gemm_stream_layout_single_calls(sm, t):
         assert same_bits(a, b), blk_h
 
 
+def test_gemm_stream_layout_random_shapes(sm):
+    """Twelve seeded shapes within the M <= 16 kernels' range (N, K, T, epilogue, X type, q8 scale mode drawn at
+    random): each single multiply on the stream layout gives the bits of the same call on the packed matrix."""
+    rng = np.random.default_rng(2024)
+    done = 0
+    while done < 12:
+        swiglu = bool(rng.integers(0, 2))
+        n = int(rng.integers(1, 40)) * (128 if swiglu else 16)
+        k = int(rng.integers(4, 22)) * 128  # (the bf16 gate/up pass stages K of at most 23 groups)
+        t = int(rng.integers(1, 17))
+        q8 = bool(rng.integers(0, 2))
+        say("stream layout random shape", n, k, t, "swiglu" if swiglu else "store", "q8" if q8 else "w8g")
+        wf = (rng.standard_normal((n, k)) * 0.02).astype(np.float16)
+        if swiglu:
+            w, s_ = sm.quantize_gate_up_s8(dev(wf[: n // 2]), dev(wf[n // 2:]), rule=1 if q8 else 0)
+        else:
+            w, s_ = sm.quantize_group_s8(dev(wf), rule=1 if q8 else 0)
+        ws_ = sm.w8g_make_stream_layout(w, swiglu)
+        ep = sm.SWIGLU if swiglu else sm.STORE
+        if q8:
+            blk = int(rng.choice([128, k]))
+            if blk == 128 and k // 128 > 24:
+                continue  # (per 128, the M <= 16 q8 kernels stage at most 24 groups of scales)
+            xq, xs = sm.quantize_rows_s8(dev(bf16_inputs(rng, (t, k)), torch.bfloat16), block=blk)
+            a = host(sm.gemm_q8(xq, xs, w, s_, epilogue=ep, act_block=blk))
+            b = host(sm.gemm_q8_stream(xq, xs, ws_, s_, epilogue=ep, act_block=blk))
+        else:
+            xd = torch.float16 if rng.integers(0, 2) else torch.bfloat16
+            x = dev(bf16_inputs(rng, (t, k)), xd)
+            a = host(sm.gemm_w8g(x, w, s_, epilogue=ep))
+            b = host(sm.gemm_w8g_stream(x, ws_, s_, epilogue=ep))
+        assert same_bits(a, b), (n, k, t, swiglu, q8)
+        done += 1
+
+
 def test_mlp_stack_small_path_full_size(sm):
     """The M = 16 stack at the model's shape (H 2560, I 9728), two layers, against the oracle."""
     say("mlp stack small path full size")
