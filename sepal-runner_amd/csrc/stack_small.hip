@@ -100,44 +100,47 @@ __device__ __forceinline__ int tile_row(int tile, int c) {
 
 constexpr int kXChunks = 6;  // 16-byte X chunks per lane of a staged row: 64 x 6 x 8 = 3072 columns at most
 
-// The same for the stack's per-token form, whose H is binary16 (h16): one scale per row (the maximum of the gate/up
-// pass's partial maxima), so no group maxima; each lane widens and quantizes 8 values of a 16-byte load (16 lanes per
-// 128 columns, NQ loads per row cover 4 NQ groups).
+// The stack's per-token form (h16): binary16 H and one scale per row (the maximum of the gate/up pass's partial
+// maxima), so no group maxima. A row's loads: 8 values a lane per 16-byte load, 16 lanes per 128 columns (NQ loads
+// cover 4 NQ groups), and its partial maxima; staging widens and quantizes it into LDS.
 template <int NQ>
-__device__ __forceinline__ void stage_h16_q8(const PassParams& p, unsigned char* lds, float* xsc, int xpitch, int g_lo, int gpt,
-                                             int row0, int nrows, int lane) {
-    constexpr int kMaxPartials = 4;  // 64 lanes x 4: the gate/up grid has at most 256 blocks
-#pragma unroll 1
-    for (int rr = 0; rr < nrows; ++rr) {
-        const int r = row0 + rr, rs = min(r, p.t - 1);
-        const unsigned short* hrow = p.x + static_cast<std::size_t>(rs) * p.ld_x + 128 * g_lo;
-        uint4 hb[NQ];
+struct H16Row {
+    uint4 hb[NQ];
+    float pm[4];  // 64 lanes x 4: the gate/up grid has at most 256 blocks
+};
+
+template <int NQ>
+__device__ __forceinline__ void h16_issue(const PassParams& p, int g_lo, int gpt, int r, int lane, H16Row<NQ>& h) {
+    const int rs = min(r, p.t - 1);
+    const unsigned short* hrow = p.x + static_cast<std::size_t>(rs) * p.ld_x + 128 * g_lo;
 #pragma unroll
-        for (int e = 0; e < NQ; ++e)
-            hb[e] = *reinterpret_cast<const uint4*>(hrow + 128 * min(4 * e + lane / 16, gpt - 1) + 8 * (lane % 16));
-        float pm[kMaxPartials];
+    for (int e = 0; e < NQ; ++e)
+        h.hb[e] = *reinterpret_cast<const uint4*>(hrow + 128 * min(4 * e + lane / 16, gpt - 1) + 8 * (lane % 16));
 #pragma unroll
-        for (int i = 0; i < kMaxPartials; ++i)
-            pm[i] = p.hmax[static_cast<std::size_t>(rs) * p.hmax_blocks + min(lane + 64 * i, p.hmax_blocks - 1)];
-        float m = fmaxf(fmaxf(pm[0], pm[1]), fmaxf(pm[2], pm[3]));
+    for (int i = 0; i < 4; ++i)
+        h.pm[i] = p.hmax[static_cast<std::size_t>(rs) * p.hmax_blocks + min(lane + 64 * i, p.hmax_blocks - 1)];
+}
+
+template <int NQ>
+__device__ __forceinline__ void h16_stage(unsigned char* lds, float* xsc, int xpitch, int gpt, int r, int lane, const H16Row<NQ>& h) {
+    float m = fmaxf(fmaxf(h.pm[0], h.pm[1]), fmaxf(h.pm[2], h.pm[3]));
 #pragma unroll
-        for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-        const float rscale = m > 0.0f ? __fdiv_rn(m, 127.0f) : 1.0f;
-        const float rinv = __fdiv_rn(1.0f, rscale);
-        if (lane == 0) xsc[r] = rscale;
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+    const float rscale = m > 0.0f ? __fdiv_rn(m, 127.0f) : 1.0f;
+    const float rinv = __fdiv_rn(1.0f, rscale);
+    if (lane == 0) xsc[r] = rscale;
 #pragma unroll
-        for (int e = 0; e < NQ; ++e) {
-            if (4 * e >= gpt) break;  // uniform
-            const int g = 4 * e + lane / 16;
-            const unsigned w[4] = {hb[e].x, hb[e].y, hb[e].z, hb[e].w};
-            unsigned packed[2] = {0u, 0u};
+    for (int e = 0; e < NQ; ++e) {
+        if (4 * e >= gpt) break;  // uniform
+        const int g = 4 * e + lane / 16;
+        const unsigned w[4] = {h.hb[e].x, h.hb[e].y, h.hb[e].z, h.hb[e].w};
+        unsigned packed[2] = {0u, 0u};
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const float v = f16_bits_to_f32(static_cast<unsigned short>((w[j / 2] >> (16 * (j % 2))) & 0xFFFFu));
-                packed[j / 4] |= (static_cast<unsigned>(quantize_act(v, rinv)) & 0xFFu) << (8 * (j % 4));
-            }
-            if (g < gpt) *reinterpret_cast<uint2*>(lds + r * xpitch + 128 * g + 8 * (lane % 16)) = make_uint2(packed[0], packed[1]);
+        for (int j = 0; j < 8; ++j) {
+            const float v = f16_bits_to_f32(static_cast<unsigned short>((w[j / 2] >> (16 * (j % 2))) & 0xFFFFu));
+            packed[j / 4] |= (static_cast<unsigned>(quantize_act(v, rinv)) & 0xFFu) << (8 * (j % 4));
         }
+        if (g < gpt) *reinterpret_cast<uint2*>(lds + r * xpitch + 128 * g + 8 * (lane % 16)) = make_uint2(packed[0], packed[1]);
     }
 }
 
@@ -240,7 +243,12 @@ __global__ void __launch_bounds__(kThreads) pass_kernel(const PassParams p) {
     // issued before any weight request of the block (a bare barrier orders the issue, not the arrival): behind a
     // weight burst these loads would wait in the memory queues, and waiting for them before the burst (as a block
     // barrier would) leaves the weight stream idle for their round trip. The workers wait for the loaders' flag. The
-    // q8 down pass quantizes H while it stages it, every wave one row, ahead of the burst. ----
+    // q8 down pass quantizes H while it stages it: per 128 columns every wave one row, ahead of the burst; in the
+    // stack's per-token form (binary16 H, K-parts of up to 16 groups) the loader waves issue their 4 rows' loads
+    // before any weight request, as for X, and quantize the rows while the weights stream. ----
+    constexpr bool kQ8Down = XT == kActI8 && !SWIGLU;
+    [[maybe_unused]] H16Row<4> hrows[4];
+    const bool h16_loaders = kQ8Down && p.h16 && gpt <= 16;  // (uniform)
     constexpr bool kEarly = !(XT == kActI8 && !SWIGLU);  // X loads in flight under the weight issue
     float xsv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     // the loaders' share of the block's weight scales (row runs of gpt words)
@@ -258,15 +266,22 @@ __global__ void __launch_bounds__(kThreads) pass_kernel(const PassParams p) {
         // q8 down: H (float32 per 128 columns; binary16 in the stack's per-token form) quantized as the activation
         // quantizer does (rule RECIPROCAL, scale = max / 127), per 128 columns or with the row maximum of the gate/up
         // pass's partial maxima (per token)
-        if (p.h16) {
-            if (gpt <= 16) stage_h16_q8<4>(p, lds, xsc, xpitch, g_lo, gpt, wave, 1, lane);
-            else stage_h16_q8<6>(p, lds, xsc, xpitch, g_lo, gpt, wave, 1, lane);
-        } else if (gpt <= 14) {
-            stage_h_q8<7, 1>(p, lds, xsc, xpitch, g_lo, gpt, wave, 1, lane);
+        if (h16_loaders) {
+            if (wave < kLoaders) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) h16_issue<4>(p, g_lo, gpt, 4 * wave + j, lane, hrows[j]);
+            }
+            __builtin_amdgcn_s_barrier();  // the loaders' H requests are issued before any weight request
+        } else if (p.h16) {
+            H16Row<6> h6;
+            h16_issue<6>(p, g_lo, gpt, wave, lane, h6);
+            h16_stage<6>(lds, xsc, xpitch, gpt, wave, lane, h6);
+            __syncthreads();
         } else {
-            stage_h_q8<12, 1>(p, lds, xsc, xpitch, g_lo, gpt, wave, 1, lane);
+            if (gpt <= 14) stage_h_q8<7, 1>(p, lds, xsc, xpitch, g_lo, gpt, wave, 1, lane);
+            else stage_h_q8<12, 1>(p, lds, xsc, xpitch, g_lo, gpt, wave, 1, lane);
+            __syncthreads();
         }
-        __syncthreads();
     } else {
         if (wave < kLoaders) {
             const int chunks = Q8 ? kw / 16 : kw / 8;  // 16-byte chunks of a row
@@ -304,6 +319,12 @@ __global__ void __launch_bounds__(kThreads) pass_kernel(const PassParams p) {
                     if (lane < nsc) xsc[p.per_token ? 4 * wave + j : (4 * wave + j) * gpt + lane] = xsv[j];
             }
             __builtin_amdgcn_s_waitcnt(0);  // vmcnt(0) lgkmcnt(0): the direct X loads have landed in LDS
+        }
+        if constexpr (kQ8Down) {
+            if (h16_loaders) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) h16_stage<4>(lds, xsc, xpitch, gpt, 4 * wave + j, lane, hrows[j]);
+            }
         }
         __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS writes are done
         if (lane == 0) __hip_atomic_fetch_add(&ready, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
