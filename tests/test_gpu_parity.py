@@ -1036,6 +1036,20 @@ def test_mlp_stack_small_q8(sm, t, act):
     assert err1 < 2e-3, err1
 
 
+def test_mlp_stack_small_q8_wide_k_parts(sm):
+    """Per token, a shape whose down pass takes K-parts of 18 groups (hidden 768, inter 11008): the binary16 H is
+    staged by every wave before the weight burst there (the loaders' form takes parts of up to 16 groups), against the
+    oracle with binary16 H."""
+    say("mlp stack small q8 wide K-parts")
+    rng = np.random.default_rng(17)
+    layers = _stack_weights(sm, rng, 2, 768, 11008, rule=1)
+    x = bf16_inputs(rng, (5, 768))
+    y1 = host(sm.mlp_stack(1, dev(x, torch.bfloat16), layers[:1], act_block=0))
+    assert rel_rms(y1, _oracle_stack(1, x, layers[:1], 0, h16=True)) < 2e-3
+    y = host(sm.mlp_stack(1, dev(x, torch.bfloat16), layers, act_block=0))
+    assert rel_rms(y, _oracle_stack(1, x, layers, 0, h16=True)) < STACK3_DRIFT_Q8_TOKEN
+
+
 @pytest.mark.parametrize("act", [0, 128])
 def test_mlp_stack_small_q8_full_size(sm, act):
     """The M = 16 q8 stack at the model's shape (H 2560, I 9728), two layers, against the oracle."""
