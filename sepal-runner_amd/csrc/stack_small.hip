@@ -212,8 +212,9 @@ __device__ __forceinline__ void stage_h_q8(const PassParams& p, unsigned char* l
 // pairs at once, wait for the flag, and multiply. The weights are in flight while the scales arrive, and no worker's
 // load issue (which stalls when the memory queues are full) holds up a barrier.
 // STREAM: the weights in the stream layout (make_stream_layout): each (tile, group) pair's 2 KB contiguous, already in
-// the MFMA operand order, so a pair is two 1 KB loads and needs no LDS transpose.
-template <int XT, bool SWIGLU, int YT, bool STREAM = false>
+// the MFMA operand order, so a pair is two 1 KB loads and needs no LDS transpose. H16: the q8 down pass of the stack's
+// per-token form (binary16 H, p.h16 set), an instance of its own so that the per-128 form keeps its own code.
+template <int XT, bool SWIGLU, int YT, bool STREAM = false, bool H16 = false>
 __global__ void __launch_bounds__(kThreads) pass_kernel(const PassParams p) {
     extern __shared__ __align__(16) unsigned char lds[];
     __shared__ unsigned ready;
@@ -248,7 +249,7 @@ __global__ void __launch_bounds__(kThreads) pass_kernel(const PassParams p) {
     // before any weight request, as for X, and quantize the rows while the weights stream. ----
     constexpr bool kQ8Down = XT == kActI8 && !SWIGLU;
     [[maybe_unused]] H16Row<4> hrows[4];
-    const bool h16_loaders = kQ8Down && p.h16 && gpt <= 16;  // (uniform)
+    const bool h16_loaders = kQ8Down && H16 && gpt <= 16;  // (uniform)
     constexpr bool kEarly = !(XT == kActI8 && !SWIGLU);  // X loads in flight under the weight issue
     float xsv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     // the loaders' share of the block's weight scales (row runs of gpt words)
@@ -272,7 +273,7 @@ __global__ void __launch_bounds__(kThreads) pass_kernel(const PassParams p) {
                 for (int j = 0; j < 4; ++j) h16_issue<4>(p, g_lo, gpt, 4 * wave + j, lane, hrows[j]);
             }
             __builtin_amdgcn_s_barrier();  // the loaders' H requests are issued before any weight request
-        } else if (p.h16) {
+        } else if (H16) {
             H16Row<6> h6;
             h16_issue<6>(p, g_lo, gpt, wave, lane, h6);
             h16_stage<6>(lds, xsc, xpitch, gpt, wave, lane, h6);
@@ -940,11 +941,12 @@ void launch_small_layer_q8(const SmallStackPlan& plan, std::size_t t, std::size_
     d.hmax = hmax;
     d.hmax_blocks = a.blocks_per_part;
 
-    const auto kd = stream_w ? pass_kernel<kActI8, false, SEPAL_HIP_F32, true> : pass_kernel<kActI8, false, SEPAL_HIP_F32>;
-    static std::size_t raised_d[2] = {0, 0};
+    const auto kd = per_token ? (stream_w ? pass_kernel<kActI8, false, SEPAL_HIP_F32, true, true> : pass_kernel<kActI8, false, SEPAL_HIP_F32, false, true>)
+                              : (stream_w ? pass_kernel<kActI8, false, SEPAL_HIP_F32, true> : pass_kernel<kActI8, false, SEPAL_HIP_F32>);
+    static std::size_t raised_d[4] = {0, 0, 0, 0};
     const std::size_t gpt = (inter / 128 + plan.parts - 1) / plan.parts;
     const std::size_t lds_d = pass_lds(gpt * 128);
-    raise_lds(kd, lds_d, raised_d[stream_w ? 1 : 0]);
+    raise_lds(kd, lds_d, raised_d[(stream_w ? 1 : 0) + (per_token ? 2 : 0)]);
     kd<<<dim3(d.parts * d.blocks_per_part), dim3(kThreads), lds_d, stream>>>(d);
     check_launch("small-M q8 stack down launch");
     // y = sum of the parts; the next layer's bf16 input (xn) and its int8 form
