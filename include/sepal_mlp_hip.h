@@ -261,15 +261,15 @@ SEPAL_HIP_API int32_t sepal_hip_packed_load(const char* path, int8_t* q, size_t 
  * kind 0 = w8g (x bf16 [T, hidden]; H binary16: within the 2e-3 bar of the reference's float32 H, about 8e-4 at the
  * model's shape), kind 2 = w8g with H float32 as the reference keeps it (the down multiply on its bf16 hi + lo pairs,
  * twice that multiply's MFMA work; above 64 rows the gate/up epilogue writes the pairs itself), kind 1 = q8 (x bf16; activations quantised per act_block before each multiply;
- * H float32). Weight arrays hold `layers` device pointers each: gate_up int8 [2*inter, hidden] + scales
+ * H float32 per 128 columns, binary16 with one scale per token as the reference's GPU int8 path quantizes it). Weight arrays hold `layers` device pointers each: gate_up int8 [2*inter, hidden] + scales
  * [2*inter, hidden/128]; down int8 [hidden, inter] + scales [hidden, inter/128]. x is overwritten with the last layer's
  * input. Scratch (H, quantised activations, partial sums) comes from the workspace of (device, stream).
  * For kind 0 with T <= 16 (and hidden <= 3072, both multiples of 128 with at least 512 for hidden) the layer runs as
  * three launches: whole-K gate/up tiles per CU, the down multiply in K-parts, and a pass that adds the parts in order
  * and applies the RMSNorm; the float32 sums there are rounded in another order than gemm_w8g's (within tolerance).
  * For kind 1 with T <= 16 (same shape limits) the layer runs the same three-launch scheme on int8 MFMAs: the gate/up
- * pass writes H in float32 (with, per token, its partial row maxima), the down pass quantizes its slice of H while
- * staging it, and the finish pass quantizes the next layer's input; the int8 products are exact, the float sums
+ * pass writes H (float32 per 128 columns; per token binary16, with its partial row maxima), the down pass quantizes its
+ * slice of H while staging it, and the finish pass quantizes the next layer's input; the int8 products are exact, the float sums
  * are rounded in another order than gemm_q8's (within tolerance). */
 SEPAL_HIP_API int32_t sepal_hip_mlp_stack(int32_t kind, size_t layers, size_t t, size_t hidden, size_t inter, void* x,
                             const int8_t* const* w_gate_up, const float* const* s_gate_up, const int8_t* const* w_down,
