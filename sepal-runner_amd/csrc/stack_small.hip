@@ -23,6 +23,7 @@
 // The q8 form multiplies int8 X (H quantized while the down pass stages it) by the int8 weights on int8 MFMAs: exact
 // int32 group sums, then the cpu-q8 float chain per group.
 #include <algorithm>
+#include <type_traits>
 
 #include "common.hpp"
 #include "gemm_kernels.hpp"
@@ -239,8 +240,9 @@ __global__ void __launch_bounds__(kThreads) pass_kernel(const PassParams p) {
     if (tid == 0) ready = 0u;
     if (tid < 16) row_max[tid] = 0u;
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the counter is zero before the barrier below lets any wave count
-    // ---- X (rows past T repeat row T - 1 and feed only outputs that are never stored). The loader waves stage all 16
-    // rows straight from global memory into LDS (direct loads, no registers; 4 rows a wave), and their requests are
+    // ---- X (rows past T are not loaded: each MFMA output row depends on its own X row only, and rows past T feed
+    // only outputs that are never stored). The loader waves stage the rows straight from global memory into LDS
+    // (direct loads, no registers; 4 rows a wave), and their requests are
     // issued before any weight request of the block (a bare barrier orders the issue, not the arrival): behind a
     // weight burst these loads would wait in the memory queues, and waiting for them before the burst (as a block
     // barrier would) leaves the weight stream idle for their round trip. The workers wait for the loaders' flag. The
@@ -274,33 +276,44 @@ __global__ void __launch_bounds__(kThreads) pass_kernel(const PassParams p) {
             }
             __builtin_amdgcn_s_barrier();  // the loaders' H requests are issued before any weight request
         } else if (H16) {
-            H16Row<6> h6;
-            h16_issue<6>(p, g_lo, gpt, wave, lane, h6);
-            h16_stage<6>(lds, xsc, xpitch, gpt, wave, lane, h6);
+            if (wave < p.t) {
+                H16Row<6> h6;
+                h16_issue<6>(p, g_lo, gpt, wave, lane, h6);
+                h16_stage<6>(lds, xsc, xpitch, gpt, wave, lane, h6);
+            }
             __syncthreads();
         } else {
-            if (gpt <= 14) stage_h_q8<7, 1>(p, lds, xsc, xpitch, g_lo, gpt, wave, 1, lane);
-            else stage_h_q8<12, 1>(p, lds, xsc, xpitch, g_lo, gpt, wave, 1, lane);
+            if (wave >= p.t) {
+            } else if (gpt <= 14) {
+                stage_h_q8<7, 1>(p, lds, xsc, xpitch, g_lo, gpt, wave, 1, lane);
+            } else {
+                stage_h_q8<12, 1>(p, lds, xsc, xpitch, g_lo, gpt, wave, 1, lane);
+            }
             __syncthreads();
         }
     } else {
         if (wave < kLoaders) {
             const int chunks = Q8 ? kw / 16 : kw / 8;  // 16-byte chunks of a row
             const int esz = Q8 ? 1 : 2;
+            const auto stage_rows = [&](auto all_live) __attribute__((always_inline)) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int r = 4 * wave + j, xr = min(r, p.t - 1);
-                const unsigned char* xrow = reinterpret_cast<const unsigned char*>(p.x) + (static_cast<std::size_t>(xr) * p.ld_x + 128 * g_lo) * esz;
+                for (int j = 0; j < 4; ++j) {
+                    const int r = 4 * wave + j, xr = min(r, p.t - 1);
+                    const unsigned char* xrow = reinterpret_cast<const unsigned char*>(p.x) + (static_cast<std::size_t>(xr) * p.ld_x + 128 * g_lo) * esz;
 #pragma unroll
-                for (int e = 0; e < (Q8 ? kXChunks / 2 : kXChunks); ++e)
-                    if (lane + 64 * e < chunks)
-                        __builtin_amdgcn_global_load_lds((global_void*)(xrow + 16 * (lane + 64 * e)),
-                                                         (lds_void*)(lds + r * xpitch + 1024 * e), 16, 0, 0);
-                if constexpr (Q8) {
-                    const int nsc = p.per_token ? 1 : gpt;
-                    xsv[j] = p.xs[static_cast<std::size_t>(xr) * p.ld_xs + (p.per_token ? 0 : g_lo + min(lane, nsc - 1))];
+                    for (int e = 0; e < (Q8 ? kXChunks / 2 : kXChunks); ++e)
+                        if ((decltype(all_live)::value || r < p.t) && lane + 64 * e < chunks)
+                            __builtin_amdgcn_global_load_lds((global_void*)(xrow + 16 * (lane + 64 * e)),
+                                                             (lds_void*)(lds + r * xpitch + 1024 * e), 16, 0, 0);
+                    if constexpr (Q8) {
+                        const int nsc = p.per_token ? 1 : gpt;
+                        xsv[j] = p.xs[static_cast<std::size_t>(xr) * p.ld_xs + (p.per_token ? 0 : g_lo + min(lane, nsc - 1))];
+                    }
                 }
-            }
+            };
+            // (a wave whose four rows are all below T runs the unguarded loop)
+            if (4 * wave + 3 < p.t) stage_rows(std::true_type{});
+            else stage_rows(std::false_type{});
         }
         __builtin_amdgcn_s_barrier();  // the loaders' X requests are issued before any weight request
     }
