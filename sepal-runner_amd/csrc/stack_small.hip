@@ -240,15 +240,15 @@ __global__ void __launch_bounds__(kThreads) pass_kernel(const PassParams p) {
     if (tid == 0) ready = 0u;
     if (tid < 16) row_max[tid] = 0u;
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the counter is zero before the barrier below lets any wave count
-    // ---- X (rows past T are not loaded: each MFMA output row depends on its own X row only, and rows past T feed
-    // only outputs that are never stored). The loader waves stage the rows straight from global memory into LDS
-    // (direct loads, no registers; 4 rows a wave), and their requests are
-    // issued before any weight request of the block (a bare barrier orders the issue, not the arrival): behind a
-    // weight burst these loads would wait in the memory queues, and waiting for them before the burst (as a block
-    // barrier would) leaves the weight stream idle for their round trip. The workers wait for the loaders' flag. The
-    // q8 down pass quantizes H while it stages it: per 128 columns every wave one row, ahead of the burst; in the
-    // stack's per-token form (binary16 H, K-parts of up to 16 groups) the loader waves issue their 4 rows' loads
-    // before any weight request, as for X, and quantize the rows while the weights stream. ----
+    // ---- X. The loader waves stage the rows straight from global memory into LDS (direct loads, no registers; 4 rows
+    // a wave), and their requests are issued before any weight request of the block (a bare barrier orders the issue,
+    // not the arrival): behind a weight burst these loads would wait in the memory queues, and waiting for them before
+    // the burst (as a block barrier would) leaves the weight stream idle for their round trip. The workers wait for
+    // the loaders' flag. Rows past T are not loaded (each MFMA output row depends on its own X row only, and those
+    // rows feed only outputs that are never stored). The q8 down pass quantizes H while it stages it: per 128 columns
+    // every wave one row, ahead of the burst; in the stack's per-token form (binary16 H, K-parts of up to 16 groups)
+    // the loader waves issue their 4 rows' loads before any weight request, as for X, and quantize the rows while the
+    // weights stream (all 16 rows: guarding them measured slower). ----
     constexpr bool kQ8Down = XT == kActI8 && !SWIGLU;
     [[maybe_unused]] H16Row<4> hrows[4];
     const bool h16_loaders = kQ8Down && H16 && gpt <= 16;  // (uniform)
@@ -283,11 +283,9 @@ __global__ void __launch_bounds__(kThreads) pass_kernel(const PassParams p) {
             }
             __syncthreads();
         } else {
-            if (wave >= p.t) {
-            } else if (gpt <= 14) {
-                stage_h_q8<7, 1>(p, lds, xsc, xpitch, g_lo, gpt, wave, 1, lane);
-            } else {
-                stage_h_q8<12, 1>(p, lds, xsc, xpitch, g_lo, gpt, wave, 1, lane);
+            if (wave < p.t) {
+                if (gpt <= 14) stage_h_q8<7, 1>(p, lds, xsc, xpitch, g_lo, gpt, wave, 1, lane);
+                else stage_h_q8<12, 1>(p, lds, xsc, xpitch, g_lo, gpt, wave, 1, lane);
             }
             __syncthreads();
         }
