@@ -339,7 +339,9 @@ def main():
 
     extra = {"c3_down_kernel": {"ms": round(ms_dn, 4), "tflops": round(dn_tflops, 1),
                                 "frac_bf16_peak": round(dn_tflops / PEAK["bf16_tflops"], 4)}}
-    if not args.no_extra:
+
+    def measure_extras():
+        nonlocal layers, hbuf
         # ---- the practical ceiling of these shapes: hipBLASLt's plain bf16 GEMM (torch.matmul, no dequantization, no
         # group scales, no epilogue) at the C3 gate/up and down shapes, X [M, K] times W[N, K]^T, timed the same way ----
         ceil = {}
@@ -588,6 +590,13 @@ def main():
             del w_o, wq_o, sw_o, x_o, xq_o, sx_o, wqy, wsy, xqy, xsy
         extra["per_channel_int8_m15872"] = s8
         log(f"per-channel int8 family and the AVX2 int8 multiply (M=15872): {s8}")
+
+    if not args.no_extra:
+        try:
+            measure_extras()
+        except Exception as e:  # an extra that fails is reported in the line; the headline value stands
+            log(f"extra measurements stopped: {e!r}")
+            extra["error"] = repr(e)[:300]
 
     cpu = None
     if not args.no_cpu:
