@@ -1066,6 +1066,41 @@ def test_mlp_stack_small_q8_full_size(sm, act):
     assert rel_rms(y, _oracle_stack(1, x, layers, act, h16=h16)) < 2e-3
 
 
+def _stream_layout_np(w, interleave):
+    """The stream layout as the header states it, restated: pair (tile, group) is 2 KB at (tile * K/128 + group) *
+    2048; its half h at + 1024 h holds, for lane l, the 16 bytes of weight row tile_row(tile, l % 16) at k = 128 group
+    + 64 h + 16 (l // 16); tile_row takes 8 gate rows and the 8 up rows of the same features under the 64-row gate/up
+    interleave (packed row 128 b + r is gate feature 64 b + r, row 128 b + 64 + r its up row), else rows 16 tile + c."""
+    n, k = w.shape
+    out = np.empty(n * k, dtype=np.int8)
+    for tile in range(n // 16):
+        for c in range(16):
+            if interleave:
+                b, r0 = tile // 8, 8 * (tile % 8)
+                row = 128 * b + r0 + c if c < 8 else 128 * b + 64 + r0 + (c - 8)
+            else:
+                row = 16 * tile + c
+            for g in range(k // 128):
+                base = (tile * (k // 128) + g) * 2048
+                for h in range(2):
+                    for q in range(4):
+                        lane = c + 16 * q
+                        o = base + 1024 * h + 16 * lane
+                        out[o:o + 16] = w[row, 128 * g + 64 * h + 16 * q:128 * g + 64 * h + 16 * q + 16]
+    return out
+
+
+@pytest.mark.parametrize("interleave", [False, True])
+def test_stream_layout_bytes_are_the_documented_permutation(sm, interleave):
+    """sepal_hip_w8g_make_stream_layout writes exactly the permutation the header documents (a format integrators
+    may build or check on their own), on a matrix with a row stride above K."""
+    rng = np.random.default_rng(12 + interleave)
+    n, k, ld = 256, 512, 640
+    w = rng.integers(-127, 128, size=(n, ld), dtype=np.int8)
+    got = host(sm.w8g_make_stream_layout(dev(w)[:, :k], interleave))
+    assert np.array_equal(got, _stream_layout_np(w[:, :k], interleave))
+
+
 @pytest.mark.parametrize("kind,act_block", [(0, 128), (1, 0), (1, 128)])
 @pytest.mark.parametrize("t", [1, 5, 16])
 def test_mlp_stack_stream_layout(sm, t, kind, act_block):
