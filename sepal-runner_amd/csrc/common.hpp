@@ -5,9 +5,11 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <map>
 #include <stdexcept>
 #include <mutex>
 #include <string>
+#include <utility>
 
 #include "sepal_mlp_hip.h"
 
@@ -35,6 +37,22 @@ inline void check_launch(const char* what) {
 
 inline void require(bool ok, const std::string& message) {
     if (!ok) throw InvalidArgument(message);
+}
+
+// Allows `kernel` up to `lds` bytes of dynamic LDS on the current device. The largest size allowed so far is kept per
+// (kernel, device) pair, and a mutex orders the check and the attribute call, so launches from several threads or on
+// several devices each see the attribute set before their launch.
+inline void raise_dynamic_lds(const void* kernel, std::size_t lds, const char* what) {
+    int device = 0;
+    if (hipGetDevice(&device) != hipSuccess) throw LaunchError(std::string(what) + ": hipGetDevice failed");
+    static std::mutex mutex;
+    static std::map<std::pair<const void*, int>, std::size_t> raised;
+    std::lock_guard<std::mutex> lock(mutex);
+    std::size_t& done = raised[{kernel, device}];
+    if (lds <= done) return;
+    if (hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)) != hipSuccess)
+        throw LaunchError(std::string(what) + ": hipFuncSetAttribute(MaxDynamicSharedMemorySize) failed");
+    done = lds;
 }
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<std::uintptr_t>(p) & 15u) == 0; }

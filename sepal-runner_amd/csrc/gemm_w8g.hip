@@ -1095,13 +1095,7 @@ void launch_big2(const BigParams& p, hipStream_t stream) {
     const auto kernel = v2::gemm_big2<XT, EP, YT, WN>;
     const std::size_t lds = v2::lds_bytes<WN>();
     static_assert(v2::lds_bytes<WN>() <= (160u << 10), "LDS of one CU");
-    static std::size_t raised = 0;
-    if (lds > raised) {
-        if (hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                static_cast<int>(lds)) != hipSuccess)
-            throw LaunchError("gemm_w8g large-M: hipFuncSetAttribute(MaxDynamicSharedMemorySize) failed");
-        raised = lds;
-    }
+    raise_dynamic_lds(reinterpret_cast<const void*>(kernel), lds, "gemm_w8g large-M");
     kernel<<<dim3(p.tiles_m * p.tiles_n), dim3(128 * WN), lds, stream>>>(p);
 }
 

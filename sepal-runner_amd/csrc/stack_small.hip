@@ -762,13 +762,8 @@ std::size_t pass_lds(std::size_t row_bytes) {
 }
 
 template <typename Kernel>
-void raise_lds(Kernel kernel, std::size_t lds, std::size_t& raised) {
-    if (lds > raised) {
-        if (hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                static_cast<int>(lds)) != hipSuccess)
-            throw LaunchError("small-M stack: hipFuncSetAttribute(MaxDynamicSharedMemorySize) failed");
-        raised = lds;
-    }
+void raise_lds(Kernel kernel, std::size_t lds) {
+    raise_dynamic_lds(reinterpret_cast<const void*>(kernel), lds, "small-M stack");
 }
 
 } // namespace
@@ -850,9 +845,8 @@ void launch_small_layer(const SmallStackPlan& plan, std::size_t t, std::size_t h
     a.per_block = plan.tiles_per_block;
     a.blocks_per_part = (a.tiles + a.per_block - 1) / a.per_block;
     const auto ka = stream_w ? pass_kernel<SEPAL_HIP_BF16, true, SEPAL_HIP_F16, true> : pass_kernel<SEPAL_HIP_BF16, true, SEPAL_HIP_F16>;
-    static std::size_t raised_a[2] = {0, 0};
     const std::size_t lds_a = pass_lds(2 * hidden);
-    raise_lds(ka, lds_a, raised_a[stream_w ? 1 : 0]);
+    raise_lds(ka, lds_a);
     ka<<<dim3(a.blocks_per_part), dim3(kThreads), lds_a, stream>>>(a);
     check_launch("small-M stack gate/up launch");
     // down: H [t, inter] -> P [parts][t][hidden]
@@ -873,10 +867,9 @@ void launch_small_layer(const SmallStackPlan& plan, std::size_t t, std::size_t h
     d.per_block = plan.units_per_block;
     d.blocks_per_part = (d.tiles + d.per_block - 1) / d.per_block;
     const auto kd = stream_w ? pass_kernel<SEPAL_HIP_F16, false, SEPAL_HIP_F32, true> : pass_kernel<SEPAL_HIP_F16, false, SEPAL_HIP_F32>;
-    static std::size_t raised_d[2] = {0, 0};
     const std::size_t gpt = (inter / 128 + plan.parts - 1) / plan.parts;
     const std::size_t lds_d = pass_lds(gpt * 256);
-    raise_lds(kd, lds_d, raised_d[stream_w ? 1 : 0]);
+    raise_lds(kd, lds_d);
     kd<<<dim3(d.parts * d.blocks_per_part), dim3(kThreads), lds_d, stream>>>(d);
     check_launch("small-M stack down launch");
     // y = sum of the parts; next layer's input
@@ -924,9 +917,8 @@ void launch_small_layer_q8(const SmallStackPlan& plan, std::size_t t, std::size_
     a.h16 = per_token ? 1 : 0;
     a.pmax = hmax;
     const auto ka = stream_w ? pass_kernel<kActI8, true, SEPAL_HIP_F32, true> : pass_kernel<kActI8, true, SEPAL_HIP_F32>;
-    static std::size_t raised_a[2] = {0, 0};
     const std::size_t lds_a = pass_lds(hidden);
-    raise_lds(ka, lds_a, raised_a[stream_w ? 1 : 0]);
+    raise_lds(ka, lds_a);
     ka<<<dim3(a.blocks_per_part), dim3(kThreads), lds_a, stream>>>(a);
     check_launch("small-M q8 stack gate/up launch");
     // down: H quantized per block of 128 or per token while staged -> P [parts][t][hidden]
@@ -954,10 +946,9 @@ void launch_small_layer_q8(const SmallStackPlan& plan, std::size_t t, std::size_
 
     const auto kd = per_token ? (stream_w ? pass_kernel<kActI8, false, SEPAL_HIP_F32, true, true> : pass_kernel<kActI8, false, SEPAL_HIP_F32, false, true>)
                               : (stream_w ? pass_kernel<kActI8, false, SEPAL_HIP_F32, true> : pass_kernel<kActI8, false, SEPAL_HIP_F32>);
-    static std::size_t raised_d[4] = {0, 0, 0, 0};
     const std::size_t gpt = (inter / 128 + plan.parts - 1) / plan.parts;
     const std::size_t lds_d = pass_lds(gpt * 128);
-    raise_lds(kd, lds_d, raised_d[(stream_w ? 1 : 0) + (per_token ? 2 : 0)]);
+    raise_lds(kd, lds_d);
     kd<<<dim3(d.parts * d.blocks_per_part), dim3(kThreads), lds_d, stream>>>(d);
     check_launch("small-M q8 stack down launch");
     // y = sum of the parts; the next layer's bf16 input (xn) and its int8 form
@@ -989,8 +980,7 @@ void launch_parts_sum(int parts, bool add, std::size_t t, std::size_t n, const f
 template <int XT, bool SWIGLU, int YT, bool STREAM = false>
 void launch_pass(const stack::PassParams& p, std::size_t lds, hipStream_t stream) {
     const auto kernel = stack::pass_kernel<XT, SWIGLU, YT, STREAM>;
-    static std::size_t raised = 0;
-    raise_lds(kernel, lds, raised);
+    raise_lds(kernel, lds);
     kernel<<<dim3(p.parts * p.blocks_per_part), dim3(stack::kThreads), lds, stream>>>(p);
     check_launch("small-M multiply pass launch");
 }

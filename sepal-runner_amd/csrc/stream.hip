@@ -387,13 +387,7 @@ void launch_mt(const GemmArgs& a, hipStream_t stream) {
         p.partial = reinterpret_cast<float*>(ws + kCounterBytes);
     }
     if (lds > (64u << 10)) {
-        static std::size_t raised = 0;  // per kernel instance: the largest dynamic LDS size allowed so far
-        if (lds > raised) {
-            if (hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                    static_cast<int>(lds)) != hipSuccess)
-                throw LaunchError("small-M multiply: hipFuncSetAttribute(MaxDynamicSharedMemorySize) failed");
-            raised = lds;
-        }
+        raise_dynamic_lds(reinterpret_cast<const void*>(kernel), lds, "small-M multiply");
     }
     kernel<<<dim3(p.spans * p.splits), dim3(256), lds, stream>>>(p);
     check_launch("small-M stream kernel launch");
