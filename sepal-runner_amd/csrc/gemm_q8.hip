@@ -14,6 +14,8 @@
 // the next group starts (a second set of accumulators holds the chain).
 // Small-M path: stream.hip (MFMA 16x16x64 i8; a split of K keeps the sums exact but adds the splits' partial chains in
 // split order, within tolerance, not bit for bit).
+#include <atomic>
+
 #include "common.hpp"
 #include "gemm_kernels.hpp"
 
@@ -1000,14 +1002,17 @@ inline Params make_params(const GemmArgs& a) {
 
 // Compute units of the current device (cached per device).
 inline int device_cus() {
-    static int cached[64] = {};
+    static std::atomic<int> cached[64] = {};
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0) throw LaunchError("gemm_s8: hipGetDevice failed");
-    if (dev < 64 && cached[dev] > 0) return cached[dev];
+    if (dev < 64) {
+        const int known = cached[dev].load(std::memory_order_relaxed);
+        if (known > 0) return known;
+    }
     int cus = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
         throw LaunchError("gemm_s8: device query failed");
-    if (dev < 64) cached[dev] = cus;
+    if (dev < 64) cached[dev].store(cus, std::memory_order_relaxed);
     return cus;
 }
 

@@ -25,6 +25,7 @@
 //   small M: at T <= 16 the M <= 16 stack's pass kernels (stack_small.hip) where the shape fits them; else, at
 //            T <= 32 with N < 8192, stream.hip (the weights streamed once, HBM-bound); else the large-M plan.
 #include <algorithm>
+#include <atomic>
 
 #include "common.hpp"
 #include "gemm_kernels.hpp"
@@ -1101,14 +1102,17 @@ void launch_big2(const BigParams& p, hipStream_t stream) {
 
 // Compute units of the current device (cached per device).
 inline int device_cus() {
-    static int cached[64] = {};
+    static std::atomic<int> cached[64] = {};
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0) throw LaunchError("gemm_w8g: hipGetDevice failed");
-    if (dev < 64 && cached[dev] > 0) return cached[dev];
+    if (dev < 64) {
+        const int known = cached[dev].load(std::memory_order_relaxed);
+        if (known > 0) return known;
+    }
     int cus = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
         throw LaunchError("gemm_w8g: device query failed");
-    if (dev < 64) cached[dev] = cus;
+    if (dev < 64) cached[dev].store(cus, std::memory_order_relaxed);
     return cus;
 }
 
