@@ -509,14 +509,15 @@ __global__ void __launch_bounds__(512) gemm_big(const Params p) {
     chain_epilogue<EP, YT, PER_TOKEN, PER_TOKEN && MODE == MODE_CHAIN>(p, acc, m0, n0, wm, ib, hh, lane, tid, col, reinterpret_cast<float*>(lw0));
 }
 
-// ---- the chain with one activation scale per token: two wave groups in alternation (gemm_chain) ---------------------
+// ---- the chain, two wave groups in alternation (gemm_chain) ---------------------------------------------------------
 //
 // The 128 x 256 tile of gemm_big's chain mode: 8 waves of 64 x 64 outputs (2 x 2 blocks of MFMA 32x32x32 i8), K in
 // steps of one group (128 bytes) through three LDS stages of 128-byte rows (chunk c of row r at c ^ sw8(r)), filled
 // straight from global memory through buffer descriptors (a 32-bit lane offset: the row, clamped to the last row, and
 // the swizzled chunk; the group's offset in the scalar offset; the LDS destination in scalar registers). Each block's
 // four MFMAs give its exact int32 group sums, and the cpu-q8 chain links them into the float accumulators
-// (acc = f_0 ws_0, then acc = fma(f_g, ws_g, acc); times the token's scale in the epilogue), each output's links in
+// (per token acc = f_0 ws_0, then acc = fma(f_g, ws_g, acc), times the token's scale in the epilogue; per 128 the
+// scale of a link is ws_g x xs_g of the output's row, from an LDS ring of the tile rows' scales), each output's links in
 // group order, so the results do not depend on how the work is scheduled.
 // Schedule: waves 0-3 (group A, one per SIMD) and 4-7 (group B) each alternate two slots per group, separated by
 // block barriers, so that in every slot one wave of each SIMD reads the LDS while the other runs MFMAs and the chain's
@@ -524,8 +525,9 @@ __global__ void __launch_bounds__(512) gemm_big(const Params p) {
 // the LDS together and then competed for the MFMA and VALU units together: 8% slower at C4). L(g) issues the wave's
 // share of group g + 2's direct loads (2 of the activations' and 4 of the weights' 1 KB loads, and its two weight
 // scales) into the stage of group g - 1 and reads all 16 operand fragments of group g; M(g) runs the group's four
-// blocks, each block's MFMAs with the link of the block two before it (whose sums were complete a block ago, so the
-// link's converts and fused multiply-adds interleave with the MFMAs). Group B runs one slot behind group A: slot 2g is
+// blocks, each block's MFMAs with the link of the block LAG before it (two per token, whose sums were complete a block
+// ago; one per 128, issued after the block's own MFMAs), so the link's converts and fused multiply-adds interleave with
+// the MFMAs. Group B runs one slot behind group A: slot 2g is
 // A L(g) and B M(g - 1), slot 2g + 1 is A M(g) and B L(g). Stage g mod 3 is last read in slot 2g + 1 and reloaded
 // (with group g + 3) from slot 2g + 2. At the end of L(g) a wave waits for its share of group g + 1 (issued in its
 // previous L slot), so both shares are complete by the barrier that ends slot 2g + 1, before group g + 1 is first
@@ -538,12 +540,17 @@ struct ChainParams {
 
 template <int EP, int YT, bool PER_TOKEN>
 __global__ void __launch_bounds__(512) gemm_chain(const ChainParams cp) {
-    static_assert(PER_TOKEN, "one activation scale per token (the chain's scale is the weight scale alone)");
     const Params& p = cp.p;
     constexpr int BM = 128, BN = 256;
-    constexpr int XDMA = BM / 64, WDMA = BN / 64, NLD = XDMA + WDMA + 2;  // a wave's loads per group (with 2 scales)
+    // a wave's loads per group: its operand shares, its 2 weight scales and, per 128, one activation scale
+    constexpr int XDMA = BM / 64, WDMA = BN / 64, NLD = XDMA + WDMA + 2 + (PER_TOKEN ? 0 : 1);
     __shared__ __align__(1024) u32x4 lx0[BM * 8], lx1[BM * 8], lx2[BM * 8];
     __shared__ __align__(1024) u32x4 lw0[BN * 8], lw1[BN * 8], lw2[BN * 8];
+    // per 128: the tile rows' activation scales of group g in ring slot (xb + g) mod 4. Four slots, not three: group
+    // B's M slot of group g reads the scales of groups g and g - 1 in the slot where group A writes those of group
+    // g + 2 (xb carries the ring on from tile to tile, so a tile's first write never meets the previous tile's last
+    // links)
+    __shared__ __align__(16) float lds_xs[4][BM];
     typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
     const auto xstage = [&](auto it) -> lds_u32x4* {
         constexpr int i = decltype(it)::value;
@@ -581,6 +588,7 @@ __global__ void __launch_bounds__(512) gemm_chain(const ChainParams cp) {
     const __amdgpu_buffer_rsrc_t xres = __builtin_amdgcn_make_buffer_rsrc(const_cast<signed char*>(p.x), 0, static_cast<int>(cp.x_bytes), 0x00020000);
     const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(const_cast<signed char*>(p.w), 0, static_cast<int>(cp.w_bytes), 0x00020000);
     const __amdgpu_buffer_rsrc_t wsres = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(p.ws), 0, static_cast<int>(cp.ws_bytes), 0x00020000);
+    const __amdgpu_buffer_rsrc_t xsres = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(p.xs), 0, static_cast<int>(cp.xs_bytes), 0x00020000);
     // a wave's share of a group's loads: direct load e fills LDS kilobyte wave + 8 e = rows 8 wave + 64 e + {0..7};
     // lane l writes slot l % 8 of row 8 wave + 64 e + l / 8, which holds chunk (l % 8) ^ sw8(row) = (l % 8) ^
     // ((4 wave + l / 16) & 7); rows past T or N repeat the last row (never stored)
@@ -588,7 +596,7 @@ __global__ void __launch_bounds__(512) gemm_chain(const ChainParams cp) {
     const int ib = wn / 2, hh = wn % 2;
     const int colrel[2] = {128 * ib + 32 * hh + lane % 32, 128 * ib + 64 + 32 * hh + lane % 32};
     // the tile's origin and the offsets that depend on it
-    int m0, n0, xoff[XDMA], woff[WDMA], ws_off0, ws_off1;
+    int m0, n0, xoff[XDMA], woff[WDMA], ws_off0, ws_off1, xs_off;
     const auto set_tile = [&]() __attribute__((always_inline)) {
         int tm, tn;
         tile_from_id(cur, p.tiles_m, p.tiles_n, tm, tn);
@@ -602,6 +610,8 @@ __global__ void __launch_bounds__(512) gemm_chain(const ChainParams cp) {
             woff[e] = min(n0 + 8 * wave + 64 * e + lane / 8, p.n - 1) * static_cast<int>(p.ld_w) + 16 * chunk;
         ws_off0 = min(n0 + colrel[0], p.n - 1) * static_cast<int>(p.ld_ws) * 4;
         ws_off1 = min(n0 + colrel[1], p.n - 1) * static_cast<int>(p.ld_ws) * 4;
+        // per 128: lane l % 16 of wave w loads the scale of tile row 16 w + l % 16 (clamped like the operands)
+        xs_off = min(m0 + 16 * wave + lane % 16, p.t - 1) * static_cast<int>(p.ld_xs) * 4;
     };
     set_tile();
     int ra[4], rb[4];
@@ -617,8 +627,9 @@ __global__ void __launch_bounds__(512) gemm_chain(const ChainParams cp) {
 
     struct Set {
         float ws[2];
+        float xs;  // per 128: the activation scale of this lane's staging row
     };
-    Set s0, s1, s2;  // group g's weight scales in set g mod 3
+    Set s0, s1, s2;  // group g's scales in set g mod 3
     // the wave's loads of group g: its share of one operand's stage, then its two weight scales
     const auto issue = [&](int g, lds_u32x4* xd, lds_u32x4* wd, Set& s) {
         const int k0 = g * 128;
@@ -632,6 +643,18 @@ __global__ void __launch_bounds__(512) gemm_chain(const ChainParams cp) {
                                                      woff[e], k0, 0, 0);
         s.ws[0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(wsres, ws_off0, g * 4, 0));
         s.ws[1] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(wsres, ws_off1, g * 4, 0));
+        if constexpr (!PER_TOKEN)
+            s.xs = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(xsres, xs_off, (g >> p.act_shift) * 4, 0));
+    };
+    int xb = 0;  // ring slot of the current tile's group 0
+    // per 128: group g's scales (landed) from set s into their ring slot; the LDS write is complete on return
+    const auto put_xs = [&](int g, const Set& s) __attribute__((always_inline)) {
+        if constexpr (!PER_TOKEN) {
+            // every lane writes (lanes l, l + 16, l + 32, l + 48 the same value): no branch, which costs the kernel its
+            // registers
+            lds_xs[(xb + g) & 3][16 * wave + lane % 16] = s.xs;
+            wait_vm_lgkm0<NLD>();
+        }
     };
     const auto barrier = [&]() __attribute__((always_inline)) {
         __builtin_amdgcn_sched_barrier(0);
@@ -645,13 +668,36 @@ __global__ void __launch_bounds__(512) gemm_chain(const ChainParams cp) {
     const i32x16 zero16 = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
     // int32 sums of the blocks in flight: block n = 4 g + b (group g, block b) in T[n mod 3] (with three groups a turn
     // the index is a constant: (4 (g mod 3) + b) mod 3)
-    i32x16 T[3];
+    // Per 128 the links run one block behind (two buffers, index n mod 2): each link also reads 16 activation scales,
+    // and beside a third buffer's 16 registers the SwiGLU -> int8 form spilled 44 registers and took 1.77 against
+    // 1.52 ms at C4's gate/up (the down multiply ran alike both ways). The block's four MFMAs are issued before its
+    // link, so the converts still find the previous block's sums complete.
+    constexpr int NT = PER_TOKEN ? 3 : 2, LAG = NT - 1;
+    i32x16 T[NT];
     u32x4 a[2][4], b[2][4];
-    const auto link = [&](const i32x16& S, int i, int q, float ws, bool first) {
+    // one link: per token acc = f ws (first group) or fma(f, ws, acc); per 128 the scale is ws x xs of the output's
+    // row in group g (the cpu-q8 chain, as gemm_big's)
+    const auto link = [&](const i32x16& S, int i, int q, float ws, bool first, int g) {
+        if constexpr (PER_TOKEN) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const float f = static_cast<float>(S[r]);
-            acc[i][q][r] = first ? __fmul_rn(f, ws) : __builtin_fmaf(f, ws, acc[i][q][r]);
+            for (int r = 0; r < 16; ++r) {
+                const float f = static_cast<float>(S[r]);
+                acc[i][q][r] = first ? __fmul_rn(f, ws) : __builtin_fmaf(f, ws, acc[i][q][r]);
+            }
+        } else {
+            const float* xr = lds_xs[(xb + g) & 3] + wm * 64 + i * 32 + 4 * (lane / 32);
+#pragma unroll
+            for (int r4 = 0; r4 < 4; ++r4) {
+                const float4 x4 = *reinterpret_cast<const float4*>(xr + 8 * r4);
+                const float xv[4] = {x4.x, x4.y, x4.z, x4.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int r = 4 * r4 + e;
+                    const float f = static_cast<float>(S[r]);
+                    const float sc = __fmul_rn(ws, xv[e]);
+                    acc[i][q][r] = first ? __fmul_rn(f, sc) : __builtin_fmaf(f, sc, acc[i][q][r]);
+                }
+            }
         }
     };
 
@@ -661,6 +707,7 @@ __global__ void __launch_bounds__(512) gemm_chain(const ChainParams cp) {
     const auto slot_l = [&](int g, auto jt) __attribute__((always_inline)) {
         constexpr int j = decltype(jt)::value;
         Set& nxt = j == 0 ? s2 : (j == 1 ? s0 : s1);
+        const Set& following = j == 0 ? s1 : (j == 1 ? s2 : s0);  // group g + 1's
         issue(min(g + 2, groups - 1), xstage(std::integral_constant<int, (j + 2) % 3>{}),
               wstage(std::integral_constant<int, (j + 2) % 3>{}), nxt);
         __builtin_amdgcn_sched_barrier(0);
@@ -679,16 +726,20 @@ __global__ void __launch_bounds__(512) gemm_chain(const ChainParams cp) {
         __builtin_amdgcn_sched_barrier(0);
         asm volatile("" ::: "memory");
         wait_vm_lgkm0<NLD>();  // and the wave's loads of group g + 1 (its loads of group g + 2 stay in flight)
+        // (unconditional, as a branch here also costs registers: past the last group the write puts the clamped repeat
+        // into the slot of the next tile's group 0, which held group groups - 4, read by no slot still running; the next
+        // tile writes that slot again after the barriers that end this tile)
+        put_xs(g + 1, following);
         barrier();
     };
-    // M(g): blocks 0..3, each block's four MFMAs with the link of the block two before it (blocks 2 and 3 of group
-    // g - 1 at blocks 0 and 1): those sums were complete a block ago, so the link's converts and fused multiply-adds
-    // interleave with the MFMAs instead of waiting for the last one; every output's links still run in group order. The
-    // last group's blocks 2 and 3 are linked after its M slot.
+    // M(g): blocks 0..3, each block's four MFMAs with the link of the block LAG before it (the last LAG blocks of group
+    // g - 1 at the first LAG blocks), so the link's converts and fused multiply-adds interleave with the MFMAs instead
+    // of waiting for the last one; every output's links still run in group order. The last group's last LAG blocks are
+    // linked after its M slot.
     float pw0 = 0.0f, pw1 = 0.0f;  // group g - 1's weight scales
-    const auto slot_m = [&](auto jt, auto prev_t) __attribute__((always_inline)) {
+    const auto slot_m = [&](int g, auto jt, auto prev_t) __attribute__((always_inline)) {
         constexpr int j = decltype(jt)::value;
-        // 0: group 0 (no previous group; its own links multiply); 1: group 1 (group 0's blocks 2 and 3 link by a
+        // 0: group 0 (no previous group; its own links multiply); 1: group 1 (group 0's last blocks link by a
         // multiply); 2: later groups
         constexpr int pmode = decltype(prev_t)::value;
         constexpr bool first = pmode == 0;
@@ -697,14 +748,15 @@ __global__ void __launch_bounds__(512) gemm_chain(const ChainParams cp) {
 #pragma unroll
         for (int blk = 0; blk < 4; ++blk) {
             const int i = blk / 2, q = blk % 2;
-            i32x16& S = T[(4 * j + blk) % 3];
+            i32x16& S = T[(4 * j + blk) % NT];
 #pragma unroll
             for (int st = 0; st < 4; ++st) S = mfma_i8_32(a[i][st], b[q][st], st == 0 ? zero16 : S);
-            if (blk >= 2) {
-                const int pq = (blk - 2) % 2;
-                link(T[(4 * j + blk - 2) % 3], (blk - 2) / 2, pq, pq == 0 ? gws0 : gws1, first);
+            if (blk >= LAG) {
+                const int pb = blk - LAG;  // this group's block pb
+                link(T[(4 * j + pb) % NT], pb / 2, pb % 2, pb % 2 == 0 ? gws0 : gws1, first, g);
             } else if constexpr (pmode > 0) {
-                link(T[(4 * j + blk + 1) % 3], 1, blk, blk == 0 ? pw0 : pw1, pmode == 1);
+                const int pb = blk + 4 - LAG;  // the previous group's block pb
+                link(T[(4 * j + blk + NT - LAG) % NT], pb / 2, pb % 2, pb % 2 == 0 ? pw0 : pw1, pmode == 1, g - 1);
             }
         }
         pw0 = gws0;
@@ -734,39 +786,41 @@ __global__ void __launch_bounds__(512) gemm_chain(const ChainParams cp) {
 #pragma unroll
                 for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
         wait_vm_lgkm0<NLD>();  // group 0's loads
+        put_xs(0, s0);
         barrier();
         if (group_b) barrier();  // B runs one slot behind A
         // group g in stage and scale set g mod 3; M of group 0 and group 1 by their own modes, then three groups a turn
         slot_l(0, I0{});
-        slot_m(I0{}, I0{});
+        slot_m(0, I0{}, I0{});
         int g = 1;
         if (groups > 1) {
             slot_l(1, I1{});
-            slot_m(I1{}, I1{});
+            slot_m(1, I1{}, I1{});
             g = 2;
         }
         for (; g + 3 <= groups; g += 3) {
             slot_l(g, I2{});
-            slot_m(I2{}, I2{});
+            slot_m(g, I2{}, I2{});
             slot_l(g + 1, I0{});
-            slot_m(I0{}, I2{});
+            slot_m(g + 1, I0{}, I2{});
             slot_l(g + 2, I1{});
-            slot_m(I1{}, I2{});
+            slot_m(g + 2, I1{}, I2{});
         }
         if (g < groups) {
             slot_l(g, I2{});
-            slot_m(I2{}, I2{});
+            slot_m(g, I2{}, I2{});
         }
         if (g + 1 < groups) {
             slot_l(g + 1, I0{});
-            slot_m(I0{}, I2{});
+            slot_m(g + 1, I0{}, I2{});
         }
         if (!group_b) barrier();  // matches group B's extra barrier
-        // the last group's blocks 2 and 3 (group groups - 1, stage index (groups - 1) mod 3)
+        // the last group's last LAG blocks (group groups - 1, stage index (groups - 1) mod 3)
         const auto last_links = [&](auto jt) __attribute__((always_inline)) {
             constexpr int j = decltype(jt)::value;
-            link(T[(4 * j + 2) % 3], 1, 0, pw0, groups == 1);
-            link(T[(4 * j + 3) % 3], 1, 1, pw1, groups == 1);
+#pragma unroll
+            for (int pb = 4 - LAG; pb < 4; ++pb)
+                link(T[(4 * j + pb) % NT], pb / 2, pb % 2, pb % 2 == 0 ? pw0 : pw1, groups == 1, groups - 1);
         };
         switch ((groups - 1) % 3) {
         case 0: last_links(I0{}); break;
@@ -778,6 +832,7 @@ __global__ void __launch_bounds__(512) gemm_chain(const ChainParams cp) {
         const int col[2] = {nc + colrel[0], nc + colrel[1]};
         cur += stride;
         const bool more = cur < hi;
+        xb = (xb + groups) & 3;  // the next tile's group 0 takes the ring slot after this tile's last group
         if constexpr (EP == kSwigluQ8) {
             __syncthreads();
             chain_epilogue<EP, YT, PER_TOKEN>(p, acc, mc, nc, wm, ib, hh, lane, tid, col, reinterpret_cast<float*>(lw0));
@@ -1025,7 +1080,7 @@ void launch_big(const GemmArgs& a, hipStream_t stream) {
     const std::size_t ws_bytes = MODE == MODE_CHAIN ? ((a.n - 1) * a.ld_s + a.k / 128) * 4 : 0;
     const std::size_t xs_bytes = MODE == MODE_CHAIN ? ((a.t - 1) * a.ld_xs + a.k / a.act_block) * 4 : 0;
     const std::size_t lim = std::size_t{1} << 31;
-    if constexpr (MODE == MODE_CHAIN && PT) {
+    if constexpr (MODE == MODE_CHAIN) {
         if (x_bytes < lim && w_bytes < lim && ws_bytes < lim && xs_bytes < lim) {
             const ChainParams cp{p, static_cast<unsigned>(x_bytes), static_cast<unsigned>(w_bytes),
                                  static_cast<unsigned>(ws_bytes), static_cast<unsigned>(xs_bytes)};

@@ -822,24 +822,28 @@ def test_q8_group_sums_exact_with_outliers(sm):
 
 
 @pytest.mark.parametrize("t,n", [(100, 256), (130, 256), (130, 768), (300, 512), (300, 1280), (1000, 2560)])
-def test_q8_per_token_persistent_grids(sm, t, n):
-    """The per-token large-M kernel is persistent (a whole number of blocks per XCD, each walking its XCD's tiles):
-    grids of 1 to 80 tiles, most not a multiple of 8 (the blocks past the tiles leave at once), at config 0. Bit for
-    bit against the oracle's per-token chain, Store and Add."""
-    say("q8 per-token persistent grid", t, n)
-    k = 512
-    rng = np.random.default_rng(t + n)
+@pytest.mark.parametrize("act", ["token", "128"])
+def test_q8_persistent_grids(sm, t, n, act):
+    """The large-M chain kernel is persistent (a whole number of blocks per XCD, each walking its XCD's tiles): grids
+    of 1 to 80 tiles, most not a multiple of 8 (the blocks past the tiles leave at once), at config 0, with one
+    activation scale per token or per 128 values (the per-128 scales pass through a ring of LDS slots that runs on
+    from tile to tile; K = 640 is 5 groups, so consecutive tiles start at different slots). Bit for bit against the
+    oracle's chain, Store and Add."""
+    say("q8 persistent grid", t, n, act)
+    k = 640
+    ab = k if act == "token" else 128
+    rng = np.random.default_rng(t + n + ab)
     x = bf16_inputs(rng, (t, k), outlier_frac=0.01)
     w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
-    xq, xs = sm.quantize_rows_s8(dev(x, torch.bfloat16), block=k)
+    xq, xs = sm.quantize_rows_s8(dev(x, torch.bfloat16), block=ab)
     wq, ws = sm.quantize_group_s8(dev(w), rule=1)
-    y = host(sm.gemm_q8(xq, xs, wq, ws, act_block=k, config=0))
-    ref = orc.gemm_q8(host(xq), host(xs), host(wq), host(ws), act_block=k)
+    y = host(sm.gemm_q8(xq, xs, wq, ws, act_block=ab, config=0))
+    ref = orc.gemm_q8(host(xq), host(xs), host(wq), host(ws), act_block=ab)
     assert same_bits(y, ref)
     base = rng.standard_normal((t, n)).astype(np.float32)
     ya = dev(base)
-    sm.gemm_q8(xq, xs, wq, ws, y=ya, epilogue=sm.ADD, act_block=k, config=0)
-    assert same_bits(host(ya), orc.gemm_q8(host(xq), host(xs), host(wq), host(ws), act_block=k, epilogue=orc.ADD, y=base))
+    sm.gemm_q8(xq, xs, wq, ws, y=ya, epilogue=sm.ADD, act_block=ab, config=0)
+    assert same_bits(host(ya), orc.gemm_q8(host(xq), host(xs), host(wq), host(ws), act_block=ab, epilogue=orc.ADD, y=base))
 
 
 @pytest.mark.parametrize("t,n,k", [(1, 19456, 2560), (16, 19456, 2560), (1, 2560, 9728), (16, 2560, 9728), (5, 1024, 512)])
