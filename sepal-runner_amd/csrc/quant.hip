@@ -147,6 +147,44 @@ __global__ void __launch_bounds__(256) quantize_rows_token_kernel(const void* __
         for (int i = 1; i < 4; ++i) m = red[i] > m ? red[i] : m;
         return m;
     };
+    if (ST != SEPAL_HIP_F32 && chunks <= 256 * kTokChunks) {
+        // 16-bit rows stay in registers as loaded (half the registers of the float32 values) and are widened twice,
+        // for the maximum and for the quantization: 84-85 against 89-92 us at C4's H (15872 x 9728), same bits
+        u32x4 raw[kTokChunks];
+        float m = 0.0f;
+#pragma unroll
+        for (int j = 0; j < kTokChunks; ++j) {
+            const int c = threadIdx.x + 256 * j;
+            raw[j] = c < chunks ? *reinterpret_cast<const u32x4*>(static_cast<const unsigned short*>(x) + row * ld_x + 8 * c) : u32x4{0u, 0u, 0u, 0u};
+        }
+#pragma unroll
+        for (int j = 0; j < kTokChunks; ++j) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const unsigned short b = static_cast<unsigned short>(raw[j][i / 2] >> (16 * (i % 2)));
+                const float a = fabsf(ST == SEPAL_HIP_BF16 ? bf16_bits_to_f32(b) : f16_bits_to_f32(b));
+                m = a > m ? a : m;
+            }
+        }
+        m = block_max(m);
+        const float scale = m > 0.0f ? __fdiv_rn(m, 127.0f) : 1.0f;
+        const float inverse = __fdiv_rn(1.0f, scale);
+        if (threadIdx.x == 0) scales[row * ld_s] = scale;
+#pragma unroll
+        for (int j = 0; j < kTokChunks; ++j) {
+            const int c = threadIdx.x + 256 * j;
+            if (c >= chunks) continue;
+            unsigned packed[2] = {0u, 0u};
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const unsigned short b = static_cast<unsigned short>(raw[j][i / 2] >> (16 * (i % 2)));
+                const float v = ST == SEPAL_HIP_BF16 ? bf16_bits_to_f32(b) : f16_bits_to_f32(b);
+                packed[i / 4] |= (static_cast<unsigned>(quantize_value<SEPAL_HIP_RULE_RECIPROCAL>(v, scale, inverse)) & 0xFFu) << (8 * (i % 4));
+            }
+            *reinterpret_cast<uint2*>(q + row * ld_q + 8 * c) = make_uint2(packed[0], packed[1]);
+        }
+        return;
+    }
     if (chunks <= 256 * kTokChunks) {
         float v[kTokChunks][8];
         float m = 0.0f;
