@@ -82,3 +82,63 @@ def test_release_returns_device_memory(sm):
     s.synchronize()
     assert torch.equal(y, want)
     sm.release_workspace(stream=s)
+
+
+def test_host_threads_share_the_library(sm):
+    """Two host threads, each on its own stream, call the library at once (the bindings drop the interpreter lock
+    during each call, so the library's host code runs concurrently): the M <= 16 stack (w8g and q8), the large-M w8g
+    multiply and the per-128 q8 multiply, five times each. The library's per-process state (the workspaces keyed by
+    stream, the kernels' dynamic-LDS limits, the occupancy caches) is shared between them, and the threads come
+    first, so that in a fresh process they also meet each kernel's first launch together; every output equals the
+    one computed afterwards on one thread, bit for bit."""
+    import threading
+
+    H, I = 2560, 9728
+    g = torch.Generator(device="cuda").manual_seed(11)
+    layers = []
+    for _ in range(2):
+        gate = (torch.randn(I, H, generator=g, device="cuda") * 0.02).half()
+        up = (torch.randn(I, H, generator=g, device="cuda") * 0.02).half()
+        down = (torch.randn(H, I, generator=g, device="cuda") * 0.02).half()
+        layers.append((*sm.quantize_gate_up_s8(gate, up, rule=sm.RULE_RECIPROCAL),
+                       *sm.quantize_group_s8(down, rule=sm.RULE_RECIPROCAL)))
+    x16 = torch.randn(16, H, generator=g, device="cuda").bfloat16()
+    x300 = torch.randn(300, H, generator=g, device="cuda").bfloat16()
+    xq, xs = sm.quantize_rows_s8(x300, block=128)
+    wgu, sgu, wd, sd = layers[0]
+
+    def work(stream):
+        outs = []
+        for kind in (0, 1):
+            xc = x16.clone()
+            y = torch.empty(16, H, dtype=torch.float32, device="cuda")
+            sm.mlp_stack(kind, xc, layers, y=y, act_block=128, stream=stream)
+            outs.append(y)
+        outs.append(sm.gemm_w8g(x300, wgu, sgu, epilogue=sm.SWIGLU, y_dtype=torch.float16, stream=stream))
+        outs.append(sm.gemm_q8(xq, xs, wgu, sgu, act_block=128, stream=stream))
+        return outs
+
+    results = {}
+
+    def run(tid):
+        s = torch.cuda.Stream()
+        with torch.cuda.stream(s):
+            for it in range(5):
+                results[(tid, it)] = work(s)
+        s.synchronize()
+
+    say("host threads: two threads, five rounds each")
+    threads = [threading.Thread(target=run, args=(t,)) for t in range(2)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=60)
+    assert not any(t.is_alive() for t in threads)
+    torch.cuda.synchronize()
+    assert len(results) == 10
+    say("host threads: reference on one thread")
+    want = work(torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    for key, outs in results.items():
+        for a, b in zip(outs, want):
+            assert torch.equal(a, b), key
