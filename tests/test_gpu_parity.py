@@ -846,6 +846,37 @@ def test_q8_persistent_grids(sm, t, n, act):
     assert same_bits(host(ya), orc.gemm_q8(host(xq), host(xs), host(wq), host(ws), act_block=ab, epilogue=orc.ADD, y=base))
 
 
+@pytest.mark.parametrize("act", ["token", "128"])
+@pytest.mark.parametrize("epi", ["store", "swiglu"])
+def test_q8_large_path_strided_operands(sm, act, epi):
+    """The large-M chain with padded rows: X, its scales and Y as column slices of wider buffers (the scales' row
+    stride sets each staging lane's offset, per 128 too), against the same call on contiguous copies, bit for bit."""
+    say("q8 strided operands", act, epi)
+    t, n, k = 300, 512, 640
+    ab = k if act == "token" else 128
+    rng = np.random.default_rng(17)
+    x = bf16_inputs(rng, (t, k), outlier_frac=0.01)
+    gate = (rng.standard_normal((n // 2, k)) * 0.02).astype(np.float32)
+    up = (rng.standard_normal((n // 2, k)) * 0.02).astype(np.float32)
+    if epi == "swiglu":
+        wq, ws = sm.quantize_gate_up_s8(dev(gate), dev(up), rule=1)
+    else:
+        wq, ws = sm.quantize_group_s8(dev(np.concatenate([gate, up])), rule=1)
+    xq, xs = sm.quantize_rows_s8(dev(x, torch.bfloat16), block=ab)
+    ep = sm.SWIGLU if epi == "swiglu" else sm.STORE
+    want = host(sm.gemm_q8(xq, xs, wq, ws, epilogue=ep, act_block=ab, config=0))
+    xqw = torch.zeros(t, k + 48, dtype=torch.int8, device="cuda")
+    xqw[:, :k] = xq
+    xsw = torch.full((t, xs.shape[1] + 3), -1.0, dtype=torch.float32, device="cuda")
+    xsw[:, :xs.shape[1]] = xs
+    cols = n // 2 if epi == "swiglu" else n
+    yw = torch.full((t, cols + 16), 7.0, dtype=torch.float32, device="cuda")
+    sm.gemm_q8(xqw[:, :k], xsw[:, :xs.shape[1]], wq, ws, y=yw[:, :cols], epilogue=ep, act_block=ab, config=0)
+    got = host(yw)
+    assert same_bits(got[:, :cols], want)
+    assert np.all(got[:, cols:] == 7.0)
+
+
 @pytest.mark.parametrize("t,n,k", [(1, 19456, 2560), (16, 19456, 2560), (1, 2560, 9728), (16, 2560, 9728), (5, 1024, 512)])
 def test_q8_small_m_group_sums_exact(sm, t, n, k):
     """At T <= 16 the group sums come from the M <= 16 stack's pass kernels (the gate/up pass with its interleaved
