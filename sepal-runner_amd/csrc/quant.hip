@@ -286,6 +286,7 @@ __global__ void __launch_bounds__(256) quantize_rows_token_any_kernel(const void
 // L / 8, lane L % 8, and adds x[c]^2 for c = L, L + 32, ... in order (then, for a tail of 8 to 31 columns, lanes 0..7
 // take the remaining groups of 8). The combine and the normalising pass follow the reference.
 constexpr int kNormSeg = 2560;  // columns per LDS segment and wave (a whole row of the MLP width)
+static_assert(kNormSeg % 512 == 0, "a segment is loaded in rounds of 512 columns (8 per lane)");
 
 // OUT: NORM_STORE writes y (YT); NORM_Q_TOKEN and NORM_Q_128 round each value to bfloat16 (y, when not null, gets those
 // bits) and quantize the rounded values as quantize_rows does (one scale per row, or per 128 columns).
